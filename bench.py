@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark of the gated-mixture Linear on one MI355X.
+
+Workload (the headline shape): one gated Linear 5120 -> 17408 over 8192 tokens
+with K = 6 candidates (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0).  A step is the
+forward (mix W_eff + Y = X W_eff^T) and the backward (dX = dY W_eff and the
+gate gradients <dY^T X, W_k>), called through the C ABI with every input
+already resident in HBM.  value = 6*M*N*D / step time (TFLOP/s).
+
+Also reported in the same JSON line:
+  roofline      the dominant GEMM's achieved TFLOP/s against the bf16 MFMA peak
+                (HIP events on the stream the kernels run on)
+  kernels_ms    per-kernel average durations
+  dequant_gbps  dequant microbench (4096 x 14336, each format): algorithmic
+                bytes (packed read + fp32 write) / time, against 8 TB/s
+  cpu_baseline  the oracle's fp32 torch restatement of the reference step on
+                the host cores, on a row sample of the same layer
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "voodoo-dyn-quant_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "gated-Linear fwd+bwd TFLOP/s + dequant HBM GB/s (% roofline); train tokens/sec"
+TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
+GGML = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+BLOCK = {"Q8_0": (32, 34), "Q2_K": (256, 84), "Q3_K": (256, 110), "Q4_K": (256, 144), "Q5_K": (256, 176),
+         "Q6_K": (256, 210)}
+F16_OFFSETS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,)}
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBPS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def synthetic_qbytes(torch, qt: str, nrows: int, ncols: int, dev, gen):
+    """Random valid GGUF blocks generated on the device: random payload bytes,
+    fp16 scale fields drawn from normal numbers in [2^-8, 2)."""
+    bs, bb = BLOCK[qt]
+    nblocks = nrows * ncols // bs
+    q = torch.randint(0, 256, (nblocks, bb), dtype=torch.uint8, device=dev, generator=gen)
+    for off in F16_OFFSETS[qt]:
+        h = torch.randint(0, 1 << 16, (nblocks,), dtype=torch.int32, device=dev, generator=gen)
+        h = (h & 0x83FF) | (0x1C00 + ((h >> 10) & 0x7) * 0x0400)  # exponent 7..14
+        q[:, off] = (h & 0xFF).to(torch.uint8)
+        q[:, off + 1] = ((h >> 8) & 0xFF).to(torch.uint8)
+    return q.reshape(-1)
+
+
+def time_events(torch, fn, reps: int) -> float:
+    """Average milliseconds of fn() over reps, HIP events on the current stream."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def cpu_baseline(torch, m: int, n_total: int, d: int, budget_s: float = 12.0) -> dict:
+    """The reference step on the host: oracle fp32 torch restatement of
+    _MixedWeightFunction + F.linear + autograd backward (voodoo_quant/
+    layers.py:336-363), on rows [0, n_s) of the layer with all m tokens."""
+    import numpy as np
+
+    from oracle import cdequant, mixture
+
+    n_s = 256
+    g = torch.Generator().manual_seed(0)
+    rng = np.random.default_rng(0)
+    cands = []
+    for qt in TYPES:
+        bs, bb = BLOCK[qt]
+        qb = rng.integers(0, 256, size=(n_s * d // bs, bb), dtype=np.uint16).astype(np.uint8)
+        for off in F16_OFFSETS[qt]:
+            h = rng.integers(0, 1 << 16, size=qb.shape[0]).astype(np.uint16)
+            h = (h & 0x83FF) | (np.uint16(0x1C00) + ((h >> 10) & 0x7) * np.uint16(0x0400))
+            qb[:, off], qb[:, off + 1] = (h & 0xFF).astype(np.uint8), (h >> 8).astype(np.uint8)
+        cands.append(torch.from_numpy(cdequant.oracle_dequant_parallel(qt, qb, n_s * d).reshape(n_s, d)))
+    x = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    dy = torch.randn(m, n_s, generator=g).to(torch.bfloat16)
+    gates = torch.randn(len(TYPES), generator=g)
+    mixture.reference_step_fp32(x, dy, cands, gates, 1.0)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < 2:
+        t0 = time.perf_counter()
+        mixture.reference_step_fp32(x, dy, cands, gates, 1.0)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    t = sorted(times)[len(times) // 2]
+    flops = mixture.gated_linear_flops(m, n_s, d)
+    return {
+        "value": round(flops / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle fp32 torch step on rows 0..{n_s - 1} of the 5120->17408 layer (all {m} tokens, K=6), "
+                  f"median of {len(times)} steps, {t * 1e3:.1f} ms/step; per-row work is the same as the full layer",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the gated Linear's multi-GPU sharding is a design note, not a run)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from voodoo_quant import _hip
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    m, n, d = 8192, 17408, 5120
+    d_pad = d
+    ids = [GGML[t] for t in TYPES]
+    gen = torch.Generator(device=dev).manual_seed(0)
+    log(f"building synthetic candidates {TYPES} for {n}x{d}")
+    qbytes = [synthetic_qbytes(torch, qt, n, d_pad, dev, gen) for qt in TYPES]
+    x = torch.randn(m, d, device=dev, generator=gen).to(torch.bfloat16)
+    dy = torch.randn(m, n, device=dev, generator=gen).to(torch.bfloat16)
+    probs = torch.softmax(torch.randn(len(TYPES), device=dev, generator=gen), 0)
+    w_eff = torch.empty(n, d_pad, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    dx = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    dp = torch.empty(len(TYPES), dtype=torch.float32, device=dev)
+    ws = torch.empty(_hip.bwd_workspace_bytes(n, d, d_pad, len(TYPES), False), dtype=torch.uint8, device=dev)
+
+    def fwd():
+        _hip.gated_linear_fwd(x, ids, qbytes, probs, n, d_pad, w_eff, y)
+
+    def bwd():
+        _hip.gated_linear_bwd(dy, x, ids, qbytes, probs, n, d_pad, w_eff, dx, dp, ws)
+
+    def step():
+        fwd()
+        bwd()
+
+    log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) / max(args.steps, 1) * 1e3
+    flops = 6.0 * m * n * d
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"step {ms:.3f} ms -> {tflops:.1f} TFLOP/s")
+
+    # per-kernel durations (HIP events on torch's current stream, which the C ABI uses)
+    reps = 5
+    t_mix = time_events(torch, lambda: _hip.mix_weight(ids, qbytes, probs, n, d_pad, w_eff), reps)
+    t_fwd = time_events(torch, fwd, reps)
+    t_dx = time_events(torch, lambda: _hip.gated_linear_bwd(dy, x, ids, qbytes, probs, n, d_pad, w_eff, dx, None,
+                                                            None), reps)
+    t_gate = time_events(torch, lambda: _hip.gated_linear_bwd(dy, x, ids, qbytes, probs, n, d_pad, w_eff, None, dp,
+                                                              ws), reps)
+    gemm_flops = 2.0 * m * n * d
+    kernels = {"mix_w_eff": t_mix, "fwd_gemm": t_fwd - t_mix, "dx_gemm": t_dx, "gate_gemm": t_gate}
+    dom = max(("fwd_gemm", "dx_gemm", "gate_gemm"), key=lambda k: kernels[k])
+    achieved = gemm_flops / (kernels[dom] * 1e-3) / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get(dom)
+    log("kernels ms: " + ", ".join(f"{k} {v:.3f}" for k, v in kernels.items()))
+
+    # dequant microbench, 4096 x 14336
+    dq = {}
+    nr, nc = 4096, 14336
+    out = torch.empty(nr, nc, dtype=torch.float32, device=dev)
+    for qt in TYPES:
+        qb = synthetic_qbytes(torch, qt, nr, nc, dev, gen)
+        t = time_events(torch, lambda: _hip.dequant(GGML[qt], qb, nr, nc, out), 10)
+        nbytes = qb.numel() + 4 * nr * nc
+        dq[qt] = {"GBps": round(nbytes / (t * 1e-3) / 1e9, 1), "ms": round(t, 4),
+                  "frac": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 3)}
+        del qb
+    log("dequant GB/s: " + ", ".join(f"{k} {v['GBps']}" for k, v in dq.items()))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(torch, m, n, d)
+
+    rec = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "gated Linear fwd+bwd, 8192 tokens x 5120->17408, K=6 candidates",
+            "tokens": m, "in_features": d, "out_features": n, "candidates": TYPES,
+            "candidate_bytes": "random valid GGUF blocks (no libggml on the box)",
+        },
+        "roofline": {
+            "kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+        },
+        "kernels_ms": {k: round(v, 4) for k, v in kernels.items()},
+        "dequant_gbps": dq,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

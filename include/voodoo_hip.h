@@ -1,0 +1,97 @@
+/*
+ * voodoo_hip.h - C ABI of libvoodoo_hip.so, the MI355X (gfx950) kernels of the
+ * gated-mixture Linear:
+ *
+ *     W_eff = sum_k softmax(g / T)_k * W_k        (K GGUF-packed candidates)
+ *     Y     = X . W_eff^T
+ *     dX    = dY . W_eff,   dL/dp_k = <dY^T X, W_k>
+ *
+ * Conventions
+ *   - Matrices are row-major.  bf16 values travel as uint16_t bit patterns.
+ *   - qtype is the ggml type id: 8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K,
+ *     14 Q6_K.  A candidate is the ggml byte stream of an [N][D_pad] weight
+ *     (rows back to back, D_pad a multiple of 256 as in the reference's
+ *     256-padding of in_features, voodoo_quant/layers.py:973-997).
+ *   - Every pointer except `stream` and the host arrays `qtypes`/`qbytes` is a
+ *     device pointer.  The caller owns all memory; the library allocates none.
+ *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = the default
+ *     stream) and never synchronise the host.
+ *   - Return value: VQ_OK or a VQ_ERR_* code; vq_last_error_string() gives the
+ *     message of the calling thread's last failure.  Validation errors mirror
+ *     the reference's ValueError cases (ggml.py:195-198, 242-253).
+ */
+#ifndef VOODOO_HIP_H
+#define VOODOO_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VQ_OK 0
+#define VQ_ERR_QTYPE 1       /* unsupported quant type */
+#define VQ_ERR_ALIGN 2       /* block or vector alignment violated */
+#define VQ_ERR_NULL 3        /* a required pointer is NULL */
+#define VQ_ERR_SHAPE 4       /* inconsistent or unsupported sizes */
+#define VQ_ERR_HIP 5         /* a HIP runtime call failed */
+#define VQ_ERR_WORKSPACE 6   /* workspace missing or too small */
+
+/* Library ABI version (major * 100 + minor). */
+int vq_version(void);
+
+/* Message of the calling thread's most recent failed call ("" if none). */
+const char *vq_last_error_string(void);
+
+/* Bytes of one 256-weight group of `qtype` (Q8_0: eight 34-byte blocks = 272),
+ * 0 when the type is unsupported.  Replaces QuantTypeInfo.block_bytes /
+ * block_size arithmetic of voodoo_quant/ggml.py:30-48 for the six formats. */
+int64_t vq_group_bytes(int qtype);
+
+/* Packed size of an [nrows][ncols] tensor, or -1 when ncols is not a multiple
+ * of the type's block size (the reference's ValueError, ggml.py:195-198). */
+int64_t vq_qbytes_size(int qtype, int64_t nrows, int64_t ncols);
+
+/* Host-side checks of a candidate set (no GPU work): supported types, D_pad a
+ * multiple of 256, D <= D_pad, N and D multiples of 8, 1 <= ncand <= 12. */
+int vq_validate_candidates(int ncand, const int *qtypes, int64_t n, int64_t d, int64_t d_pad);
+
+/* out[nrows*ncols] fp32 = ggml dequantize_row_<qtype>(qbytes) bit for bit.
+ * Replaces dequantize_tensor_gpu (voodoo_quant/layers.py:298-319) and the
+ * per-type torch decoders (layers.py:62-213). */
+int vq_dequant(int qtype, const void *qbytes, float *out, int64_t nrows, int64_t ncols, void *stream);
+
+/* w_eff[n][d_pad] bf16 = bf16(sum_k probs[k] * dequant(qbytes[k])), mixed in
+ * fp32 in k order with separately rounded products and sums.  Replaces
+ * _MixedWeightFunction.forward (voodoo_quant/layers.py:336-352). */
+int vq_mix_weight(int ncand, const int *qtypes, const void *const *qbytes, const float *probs, int64_t n,
+                  int64_t d_pad, uint16_t *w_eff, void *stream);
+
+/* Forward of the gated Linear: mixes W_eff into `w_eff` ([n][d_pad] bf16,
+ * caller-owned, kept for the backward) and writes y[m][n] = x[m][d] . W_eff^T.
+ * Replaces get_mixed_weight + F.linear in MixedQuantLinear.forward
+ * (voodoo_quant/layers.py:1729-1731). */
+int vq_gated_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                        const int *qtypes, const void *const *qbytes, const float *probs, uint16_t *w_eff,
+                        uint16_t *y, void *stream);
+
+/* Workspace bytes vq_gated_linear_bwd needs (gate partials; plus the W_eff
+ * buffer when it will be called with w_eff == NULL and dx != NULL). */
+int64_t vq_gated_linear_bwd_workspace(int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff);
+
+/* Backward of the gated Linear.  dx (nullable) = dy . W_eff;
+ * dprobs (nullable) [ncand] fp32 = <dy^T x, W_k> with the dW tiles kept in
+ * registers (never written) and the candidates decoded exactly.  `w_eff` is
+ * the forward's buffer, or NULL to re-mix into the workspace.  Replaces the
+ * F.linear autograd backward and _MixedWeightFunction.backward
+ * (voodoo_quant/layers.py:354-363). */
+int vq_gated_linear_bwd(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
+                        int ncand, const int *qtypes, const void *const *qbytes, const float *probs,
+                        const uint16_t *w_eff, uint16_t *dx, float *dprobs, void *workspace, int64_t ws_bytes,
+                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOODOO_HIP_H */

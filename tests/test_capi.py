@@ -1,0 +1,78 @@
+"""The C ABI library loads and exports every entry point of include/voodoo_hip.h;
+host-side validation returns the documented error codes (no GPU work)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from voodoo_quant import _hip
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "voodoo_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.lib()
+    names = declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in voodoo_hip.h but not exported"
+    assert set(names) == set(_hip.EXPORTED), "ctypes binding and header disagree"
+
+
+def test_version_and_group_bytes():
+    lib = _hip.lib()
+    assert lib.vq_version() >= 100
+    expect = {8: 272, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210}
+    for t, gb in expect.items():
+        assert _hip.group_bytes(t) == gb
+    assert _hip.group_bytes(16) == 0  # IQ2_XXS: no HIP decoder
+
+
+def test_qbytes_size_matches_reference_arithmetic():
+    from voodoo_quant.ggml import get_quant_info
+
+    for qt in ("Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"):
+        info = get_quant_info(qt)
+        assert _hip.qbytes_size(info.ggml_type, 17, 1024) == 17 * 1024 // info.block_size * info.block_bytes
+    with pytest.raises(ValueError, match="in_features"):
+        _hip.qbytes_size(12, 4, 100)  # Q4_K needs 256-aligned rows (ggml.py:195-198)
+
+
+def test_validate_candidates_errors():
+    lib = _hip.lib()
+    ok = (ctypes.c_int * 2)(8, 12)
+    assert lib.vq_validate_candidates(2, ok, 64, 512, 512) == _hip.VQ_OK
+    assert lib.vq_validate_candidates(2, ok, 64, 512, 500) == _hip.VQ_ERR_ALIGN
+    assert b"256" in lib.vq_last_error_string()
+    bad = (ctypes.c_int * 2)(8, 16)
+    assert lib.vq_validate_candidates(2, bad, 64, 512, 512) == _hip.VQ_ERR_QTYPE
+    assert lib.vq_validate_candidates(0, ok, 64, 512, 512) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_validate_candidates(2, ok, 64, 768, 512) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_validate_candidates(2, ok, 60, 512, 512) == _hip.VQ_ERR_ALIGN
+    assert lib.vq_validate_candidates(2, None, 64, 512, 512) == _hip.VQ_ERR_NULL
+    with pytest.raises(ValueError):
+        _hip.validate_candidates([8, 99], 64, 512, 512)
+
+
+def test_null_pointers_rejected_before_any_gpu_work():
+    lib = _hip.lib()
+    types = (ctypes.c_int * 1)(8)
+    assert lib.vq_dequant(8, None, None, 4, 256, None) == _hip.VQ_ERR_NULL
+    assert lib.vq_dequant(99, None, None, 4, 256, None) == _hip.VQ_ERR_QTYPE
+    assert lib.vq_mix_weight(1, types, None, None, 8, 256, None, None) == _hip.VQ_ERR_NULL
+    assert lib.vq_gated_linear_fwd(None, 4, 8, 256, 256, 1, types, None, None, None, None, None) == _hip.VQ_ERR_NULL
+
+
+def test_workspace_size():
+    n = _hip.bwd_workspace_bytes(17408, 5120, 5120, 6, False)
+    tiles = (17408 // 256) * (5120 // 256)
+    assert n >= tiles * 6 * 4 and n % 256 == 0
+    assert _hip.bwd_workspace_bytes(17408, 5120, 5120, 6, True) >= n + 17408 * 5120 * 2

@@ -1,0 +1,255 @@
+"""Host logic of the drop-in package (CPU only): registry, RTN candidate bytes,
+candidate cache, module construction, budget, temperature, ST-Gumbel, menus,
+TP slicing and the refusal to run the mixture off-GPU.
+
+Ports of the reference's CPU assertions: tests/test_ggml.py:13-33,
+tests/test_invariants.py:20-52, 57-128."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cdequant
+from voodoo_quant import cache, ggml, layers, rtn
+from voodoo_quant.training import trainer
+
+SIX = ["Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"]
+
+
+def test_registry_and_ladder():
+    types = ggml.list_quant_types()
+    assert "IQ4_XS" in types and "Q8_0" in types and "Q2_K" in types and "Q3_K" in types
+    ladder = ggml.QUANT_LADDER
+    assert set(ladder) <= set(types)
+    bpw = [ggml.bytes_per_weight(qt) for qt in ladder]
+    assert bpw == sorted(bpw)
+    assert ggml.get_quant_info("Q2_K").ggml_type == 10 and ggml.get_quant_info("Q2_K").block_bytes == 84
+    assert ggml.get_quant_info("Q3_K").ggml_type == 11 and ggml.get_quant_info("Q3_K").block_bytes == 110
+    assert ggml.get_quant_info("Q3_K").dequant_func == "dequantize_row_q3_K"
+
+
+def test_default_candidates_exclude_ternary():
+    cands = ggml.default_candidate_types()
+    assert "TQ1_0" not in cands and "TQ2_0" not in cands
+    assert cands[0] == "IQ1_S" and cands[-1] == "Q8_0"
+
+
+def test_bytes_per_weight_matches_registry():
+    assert ggml.bytes_per_weight("Q8_0") == pytest.approx(34 / 32)
+    assert ggml.bytes_per_weight("Q2_K") == pytest.approx(84 / 256)
+    with pytest.raises(ValueError):
+        ggml.get_quant_info("NOT_A_QUANT")
+
+
+@pytest.mark.parametrize("qt", SIX)
+def test_rtn_blocks_are_valid_and_accurate(qt):
+    torch.manual_seed(0)
+    w = torch.randn(8, 512)
+    qb = rtn.rtn_quantize_tensor(w, qt)
+    bs, bb = rtn.BLOCK[qt]
+    assert qb.shape == (8 * 512 // bs, bb)
+    y = torch.from_numpy(cdequant.oracle_dequant(qt, qb.numpy(), w.numel()).reshape(w.shape))
+    err = ((y - w).abs().mean() / w.abs().mean()).item()
+    ceil = {"Q8_0": 0.02, "Q6_K": 0.05, "Q5_K": 0.08, "Q4_K": 0.12, "Q3_K": 0.25, "Q2_K": 0.45}[qt]
+    assert err < ceil, f"{qt} roundtrip error {err:.3f}"
+
+
+def test_rtn_error_ladder_is_monotone():
+    torch.manual_seed(1)
+    w = torch.randn(16, 1024) * 0.02
+    errs = []
+    for qt in ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]:
+        y = cdequant.oracle_dequant(qt, rtn.rtn_quantize_tensor(w, qt).numpy(), w.numel())
+        errs.append(float(np.abs(y - w.numpy().reshape(-1)).mean()))
+    assert errs == sorted(errs, reverse=True)
+
+
+def test_rtn_q8_0_is_ggml_round_to_nearest():
+    """Q8_0 codes are roundf(x / (amax / 127)) with d stored as fp16."""
+    x = torch.tensor([[0.5, -1.0, 0.25, 0.0] * 8])
+    qb = rtn.rtn_quantize_tensor(x, "Q8_0").numpy()[0]
+    d = np.frombuffer(qb[:2].tobytes(), np.float16)[0]
+    assert d == np.float16(1.0 / 127)
+    q = qb[2:].view(np.int8)
+    assert list(q[:4]) == [64, -127, 32, 0]
+
+
+def test_rtn_rejects_unaligned():
+    with pytest.raises(ValueError):
+        rtn.rtn_quantize_tensor(torch.randn(4, 100), "Q4_K")
+
+
+def test_shape_validation_matches_reference():
+    with pytest.raises(ValueError):
+        ggml.quantize_tensor(torch.randn(4, 100), "Q4_K") if ggml.find_libggml() else \
+            rtn.rtn_quantize_tensor(torch.randn(4, 100), "Q4_K")
+
+
+# ------------------------------------------------------------------ cache
+def test_tensor_hash_is_sha256_of_fp32_bytes():
+    import hashlib
+
+    t = torch.arange(12, dtype=torch.float32).reshape(3, 4)
+    assert cache.tensor_hash(t) == hashlib.sha256(t.numpy().tobytes()).hexdigest()[:16]
+    assert cache.tensor_hash(t.to(torch.bfloat16)) == cache.tensor_hash(t.to(torch.bfloat16).float())
+    assert cache.tensor_hash(None) == "none"
+
+
+def test_cache_paths_and_roundtrip(tmp_path):
+    p = cache.combined_cache_path("model.layers.0.mlp.up_proj", "lazy", "w" * 16, "none", tmp_path)
+    assert p.parent.name == "model_layers_0_mlp_up_proj"
+    assert p.name == f"combined_lazy_w{'w' * 16}_inone.pt"
+    cands = {"Q4_K": torch.arange(144, dtype=torch.uint8).reshape(1, 144)}
+    cache.save_candidates("layers.0.mlp.up_proj", cands, "lazy", "a" * 16, "none", tmp_path)
+    # found under the name with the `model.` prefix too (reference layers.py:1116-1121)
+    got = cache.load_candidates("model.layers.0.mlp.up_proj", ["Q4_K", "Q8_0"], "lazy", "a" * 16, "none", tmp_path)
+    assert list(got) == ["Q4_K"] and torch.equal(got["Q4_K"], cands["Q4_K"])
+    # per-type files are read when the combined file lacks a type
+    pt = cache.candidate_cache_path("layers.0.mlp.up_proj", "Q8_0", "lazy", "a" * 16, "none", tmp_path)
+    cache.atomic_torch_save(torch.zeros(8, 34, dtype=torch.uint8), pt)
+    got = cache.load_candidates("layers.0.mlp.up_proj", ["Q4_K", "Q8_0"], "lazy", "a" * 16, "none", tmp_path)
+    assert set(got) == {"Q4_K", "Q8_0"}
+    assert not list(tmp_path.rglob("*.tmp*"))
+
+
+# ------------------------------------------------------------------ module (host side)
+@pytest.fixture
+def isolated_cache(tmp_path, monkeypatch):
+    monkeypatch.setattr(layers, "CANDIDATE_CACHE_DIR", tmp_path)
+    return tmp_path
+
+
+def _lin(types=("Q2_K", "Q4_K", "Q8_0"), out_f=64, in_f=512, name="test.proj", seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return layers.MixedQuantLinear(in_f, out_f, list(types), torch.randn(out_f, in_f, generator=g) * 0.02,
+                                   tensor_name=name)
+
+
+def test_module_construction_and_cache_reuse(isolated_cache):
+    lin = _lin()
+    assert lin.num_candidates == 3 and lin.gates.shape == (3,)
+    assert lin.padded_in_features == 512
+    assert lin.candidate_source in ("rtn", "ggml")
+    assert list(isolated_cache.rglob("combined_lazy_*.pt"))
+    lin2 = _lin()
+    assert lin2.candidate_source == "cache"
+    for k in range(3):
+        assert torch.equal(getattr(lin, f"_qweight_{k}"), getattr(lin2, f"_qweight_{k}"))
+    assert "_qweight_0" not in lin.state_dict()  # packed bytes are not checkpointed
+
+
+def test_padding_to_256(isolated_cache):
+    lin = _lin(in_f=300, name="pad.proj")
+    assert lin.padded_in_features == 512 and lin.in_features == 300
+    w, im, orig = layers.pad_weight_and_imatrix(torch.ones(2, 300), torch.ones(300) * 2)
+    assert w.shape == (2, 512) and orig == 300 and float(w[:, 300:].abs().sum()) == 0
+    assert float(im[300:].min()) == 1.0 and float(im[:300].max()) == 2.0
+
+
+def test_rejects_types_without_hip_decoder(isolated_cache):
+    with pytest.raises(ValueError, match="HIP decoder"):
+        _lin(types=("IQ2_XXS", "Q8_0"), name="bad.proj")
+
+
+def test_effective_bytes_and_assignment(isolated_cache):
+    lin = _lin()
+    p = lin.soft_probs().detach()
+    expect = sum(float(p[k]) * ggml.bytes_per_weight(qt) * 64 * 512 for k, qt in enumerate(lin.candidate_types))
+    assert float(lin.effective_bytes()) == pytest.approx(expect, rel=1e-6)
+    with torch.no_grad():
+        lin.gates.copy_(torch.tensor([0.0, 2.0, 1.0]))
+    assert lin.get_assignment() == "Q4_K"
+    assert lin.get_assignment_prob() == pytest.approx(float(torch.softmax(lin.gates, 0)[1]))
+    total = layers.total_effective_bytes({"a": lin, "b": _lin(name="b.proj")})
+    assert float(total) > float(lin.effective_bytes())
+
+
+def test_temperature(isolated_cache):
+    lin = _lin()
+    lin.set_temperature(0.0)
+    assert lin.temperature == 1e-6
+    with torch.no_grad():
+        lin.gates.copy_(torch.tensor([0.0, 0.1, 0.0]))
+    lin.set_temperature(0.01)
+    assert float(lin.soft_probs()[1]) > 0.99
+
+
+def test_st_gumbel_hardening(isolated_cache):
+    """Port of tests/test_invariants.py:88-118."""
+    lin = _lin()
+    try:
+        layers.set_st_gumbel(False, 0.0, 1.0)
+        assert torch.allclose(lin.get_probs(), torch.softmax(lin.gates / lin.temperature, 0))
+        layers.set_st_gumbel(True, 1.0, 0.5)
+        for _ in range(10):
+            p = lin.get_probs()
+            assert p.sum() == 1 and ((p == 0) | (p == 1)).all()
+        c = torch.tensor([0.1, 0.9, -0.4])
+        (lin.get_probs() * c).sum().backward()
+        hard = lin.gates.grad.clone()
+        lin.gates.grad = None
+        layers.set_st_gumbel(False, 0.0, 1.0)
+        (lin.get_probs() * c).sum().backward()
+        assert torch.allclose(hard, lin.gates.grad, atol=1e-6)
+    finally:
+        layers.set_st_gumbel(False, 0.0, 1.0)
+
+
+def test_role_menus():
+    base = ["Q8_0", "Q5_K", "Q3_K", "Q2_K"]
+    attn = ["Q5_K", "Q3_K", "Q2_K"]
+    assert "Q8_0" not in layers.resolve_candidate_types("layers.0.self_attn.q_proj", base, attn, None)
+    assert layers.resolve_candidate_types("layers.0.mlp.up_proj", base, attn, None) == base
+
+
+def test_forward_refuses_cpu(isolated_cache):
+    lin = _lin()
+    with pytest.raises(RuntimeError, match="ROCm"):
+        lin(torch.randn(2, 512))
+
+
+def test_row_slice_bit_identical(isolated_cache):
+    """Row slices of candidates equal quantizing the slice (test_invariants.py:20-31)."""
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(8, 1024, generator=g)
+    lin = layers.MixedQuantLinear(1024, 8, ["Q4_K", "Q6_K"], w, tensor_name="slice.proj")
+    lin.shard_rows([(2, 5)])
+    for k, qt in enumerate(["Q4_K", "Q6_K"]):
+        direct = rtn.rtn_quantize_tensor(w[2:5].contiguous(), qt) if lin.candidate_source != "ggml" \
+            else ggml.quantize_tensor(w[2:5].contiguous(), qt)
+        assert torch.equal(getattr(lin, f"_qweight_{k}").reshape(-1), direct.reshape(-1))
+    assert lin.out_features == 3 and lin._full_out_features == 8
+
+
+def test_col_slice_alignment(isolated_cache):
+    lin = layers.MixedQuantLinear(1024, 8, ["Q4_K"], torch.randn(8, 1024), tensor_name="cols.proj")
+    with pytest.raises(ValueError):
+        lin.shard_cols((128, 384))
+    lin.shard_cols((256, 512))
+    assert lin.in_features == 256 and lin.padded_in_features == 256
+
+
+def test_replace_linear_walker(isolated_cache):
+    net = torch.nn.Sequential(torch.nn.Linear(512, 64, bias=False), torch.nn.ReLU(),
+                              torch.nn.Sequential(torch.nn.Linear(64 * 4, 32, bias=False)))
+    # second Linear's in_features (256) after padding stays 256
+    net[2][0] = torch.nn.Linear(256, 32, bias=False)
+    replaced = layers.replace_linear_with_mixed_quant(net, ["Q4_K", "Q8_0"])
+    assert set(replaced) == {"0", "2.0"}
+    assert isinstance(net[0], layers.MixedQuantLinear) and isinstance(net[2][0], layers.MixedQuantLinear)
+    with pytest.raises(NotImplementedError):
+        layers.replace_linear_with_mixed_quant(torch.nn.Sequential(torch.nn.Linear(256, 8)), ["Q4_K"])
+
+
+def test_trainer_calls():
+    assert trainer.anneal_temperature(0, 200, 2.0, 0.1) == 2.0
+    assert trainer.anneal_temperature(199, 200, 2.0, 0.1) == pytest.approx(0.1)
+    meta = {"a": (1, 10), "b": (1, 10), "c": (2, 5)}
+    assert trainer.compute_total_8bit_bytes(meta) == 15.0
+    assert trainer.compute_non_targeted_8bit_bytes(meta, {"a"}) == 5.0
+    assert float(trainer.size_loss(torch.tensor(100.0), 100.0, 0.02)) == 0.0
+    p = torch.nn.Parameter(torch.zeros(3))
+    opt, sched = trainer.build_gate_optimizer([p], lr=0.5, max_steps=10)
+    p.grad = torch.tensor([1.0, -1.0, 0.0])
+    trainer.gate_optimizer_step([p], opt, sched)
+    assert float(p[0]) < 0 < float(p[1]) and p.grad is None or float(p.grad.abs().sum()) == 0

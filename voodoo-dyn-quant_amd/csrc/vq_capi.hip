@@ -1,0 +1,219 @@
+// C ABI of libvoodoo_hip.so (declared in include/voodoo_hip.h): argument
+// validation, error strings and kernel sequencing.  No entry point allocates.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/voodoo_hip.h"
+#include "vq_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return VQ_OK;
+}
+
+int hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(VQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return VQ_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+const char* qtype_name(int qt) {
+    switch (qt) {
+    case vq::Q8_0: return "Q8_0";
+    case vq::Q2_K: return "Q2_K";
+    case vq::Q3_K: return "Q3_K";
+    case vq::Q4_K: return "Q4_K";
+    case vq::Q5_K: return "Q5_K";
+    case vq::Q6_K: return "Q6_K";
+    default: return "?";
+    }
+}
+
+int block_size(int qt) { return qt == vq::Q8_0 ? 32 : 256; }
+
+int check_candidates(int ncand, const int* qtypes, const void* const* qbytes, int64_t n, int64_t d, int64_t d_pad,
+                     bool need_ptrs) {
+    if (ncand < 1 || ncand > vq::kMaxCand)
+        return fail(VQ_ERR_SHAPE, "ncand=%d outside [1, %d]", ncand, vq::kMaxCand);
+    if (!qtypes) return fail(VQ_ERR_NULL, "qtypes is NULL");
+    if (need_ptrs && !qbytes) return fail(VQ_ERR_NULL, "qbytes is NULL");
+    for (int k = 0; k < ncand; ++k) {
+        if (!vq::qtype_supported(qtypes[k]))
+            return fail(VQ_ERR_QTYPE, "candidate %d: unsupported ggml type %d (supported: Q8_0, Q2_K..Q6_K)", k,
+                        qtypes[k]);
+        if (need_ptrs) {
+            if (!qbytes[k]) return fail(VQ_ERR_NULL, "candidate %d (%s): qbytes is NULL", k, qtype_name(qtypes[k]));
+            if (!aligned16(qbytes[k]))
+                return fail(VQ_ERR_ALIGN, "candidate %d (%s): qbytes not 16-byte aligned", k, qtype_name(qtypes[k]));
+        }
+    }
+    if (n <= 0 || d <= 0 || d_pad <= 0) return fail(VQ_ERR_SHAPE, "n=%lld d=%lld d_pad=%lld must be positive",
+                                                   (long long)n, (long long)d, (long long)d_pad);
+    if (d_pad % 256 != 0) return fail(VQ_ERR_ALIGN, "d_pad=%lld is not a multiple of 256", (long long)d_pad);
+    if (d > d_pad) return fail(VQ_ERR_SHAPE, "d=%lld exceeds d_pad=%lld", (long long)d, (long long)d_pad);
+    if (n % 8 != 0 || d % 8 != 0)
+        return fail(VQ_ERR_ALIGN, "n=%lld and d=%lld must be multiples of 8", (long long)n, (long long)d);
+    // GEMM tiles address at most 256 rows of a row-major operand from a rebased
+    // buffer descriptor: keep 256 * 2 * (row length) below 2^30.
+    if (n > (1 << 21) || d_pad > (1 << 21))
+        return fail(VQ_ERR_SHAPE, "n=%lld / d_pad=%lld exceed the 2^21 limit of one dimension", (long long)n,
+                    (long long)d_pad);
+    return VQ_OK;
+}
+
+vq::CandSet make_set(int ncand, const int* qtypes, const void* const* qbytes, int64_t d_pad) {
+    vq::CandSet cs{};
+    cs.ncand = ncand;
+    cs.row_groups = d_pad / 256;
+    for (int k = 0; k < ncand; ++k) {
+        cs.qtype[k] = qtypes[k];
+        cs.qbytes[k] = static_cast<const uint8_t*>(qbytes[k]);
+    }
+    return cs;
+}
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+}  // namespace
+
+extern "C" {
+
+int vq_version(void) { return 100; }
+
+const char* vq_last_error_string(void) { return g_last_error.c_str(); }
+
+int64_t vq_group_bytes(int qtype) { return vq::group_bytes(qtype); }
+
+int64_t vq_qbytes_size(int qtype, int64_t nrows, int64_t ncols) {
+    if (!vq::qtype_supported(qtype)) return fail(VQ_ERR_QTYPE, "unsupported ggml type %d", qtype), -1;
+    if (nrows < 0 || ncols < 0 || ncols % block_size(qtype) != 0) {
+        fail(VQ_ERR_ALIGN, "%s requires in_features %% %d == 0, got %lld", qtype_name(qtype), block_size(qtype),
+             (long long)ncols);
+        return -1;
+    }
+    const int64_t bytes_per_block = qtype == vq::Q8_0 ? 34 : vq::group_bytes(qtype);
+    return nrows * (ncols / block_size(qtype)) * bytes_per_block;
+}
+
+int vq_validate_candidates(int ncand, const int* qtypes, int64_t n, int64_t d, int64_t d_pad) {
+    const int rc = check_candidates(ncand, qtypes, nullptr, n, d, d_pad, false);
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_dequant(int qtype, const void* qbytes, float* out, int64_t nrows, int64_t ncols, void* stream) {
+    if (!vq::qtype_supported(qtype)) return fail(VQ_ERR_QTYPE, "unsupported ggml type %d", qtype);
+    if (!qbytes || !out) return fail(VQ_ERR_NULL, "qbytes/out is NULL");
+    if (nrows < 0 || ncols < 0) return fail(VQ_ERR_SHAPE, "negative size");
+    if (ncols % block_size(qtype) != 0)
+        return fail(VQ_ERR_ALIGN, "%s requires in_features %% %d == 0, got %lld", qtype_name(qtype),
+                    block_size(qtype), (long long)ncols);
+    const int64_t total = nrows * ncols;
+    if (total % 256 != 0)
+        return fail(VQ_ERR_ALIGN, "%s: weight count %lld is not a multiple of 256", qtype_name(qtype),
+                    (long long)total);
+    if (!aligned16(qbytes) || !aligned16(out)) return fail(VQ_ERR_ALIGN, "qbytes/out not 16-byte aligned");
+    int rc = hip_check(vq::launch_dequant(qtype, static_cast<const uint8_t*>(qbytes), out, total / 256,
+                                          static_cast<hipStream_t>(stream)),
+                       "dequant launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_mix_weight(int ncand, const int* qtypes, const void* const* qbytes, const float* probs, int64_t n,
+                  int64_t d_pad, uint16_t* w_eff, void* stream) {
+    int rc = check_candidates(ncand, qtypes, qbytes, n, d_pad, d_pad, true);
+    if (rc != VQ_OK) return rc;
+    if (!probs || !w_eff) return fail(VQ_ERR_NULL, "probs/w_eff is NULL");
+    if (!aligned16(w_eff)) return fail(VQ_ERR_ALIGN, "w_eff not 16-byte aligned");
+    const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);
+    rc = hip_check(vq::launch_mix(cs, probs, w_eff, n * d_pad / 256, static_cast<hipStream_t>(stream)),
+                   "mix launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_gated_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                        const int* qtypes, const void* const* qbytes, const float* probs, uint16_t* w_eff,
+                        uint16_t* y, void* stream) {
+    int rc = check_candidates(ncand, qtypes, qbytes, n, d, d_pad, true);
+    if (rc != VQ_OK) return rc;
+    if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
+    if (!x || !probs || !w_eff || !y) return fail(VQ_ERR_NULL, "x/probs/w_eff/y is NULL");
+    if (!aligned16(x) || !aligned16(w_eff) || !aligned16(y))
+        return fail(VQ_ERR_ALIGN, "x/w_eff/y not 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);
+    rc = hip_check(vq::launch_mix(cs, probs, w_eff, n * d_pad / 256, s), "mix launch");
+    if (rc != VQ_OK) return rc;
+    if (m == 0) return ok();
+    rc = hip_check(vq::launch_gemm_fwd(x, w_eff, d_pad, y, (int)m, (int)n, (int)d, s), "forward GEMM launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int64_t vq_gated_linear_bwd_workspace(int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff) {
+    if (n <= 0 || d <= 0 || ncand < 1 || n > INT32_MAX || d > INT32_MAX) return -1;
+    int64_t bytes = align256(vq::gate_partial_count((int)n, (int)d) * ncand * (int64_t)sizeof(float));
+    if (need_w_eff) bytes += align256(n * d_pad * 2);
+    return bytes;
+}
+
+int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
+                        int ncand, const int* qtypes, const void* const* qbytes, const float* probs,
+                        const uint16_t* w_eff, uint16_t* dx, float* dprobs, void* workspace, int64_t ws_bytes,
+                        void* stream) {
+    int rc = check_candidates(ncand, qtypes, qbytes, n, d, d_pad, true);
+    if (rc != VQ_OK) return rc;
+    if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
+    if (!dy || !x) return fail(VQ_ERR_NULL, "dy/x is NULL");
+    if (!aligned16(dy) || !aligned16(x)) return fail(VQ_ERR_ALIGN, "dy/x not 16-byte aligned");
+    if (dx && !aligned16(dx)) return fail(VQ_ERR_ALIGN, "dx not 16-byte aligned");
+    if (w_eff && !aligned16(w_eff)) return fail(VQ_ERR_ALIGN, "w_eff not 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);
+    const bool remix = dx != nullptr && w_eff == nullptr;
+    const int64_t need = vq_gated_linear_bwd_workspace(n, d, d_pad, ncand, remix ? 1 : 0);
+    const int64_t part_bytes = align256(vq::gate_partial_count((int)n, (int)d) * ncand * (int64_t)sizeof(float));
+    if ((dprobs || remix) && (!workspace || ws_bytes < need))
+        return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
+                    (long long)(workspace ? ws_bytes : 0));
+    if (workspace && !aligned16(workspace)) return fail(VQ_ERR_ALIGN, "workspace not 16-byte aligned");
+    float* partials = static_cast<float*>(workspace);
+    if (dx) {
+        const uint16_t* w = w_eff;
+        if (remix) {
+            if (!probs) return fail(VQ_ERR_NULL, "probs is NULL");
+            uint16_t* wbuf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes);
+            rc = hip_check(vq::launch_mix(cs, probs, wbuf, n * d_pad / 256, s), "mix launch");
+            if (rc != VQ_OK) return rc;
+            w = wbuf;
+        }
+        if (m > 0) {
+            rc = hip_check(vq::launch_gemm_dx(dy, w, d_pad, dx, (int)m, (int)n, (int)d, s), "dX GEMM launch");
+            if (rc != VQ_OK) return rc;
+        }
+    }
+    if (dprobs) {
+        rc = hip_check(vq::launch_gemm_gate(dy, x, cs, partials, (int)m, (int)n, (int)d, s), "gate GEMM launch");
+        if (rc != VQ_OK) return rc;
+        rc = hip_check(vq::launch_gate_reduce(partials, vq::gate_partial_count((int)n, (int)d), ncand, dprobs, s),
+                       "gate reduce launch");
+        if (rc != VQ_OK) return rc;
+    }
+    return ok();
+}
+
+}  // extern "C"

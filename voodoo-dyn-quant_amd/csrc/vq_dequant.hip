@@ -1,0 +1,119 @@
+// HBM-bound streaming kernels: GGUF block dequantisation to fp32 (bit-exact
+// to ggml's dequantize_row_*) and the softmax mixture of K candidates to a bf16
+// W_eff (bit-exact to the fp32 k-ordered mixture of the reference's
+// _MixedWeightFunction.forward, voodoo_quant/layers.py:336-352, followed by
+// the source-dtype cast).
+//
+// Data layout: a candidate is N rows of D_pad/256 groups; every format packs a
+// row's groups contiguously and rows back to back, so the flattened group index
+// g covers weights [256 g, 256 g + 256) of the row-major [N][D_pad] matrix.
+// A workgroup streams kGroupsPerBlock consecutive groups of every candidate
+// into LDS with 16-byte loads (the byte range of 16 groups is a multiple of 16
+// for every format), then each thread decodes runs of 8 weights from LDS and
+// writes them with 16-byte (bf16 x8) or 2x16-byte (fp32 x8) stores.
+#include "vq_internal.h"
+
+namespace vq {
+
+// Copy `len` bytes at `src` (16-byte aligned) to LDS `dst`.
+__device__ __forceinline__ void stage_bytes(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, int len) {
+    const int nvec = len >> 4;
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
+    u32x4* d4 = reinterpret_cast<u32x4*>(dst);
+    for (int i = threadIdx.x; i < nvec; i += blockDim.x) d4[i] = __builtin_nontemporal_load(s4 + i);
+    const int tail = len & 15;
+    if ((int)threadIdx.x < tail) dst[(nvec << 4) + threadIdx.x] = src[(nvec << 4) + threadIdx.x];
+}
+
+template <int QT>
+__global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* __restrict__ q,
+                                                                 float* __restrict__ out, int64_t ngroups) {
+    constexpr int GB = group_bytes(QT);
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kGroupsPerBlock * GB + 16];
+    const int64_t g0 = (int64_t)blockIdx.x * kGroupsPerBlock;
+    const int ng = (int)min<int64_t>(kGroupsPerBlock, ngroups - g0);
+    stage_bytes(lds, q + g0 * GB, ng * GB);
+    __syncthreads();
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kRunsPerThread; ++u) {
+        const int j = (t >> 5) + 8 * u;
+        if (j < ng) {
+            float y[8];
+            decode_run<QT, 8>(lds + j * GB, 8 * (t & 31), y);
+            float4* o = reinterpret_cast<float4*>(out + (g0 + j) * 256 + 8 * (t & 31));
+            o[0] = make_float4(y[0], y[1], y[2], y[3]);
+            o[1] = make_float4(y[4], y[5], y[6], y[7]);
+        }
+    }
+}
+
+hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s) {
+    if (ngroups <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((ngroups + kGroupsPerBlock - 1) / kGroupsPerBlock));
+    switch (qtype) {
+    case Q8_0: dequant_kernel<Q8_0><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q2_K: dequant_kernel<Q2_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q3_K: dequant_kernel<Q3_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q4_K: dequant_kernel<Q4_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q5_K: dequant_kernel<Q5_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q6_K: dequant_kernel<Q6_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Mixture: W_eff = bf16( (((0 + p0 W0) + p1 W1) + ...) ) with every product and
+// sum rounded separately, exactly as the fp32 torch ops of the reference.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kStreamThreads) void mix_kernel(CandSet cs, const float* __restrict__ probs,
+                                                             bf16_t* __restrict__ w_eff, int64_t ngroups) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int64_t g0 = (int64_t)blockIdx.x * kGroupsPerBlock;
+    const int ng = (int)min<int64_t>(kGroupsPerBlock, ngroups - g0);
+    int acc = 0;
+    for (int k = 0; k < cs.ncand; ++k) {
+        const int gb = group_bytes(cs.qtype[k]);
+        stage_bytes(lds + acc, cs.qbytes[k] + g0 * gb, ng * gb);
+        acc += (kGroupsPerBlock * gb + 15) & ~15;
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kRunsPerThread; ++u) {
+        const int j = (t >> 5) + 8 * u;
+        if (j >= ng) continue;
+        float mixed[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) mixed[r] = 0.0f;
+        int off = 0;
+        for (int k = 0; k < cs.ncand; ++k) {
+            const int qt = cs.qtype[k];
+            const int gb = group_bytes(qt);
+            float w[8];
+            decode_run_rt<8>(qt, lds + off + j * gb, 8 * (t & 31), w);
+            off += (kGroupsPerBlock * gb + 15) & ~15;
+            const float pk = probs[k];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) mixed[r] = __fadd_rn(mixed[r], __fmul_rn(pk, w[r]));
+        }
+        uint4 v;
+        v.x = (uint32_t)f2bf(mixed[0]) | ((uint32_t)f2bf(mixed[1]) << 16);
+        v.y = (uint32_t)f2bf(mixed[2]) | ((uint32_t)f2bf(mixed[3]) << 16);
+        v.z = (uint32_t)f2bf(mixed[4]) | ((uint32_t)f2bf(mixed[5]) << 16);
+        v.w = (uint32_t)f2bf(mixed[6]) | ((uint32_t)f2bf(mixed[7]) << 16);
+        *reinterpret_cast<uint4*>(w_eff + (g0 + j) * 256 + 8 * (t & 31)) = v;
+    }
+}
+
+hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int64_t ngroups, hipStream_t s) {
+    if (ngroups <= 0) return hipSuccess;
+    size_t lds = 0;
+    for (int k = 0; k < cs.ncand; ++k) lds += (kGroupsPerBlock * group_bytes(cs.qtype[k]) + 15) & ~15;
+    const dim3 grid((unsigned)((ngroups + kGroupsPerBlock - 1) / kGroupsPerBlock));
+    mix_kernel<<<grid, kStreamThreads, lds, s>>>(cs, probs, w_eff, ngroups);
+    return hipGetLastError();
+}
+
+}  // namespace vq

@@ -1,0 +1,34 @@
+// Internal launch interface between the C-ABI (vq_capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vq_common.h"
+
+namespace vq {
+
+// Workgroup geometry of the streaming kernels: 256 threads, each decoding
+// kRunsPerThread runs of 8 weights, so one workgroup covers
+// kGroupsPerBlock groups of 256 weights.
+constexpr int kStreamThreads = 256;
+constexpr int kRunsPerThread = 2;
+constexpr int kGroupsPerBlock = kStreamThreads * 8 * kRunsPerThread / 256;  // 16
+
+hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s);
+hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int64_t ngroups, hipStream_t s);
+
+// Gated-Linear GEMMs (vq_gemm.hip).  All matrices are row-major bf16.
+//   fwd:  Y[M][N]  = X[M][D] . W[N][D]^T          (W row stride ldw)
+//   dx:   dX[M][D] = dY[M][N] . W[N][D]
+//   gate: part[t][k] = sum over tile t of (dY^T X)[n][d] * W_k[n][d]
+hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D,
+                           hipStream_t s);
+hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,
+                          hipStream_t s);
+int64_t gate_partial_count(int N, int D);  // number of tile partials per candidate
+hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
+                            int D, hipStream_t s);
+hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
+
+}  // namespace vq

@@ -1,0 +1,163 @@
+"""ctypes binding of ``libvoodoo_hip.so`` (declared in ``include/voodoo_hip.h``).
+
+Tensors cross the boundary as raw device pointers; every call is enqueued on
+the caller's current HIP stream.  There is no fallback: if the library is not
+built, or a tensor is not on a ROCm device, calls raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+_LIB_PATH = Path(os.environ.get("VOODOO_HIP_LIB", Path(__file__).resolve().parent / "libvoodoo_hip.so"))
+_LIB = None
+
+VQ_OK, VQ_ERR_QTYPE, VQ_ERR_ALIGN, VQ_ERR_NULL, VQ_ERR_SHAPE, VQ_ERR_HIP, VQ_ERR_WORKSPACE = range(7)
+
+# (name, restype, argtypes) for every entry point of include/voodoo_hip.h
+_i, _i64, _p = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+_SIGNATURES = [
+    ("vq_version", _i, []),
+    ("vq_last_error_string", ctypes.c_char_p, []),
+    ("vq_group_bytes", _i64, [_i]),
+    ("vq_qbytes_size", _i64, [_i, _i64, _i64]),
+    ("vq_validate_candidates", _i, [_i, _p, _i64, _i64, _i64]),
+    ("vq_dequant", _i, [_i, _p, _p, _i64, _i64, _p]),
+    ("vq_mix_weight", _i, [_i, _p, _p, _p, _i64, _i64, _p, _p]),
+    ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p]),
+    ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i, _i]),
+    ("vq_gated_linear_bwd", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+]
+EXPORTED = [s[0] for s in _SIGNATURES]
+
+
+class HipLibraryError(RuntimeError):
+    pass
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def lib():
+    """Load the shared library (once).  Raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not _LIB_PATH.exists():
+            raise HipLibraryError(
+                f"{_LIB_PATH} not found: build it with `python voodoo-dyn-quant_amd/build.py` "
+                "(or __graft_entry__.build()); the gated Linear has no non-HIP path"
+            )
+        L = ctypes.CDLL(str(_LIB_PATH))
+        for name, res, args in _SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def _raise(rc: int, what: str) -> None:
+    msg = lib().vq_last_error_string().decode(errors="replace")
+    if rc in (VQ_ERR_QTYPE, VQ_ERR_ALIGN, VQ_ERR_NULL, VQ_ERR_SHAPE):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != VQ_OK:
+        _raise(rc, what)
+
+
+def _dev_ptr(t: torch.Tensor | None, name: str) -> int | None:
+    if t is None:
+        return None
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a ROCm device, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _int_array(vals):
+    arr = (ctypes.c_int * len(vals))(*vals)
+    return arr
+
+
+def _ptr_array(tensors, name):
+    return (ctypes.c_void_p * len(tensors))(*[_dev_ptr(t, f"{name}[{i}]") for i, t in enumerate(tensors)])
+
+
+# ----------------------------------------------------------------------------- host-side queries
+def group_bytes(ggml_type: int) -> int:
+    return int(lib().vq_group_bytes(ggml_type))
+
+
+def qbytes_size(ggml_type: int, nrows: int, ncols: int) -> int:
+    n = int(lib().vq_qbytes_size(ggml_type, nrows, ncols))
+    if n < 0:
+        _raise(VQ_ERR_ALIGN, "vq_qbytes_size")
+    return n
+
+
+def validate_candidates(ggml_types: list[int], n: int, d: int, d_pad: int) -> None:
+    _check(lib().vq_validate_candidates(len(ggml_types), _int_array(ggml_types), n, d, d_pad),
+           "vq_validate_candidates")
+
+
+# ----------------------------------------------------------------------------- device calls
+def dequant(ggml_type: int, qbytes: torch.Tensor, nrows: int, ncols: int, out: torch.Tensor | None = None):
+    """fp32 [nrows, ncols] decode of packed bytes, bit-exact to ggml."""
+    if out is None:
+        out = torch.empty(nrows, ncols, dtype=torch.float32, device=qbytes.device)
+    _check(lib().vq_dequant(ggml_type, _dev_ptr(qbytes, "qbytes"), _dev_ptr(out, "out"), nrows, ncols,
+                            _stream(qbytes.device)), "vq_dequant")
+    return out
+
+
+def mix_weight(ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int, out: torch.Tensor | None = None):
+    """bf16 [n, d_pad] W_eff = sum_k probs[k] * W_k (fp32, k-ordered)."""
+    dev = probs.device
+    if out is None:
+        out = torch.empty(n, d_pad, dtype=torch.bfloat16, device=dev)
+    _check(lib().vq_mix_weight(len(ggml_types), _int_array(ggml_types), _ptr_array(qbytes, "qbytes"),
+                               _dev_ptr(probs, "probs"), n, d_pad, _dev_ptr(out, "w_eff"), _stream(dev)),
+           "vq_mix_weight")
+    return out
+
+
+def gated_linear_fwd(x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int,
+                     w_eff: torch.Tensor, y: torch.Tensor) -> None:
+    m, d = x.shape
+    _check(lib().vq_gated_linear_fwd(_dev_ptr(x, "x"), m, n, d, d_pad, len(ggml_types), _int_array(ggml_types),
+                                     _ptr_array(qbytes, "qbytes"), _dev_ptr(probs, "probs"),
+                                     _dev_ptr(w_eff, "w_eff"), _dev_ptr(y, "y"), _stream(x.device)),
+           "vq_gated_linear_fwd")
+
+
+def bwd_workspace_bytes(n: int, d: int, d_pad: int, ncand: int, need_w_eff: bool) -> int:
+    v = int(lib().vq_gated_linear_bwd_workspace(n, d, d_pad, ncand, int(need_w_eff)))
+    if v < 0:
+        raise ValueError(f"invalid backward sizes n={n} d={d} ncand={ncand}")
+    return v
+
+
+def gated_linear_bwd(dy: torch.Tensor, x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor | None, n: int,
+                     d_pad: int, w_eff: torch.Tensor | None, dx: torch.Tensor | None,
+                     dprobs: torch.Tensor | None, workspace: torch.Tensor | None) -> None:
+    m, d = x.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().vq_gated_linear_bwd(_dev_ptr(dy, "dy"), _dev_ptr(x, "x"), m, n, d, d_pad, len(ggml_types),
+                                     _int_array(ggml_types), _ptr_array(qbytes, "qbytes"),
+                                     _dev_ptr(probs, "probs"), _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"),
+                                     _dev_ptr(dprobs, "dprobs"), _dev_ptr(workspace, "workspace"), ws_bytes,
+                                     _stream(dy.device)),
+           "vq_gated_linear_bwd")

@@ -1,0 +1,555 @@
+"""Gated-mixture layers on the MI355X kernels.
+
+Drop-in for the gated-Linear path of the reference's ``voodoo_quant/layers.py``:
+``MixedQuantLinear`` keeps the reference's constructor, attributes and methods
+(``layers.py:1000-1557, 1640-1740``), the module walkers keep their signatures
+(``layers.py:1845-2083``), and the trainer-facing helpers
+(``set_temperature``, ``total_effective_bytes``, ``invalidate_candidate_cache``,
+``get_assignment``) behave the same.  What changes is underneath:
+
+* candidates stay packed (GGUF bytes, the reference's "lazy" layout) and live
+  on the GPU next to the layer;
+* the forward is one autograd Function, :class:`GatedLinearFunction`, whose
+  forward calls ``vq_gated_linear_fwd`` (mix K candidates -> bf16 W_eff ->
+  MFMA GEMM) and whose backward calls ``vq_gated_linear_bwd`` (dX GEMM, and the
+  per-candidate gate gradients <dY^T X, W_k> with dW kept in registers).  The
+  softmax Jacobian is applied by autograd, exactly as for the reference's
+  ``_MixedWeightFunction`` (``layers.py:336-363``).
+
+There is no CPU or PyTorch-op implementation of the mixture: inputs must be on
+a ROCm device and ``libvoodoo_hip.so`` must be built.
+"""
+
+from __future__ import annotations
+
+import random
+import sys
+import time
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.autograd import Function
+
+from voodoo_quant import _hip, cache
+from voodoo_quant.ggml import HIP_TYPES, bytes_per_weight, find_libggml, get_quant_info, quantize_tensor
+from voodoo_quant.rtn import rtn_quantize_tensor
+
+CANDIDATE_CACHE_DIR = cache.CANDIDATE_CACHE_DIR
+_tensor_hash = cache.tensor_hash
+_candidate_cache_path = cache.candidate_cache_path
+_combined_cache_path = cache.combined_cache_path
+_atomic_torch_save = cache.atomic_torch_save
+
+
+def _ggml_id(qt: str) -> int:
+    return get_quant_info(qt).ggml_type
+
+
+# ---------------------------------------------------------------------------
+# straight-through Gumbel hardening and PTQR switches (reference layers.py:803-865)
+# ---------------------------------------------------------------------------
+class _STGumbelState:
+    enabled: bool = False
+    fraction: float = 0.0
+    gs_tau: float = 1.0
+    f_start: float | None = None
+    f_end: float | None = None
+    total_steps: int = 1
+    step: int = 0
+
+
+_ST_GUMBEL_STATE = _STGumbelState()
+
+
+def set_st_gumbel(enabled: bool, fraction: float, gs_tau: float) -> None:
+    _ST_GUMBEL_STATE.enabled = enabled
+    _ST_GUMBEL_STATE.fraction = float(fraction)
+    _ST_GUMBEL_STATE.gs_tau = float(gs_tau)
+
+
+def set_st_gumbel_anneal(f_start: float, f_end: float, total_steps: int) -> None:
+    _ST_GUMBEL_STATE.f_start = float(f_start)
+    _ST_GUMBEL_STATE.f_end = float(f_end)
+    _ST_GUMBEL_STATE.total_steps = max(int(total_steps), 1)
+
+
+def st_gumbel_step(step: int) -> None:
+    _ST_GUMBEL_STATE.step = int(step)
+
+
+def _effective_fraction() -> float:
+    st = _ST_GUMBEL_STATE
+    if st.f_start is None:
+        return st.fraction
+    t = min(max(st.step / max(st.total_steps - 1, 1), 0.0), 1.0)
+    return st.f_start + (st.f_end - st.f_start) * t
+
+
+class _PTQRState:
+    enabled: bool = False
+
+
+_PTQR_STATE = _PTQRState()
+
+
+def set_ptqr(enabled: bool) -> None:
+    """Per-token routing switch (reference ``layers.py:864-865``).  The routed
+    forward is not implemented on the HIP path yet; enabling it makes the
+    gated Linear forward raise rather than silently run the soft mixture."""
+    _PTQR_STATE.enabled = bool(enabled)
+
+
+# ---------------------------------------------------------------------------
+# padding (reference layers.py:973-997)
+# ---------------------------------------------------------------------------
+def _pad_weight_and_imatrix(weight: torch.Tensor, imatrix: torch.Tensor | None):
+    orig_in = weight.shape[1]
+    if orig_in % 256 == 0:
+        return weight, imatrix, orig_in
+    pad = 256 - orig_in % 256
+    padded = F.pad(weight, (0, pad), "constant", 0)
+    if imatrix is not None:
+        imatrix = F.pad(imatrix.to(torch.float32).contiguous(), (0, pad), "constant", 1.0)
+    return padded, imatrix, orig_in
+
+
+pad_weight_and_imatrix = _pad_weight_and_imatrix
+
+
+# ---------------------------------------------------------------------------
+# device dequant (reference layers.py:298-319)
+# ---------------------------------------------------------------------------
+def dequantize_tensor_gpu(qweight: torch.Tensor, quant_type: str, out_features: int, in_features: int,
+                          device) -> torch.Tensor:
+    """Decode packed bytes on the GPU with the HIP kernel -> bf16 [out, in].
+
+    The fp32 intermediate is bit-identical to ggml's ``dequantize_row_*``."""
+    if quant_type not in HIP_TYPES:
+        raise NotImplementedError(f"{quant_type}: the HIP decoders cover {HIP_TYPES}")
+    device = torch.device(device)
+    qb = qweight.to(device).contiguous().reshape(-1)
+    w = _hip.dequant(_ggml_id(quant_type), qb, out_features, in_features)
+    return w[:, :in_features].to(torch.bfloat16)
+
+
+def dequantize_tensor_gpu_fp32(qweight: torch.Tensor, quant_type: str, out_features: int, in_features: int,
+                               device) -> torch.Tensor:
+    if quant_type not in HIP_TYPES:
+        raise NotImplementedError(f"{quant_type}: the HIP decoders cover {HIP_TYPES}")
+    qb = qweight.to(torch.device(device)).contiguous().reshape(-1)
+    return _hip.dequant(_ggml_id(quant_type), qb, out_features, in_features)
+
+
+# ---------------------------------------------------------------------------
+# autograd Functions
+# ---------------------------------------------------------------------------
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class GatedLinearFunction(Function):
+    """y = x W_eff^T with W_eff = sum_k probs_k W_k, on libvoodoo_hip.
+
+    forward(ctx, x [M, D] bf16, probs [K] fp32, meta, *qbytes) -> y [M, N] bf16
+    where meta = (ggml type ids, N, D_pad).  The backward returns dX and
+    dL/dprobs; qbytes receive no gradient (they are constants, as the
+    candidates are for the reference's ``_MixedWeightFunction``)."""
+
+    @staticmethod
+    def forward(ctx, x, probs, meta, *qbytes):
+        types, n, d_pad = meta
+        x2 = _aligned(x)
+        p = probs.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        w_eff = torch.empty(n, d_pad, dtype=torch.bfloat16, device=x.device)
+        y = torch.empty(x2.shape[0], n, dtype=torch.bfloat16, device=x.device)
+        _hip.gated_linear_fwd(x2, types, qbytes, p, n, d_pad, w_eff, y)
+        ctx.save_for_backward(x2, p, w_eff)
+        ctx.meta = meta
+        ctx.qbytes = qbytes
+        ctx.probs_device = probs.device
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, p, w_eff = ctx.saved_tensors
+        types, n, d_pad = ctx.meta
+        need_dx, need_dp = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dy2 = _aligned(dy.to(torch.bfloat16))
+        dx = torch.empty_like(x2) if need_dx else None
+        dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device) if need_dp else None
+        ws = None
+        if need_dp:
+            nbytes = _hip.bwd_workspace_bytes(n, x2.shape[1], d_pad, len(types), False)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
+        if need_dx or need_dp:
+            _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, w_eff, dx, dprobs, ws)
+        if dprobs is not None:
+            dprobs = dprobs.to(ctx.probs_device)
+        return (dx, dprobs, None) + (None,) * len(ctx.qbytes)
+
+
+class MixedWeightFunction(Function):
+    """W_eff [N, D] in the source dtype, differentiable w.r.t. probs
+    (reference ``_MixedWeightFunction``, ``layers.py:322-363``).  Serves the
+    non-fused consumers of ``get_mixed_weight``; the gated Linear's own
+    forward never materialises it outside its workspace."""
+
+    @staticmethod
+    def forward(ctx, probs, meta, *qbytes):
+        types, n, d, d_pad, out_dtype = meta
+        p = probs.detach().to(dtype=torch.float32).contiguous()
+        w = _hip.mix_weight(types, qbytes, p, n, d_pad)[:, :d]
+        ctx.meta = meta
+        ctx.qbytes = qbytes
+        return w.to(out_dtype)
+
+    @staticmethod
+    def backward(ctx, grad_w):
+        types, n, d, d_pad, _ = ctx.meta
+        g = grad_w.to(torch.float32)
+        gp = torch.empty(len(types), dtype=torch.float32, device=grad_w.device)
+        for k, (t, qb) in enumerate(zip(types, ctx.qbytes)):
+            wk = _hip.dequant(t, qb.reshape(-1), n, d_pad)[:, :d]
+            gp[k] = (g * wk).sum()
+        return (gp, None) + (None,) * len(ctx.qbytes)
+
+
+# ---------------------------------------------------------------------------
+# gated modules
+# ---------------------------------------------------------------------------
+class _MixedQuantBase(nn.Module):
+    """Candidate production, storage and gate logic shared by gated layers
+    (reference ``_MixedQuantBase``, ``layers.py:1000-1557``)."""
+
+    def __init__(self, candidate_types: list[str], source_weight: torch.Tensor, out_features: int,
+                 in_features: int, imatrix: torch.Tensor | None = None, device=None, lazy: bool = False,
+                 tensor_name: str = "unknown", qbytes_device=None, shard_spec=None,
+                 full_source_weight: torch.Tensor | None = None):
+        super().__init__()
+        self.candidate_types = list(candidate_types)
+        bad = [qt for qt in self.candidate_types if qt not in HIP_TYPES]
+        if bad:
+            raise ValueError(f"{tensor_name}: candidate types {bad} have no HIP decoder (supported: {HIP_TYPES})")
+        if not self.candidate_types:
+            raise ValueError(f"{tensor_name}: empty candidate list")
+        self.num_candidates = len(self.candidate_types)
+        self.out_features = out_features
+        self.in_features = in_features
+        self.lazy = lazy
+        self._tensor_name = tensor_name
+        self._qbytes_device = torch.device(qbytes_device) if qbytes_device is not None else None
+        self.shard_spec = shard_spec
+        if shard_spec is not None and full_source_weight is None:
+            raise ValueError(f"{tensor_name}: shard_spec requires full_source_weight")
+        if device is None:
+            device = source_weight.device
+        self._device = torch.device(device)
+        self.gates = nn.Parameter(torch.zeros(self.num_candidates, device=self._device))
+        self.temperature = 1.0
+        self.source_dtype = source_weight.dtype
+
+        src = (full_source_weight if shard_spec is not None else source_weight).detach().to("cpu").contiguous()
+        if imatrix is not None:
+            imatrix = imatrix.detach().to(torch.float32).cpu()
+        padded, padded_imatrix, _ = _pad_weight_and_imatrix(src.to(torch.float32), imatrix)
+        self.padded_in_features = padded.shape[1]
+        self._full_padded_in_features = self.padded_in_features
+        weight_hash = cache.tensor_hash(padded)
+        imatrix_hash = cache.tensor_hash(padded_imatrix) if imatrix is not None else "none"
+        root = CANDIDATE_CACHE_DIR if CANDIDATE_CACHE_DIR != cache.CANDIDATE_CACHE_DIR else None
+        found = cache.load_candidates(tensor_name, self.candidate_types, "lazy", weight_hash, imatrix_hash, root)
+        missing = [qt for qt in self.candidate_types if qt not in found]
+        self.candidate_source = "cache" if not missing else None
+        if missing:
+            made, source = _quantize_candidates(padded, padded_imatrix, missing)
+            self.candidate_source = source
+            found.update(made)
+            try:
+                cache.save_candidates(tensor_name, made, "lazy", weight_hash, imatrix_hash, root)
+            except OSError as e:  # a read-only cache is not fatal
+                print(f"  [cache] {tensor_name}: not saved ({e})", file=sys.stderr)
+        full_out = shard_spec.full_out if shard_spec is not None else out_features
+        for k, qt in enumerate(self.candidate_types):
+            info = get_quant_info(qt)
+            qb = found[qt].reshape(-1)
+            expect = full_out * (self.padded_in_features // info.block_size) * info.block_bytes
+            if qb.numel() != expect:
+                raise ValueError(f"{tensor_name}: cached {qt} holds {qb.numel()} bytes, expected {expect}")
+            self.register_buffer(f"_qweight_{k}", qb.contiguous(), persistent=False)
+        if shard_spec is not None:
+            self._apply_shard_to_candidates()
+        self.imatrix = imatrix
+        if self._qbytes_device is not None:
+            self._move_qbytes(self._qbytes_device)
+
+    # -- candidate storage ----------------------------------------------------
+    def _qbytes(self) -> list[torch.Tensor]:
+        return [getattr(self, f"_qweight_{k}") for k in range(self.num_candidates)]
+
+    def _move_qbytes(self, device) -> None:
+        device = torch.device(device)
+        for k in range(self.num_candidates):
+            qb = getattr(self, f"_qweight_{k}")
+            if qb.device != device:
+                setattr(self, f"_qweight_{k}", qb.to(device, non_blocking=False).contiguous())
+
+    def _ggml_types(self) -> tuple[int, ...]:
+        return tuple(_ggml_id(qt) for qt in self.candidate_types)
+
+    def _apply_shard_to_candidates(self) -> None:
+        spec = self.shard_spec
+        for k, qt in enumerate(self.candidate_types):
+            qb = getattr(self, f"_qweight_{k}")
+            setattr(self, f"_qweight_{k}", spec.slice_qbytes(qb, qt, self._full_padded_in_features).reshape(-1)
+                    .contiguous())
+        self.padded_in_features = spec.local_padded_in(self._full_padded_in_features, self.candidate_types)
+
+    def __getattr__(self, name: str):
+        # The reference's non-lazy modules expose decoded candidates as _w_{k}.
+        if name.startswith("_w_") and name[3:].isdigit():
+            return self._get_candidate(int(name[3:]))
+        return super().__getattr__(name)
+
+    def _get_candidate(self, k: int) -> torch.Tensor:
+        qt = self.candidate_types[k]
+        qb = getattr(self, f"_qweight_{k}")
+        dev = qb.device if qb.device.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
+        w = dequantize_tensor_gpu_fp32(qb, qt, self.out_features, self.padded_in_features, dev)
+        return w[:, : self.in_features].to(self.source_dtype)
+
+    def invalidate_candidate_cache(self):
+        """Kept for the trainer's calls (``trainer.py:2502-2506``).  Nothing is
+        cached between steps: candidates are decoded inside the kernels."""
+        return None
+
+    # -- gates ----------------------------------------------------------------
+    def set_temperature(self, temperature: float):
+        self.temperature = max(temperature, 1e-6)
+
+    def soft_probs(self) -> torch.Tensor:
+        return F.softmax(self.gates / self.temperature, dim=0)
+
+    def get_probs(self) -> torch.Tensor:
+        probs = self.soft_probs()
+        if _ST_GUMBEL_STATE.enabled and random.random() < _effective_fraction():
+            u = torch.rand_like(probs)
+            gumbel = -torch.log((-torch.log(u.clamp_min(1e-9))).clamp_min(1e-9))
+            scores = (torch.log(probs.clamp_min(1e-9)) + gumbel) / max(_ST_GUMBEL_STATE.gs_tau, 1e-3)
+            hard = F.one_hot(scores.argmax(dim=0), num_classes=probs.shape[0]).to(probs.dtype)
+            return (hard - probs).detach() + probs
+        return probs
+
+    def get_mixed_weight(self) -> torch.Tensor:
+        probs = self.get_probs()
+        dev = self._compute_device()
+        self._move_qbytes(dev)
+        meta = (self._ggml_types(), self.out_features, self.in_features, self.padded_in_features, self.source_dtype)
+        return MixedWeightFunction.apply(probs.to(dev), meta, *self._qbytes())
+
+    def _compute_device(self) -> torch.device:
+        qb = getattr(self, "_qweight_0")
+        if qb.device.type == "cuda":
+            return qb.device
+        if self.gates.device.type == "cuda":
+            return self.gates.device
+        if not torch.cuda.is_available():
+            raise RuntimeError(f"{self._tensor_name}: the gated layers run on ROCm devices only")
+        return torch.device("cuda", torch.cuda.current_device())
+
+    def effective_bytes(self) -> torch.Tensor:
+        probs = self.soft_probs()
+        out_eff = getattr(self, "_full_out_features", None) or self.out_features
+        in_eff = getattr(self, "_full_in_features", None) or self.in_features
+        n = in_eff * out_eff
+        total = torch.tensor(0.0, device=probs.device)
+        for k, qt in enumerate(self.candidate_types):
+            total = total + probs[k] * bytes_per_weight(qt) * n
+        return total
+
+    def get_assignment(self) -> str:
+        return self.candidate_types[self.gates.argmax().item()]
+
+    def get_assignment_prob(self) -> float:
+        probs = self.soft_probs().detach()
+        return probs[self.gates.argmax().item()].item()
+
+    # -- tensor-parallel slicing (reference layers.py:1400-1472) ---------------
+    def shard_rows(self, row_ranges: list[tuple[int, int]]) -> None:
+        if getattr(self, "_full_out_features", None) is not None or getattr(self, "_full_in_features", None):
+            raise RuntimeError(f"{self._tensor_name}: already row/col-sharded")
+        shard_out = sum(e - s for s, e in row_ranges)
+        if shard_out <= 0 or shard_out > self.out_features:
+            raise ValueError(f"{self._tensor_name}: invalid row ranges {row_ranges} for out_features={self.out_features}")
+        for k in range(self.num_candidates):
+            q2d = getattr(self, f"_qweight_{k}").view(self.out_features, -1)
+            setattr(self, f"_qweight_{k}", torch.cat([q2d[s:e] for s, e in row_ranges], 0).reshape(-1).contiguous())
+        self._full_out_features = self.out_features
+        self.out_features = shard_out
+
+    def shard_cols(self, col_range: tuple[int, int]) -> None:
+        if getattr(self, "_full_out_features", None) is not None or getattr(self, "_full_in_features", None):
+            raise RuntimeError(f"{self._tensor_name}: already row/col-sharded")
+        s, e = col_range
+        if s < 0 or e > self.in_features or e <= s:
+            raise ValueError(f"{self._tensor_name}: invalid column range {col_range} for in_features={self.in_features}")
+        if s % 256 or e % 256:
+            raise ValueError(f"{self._tensor_name}: column range {col_range} is not 256-aligned (gated layers "
+                             "keep whole 256-weight groups)")
+        for k, qt in enumerate(self.candidate_types):
+            info = get_quant_info(qt)
+            nbpr = self.padded_in_features // info.block_size
+            b0, b1 = s // info.block_size, e // info.block_size
+            q3 = getattr(self, f"_qweight_{k}").view(self.out_features, nbpr, info.block_bytes)[:, b0:b1, :]
+            setattr(self, f"_qweight_{k}", q3.reshape(-1).contiguous())
+        self._full_in_features = self.in_features
+        self.in_features = e - s
+        self.padded_in_features = e - s
+
+
+def _quantize_candidates(padded: torch.Tensor, padded_imatrix: torch.Tensor | None,
+                         types: list[str]) -> tuple[dict[str, torch.Tensor], str]:
+    """Candidate bytes from libggml when it loads, else from the RTN encoder."""
+    if find_libggml() is not None:
+        return {qt: quantize_tensor(padded, qt, padded_imatrix) for qt in types}, "ggml"
+    if not getattr(_quantize_candidates, "_warned", False):
+        print("voodoo_quant: libggml-base not found; candidates come from the non-ggml RTN encoder "
+              "(valid GGUF blocks, not llama.cpp-exact bytes)", file=sys.stderr)
+        _quantize_candidates._warned = True
+    return {qt: rtn_quantize_tensor(padded, qt) for qt in types}, "rtn"
+
+
+class MixedQuantLinear(_MixedQuantBase):
+    """Linear layer whose weight is a softmax mixture of K packed candidates
+    (reference ``layers.py:1640-1740``)."""
+
+    def __init__(self, in_features: int, out_features: int, candidate_types: list[str],
+                 source_weight: torch.Tensor, imatrix: torch.Tensor | None = None, device=None, lazy: bool = False,
+                 tensor_name: str = "unknown", qbytes_device=None, shard_spec=None,
+                 full_source_weight: torch.Tensor | None = None):
+        super().__init__(candidate_types=candidate_types, source_weight=source_weight, out_features=out_features,
+                         in_features=in_features, imatrix=imatrix, device=device, lazy=lazy,
+                         tensor_name=tensor_name, qbytes_device=qbytes_device, shard_spec=shard_spec,
+                         full_source_weight=full_source_weight)
+        if shard_spec is not None and getattr(shard_spec, "vocab_start", None) is not None:
+            self.tp_vocab_start = shard_spec.vocab_start
+            self.tp_vocab_end = shard_spec.vocab_start + out_features
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.device.type != "cuda":
+            raise RuntimeError(f"{self._tensor_name}: MixedQuantLinear runs on a ROCm device only (got {x.device})")
+        if _PTQR_STATE.enabled:
+            raise NotImplementedError("per-token quant routing (set_ptqr) has no HIP forward yet")
+        self._move_qbytes(x.device)
+        probs = self.get_probs()
+        if probs.device != x.device:
+            probs = probs.to(x.device)
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.dtype != torch.bfloat16:
+            x2 = x2.to(torch.bfloat16)
+        meta = (self._ggml_types(), self.out_features, self.padded_in_features)
+        y = GatedLinearFunction.apply(x2, probs, meta, *self._qbytes())
+        if x.dtype != torch.bfloat16:
+            y = y.to(x.dtype)
+        out = y.reshape(*lead, self.out_features)
+        spec = self.shard_spec
+        if spec is not None and getattr(spec, "col_offset", None) is not None:
+            raise NotImplementedError("row-parallel (column-sharded) gated Linear needs the TP all-reduce")
+        return out
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"candidates={self.candidate_types}, source={self.candidate_source}")
+
+
+# ---------------------------------------------------------------------------
+# module walkers (reference layers.py:1845-2160)
+# ---------------------------------------------------------------------------
+DEFAULT_ATTENTION_SEGMENTS: frozenset = frozenset({"self_attn", "linear_attn", "attn", "conv", "shortconv"})
+_ATTENTION_SEGMENTS: frozenset = DEFAULT_ATTENTION_SEGMENTS
+
+
+def resolve_candidate_types(tensor_name: str, base_candidates: list[str],
+                            attention_candidates: list[str] | None = None,
+                            non_attention_candidates: list[str] | None = None) -> list[str]:
+    if attention_candidates is None and non_attention_candidates is None:
+        return list(base_candidates)
+    is_attn = any(seg in _ATTENTION_SEGMENTS for seg in tensor_name.split("."))
+    group = attention_candidates if (is_attn and attention_candidates) else non_attention_candidates
+    if not group:
+        return list(base_candidates)
+    base = set(base_candidates)
+    return [qt for qt in group if qt in base]
+
+
+def _count_selectable_linears(module: nn.Module, target_names: Optional[set[str]], skip_names: set[str]) -> int:
+    total = 0
+    for name, child in module.named_children():
+        if name in skip_names:
+            continue
+        if isinstance(child, nn.Linear):
+            if target_names is None or name in target_names:
+                total += 1
+        else:
+            total += _count_selectable_linears(child, target_names, skip_names)
+    return total
+
+
+def replace_linear_with_mixed_quant(module: nn.Module, candidate_types: list[str] | None, prefix: str = "",
+                                    target_names: Optional[set[str]] = None,
+                                    skip_names: Optional[set[str]] = None,
+                                    imatrix_dict: Optional[dict[str, torch.Tensor]] = None, device=None,
+                                    lazy: bool = False, attention_candidates: Optional[list[str]] = None,
+                                    non_attention_candidates: Optional[list[str]] = None,
+                                    qbytes_device=None) -> dict[str, _MixedQuantBase]:
+    """Recursively replace nn.Linear children with MixedQuantLinear; returns
+    {full_name: module}.  Same arguments as the reference (``layers.py:1908-1920``)."""
+    if candidate_types is None:
+        candidate_types = list(HIP_TYPES)
+    skip_names = skip_names or set()
+    imatrix_dict = imatrix_dict or {}
+    if prefix == "":
+        total = _count_selectable_linears(module, target_names, skip_names)
+        replace_linear_with_mixed_quant._mq_counter = 0
+        replace_linear_with_mixed_quant._mq_start = time.monotonic()
+        print(f"Preparing {total} selectable layers x {len(candidate_types)} candidates ...", flush=True)
+    replaced: dict[str, _MixedQuantBase] = {}
+    for name, child in list(module.named_children()):
+        full_name = f"{prefix}.{name}" if prefix else name
+        if name in skip_names:
+            continue
+        if isinstance(child, nn.Linear):
+            if child.bias is not None:
+                raise NotImplementedError(f"MixedQuantLinear does not support bias but {full_name} has one")
+            if target_names is not None and name not in target_names:
+                continue
+            imatrix = imatrix_dict.get(full_name)
+            if imatrix is None:
+                imatrix = imatrix_dict.get(full_name + ".weight")
+            new_child = MixedQuantLinear(
+                in_features=child.in_features, out_features=child.out_features,
+                candidate_types=resolve_candidate_types(full_name, candidate_types, attention_candidates,
+                                                        non_attention_candidates),
+                source_weight=child.weight.data, imatrix=imatrix, device=device, lazy=lazy, tensor_name=full_name,
+                qbytes_device=qbytes_device, shard_spec=getattr(child, "tp_shard_spec", None),
+                full_source_weight=getattr(child, "tp_full_weight", None))
+            setattr(module, name, new_child)
+            replaced[full_name] = new_child
+            replace_linear_with_mixed_quant._mq_counter = getattr(replace_linear_with_mixed_quant, "_mq_counter", 0) + 1
+        else:
+            replaced.update(replace_linear_with_mixed_quant(
+                child, candidate_types=candidate_types, prefix=full_name, target_names=target_names,
+                skip_names=skip_names, imatrix_dict=imatrix_dict, device=device, lazy=lazy,
+                attention_candidates=attention_candidates, non_attention_candidates=non_attention_candidates,
+                qbytes_device=qbytes_device))
+    return replaced
+
+
+def total_effective_bytes(replaced: dict[str, _MixedQuantBase]) -> torch.Tensor:
+    total = torch.tensor(0.0)
+    for layer in replaced.values():
+        total = total + layer.effective_bytes()
+    return total
