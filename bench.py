@@ -123,6 +123,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -205,6 +207,15 @@ def main() -> int:
                   "frac": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 3)}
         del qb
     log("dequant GB/s: " + ", ".join(f"{k} {v['GBps']}" for k, v in dq.items()))
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 1 GiB device-to-device copies")
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -95,8 +95,12 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(CandSet cs, const f
             decode_run_rt<8>(qt, lds + off + j * gb, 8 * (t & 31), w);
             off += (kGroupsPerBlock * gb + 15) & ~15;
             const float pk = probs[k];
+            {
+                // product and sum rounded separately, like the two torch ops
+#pragma clang fp contract(off)
 #pragma unroll
-            for (int r = 0; r < 8; ++r) mixed[r] = __fadd_rn(mixed[r], __fmul_rn(pk, w[r]));
+                for (int r = 0; r < 8; ++r) mixed[r] = mixed[r] + pk * w[r];
+            }
         }
         uint4 v;
         v.x = (uint32_t)f2bf(mixed[0]) | ((uint32_t)f2bf(mixed[1]) << 16);
