@@ -150,7 +150,7 @@ def main() -> int:
     y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
     dx = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
     dp = torch.empty(len(TYPES), dtype=torch.float32, device=dev)
-    ws = torch.empty(_hip.bwd_workspace_bytes(n, d, d_pad, len(TYPES), False), dtype=torch.uint8, device=dev)
+    ws = torch.empty(_hip.bwd_workspace_bytes(m, n, d, d_pad, len(TYPES), False), dtype=torch.uint8, device=dev)
 
     def fwd():
         _hip.gated_linear_fwd(x, ids, qbytes, probs, n, d_pad, w_eff, y)

@@ -77,11 +77,12 @@ int vq_gated_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int6
 
 /* Workspace bytes vq_gated_linear_bwd needs (gate partials; plus the W_eff
  * buffer when it will be called with w_eff == NULL and dx != NULL). */
-int64_t vq_gated_linear_bwd_workspace(int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff);
+int64_t vq_gated_linear_bwd_workspace(int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff);
 
 /* Backward of the gated Linear.  dx (nullable) = dy . W_eff;
- * dprobs (nullable) [ncand] fp32 = <dy^T x, W_k> with the dW tiles kept in
- * registers (never written) and the candidates decoded exactly.  `w_eff` is
+ * dprobs (nullable) [ncand] fp32 = <dy^T x, W_k> with the dW tiles kept on
+ * chip (registers and LDS, never written to memory) and the candidates decoded
+ * exactly.  `w_eff` is
  * the forward's buffer, or NULL to re-mix into the workspace.  Replaces the
  * F.linear autograd backward and _MixedWeightFunction.backward
  * (voodoo_quant/layers.py:354-363). */

@@ -72,7 +72,8 @@ def test_null_pointers_rejected_before_any_gpu_work():
 
 
 def test_workspace_size():
-    n = _hip.bwd_workspace_bytes(17408, 5120, 5120, 6, False)
+    n = _hip.bwd_workspace_bytes(8192, 17408, 5120, 5120, 6, False)
     tiles = (17408 // 256) * (5120 // 256)
     assert n >= tiles * 6 * 4 and n % 256 == 0
-    assert _hip.bwd_workspace_bytes(17408, 5120, 5120, 6, True) >= n + 17408 * 5120 * 2
+    assert _hip.bwd_workspace_bytes(8192, 17408, 5120, 5120, 6, True) >= n + 17408 * 5120 * 2
+    assert _hip.bwd_workspace_bytes(0, 64, 256, 256, 2, False) > 0

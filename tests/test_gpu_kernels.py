@@ -153,7 +153,7 @@ def _run_fwd_bwd(hip, types, m, n, d, d_pad, qbs, probs, x, dy):
     hip.gated_linear_fwd(xd, ids, dev_q, pd, n, d_pad, w_eff, y)
     dx = torch.empty(m, d, dtype=torch.bfloat16, device="cuda")
     dp = torch.empty(len(types), dtype=torch.float32, device="cuda")
-    ws = torch.empty(hip.bwd_workspace_bytes(n, d, d_pad, len(types), False), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(hip.bwd_workspace_bytes(m, n, d, d_pad, len(types), False), dtype=torch.uint8, device="cuda")
     hip.gated_linear_bwd(dyd, xd, ids, dev_q, pd, n, d_pad, w_eff, dx, dp, ws)
     torch.cuda.synchronize()
     return w_eff.cpu(), y.cpu(), dx.cpu(), dp.cpu()

@@ -164,9 +164,9 @@ int vq_gated_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int6
     return rc == VQ_OK ? ok() : rc;
 }
 
-int64_t vq_gated_linear_bwd_workspace(int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff) {
-    if (n <= 0 || d <= 0 || ncand < 1 || n > INT32_MAX || d > INT32_MAX) return -1;
-    int64_t bytes = align256(vq::gate_partial_count((int)n, (int)d) * ncand * (int64_t)sizeof(float));
+int64_t vq_gated_linear_bwd_workspace(int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff) {
+    if (m < 0 || n <= 0 || d <= 0 || ncand < 1 || m > INT32_MAX || n > INT32_MAX || d > INT32_MAX) return -1;
+    int64_t bytes = align256(vq::gate_partial_count((int)m, (int)n, (int)d) * ncand * (int64_t)sizeof(float));
     if (need_w_eff) bytes += align256(n * d_pad * 2);
     return bytes;
 }
@@ -185,8 +185,9 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
     hipStream_t s = static_cast<hipStream_t>(stream);
     const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);
     const bool remix = dx != nullptr && w_eff == nullptr;
-    const int64_t need = vq_gated_linear_bwd_workspace(n, d, d_pad, ncand, remix ? 1 : 0);
-    const int64_t part_bytes = align256(vq::gate_partial_count((int)n, (int)d) * ncand * (int64_t)sizeof(float));
+    const int64_t need = vq_gated_linear_bwd_workspace(m, n, d, d_pad, ncand, remix ? 1 : 0);
+    const int64_t nparts = vq::gate_partial_count((int)m, (int)n, (int)d);
+    const int64_t part_bytes = align256(nparts * ncand * (int64_t)sizeof(float));
     if ((dprobs || remix) && (!workspace || ws_bytes < need))
         return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
                     (long long)(workspace ? ws_bytes : 0));
@@ -209,7 +210,7 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
     if (dprobs) {
         rc = hip_check(vq::launch_gemm_gate(dy, x, cs, partials, (int)m, (int)n, (int)d, s), "gate GEMM launch");
         if (rc != VQ_OK) return rc;
-        rc = hip_check(vq::launch_gate_reduce(partials, vq::gate_partial_count((int)n, (int)d), ncand, dprobs, s),
+        rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, s),
                        "gate reduce launch");
         if (rc != VQ_OK) return rc;
     }

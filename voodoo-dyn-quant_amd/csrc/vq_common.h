@@ -54,21 +54,18 @@ __device__ __forceinline__ uint32_t rd_u8(const uint8_t* p) { return p[0]; }
 __device__ __forceinline__ uint32_t rd_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
 
 // ---------------------------------------------------------------------------
-// decode_run<QT, R>(g, p, y): weights p .. p+R-1 of the 256-weight group whose
-// bytes start at g.  R is 4 or 8 and p is a multiple of R, so the run never
-// crosses a 16-weight sub-block.  g may point into LDS or global memory.
+// Block decoders.  decode_codes<QT, R>(g, p, q, dl, ml) reads weights
+// p .. p+R-1 of the 256-weight group whose bytes start at g (R is 4 or 8, p a
+// multiple of R, so the run never crosses a 16-weight sub-block) as integer
+// codes q (held in floats) and the run's scale dl and offset ml:
+//     weight = dl * q - ml          (ml = 0 for the formats without mins)
+// dl * q is exact in fp32 for every format, so decode_run's single rounding is
+// ggml's.  g may point into LDS or global memory.
 // ---------------------------------------------------------------------------
-template <int QT, int R>
-__device__ __forceinline__ void decode_run(const uint8_t* __restrict__ g, int p, float* __restrict__ y);
-
-template <int R>
-__device__ __forceinline__ void decode_q8_0(const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
-    const uint8_t* b = g + 34 * (p >> 5);
-    const float d = h2f(rd_u16(b));
-    const int o = 2 + (p & 31);
-#pragma unroll
-    for (int r = 0; r < R; ++r) y[r] = (float)(int8_t)b[o + r] * d;
-}
+template <int QT>
+struct HasMin {
+    static constexpr bool value = (QT == Q4_K || QT == Q5_K || QT == Q2_K);
+};
 
 // 6-bit scale/min pair j of the 12-byte Q4_K/Q5_K scale array
 __device__ __forceinline__ void scale_min_k4(const uint8_t* __restrict__ s, int j, uint32_t& sc, uint32_t& m) {
@@ -81,75 +78,137 @@ __device__ __forceinline__ void scale_min_k4(const uint8_t* __restrict__ s, int 
     }
 }
 
-template <int R, bool FIVE>
-__device__ __forceinline__ void decode_q45_K(const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
-    const float d = h2f(rd_u16(g)), dmin = h2f(rd_u16(g + 2));
-    const int c = p >> 6, h = (p >> 5) & 1, l = p & 31;
-    uint32_t sc, m;
-    scale_min_k4(g + 4, 2 * c + h, sc, m);
-    const float dl = d * (float)sc, ml = dmin * (float)m;
-    const uint8_t* qs = g + (FIVE ? 48 : 16) + 32 * c + l;
+// Load R (4 or 8) consecutive bytes whose address is a multiple of ALIGN
+// (a property of the format's layout: group bases are 16-byte aligned in
+// memory and in LDS, so field offsets fix the alignment), with the widest
+// loads that alignment allows.  Byte r is (w[r / 4] >> (8 * (r % 4))) & 0xff.
+template <int ALIGN, int R>
+__device__ __forceinline__ void load_run(const uint8_t* __restrict__ p, uint32_t (&w)[R / 4]) {
+    if constexpr (ALIGN >= 8 && R == 8) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        w[0] = v.x;
+        w[1] = v.y;
+    } else if constexpr (ALIGN >= 4) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        uint32_t q = (qs[r] >> (4 * h)) & 0xFu;
-        if (FIVE) q += ((g[16 + l + r] >> (2 * c + h)) & 1u) << 4;
-        y[r] = dl * (float)q - ml;
+        for (int i = 0; i < R / 4; ++i) w[i] = *reinterpret_cast<const uint32_t*>(p + 4 * i);
+    } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+        for (int i = 0; i < R / 4; ++i) w[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
     }
 }
 
 template <int R>
-__device__ __forceinline__ void decode_q6_K(const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
-    const float d = h2f(rd_u16(g + 208));
-    const int n = p >> 7, t = (p >> 5) & 3, l = p & 31;
-    const float dl = d * (float)(int8_t)g[192 + 8 * n + (l >> 4) + 2 * t];
-    const uint8_t* ql = g + 64 * n + l + 32 * (t & 1);
-    const uint8_t* qh = g + 128 + 32 * n + l;
-    const int ls = 4 * (t >> 1), hs = 2 * t;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int q = (int)(((ql[r] >> ls) & 0xFu) | (((qh[r] >> hs) & 3u) << 4)) - 32;
-        y[r] = dl * (float)q;
-    }
-}
-
-template <int R>
-__device__ __forceinline__ void decode_q3_K(const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
-    const float d = h2f(rd_u16(g + 108));
-    const int n = p >> 7, j = (p >> 5) & 3, half = (p >> 4) & 1, l = p & 15;
-    const int is = 8 * n + 2 * j + half;
-    const uint8_t* s = g + 96;
-    const uint32_t lo4 = is < 8 ? (s[is] & 0xFu) : (uint32_t)(s[is - 8] >> 4);
-    const uint32_t hi2 = (s[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
-    const float dl = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
-    const uint8_t* qs = g + 32 + 32 * n + 16 * half + l;
-    const uint8_t* hm = g + 16 * half + l;
-    const int hb = 4 * n + j;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int q = (int)((qs[r] >> (2 * j)) & 3u) - (((hm[r] >> hb) & 1u) ? 0 : 4);
-        y[r] = dl * (float)q;
-    }
-}
-
-template <int R>
-__device__ __forceinline__ void decode_q2_K(const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
-    const float d = h2f(rd_u16(g + 80)), dmin = h2f(rd_u16(g + 82));
-    const int n = p >> 7, j = (p >> 5) & 3, half = (p >> 4) & 1, l = p & 15;
-    const uint32_t s = g[8 * n + 2 * j + half];
-    const float dl = d * (float)(s & 0xFu), ml = dmin * (float)(s >> 4);
-    const uint8_t* qs = g + 16 + 32 * n + 16 * half + l;
-#pragma unroll
-    for (int r = 0; r < R; ++r) y[r] = dl * (float)((qs[r] >> (2 * j)) & 3u) - ml;
+__device__ __forceinline__ uint32_t run_byte(const uint32_t (&w)[R / 4], int r) {
+    return (w[r >> 2] >> (8 * (r & 3))) & 0xffu;
 }
 
 template <int QT, int R>
+__device__ __forceinline__ void decode_codes(const uint8_t* __restrict__ g, int p, float* __restrict__ q, float& dl,
+                                             float& ml) {
+    if constexpr (QT == Q8_0) {
+        // blocks of 34 bytes: codes start 2 bytes into a block -> 2-byte aligned
+        const uint8_t* b = g + 34 * (p >> 5);
+        dl = h2f(*reinterpret_cast<const uint16_t*>(b));
+        ml = 0.0f;
+        uint32_t w[R / 4];
+        load_run<2, R>(b + 2 + (p & 31), w);
+#pragma unroll
+        for (int r = 0; r < R; ++r) q[r] = (float)(int8_t)run_byte<R>(w, r);
+    } else if constexpr (QT == Q4_K || QT == Q5_K) {
+        // 144- and 176-byte groups keep 16-byte alignment; code runs are 8-aligned
+        constexpr bool FIVE = QT == Q5_K;
+        const uint32_t dd = *reinterpret_cast<const uint32_t*>(g);
+        const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
+        const int c = p >> 6, h = (p >> 5) & 1, l = p & 31;
+        uint32_t sc, m;
+        scale_min_k4(g + 4, 2 * c + h, sc, m);
+        dl = d * (float)sc;
+        ml = dmin * (float)m;
+        uint32_t w[R / 4];
+        load_run<8, R>(g + (FIVE ? 48 : 16) + 32 * c + l, w);
+        uint32_t hw[R / 4];
+        if (FIVE) load_run<8, R>(g + 16 + l, hw);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            uint32_t v = (run_byte<R>(w, r) >> (4 * h)) & 0xFu;
+            if (FIVE) v += ((run_byte<R>(hw, r) >> (2 * c + h)) & 1u) << 4;
+            q[r] = (float)v;
+        }
+    } else if constexpr (QT == Q6_K) {
+        // 210-byte groups: 2-byte alignment only
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 208));
+        const int n = p >> 7, t = (p >> 5) & 3, l = p & 31;
+        dl = d * (float)(int8_t)g[192 + 8 * n + (l >> 4) + 2 * t];
+        ml = 0.0f;
+        uint32_t lw[R / 4], hw[R / 4];
+        load_run<2, R>(g + 64 * n + l + 32 * (t & 1), lw);
+        load_run<2, R>(g + 128 + 32 * n + l, hw);
+        const int ls = 4 * (t >> 1), hs = 2 * t;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            q[r] = (float)((int)(((run_byte<R>(lw, r) >> ls) & 0xFu) | (((run_byte<R>(hw, r) >> hs) & 3u) << 4)) - 32);
+    } else if constexpr (QT == Q3_K) {
+        // 110-byte groups: 2-byte alignment only
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 108));
+        const int n = p >> 7, j = (p >> 5) & 3, half = (p >> 4) & 1, l = p & 15;
+        const int is = 8 * n + 2 * j + half;
+        const uint8_t* s = g + 96;
+        const uint32_t lo4 = is < 8 ? (s[is] & 0xFu) : (uint32_t)(s[is - 8] >> 4);
+        const uint32_t hi2 = (s[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
+        dl = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
+        ml = 0.0f;
+        uint32_t qw[R / 4], mw[R / 4];
+        load_run<2, R>(g + 32 + 32 * n + 16 * half + l, qw);
+        load_run<2, R>(g + 16 * half + l, mw);
+        const int hb = 4 * n + j;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            q[r] = (float)((int)((run_byte<R>(qw, r) >> (2 * j)) & 3u) - (((run_byte<R>(mw, r) >> hb) & 1u) ? 0 : 4));
+    } else {  // Q2_K: 84-byte groups keep 4-byte alignment
+        const uint32_t dd = *reinterpret_cast<const uint32_t*>(g + 80);
+        const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
+        const int n = p >> 7, j = (p >> 5) & 3, half = (p >> 4) & 1, l = p & 15;
+        const uint32_t s = g[8 * n + 2 * j + half];
+        dl = d * (float)(s & 0xFu);
+        ml = dmin * (float)(s >> 4);
+        uint32_t w[R / 4];
+        load_run<4, R>(g + 16 + 32 * n + 16 * half + l, w);
+#pragma unroll
+        for (int r = 0; r < R; ++r) q[r] = (float)((run_byte<R>(w, r) >> (2 * j)) & 3u);
+    }
+}
+
+// Exact fp32 weights (ggml's dequantize_row_* values, signed zeros included).
+template <int QT, int R>
 __device__ __forceinline__ void decode_run(const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
-    if constexpr (QT == Q8_0) decode_q8_0<R>(g, p, y);
-    else if constexpr (QT == Q4_K) decode_q45_K<R, false>(g, p, y);
-    else if constexpr (QT == Q5_K) decode_q45_K<R, true>(g, p, y);
-    else if constexpr (QT == Q6_K) decode_q6_K<R>(g, p, y);
-    else if constexpr (QT == Q3_K) decode_q3_K<R>(g, p, y);
-    else if constexpr (QT == Q2_K) decode_q2_K<R>(g, p, y);
+    float q[R], dl, ml;
+    decode_codes<QT, R>(g, p, q, dl, ml);
+    if constexpr (QT == Q8_0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) y[r] = q[r] * dl;  // ggml: qs * d
+    } else if constexpr (HasMin<QT>::value) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) y[r] = dl * q[r] - ml;
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) y[r] = dl * q[r];
+    }
+}
+
+// <v, W> over one run: sum_r v[r] * (dl * q[r] - ml) = dl * sum(v q) - ml * sum(v)
+template <int QT, int R>
+__device__ __forceinline__ float dot_run(const uint8_t* __restrict__ g, int p, const float* __restrict__ v) {
+    float q[R], dl, ml;
+    decode_codes<QT, R>(g, p, q, dl, ml);
+    float s1 = 0.0f, s0 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        s1 = fmaf(v[r], q[r], s1);
+        if constexpr (HasMin<QT>::value) s0 += v[r];
+    }
+    if constexpr (HasMin<QT>::value) return dl * s1 - ml * s0;
+    return dl * s1;
 }
 
 // Runtime-type dispatch (the type is uniform across a wave).

@@ -26,7 +26,8 @@ hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t
                            hipStream_t s);
 hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,
                           hipStream_t s);
-int64_t gate_partial_count(int N, int D);  // number of tile partials per candidate
+int gate_splits(int M, int N, int D);       // reduction splits of the gate product
+int64_t gate_partial_count(int M, int N, int D);  // work-item partials per candidate
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
                             int D, hipStream_t s);
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);

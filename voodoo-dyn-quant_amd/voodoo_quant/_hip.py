@@ -29,7 +29,7 @@ _SIGNATURES = [
     ("vq_dequant", _i, [_i, _p, _p, _i64, _i64, _p]),
     ("vq_mix_weight", _i, [_i, _p, _p, _p, _i64, _i64, _p, _p]),
     ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p]),
-    ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i, _i]),
+    ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
     ("vq_gated_linear_bwd", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
 ]
 EXPORTED = [s[0] for s in _SIGNATURES]
@@ -143,10 +143,10 @@ def gated_linear_fwd(x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, n
            "vq_gated_linear_fwd")
 
 
-def bwd_workspace_bytes(n: int, d: int, d_pad: int, ncand: int, need_w_eff: bool) -> int:
-    v = int(lib().vq_gated_linear_bwd_workspace(n, d, d_pad, ncand, int(need_w_eff)))
+def bwd_workspace_bytes(m: int, n: int, d: int, d_pad: int, ncand: int, need_w_eff: bool) -> int:
+    v = int(lib().vq_gated_linear_bwd_workspace(m, n, d, d_pad, ncand, int(need_w_eff)))
     if v < 0:
-        raise ValueError(f"invalid backward sizes n={n} d={d} ncand={ncand}")
+        raise ValueError(f"invalid backward sizes m={m} n={n} d={d} ncand={ncand}")
     return v
 
 

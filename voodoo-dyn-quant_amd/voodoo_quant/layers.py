@@ -182,7 +182,7 @@ class GatedLinearFunction(Function):
         dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device) if need_dp else None
         ws = None
         if need_dp:
-            nbytes = _hip.bwd_workspace_bytes(n, x2.shape[1], d_pad, len(types), False)
+            nbytes = _hip.bwd_workspace_bytes(x2.shape[0], n, x2.shape[1], d_pad, len(types), False)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
         if need_dx or need_dp:
             _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, w_eff, dx, dprobs, ws)
