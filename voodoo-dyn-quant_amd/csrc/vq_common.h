@@ -211,6 +211,123 @@ __device__ __forceinline__ float dot_run(const uint8_t* __restrict__ g, int p, c
     return dl * s1;
 }
 
+// <v, W> over the 16 weights p0 + 4h + 8u + t (u, t in 0..3) of the 32-weight
+// sub-block starting at p0 (a multiple of 32), with v[4u + t] their values:
+// the per-lane footprint of a 32x32 MFMA accumulator block.  Scales and mins
+// are decoded once per 16-weight half; codes are read 4 bytes at a time.
+template <int QT>
+__device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0, int h, const float* __restrict__ v) {
+    float s1[2] = {0.0f, 0.0f}, s0[2] = {0.0f, 0.0f};
+    float dl[2], ml[2] = {0.0f, 0.0f};
+    uint32_t cw[4], xw[4];  // code words (and 5th/high-bit words) of the 4 runs
+    int shift = 0, xshift = 0;
+    if constexpr (QT == Q8_0) {
+        const uint8_t* b = g + 34 * (p0 >> 5);
+        dl[0] = dl[1] = h2f(*reinterpret_cast<const uint16_t*>(b));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + 4 * h + 8 * u);
+            cw[u] = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+        }
+    } else if constexpr (QT == Q4_K || QT == Q5_K) {
+        const uint32_t dd = *reinterpret_cast<const uint32_t*>(g);
+        const int c = p0 >> 6, nib = (p0 >> 5) & 1;
+        uint32_t sc, m;
+        scale_min_k4(g + 4, 2 * c + nib, sc, m);
+        dl[0] = dl[1] = h2f(dd & 0xffffu) * (float)sc;
+        ml[0] = ml[1] = h2f(dd >> 16) * (float)m;
+        const uint8_t* qs = g + (QT == Q5_K ? 48 : 16) + 32 * c + 4 * h;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) cw[u] = *reinterpret_cast<const uint32_t*>(qs + 8 * u);
+        shift = 4 * nib;
+        if constexpr (QT == Q5_K) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) xw[u] = *reinterpret_cast<const uint32_t*>(g + 16 + 4 * h + 8 * u);
+            xshift = 2 * c + nib;
+        }
+    } else if constexpr (QT == Q6_K) {
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 208));
+        const int n = p0 >> 7, t4 = (p0 >> 5) & 3;
+        dl[0] = d * (float)(int8_t)g[192 + 8 * n + 2 * t4];
+        dl[1] = d * (float)(int8_t)g[192 + 8 * n + 1 + 2 * t4];
+        const uint8_t* ql = g + 64 * n + 32 * (t4 & 1) + 4 * h;
+        const uint8_t* qh = g + 128 + 32 * n + 4 * h;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint16_t* a = reinterpret_cast<const uint16_t*>(ql + 8 * u);
+            const uint16_t* b = reinterpret_cast<const uint16_t*>(qh + 8 * u);
+            cw[u] = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
+            xw[u] = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+        }
+        shift = 4 * (t4 >> 1);
+        xshift = 2 * t4;
+    } else if constexpr (QT == Q3_K) {
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 108));
+        const int n = p0 >> 7, j = (p0 >> 5) & 3;
+        const uint8_t* sb = g + 96;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int is = 8 * n + 2 * j + hf;
+            const uint32_t lo4 = is < 8 ? (sb[is] & 0xFu) : (uint32_t)(sb[is - 8] >> 4);
+            const uint32_t hi2 = (sb[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
+            dl[hf] = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int o = 16 * (u >> 1) + 4 * h + 8 * (u & 1);  // 16 * half + l within the 32-run
+            const uint16_t* a = reinterpret_cast<const uint16_t*>(g + 32 + 32 * n + o);
+            const uint16_t* b = reinterpret_cast<const uint16_t*>(g + o);
+            cw[u] = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
+            xw[u] = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+        }
+        shift = 2 * j;
+        xshift = 4 * n + j;
+    } else {  // Q2_K
+        const uint32_t dd = *reinterpret_cast<const uint32_t*>(g + 80);
+        const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
+        const int n = p0 >> 7, j = (p0 >> 5) & 3;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t sc = g[8 * n + 2 * j + hf];
+            dl[hf] = d * (float)(sc & 0xFu);
+            ml[hf] = dmin * (float)(sc >> 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int o = 16 * (u >> 1) + 4 * h + 8 * (u & 1);
+            cw[u] = *reinterpret_cast<const uint32_t*>(g + 16 + 32 * n + o);
+        }
+        shift = 2 * j;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int hf = u >> 1;  // runs 0,1 are weights 0..15 of the sub-block, runs 2,3 are 16..31
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t byte = (cw[u] >> (8 * t)) & 0xffu;
+            float q;
+            if constexpr (QT == Q8_0) {
+                q = (float)(int8_t)byte;
+            } else if constexpr (QT == Q4_K) {
+                q = (float)((byte >> shift) & 0xFu);
+            } else if constexpr (QT == Q5_K) {
+                q = (float)(((byte >> shift) & 0xFu) | ((((xw[u] >> (8 * t)) >> xshift) & 1u) << 4));
+            } else if constexpr (QT == Q6_K) {
+                q = (float)((int)(((byte >> shift) & 0xFu) | ((((xw[u] >> (8 * t)) >> xshift) & 3u) << 4)) - 32);
+            } else if constexpr (QT == Q3_K) {
+                q = (float)((int)((byte >> shift) & 3u) - ((((xw[u] >> (8 * t)) >> xshift) & 1u) ? 0 : 4));
+            } else {
+                q = (float)((byte >> shift) & 3u);
+            }
+            s1[hf] = fmaf(v[4 * u + t], q, s1[hf]);
+            if constexpr (HasMin<QT>::value) s0[hf] += v[4 * u + t];
+        }
+    }
+    float r = dl[0] * s1[0] + dl[1] * s1[1];
+    if constexpr (HasMin<QT>::value) r -= ml[0] * s0[0] + ml[1] * s0[1];
+    return r;
+}
+
 // Runtime-type dispatch (the type is uniform across a wave).
 template <int R>
 __device__ __forceinline__ void decode_run_rt(int qt, const uint8_t* __restrict__ g, int p, float* __restrict__ y) {

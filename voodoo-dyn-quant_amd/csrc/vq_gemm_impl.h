@@ -14,10 +14,10 @@
 //   forward  Y[m][n]  = sum_d X[m][d] W[n][d]        A=X (K), B=W (K)
 //   dX       dX[m][d] = sum_n dY[m][n] W[n][d]       A=dY (K), B=W (T)
 //   gate     dW[d][n] = sum_m X[m][d] dY[m][n]       A=X (T), B=dY (T)
-// The gate product never reaches global memory: its epilogue stages the fp32
-// tile through LDS (reusing the main-loop buffers) and dots every candidate's
-// exactly decoded weights against it, writing one partial per candidate per
-// work item.  <dW, W_k> is linear in dW, so the M reduction may also be split
+// The gate product never reaches global memory: its epilogue keeps the fp32
+// tile in the accumulators, stages each candidate's bytes for the tile into
+// LDS (reusing the main-loop buffers) and dots the exactly decoded weights
+// against it, writing one partial per candidate per work item.  <dW, W_k> is linear in dW, so the M reduction may also be split
 // across work items with no dW reduction at all.  A second kernel sums the
 // partials in a fixed order: gate gradients are deterministic.
 //
@@ -87,6 +87,11 @@ struct LoaderK {
             lds[lds_chunk<BK>(id / CPR, id % CPR)] = reg[i];
         }
     }
+    static constexpr int CHUNKS = ROWS * BK / 8;  // 16-byte LDS chunks per stage
+    // MFMA fragment: tile row `row + lane%32`, k = 16 ks + 8 (lane/32) .. +7
+    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
+        return __builtin_bit_cast(bf16x8_t, lds[lds_chunk<BK>(row + (lane & 31), 2 * ks + (lane >> 5))]);
+    }
 };
 
 // A thread moves one KB x 8 block (KB k-rows of 8 consecutive tile rows): KB
@@ -148,6 +153,61 @@ struct LoaderT {
             }
         }
     }
+    static constexpr int CHUNKS = ROWS * BK / 8;
+    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
+        return __builtin_bit_cast(bf16x8_t, lds[lds_chunk<BK>(row + (lane & 31), 2 * ks + (lane >> 5))]);
+    }
+};
+
+// Source [K][rows] (rows contiguous) kept in that orientation in LDS: k-row
+// kr of the tile is PITCH bf16 wide (ROWS + 32 of padding).  Fragments come
+// from two ds_read_b64_tr_b16 per 8 k.  That instruction, per 16-lane group,
+// gives output lane l element j = element l%4 of the 8 bytes addressed by lane
+// 16 (l/16) + 4 j + (l%16)/4 (measured on gfx950), so when lane s addresses
+//     k = kk + 8 (s/32) + (s%16)/4,   row = r + 16 ((s/16)%2) + 4 (s%4)
+// lane l receives rows r + l%32 at k = kk + 8 (l/32) + 0..3: the MFMA layout.
+// The padding puts the 4 k-rows x 2 row-halves of each 32-lane pass on
+// distinct bank groups.
+template <int ROWS, int BK, int THREADS>
+struct LoaderN {
+    static constexpr int PITCH = ROWS + 32;       // bf16 per k-row in LDS
+    static constexpr int RCH = ROWS / 8;          // 16-byte chunks per k-row
+    static constexpr int NL = BK * RCH / THREADS;
+    static_assert(NL * THREADS == BK * RCH, "tile must split evenly over threads");
+    static constexpr int CHUNKS = BK * PITCH / 8;
+    u32x4 reg[NL];
+
+    // rows [r0, r0 + ROWS) x k [k0, k0 + BK) of src[k * ld + row], zero past kend
+    __device__ __forceinline__ void load(const bf16_t* __restrict__ src, int64_t ld, int r0, int rows, int k0,
+                                         int kend) {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)k0 * ld + r0);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int id = i * THREADS + (int)threadIdx.x;
+            const int kr = id / RCH, c = id % RCH;
+            const bool ok = r0 + 8 * c < rows && k0 + kr < kend;
+            reg[i] = buf_load16(rs, ok ? (uint32_t)((kr * ld + 8 * c) * 2) : kOOB);
+        }
+    }
+    __device__ __forceinline__ void store(u32x4* __restrict__ lds) const {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int id = i * THREADS + (int)threadIdx.x;
+            lds[(id / RCH) * (PITCH / 8) + id % RCH] = reg[i];
+        }
+    }
+    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
+        typedef short v4i16 __attribute__((ext_vector_type(4)));
+        const int k = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
+        const int r = row + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        const bf16_t* base = reinterpret_cast<const bf16_t*>(lds) + k * PITCH + r;
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + 4 * PITCH));
+        typedef short v8i16 __attribute__((ext_vector_type(8)));
+        const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        return __builtin_bit_cast(bf16x8_t, v);
+    }
 };
 
 // ---------------------------------------------------------------- work order
@@ -200,23 +260,50 @@ struct GemmShape {
     static constexpr int THREADS = WI * WJ * 64;
     static constexpr int WTI = BI / WI, WTJ = BJ / WJ;  // wave tile
     static constexpr int MI = WTI / 32, NJ = WTJ / 32;
-    static constexpr int A_CH = BI * BK / 8, B_CH = BJ * BK / 8;  // 16-byte chunks per tile
-    static constexpr size_t MAIN_LDS = (size_t)2 * (A_CH + B_CH) * 16;
 };
 
-// Double-buffered main loop over k in [kbeg, kend): global loads of stage
-// s+1 are issued before the MFMAs of stage s and written to the other LDS
-// buffer after them; one barrier per stage.
+template <class LA, class LB>
+struct StageLds {
+    static constexpr int A_CH = LA::CHUNKS, B_CH = LB::CHUNKS;  // 16-byte chunks per stage
+    static constexpr size_t BYTES = (size_t)2 * (A_CH + B_CH) * 16;
+};
+
+// MFMAs of one LDS stage.
 template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ>
+__device__ __forceinline__ void gemm_stage_mfma(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, int wi,
+                                                int wj, int lane,
+                                                f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
+                                                             [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
+    using S = GemmShape<BI, BJ, BK, WI, WJ>;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8_t fa[S::MI], fb[S::NJ];
+#pragma unroll
+        for (int a = 0; a < S::MI; ++a) fa[a] = LA::read_frag(sa, wi * S::WTI + 32 * a, ks, lane);
+#pragma unroll
+        for (int b = 0; b < S::NJ; ++b) fb[b] = LB::read_frag(sb, wj * S::WTJ + 32 * b, ks, lane);
+#pragma unroll
+        for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+            for (int b = 0; b < S::NJ; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+    }
+}
+
+// Main loop over k in [kbeg, kend) with an LDS double buffer and one barrier
+// per stage.  DEPTH = 1: the global loads of stage s+1 are issued before the
+// MFMAs of stage s and written to the free LDS buffer after them.  DEPTH = 2:
+// two register stages, so the loads of stage s+2 have two stages of compute
+// to arrive (more registers).
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int DEPTH>
 __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, int i0, int j0, int kbeg, int kend,
                                               u32x4* __restrict__ smem,
                                               f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
                                                            [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
-    u32x4* const sA0 = smem;
-    u32x4* const sA1 = smem + S::A_CH;
-    u32x4* const sB0 = smem + 2 * S::A_CH;
-    u32x4* const sB1 = smem + 2 * S::A_CH + S::B_CH;
+    using L = StageLds<LA, LB>;
+    u32x4* const sA[2] = {smem, smem + L::A_CH};
+    u32x4* const sB[2] = {smem + 2 * L::A_CH, smem + 2 * L::A_CH + L::B_CH};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wi = wave / WJ, wj = wave % WJ;
 
@@ -227,78 +314,128 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, int i0, int j
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
-    LA la;
-    LB lb;
-    la.load(p.A, p.lda, i0, p.I, kbeg, kend);
-    lb.load(p.B, p.ldb, j0, p.J, kbeg, kend);
-    la.store(sA0);
-    lb.store(sB0);
+    const int nk = (kend - kbeg + BK - 1) / BK;
+    if constexpr (DEPTH == 1) {
+        LA la;
+        LB lb;
+        la.load(p.A, p.lda, i0, p.I, kbeg, kend);
+        lb.load(p.B, p.ldb, j0, p.J, kbeg, kend);
+        la.store(sA[0]);
+        lb.store(sB[0]);
+        __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+            const bool more = kt + 1 < nk;
+            if (more) {
+                la.load(p.A, p.lda, i0, p.I, kbeg + (kt + 1) * BK, kend);
+                lb.load(p.B, p.ldb, j0, p.J, kbeg + (kt + 1) * BK, kend);
+            }
+            gemm_stage_mfma<LA, LB, BI, BJ, BK, WI, WJ>(sA[kt & 1], sB[kt & 1], wi, wj, lane, acc);
+            if (more) {
+                la.store(sA[(kt + 1) & 1]);
+                lb.store(sB[(kt + 1) & 1]);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    LA la0, la1;
+    LB lb0, lb1;
+    la0.load(p.A, p.lda, i0, p.I, kbeg, kend);
+    lb0.load(p.B, p.ldb, j0, p.J, kbeg, kend);
+    if (nk > 1) {
+        la1.load(p.A, p.lda, i0, p.I, kbeg + BK, kend);
+        lb1.load(p.B, p.ldb, j0, p.J, kbeg + BK, kend);
+    }
+    la0.store(sA[0]);
+    lb0.store(sB[0]);
     __syncthreads();
 
-    const int nk = (kend - kbeg + BK - 1) / BK;
-    for (int kt = 0; kt < nk; ++kt) {
-        const bool more = kt + 1 < nk;
-        if (more) {
-            la.load(p.A, p.lda, i0, p.I, kbeg + (kt + 1) * BK, kend);
-            lb.load(p.B, p.ldb, j0, p.J, kbeg + (kt + 1) * BK, kend);
+    // stage kt: refill (holding stage kt, already in LDS) <- stage kt + 2;
+    // next (holding stage kt + 1) -> the other LDS buffer after the MFMAs
+    auto stage = [&](int kt, LA& la_refill, LB& lb_refill, const LA& la_next, const LB& lb_next) {
+        if (kt + 2 < nk) {
+            la_refill.load(p.A, p.lda, i0, p.I, kbeg + (kt + 2) * BK, kend);
+            lb_refill.load(p.B, p.ldb, j0, p.J, kbeg + (kt + 2) * BK, kend);
         }
-        const u32x4* sa = (kt & 1) ? sA1 : sA0;
-        const u32x4* sb = (kt & 1) ? sB1 : sB0;
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            bf16x8_t fa[S::MI], fb[S::NJ];
-            const int ch = 2 * ks + (lane >> 5);
-#pragma unroll
-            for (int a = 0; a < S::MI; ++a)
-                fa[a] = __builtin_bit_cast(bf16x8_t, sa[lds_chunk<BK>(wi * S::WTI + 32 * a + (lane & 31), ch)]);
-#pragma unroll
-            for (int b = 0; b < S::NJ; ++b)
-                fb[b] = __builtin_bit_cast(bf16x8_t, sb[lds_chunk<BK>(wj * S::WTJ + 32 * b + (lane & 31), ch)]);
-#pragma unroll
-            for (int a = 0; a < S::MI; ++a)
-#pragma unroll
-                for (int b = 0; b < S::NJ; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
-        }
-        if (more) {
-            la.store((kt & 1) ? sA0 : sA1);
-            lb.store((kt & 1) ? sB0 : sB1);
+        gemm_stage_mfma<LA, LB, BI, BJ, BK, WI, WJ>(sA[kt & 1], sB[kt & 1], wi, wj, lane, acc);
+        if (kt + 1 < nk) {
+            la_next.store(sA[(kt + 1) & 1]);
+            lb_next.store(sB[(kt + 1) & 1]);
         }
         __syncthreads();
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        stage(kt, la0, lb0, la1, lb1);
+        if (kt + 1 < nk) stage(kt + 1, la1, lb1, la0, lb0);
     }
 }
 
 // ---------------------------------------------------------------- gate epilogue
-// Each wave stages its own fp32 sub-tile through a private LDS region, half
-// the d rows at a time (rows a = 2h, 2h+1 of its 32-row MFMA blocks), as
-// T[n][d] with PITCH floats per n row; its lanes then dot runs of 8
-// consecutive d of one n against every candidate.  Only the half being
-// processed and the other half's accumulators are live at once.
-template <int WTI, int WTJ>
-struct GateStage {
-    static constexpr int HALF = WTI / 2;       // d rows per half
-    static constexpr int PITCH = HALF + 4;     // floats per n row (+16 B against bank conflicts)
-    static constexpr int RUNS_PER_ROW = HALF / 8;
-    static constexpr int RUNS = WTJ * RUNS_PER_ROW / 64;  // per lane
-    static constexpr size_t WAVE_LDS = (size_t)WTJ * PITCH * 4;
+// The work item's dW tile stays in the accumulators.  Its d range is exactly
+// one 256-weight group of every candidate row (BI = 256, i0 a multiple of
+// 256), so for each candidate the tile needs 256 spans of GB bytes, one per
+// row n.  Those spans are staged into LDS with coalesced 16-byte buffer loads
+// (span start rounded down to 16 bytes, so LDS copies keep the global
+// alignment of every field), double buffered: the loads of candidate k+1 are
+// in flight while candidate k is decoded in the accumulator layout straight
+// from LDS.  Rows past J read as zeros (their dW is zero too).
+constexpr int kGateMaxChunks = (272 + 15 + 15) / 16;  // 16-byte chunks per row span, worst type (Q8_0)
+
+__device__ __forceinline__ int gate_row_chunks(int qt) { return (group_bytes(qt) + 15 + 15) / 16; }
+
+template <int BJ, int THREADS>
+struct GateStager {
+    static constexpr int MAXN = (BJ * kGateMaxChunks + THREADS - 1) / THREADS;
+    u32x4 reg[MAXN];
+    int nch;  // chunks per row for the current candidate
+
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ qbytes, int qt, int64_t row_groups, int j0,
+                                         int group, int J) {
+        const int gb = group_bytes(qt);
+        nch = gate_row_chunks(qt);
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(qbytes);
+        const int total = BJ * nch;
+#pragma unroll
+        for (int i = 0; i < MAXN; ++i) {
+            const int id = i * THREADS + (int)threadIdx.x;
+            const int row = id / nch, c = id % nch;
+            const int n = j0 + row;
+            const int64_t span = ((int64_t)n * row_groups + group) * gb;
+            const bool ok = id < total && n < J;
+            reg[i] = buf_load16(rs, ok ? (uint32_t)((span & ~int64_t(15)) + 16 * c) : kOOB);
+        }
+    }
+    // Row slot pitch in LDS: kGateMaxChunks chunks.
+    __device__ __forceinline__ void store(u32x4* __restrict__ buf) const {
+        const int total = BJ * nch;
+#pragma unroll
+        for (int i = 0; i < MAXN; ++i) {
+            const int id = i * THREADS + (int)threadIdx.x;
+            if (id < total) buf[(id / nch) * kGateMaxChunks + id % nch] = reg[i];
+        }
+    }
 };
 
-template <int QT, int RUNS, int RUNS_PER_ROW>
-__device__ __forceinline__ float gate_runs(const float (&v)[RUNS][8], const uint8_t* __restrict__ qbytes,
-                                           int64_t row_groups, int nbase, int dbase, int lane, int J, int dlimit) {
+// <acc, W_k> over the lane's accumulators: block (a, b) holds, for row
+// n = 32 b + lane%32, the 16 weights 32 a + 4 (lane/32) + 8 u + t of one
+// 32-weight sub-block (relative to the wave's tile origin).
+template <int QT, int MI, int NJ, int WTI, int WTJ>
+__device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const uint8_t* __restrict__ buf,
+                                              int64_t row_groups, int j0, int group, int wi, int wj, int lane) {
     constexpr int GB = group_bytes(QT);
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < RUNS; ++i) {
-        // branch-free: out-of-range runs read row 0 / group 0 and are masked,
-        // so the loads of every run can be issued together
-        const int run = i * 64 + lane;
-        const int n = nbase + run / RUNS_PER_ROW;
-        const int d = dbase + 8 * (run % RUNS_PER_ROW);
-        const bool ok = n < J && d < dlimit;
-        const uint8_t* g = qbytes + ((int64_t)(ok ? n : 0) * row_groups + (ok ? (d >> 8) : 0)) * GB;
-        const float t = dot_run<QT, 8>(g, d & 255, v[i]);
-        s += ok ? t : 0.0f;
+    for (int b = 0; b < NJ; ++b) {
+        const int nl = wj * WTJ + 32 * b + (lane & 31);
+        const int64_t span = ((int64_t)(j0 + nl) * row_groups + group) * GB;
+        const uint8_t* g = buf + nl * (kGateMaxChunks * 16) + (int)(span & 15);
+#pragma unroll
+        for (int a = 0; a < MI; ++a) {
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = acc[a][b][r];
+            s += dot_sub32<QT>(g, wi * WTI + 32 * a, lane >> 5, v);
+        }
     }
     return s;
 }
@@ -309,57 +446,35 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkIte
                                               const f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
                                                                  [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
-    using G = GateStage<S::WTI, S::WTJ>;
+    static_assert(BI == 256, "the gate tile covers exactly one 256-weight group per row");
     constexpr int NW = WI * WJ;
-    static_assert(S::MI % 2 == 0 && G::RUNS * 64 == S::WTJ * G::RUNS_PER_ROW, "gate staging shape");
+    constexpr int BUF_CH = BJ * kGateMaxChunks;  // 16-byte chunks per candidate buffer
     __shared__ float red[NW][kMaxCand];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wi = wave / WJ, wj = wave % WJ;
-    float* T = reinterpret_cast<float*>(smem) + wave * (G::WAVE_LDS / 4);
+    const int group = i0 / 256;
+    const int64_t rg = p.cs.row_groups;
+    GateStager<BJ, S::THREADS> st;
+    st.load(p.cs.qbytes[0], p.cs.qtype[0], rg, j0, group, p.J);
     __syncthreads();  // every wave is past its last main-loop LDS read
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int a2 = 0; a2 < S::MI / 2; ++a2) {
-            const int a = h * (S::MI / 2) + a2;
-#pragma unroll
-            for (int b = 0; b < S::NJ; ++b)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int dl = 32 * a2 + 8 * g + 4 * (lane >> 5);
-                    const int nl = 32 * b + (lane & 31);
-                    *reinterpret_cast<float4*>(T + nl * G::PITCH + dl) = make_float4(
-                        acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]);
-                }
+    st.store(smem);
+    for (int k = 0; k < p.cs.ncand; ++k) {
+        __syncthreads();  // candidate k is in buffer k % 2; buffer (k+1) % 2 is free
+        if (k + 1 < p.cs.ncand) st.load(p.cs.qbytes[k + 1], p.cs.qtype[k + 1], rg, j0, group, p.J);
+        const uint8_t* buf = reinterpret_cast<const uint8_t*>(smem + (k & 1) * BUF_CH);
+        float sum;
+        switch (p.cs.qtype[k]) {
+        case Q8_0: sum = gate_dot_lds<Q8_0, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
+        case Q2_K: sum = gate_dot_lds<Q2_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
+        case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
+        case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
+        case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
+        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
         }
-        float v[G::RUNS][8];
 #pragma unroll
-        for (int i = 0; i < G::RUNS; ++i) {
-            const int run = i * 64 + lane;
-            const float* src = T + (run / G::RUNS_PER_ROW) * G::PITCH + 8 * (run % G::RUNS_PER_ROW);
-            const float4 lo = *reinterpret_cast<const float4*>(src);
-            const float4 hi = *reinterpret_cast<const float4*>(src + 4);
-            v[i][0] = lo.x; v[i][1] = lo.y; v[i][2] = lo.z; v[i][3] = lo.w;
-            v[i][4] = hi.x; v[i][5] = hi.y; v[i][6] = hi.z; v[i][7] = hi.w;
-        }
-        const int dbase = i0 + wi * S::WTI + h * G::HALF;
-        const int nbase = j0 + wj * S::WTJ;
-        for (int k = 0; k < p.cs.ncand; ++k) {
-            const uint8_t* q = p.cs.qbytes[k];
-            const int64_t rg = p.cs.row_groups;
-            float s;
-            switch (p.cs.qtype[k]) {
-            case Q8_0: s = gate_runs<Q8_0, G::RUNS, G::RUNS_PER_ROW>(v, q, rg, nbase, dbase, lane, p.J, p.dlimit); break;
-            case Q2_K: s = gate_runs<Q2_K, G::RUNS, G::RUNS_PER_ROW>(v, q, rg, nbase, dbase, lane, p.J, p.dlimit); break;
-            case Q3_K: s = gate_runs<Q3_K, G::RUNS, G::RUNS_PER_ROW>(v, q, rg, nbase, dbase, lane, p.J, p.dlimit); break;
-            case Q4_K: s = gate_runs<Q4_K, G::RUNS, G::RUNS_PER_ROW>(v, q, rg, nbase, dbase, lane, p.J, p.dlimit); break;
-            case Q5_K: s = gate_runs<Q5_K, G::RUNS, G::RUNS_PER_ROW>(v, q, rg, nbase, dbase, lane, p.J, p.dlimit); break;
-            default: s = gate_runs<Q6_K, G::RUNS, G::RUNS_PER_ROW>(v, q, rg, nbase, dbase, lane, p.J, p.dlimit); break;
-            }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-            if (lane == 0) red[wave][k] = h == 0 ? s : red[wave][k] + s;
-        }
+        for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+        if (lane == 0) red[wave][k] = sum;
+        if (k + 1 < p.cs.ncand) st.store(smem + ((k + 1) & 1) * BUF_CH);
     }
     __syncthreads();
     if ((int)threadIdx.x < p.cs.ncand) {
@@ -370,7 +485,7 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkIte
 }
 
 // ---------------------------------------------------------------- kernel
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI>
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH>
 __global__ __launch_bounds__(WI* WJ * 64) void gemm_kernel(GemmParams p) {
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     extern __shared__ u32x4 smem[];
@@ -384,7 +499,7 @@ __global__ __launch_bounds__(WI* WJ * 64) void gemm_kernel(GemmParams p) {
         kend = min(p.K, kbeg + chunk);
     }
     f32x16 acc[S::MI][S::NJ];
-    gemm_mainloop<LA, LB, BI, BJ, BK, WI, WJ>(p, i0, j0, kbeg, kend, smem, acc);
+    gemm_mainloop<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
 
     if constexpr (EPI == EPI_STORE) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -407,15 +522,15 @@ __global__ __launch_bounds__(WI* WJ * 64) void gemm_kernel(GemmParams p) {
 
 template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI>
 constexpr size_t gemm_lds_bytes() {
-    using S = GemmShape<BI, BJ, BK, WI, WJ>;
-    constexpr size_t gate = (size_t)WI * WJ * GateStage<S::WTI, S::WTJ>::WAVE_LDS;
-    return EPI == EPI_GATE && gate > S::MAIN_LDS ? gate : S::MAIN_LDS;
+    constexpr size_t main = StageLds<LA, LB>::BYTES;
+    constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16;
+    return EPI == EPI_GATE && gate > main ? gate : main;
 }
 
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI>
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH = 1>
 static hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
     if (p.I <= 0 || p.J <= 0) return hipSuccess;
-    auto kern = gemm_kernel<LA, LB, BI, BJ, BK, WI, WJ, EPI>;
+    auto kern = gemm_kernel<LA, LB, BI, BJ, BK, WI, WJ, EPI, DEPTH>;
     constexpr size_t lds = gemm_lds_bytes<LA, LB, BI, BJ, BK, WI, WJ, EPI>();
     static bool attr_set = false;  // per instantiation
     if (!attr_set) {
