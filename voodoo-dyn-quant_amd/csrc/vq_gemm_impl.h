@@ -374,61 +374,73 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, int i0, int j
 // The work item's dW tile stays in the accumulators.  Its d range is exactly
 // one 256-weight group of every candidate row (BI = 256, i0 a multiple of
 // 256), so for each candidate the tile needs 256 spans of GB bytes, one per
-// row n.  Those spans are staged into LDS with coalesced 16-byte buffer loads
-// (span start rounded down to 16 bytes, so LDS copies keep the global
-// alignment of every field), double buffered: the loads of candidate k+1 are
-// in flight while candidate k is decoded in the accumulator layout straight
-// from LDS.  Rows past J read as zeros (their dW is zero too).
+// row n.  Those spans are copied into LDS by direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds: lane l of an instruction lands at M0 + 16 l),
+// each span rounded out to whole 16-byte chunks so the LDS copy keeps the
+// global alignment of every field.  Candidate k+1 streams in while candidate k
+// is decoded in the accumulator layout.  The descriptor covers exactly the
+// candidate's bytes, so the rounded-out tail of the last span reads zeros;
+// rows past J load row 0 (their dW is zero).
 constexpr int kGateMaxChunks = (272 + 15 + 15) / 16;  // 16-byte chunks per row span, worst type (Q8_0)
 
 __device__ __forceinline__ int gate_row_chunks(int qt) { return (group_bytes(qt) + 15 + 15) / 16; }
 
+// Same copy through registers (ordinary loads, then ds_write), for the first
+// candidate, which is consumed right after it is staged.
 template <int BJ, int THREADS>
-struct GateStager {
-    static constexpr int MAXN = (BJ * kGateMaxChunks + THREADS - 1) / THREADS;
-    u32x4 reg[MAXN];
-    int nch;  // chunks per row for the current candidate
+__device__ __forceinline__ void gate_stage_regs(u32x4* __restrict__ buf, const uint8_t* __restrict__ qbytes, int qt,
+                                                int64_t row_groups, int j0, int group, int J) {
+    const int gb = group_bytes(qt), nch = gate_row_chunks(qt);
+    const int64_t bytes = (int64_t)J * row_groups * gb;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(qbytes), (short)0, (int)(bytes < (int64_t)kRange ? bytes : (int64_t)kRange), 0x00020000);
+    const int total = BJ * nch;
+    for (int id = threadIdx.x; id < total; id += THREADS) {
+        const int row = id / nch, c = id % nch;
+        const int n = j0 + row < J ? j0 + row : 0;
+        const int64_t span = ((int64_t)n * row_groups + group) * gb;
+        buf[id] = buf_load16(rs, (uint32_t)((span & ~int64_t(15)) + 16 * c));
+    }
+}
 
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ qbytes, int qt, int64_t row_groups, int j0,
-                                         int group, int J) {
-        const int gb = group_bytes(qt);
-        nch = gate_row_chunks(qt);
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(qbytes);
-        const int total = BJ * nch;
-#pragma unroll
-        for (int i = 0; i < MAXN; ++i) {
-            const int id = i * THREADS + (int)threadIdx.x;
-            const int row = id / nch, c = id % nch;
-            const int n = j0 + row;
-            const int64_t span = ((int64_t)n * row_groups + group) * gb;
-            const bool ok = id < total && n < J;
-            reg[i] = buf_load16(rs, ok ? (uint32_t)((span & ~int64_t(15)) + 16 * c) : kOOB);
-        }
+template <int BJ, int THREADS>
+__device__ __forceinline__ void gate_stage_lds(u32x4* __restrict__ buf, const uint8_t* __restrict__ qbytes, int qt,
+                                               int64_t row_groups, int j0, int group, int J) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    const int gb = group_bytes(qt), nch = gate_row_chunks(qt);
+    const int64_t bytes = (int64_t)J * row_groups * gb;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(qbytes), (short)0, (int)(bytes < (int64_t)kRange ? bytes : (int64_t)kRange), 0x00020000);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int NW = THREADS / 64;
+    const int total = BJ * nch;
+    for (int base = wave * 64; base < total; base += NW * 64) {
+        const int id = base + lane;
+        const int row = id / nch, c = id % nch;
+        const int n = (j0 + row < J && id < total) ? j0 + row : 0;
+        const int64_t span = ((int64_t)n * row_groups + group) * gb;
+        // one instruction per wave: lanes land at buf + 16 (base + lane)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(buf + base), 16,
+                                                 (uint32_t)((span & ~int64_t(15)) + 16 * c), 0, 0, 0);
     }
-    // Row slot pitch in LDS: kGateMaxChunks chunks.
-    __device__ __forceinline__ void store(u32x4* __restrict__ buf) const {
-        const int total = BJ * nch;
-#pragma unroll
-        for (int i = 0; i < MAXN; ++i) {
-            const int id = i * THREADS + (int)threadIdx.x;
-            if (id < total) buf[(id / nch) * kGateMaxChunks + id % nch] = reg[i];
-        }
-    }
-};
+}
 
 // <acc, W_k> over the lane's accumulators: block (a, b) holds, for row
 // n = 32 b + lane%32, the 16 weights 32 a + 4 (lane/32) + 8 u + t of one
 // 32-weight sub-block (relative to the wave's tile origin).
 template <int QT, int MI, int NJ, int WTI, int WTJ>
 __device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const uint8_t* __restrict__ buf,
-                                              int64_t row_groups, int j0, int group, int wi, int wj, int lane) {
+                                              int64_t row_groups, int j0, int group, int wi, int wj, int lane, int J) {
     constexpr int GB = group_bytes(QT);
+    constexpr int PITCH = 16 * ((GB + 15 + 15) / 16);  // bytes per staged row span
     float s = 0.0f;
 #pragma unroll
     for (int b = 0; b < NJ; ++b) {
         const int nl = wj * WTJ + 32 * b + (lane & 31);
-        const int64_t span = ((int64_t)(j0 + nl) * row_groups + group) * GB;
-        const uint8_t* g = buf + nl * (kGateMaxChunks * 16) + (int)(span & 15);
+        // rows past J were staged from row 0: locate their bytes the same way
+        const int n = j0 + nl < J ? j0 + nl : 0;
+        const int64_t span = ((int64_t)n * row_groups + group) * GB;
+        const uint8_t* g = buf + nl * PITCH + (int)(span & 15);
 #pragma unroll
         for (int a = 0; a < MI; ++a) {
             float v[16];
@@ -454,27 +466,29 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkIte
     const int wi = wave / WJ, wj = wave % WJ;
     const int group = i0 / 256;
     const int64_t rg = p.cs.row_groups;
-    GateStager<BJ, S::THREADS> st;
-    st.load(p.cs.qbytes[0], p.cs.qtype[0], rg, j0, group, p.J);
     __syncthreads();  // every wave is past its last main-loop LDS read
-    st.store(smem);
+    gate_stage_regs<BJ, S::THREADS>(smem, p.cs.qbytes[0], p.cs.qtype[0], rg, j0, group, p.J);
     for (int k = 0; k < p.cs.ncand; ++k) {
-        __syncthreads();  // candidate k is in buffer k % 2; buffer (k+1) % 2 is free
-        if (k + 1 < p.cs.ncand) st.load(p.cs.qbytes[k + 1], p.cs.qtype[k + 1], rg, j0, group, p.J);
+        // this wave's direct-to-LDS copies of candidate k have landed, then
+        // everyone's have; buffer (k+1) % 2 is no longer read
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (k + 1 < p.cs.ncand)
+            gate_stage_lds<BJ, S::THREADS>(smem + ((k + 1) & 1) * BUF_CH, p.cs.qbytes[k + 1], p.cs.qtype[k + 1], rg, j0,
+                                           group, p.J);
         const uint8_t* buf = reinterpret_cast<const uint8_t*>(smem + (k & 1) * BUF_CH);
         float sum;
         switch (p.cs.qtype[k]) {
-        case Q8_0: sum = gate_dot_lds<Q8_0, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
-        case Q2_K: sum = gate_dot_lds<Q2_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
-        case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
-        case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
-        case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
-        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane); break;
+        case Q8_0: sum = gate_dot_lds<Q8_0, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q2_K: sum = gate_dot_lds<Q2_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
         if (lane == 0) red[wave][k] = sum;
-        if (k + 1 < p.cs.ncand) st.store(smem + ((k + 1) & 1) * BUF_CH);
     }
     __syncthreads();
     if ((int)threadIdx.x < p.cs.ncand) {
