@@ -4,16 +4,18 @@
 
 namespace vq {
 
-// 256x256 output tiles, BK = 64, 8 waves (two per SIMD), two register
-// prefetch stages.  Wave layouts from the tile sweep on MI355X: forward and dX
-// 2x4 (128x64 wave tiles), gate 4x2 (64x128).  Operands stored [K][rows] in memory (dX's W, both gate operands)
-// use LoaderN: LDS keeps their orientation and fragments come from transpose
-// reads.
-using FwdLA = LoaderK<256, 64, 512>;
-using FwdLB = LoaderK<256, 64, 512>;
-using DxLA = LoaderK<256, 64, 512>;
-using DxLB = LoaderN<256, 64, 512>;
-using GateL = LoaderN<256, 64, 512>;
+// 256x256 output tiles, 4 waves of 128x128 (256 fp32 accumulators per lane,
+// held in AGPRs), operands copied global -> LDS by direct-to-LDS loads into two
+// padded LDS stages with the stage switch inside the MFMA stream.  BK = 64 for
+// the forward and dX products, 32 for the gate product (its epilogue, not the
+// main loop, sets the LDS size; measured on MI355X at 8192 x 5120 x 17408).
+// Operands stored [K][rows] (dX's W, both gate operands) keep that orientation
+// in LDS and are read with ds_read_b64_tr_b16.
+using FwdLA = DmaK<256, 64, 256>;
+using FwdLB = DmaK<256, 64, 256>;
+using DxLA = DmaK<256, 64, 256>;
+using DxLB = DmaN<256, 64, 256>;
+using GateL = DmaN<256, 32, 256>;
 constexpr int kGateBI = 256, kGateBJ = 256;
 
 static int device_cus() {
@@ -57,14 +59,14 @@ hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t
                            hipStream_t s) {
     GemmParams p{};
     p.A = X; p.lda = D; p.B = W; p.ldb = ldw; p.I = M; p.J = N; p.K = D; p.splits = 1; p.C = Y; p.ldc = N;
-    return launch_gemm<FwdLA, FwdLB, 256, 256, 64, 2, 4, EPI_STORE, 2>(p, s);
+    return launch_gemm<FwdLA, FwdLB, 256, 256, 64, 2, 2, EPI_STORE, 2>(p, s);
 }
 
 hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,
                           hipStream_t s) {
     GemmParams p{};
     p.A = dY; p.lda = N; p.B = W; p.ldb = ldw; p.I = M; p.J = D; p.K = N; p.splits = 1; p.C = dX; p.ldc = D;
-    return launch_gemm<DxLA, DxLB, 256, 256, 64, 2, 4, EPI_STORE, 2>(p, s);
+    return launch_gemm<DxLA, DxLB, 256, 256, 64, 2, 2, EPI_STORE, 2>(p, s);
 }
 
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
@@ -73,7 +75,7 @@ hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs
     p.A = X; p.lda = D; p.B = dY; p.ldb = N; p.I = D; p.J = N; p.K = M;
     p.splits = gate_splits(M, N, D);
     p.cs = cs; p.dlimit = D; p.partials = partials;
-    return launch_gemm<GateL, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2>(p, s);
+    return launch_gemm<GateL, GateL, kGateBI, kGateBJ, 32, 2, 2, EPI_GATE, 2>(p, s);
 }
 
 // Fixed-order fp64 sum of the work-item partials: dprobs[k] = sum_t partials[t][k].

@@ -63,6 +63,8 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
 
 template <int ROWS, int BK, int THREADS>
 struct LoaderK {
+    static constexpr bool kDma = false;
+    static constexpr int kFragReads = 1;
     static constexpr int CPR = BK / 8;
     static constexpr int NL = ROWS * CPR / THREADS;
     static_assert(NL * THREADS == ROWS * CPR, "tile must split evenly over threads");
@@ -100,6 +102,8 @@ struct LoaderK {
 // registers), else 8.
 template <int ROWS, int BK, int THREADS>
 struct LoaderT {
+    static constexpr bool kDma = false;
+    static constexpr int kFragReads = 1;
     static constexpr int RB = ROWS / 8;  // 8-row blocks along the tile rows
     static constexpr int KB = (RB * (BK / 4) >= THREADS) ? 4 : 8;
     static constexpr int NB = RB * (BK / KB);  // blocks per tile
@@ -170,6 +174,8 @@ struct LoaderT {
 // distinct bank groups.
 template <int ROWS, int BK, int THREADS>
 struct LoaderN {
+    static constexpr bool kDma = false;
+    static constexpr int kFragReads = 2;  // two ds_read_b64_tr_b16
     static constexpr int PITCH = ROWS + 32;       // bf16 per k-row in LDS
     static constexpr int RCH = ROWS / 8;          // 16-byte chunks per k-row
     static constexpr int NL = BK * RCH / THREADS;
@@ -207,6 +213,97 @@ struct LoaderN {
         typedef short v8i16 __attribute__((ext_vector_type(8)));
         const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         return __builtin_bit_cast(bf16x8_t, v);
+    }
+};
+
+// ---------------------------------------------------------------- direct-to-LDS loaders
+// buffer_load_dwordx4 ... lds: lane l of one wave instruction writes its 16
+// bytes at M0 + 16 l, so one instruction fills 64 consecutive LDS chunks and
+// no register ever holds the tile.  The stage layouts keep padding for
+// conflict-free fragment reads (one chunk per tile row in DmaK, 32 bf16 per
+// k-row in DmaN, the LoaderN layout); lanes that land on padding, or on
+// rows / k past the matrix, use an out-of-range offset and write zeros
+// without touching memory.  A lane's offset depends only on (instruction,
+// wave, lane) and the tile origin, so offsets are computed once per work
+// item and the k origin moves the descriptor base.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int ROWS, int BK, int THREADS>
+struct DmaK {
+    static constexpr bool kDma = true;
+    static constexpr int kFragReads = 1;
+    static constexpr int CPR = BK / 8;   // data chunks per tile row
+    static constexpr int PCH = CPR + 1;  // chunks per padded row
+    static constexpr int NW = THREADS / 64;
+    static constexpr int NI = (ROWS * PCH + 64 * NW - 1) / (64 * NW);  // instructions per wave per stage
+    static constexpr int CHUNKS = NI * 64 * NW;                        // LDS chunks per stage
+    uint32_t voff[NI];
+    int kpos[NI];
+
+    // tile rows [r0, r0 + ROWS) of src[row * ld + k]
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int L = (i * NW + wave) * 64 + lane;
+            const int row = L / PCH, c = L % PCH;
+            const bool ok = c < CPR && row < ROWS && r0 + row < rows;
+            voff[i] = ok ? (uint32_t)((row * ld + 8 * c) * 2) : kOOB;
+            kpos[i] = 8 * c + 8;  // k extent this lane's chunk needs
+        }
+    }
+    // k range [k0, k0 + kvalid) into the stage at lds (kvalid < BK on a ragged
+    // last tile; 0 writes zeros and reads nothing)
+    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t ld, int r0, int k0,
+                                          int kvalid) const {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)r0 * ld + k0);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
+                                                     kpos[i] <= kvalid ? voff[i] : kOOB, 0, 0, 0);
+    }
+    // MFMA fragment: tile row `row + lane%32`, k = 16 ks + 8 (lane/32) .. +7
+    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
+        return __builtin_bit_cast(bf16x8_t, lds[(row + (lane & 31)) * PCH + 2 * ks + (lane >> 5)]);
+    }
+};
+
+template <int ROWS, int BK, int THREADS>
+struct DmaN {
+    static constexpr bool kDma = true;
+    static constexpr int kFragReads = 2;
+    static constexpr int RCH = ROWS / 8;                 // data chunks per k-row
+    static constexpr int PCH = (ROWS + 32) / 8;          // chunks per padded k-row (LoaderN pitch)
+    static constexpr int NW = THREADS / 64;
+    static constexpr int NI = (BK * PCH + 64 * NW - 1) / (64 * NW);
+    static constexpr int CHUNKS = NI * 64 * NW;
+    uint32_t voff[NI];
+    int kpos[NI];
+
+    // tile rows [r0, r0 + ROWS) of src[k * ld + row]
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int L = (i * NW + wave) * 64 + lane;
+            const int kr = L / PCH, c = L % PCH;
+            const bool ok = c < RCH && kr < BK && r0 + 8 * c < rows;
+            voff[i] = ok ? (uint32_t)((kr * ld + 8 * c) * 2) : kOOB;
+            kpos[i] = kr + 1;
+        }
+    }
+    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t ld, int r0, int k0,
+                                          int kvalid) const {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)k0 * ld + r0);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
+                                                     kpos[i] <= kvalid ? voff[i] : kOOB, 0, 0, 0);
+    }
+    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
+        return LoaderN<ROWS, BK, THREADS>::read_frag(lds, row, ks, lane);
     }
 };
 
@@ -262,31 +359,60 @@ struct GemmShape {
     static constexpr int MI = WTI / 32, NJ = WTJ / 32;
 };
 
-template <class LA, class LB>
+template <class LA, class LB, int DEPTH = 1>
 struct StageLds {
     static constexpr int A_CH = LA::CHUNKS, B_CH = LB::CHUNKS;  // 16-byte chunks per stage
-    static constexpr size_t BYTES = (size_t)2 * (A_CH + B_CH) * 16;
+    // register loaders double buffer; direct-to-LDS loaders keep DEPTH stages
+    static constexpr int NSTAGE = LA::kDma ? DEPTH : 2;
+    static constexpr size_t BYTES = (size_t)NSTAGE * (A_CH + B_CH) * 16;
 };
 
 // MFMAs of one LDS stage.
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ>
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, bool SCHED = false>
 __device__ __forceinline__ void gemm_stage_mfma(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, int wi,
                                                 int wj, int lane,
                                                 f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
                                                              [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
+    constexpr int KS = BK / 16;
+    // fragments of k-step ks + 1 are read while the MFMAs of ks run
+    bf16x8_t fa[2][S::MI], fb[2][S::NJ];
+    auto read = [&](int ks, int buf) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-        bf16x8_t fa[S::MI], fb[S::NJ];
+        for (int a = 0; a < S::MI; ++a) fa[buf][a] = LA::read_frag(sa, wi * S::WTI + 32 * a, ks, lane);
 #pragma unroll
-        for (int a = 0; a < S::MI; ++a) fa[a] = LA::read_frag(sa, wi * S::WTI + 32 * a, ks, lane);
+        for (int b = 0; b < S::NJ; ++b) fb[buf][b] = LB::read_frag(sb, wj * S::WTJ + 32 * b, ks, lane);
+    };
+    read(0, 0);
 #pragma unroll
-        for (int b = 0; b < S::NJ; ++b) fb[b] = LB::read_frag(sb, wj * S::WTJ + 32 * b, ks, lane);
+    for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) read(ks + 1, (ks + 1) & 1);
 #pragma unroll
         for (int a = 0; a < S::MI; ++a)
 #pragma unroll
             for (int b = 0; b < S::NJ; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][a], fb[ks & 1][b], acc[a][b], 0, 0, 0);
+    }
+    if constexpr (SCHED) {
+        // Instruction order for the scheduler: the first k-step's fragment
+        // reads, then each k-step's MFMAs with the next k-step's reads spread
+        // among them (LDS latency hides behind the matrix pipe).
+        constexpr int FR = S::MI * S::NJ > 0 ? LA::kFragReads * S::MI + LB::kFragReads * S::NJ : 0;
+        constexpr int MF = S::MI * S::NJ;
+        constexpr int PER = (MF + FR - 1) / FR;  // MFMAs per read
+        __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + 1 < KS) {
+#pragma unroll
+                for (int r = 0; r < FR; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);
+                }
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+            }
+        }
     }
 }
 
@@ -368,6 +494,160 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, int i0, int j
         stage(kt, la0, lb0, la1, lb1);
         if (kt + 1 < nk) stage(kt + 1, la1, lb1, la0, lb0);
     }
+}
+
+// Main loop with direct-to-LDS loaders and NS LDS stages: the loads of stage
+// kt + NS - 1 are issued right after the barrier that retires stage kt - 1,
+// so NS - 1 stages are in flight while stage kt is multiplied.  One barrier
+// per stage; each wave waits (vmcnt) only for its own copies of stage kt.
+// Wait until at most N of this wave's vector-memory operations are pending,
+// then for its LDS operations, then for the other waves.  A plain
+// __syncthreads() would also drain vmcnt (its release fence), retiring the
+// stages still in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int NS>
+__device__ __forceinline__ void gemm_mainloop_dma(const GemmParams& p, int i0, int j0, int kbeg, int kend,
+                                                  u32x4* __restrict__ smem,
+                                                  f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
+                                                               [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 LDS stages");
+    using S = GemmShape<BI, BJ, BK, WI, WJ>;
+    constexpr int STAGE = LA::CHUNKS + LB::CHUNKS;
+    constexpr int NI = LA::NI + LB::NI;  // copies per wave per stage
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wi = wave / WJ, wj = wave % WJ;
+    LA la;
+    LB lb;
+    la.init(p.lda, i0, p.I);
+    lb.init(p.ldb, j0, p.J);
+#pragma unroll
+    for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+        for (int b = 0; b < S::NJ; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    const int nk = (kend - kbeg + BK - 1) / BK;
+    auto issue = [&](int kt) {
+        u32x4* st = smem + (kt % NS) * STAGE;
+        const int k0 = kbeg + kt * BK;
+        const int kvalid = min(BK, kend - k0);
+        la.issue(st, p.A, p.lda, i0, k0, kvalid);
+        lb.issue(st + LA::CHUNKS, p.B, p.ldb, j0, k0, kvalid);
+    };
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+        if (s < nk) issue(s);
+    for (int kt = 0; kt < nk; ++kt) {
+        // stages issued after kt and still allowed in flight
+        // then every wave's copies of stage kt have landed and stage kt - 1 is
+        // no longer read
+        const int newer = min(NS - 2, nk - 1 - kt);
+        if (NS >= 4 && newer >= 2) wait_vmcnt_barrier<(NS >= 4 ? 2 : 0) * NI>();
+        else if (NS >= 3 && newer >= 1) wait_vmcnt_barrier<(NS >= 3 ? 1 : 0) * NI>();
+        else wait_vmcnt_barrier<0>();
+        if (kt + NS - 1 < nk) issue(kt + NS - 1);
+        const u32x4* st = smem + (kt % NS) * STAGE;
+        gemm_stage_mfma<LA, LB, BI, BJ, BK, WI, WJ, true>(st, st + LA::CHUNKS, wi, wj, lane, acc);
+    }
+}
+
+// Two-stage variant with the stage switch inside the MFMA stream: the wait
+// for stage kt + 1 and the barrier come after the last k-step's fragments of
+// stage kt are in registers, so the next stage's first fragment reads and the
+// copies of stage kt + 2 (into the buffer stage kt just vacated) are issued
+// among the last k-step's MFMAs instead of in front of an idle matrix pipe.
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ>
+__device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, int j0, int kbeg, int kend,
+                                                 u32x4* __restrict__ smem,
+                                                 f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
+                                                              [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
+    using S = GemmShape<BI, BJ, BK, WI, WJ>;
+    constexpr int STAGE = LA::CHUNKS + LB::CHUNKS;
+    constexpr int KS = BK / 16;
+    static_assert(KS % 2 == 0, "fragment buffers alternate per k-step");
+    constexpr int FR = LA::kFragReads * S::MI + LB::kFragReads * S::NJ;  // LDS reads per k-step
+    constexpr int MF = S::MI * S::NJ;                                     // MFMAs per k-step
+    constexpr int NI = LA::NI + LB::NI;                                   // copies per stage
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wi = wave / WJ, wj = wave % WJ;
+    LA la;
+    LB lb;
+    la.init(p.lda, i0, p.I);
+    lb.init(p.ldb, j0, p.J);
+#pragma unroll
+    for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+        for (int b = 0; b < S::NJ; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    const int nk = (kend - kbeg + BK - 1) / BK;
+    // stage kt past the end copies nothing (zeros into a free buffer)
+    auto issue = [&](int kt) {
+        u32x4* st = smem + (kt & 1) * STAGE;
+        const int k0 = min(kbeg + kt * BK, kend);
+        const int kvalid = min(BK, kend - k0);
+        la.issue(st, p.A, p.lda, i0, k0, kvalid);
+        lb.issue(st + LA::CHUNKS, p.B, p.ldb, j0, k0, kvalid);
+    };
+    bf16x8_t fa[2][S::MI], fb[2][S::NJ];
+    auto read = [&](const u32x4* st, int ks, int buf) {
+#pragma unroll
+        for (int a = 0; a < S::MI; ++a) fa[buf][a] = LA::read_frag(st, wi * S::WTI + 32 * a, ks, lane);
+#pragma unroll
+        for (int b = 0; b < S::NJ; ++b) fb[buf][b] = LB::read_frag(st + LA::CHUNKS, wj * S::WTJ + 32 * b, ks, lane);
+    };
+    auto mfma = [&](int buf) {
+#pragma unroll
+        for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+            for (int b = 0; b < S::NJ; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][a], fb[buf][b], acc[a][b], 0, 0, 0);
+    };
+
+    if (nk <= 0) return;
+    issue(0);
+    wait_vmcnt_barrier<0>();
+    issue(1);
+    read(smem, 0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const u32x4* st = smem + (kt & 1) * STAGE;
+#pragma unroll
+        for (int ks = 0; ks + 1 < KS; ++ks) {
+            read(st, ks + 1, (ks + 1) & 1);
+            mfma(ks & 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);  // reads of k-step 1 first
+#pragma unroll
+        for (int ks = 1; ks + 1 < KS; ++ks) {
+#pragma unroll
+            for (int r = 0; r < FR; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, (MF + FR - 1) / FR, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+        // all of stage kt is in registers: wait for stage kt + 1, then stage
+        // kt's buffer is free for stage kt + 2 (past the end: harmless zeros
+        // and reads, so the body has no branch and one set of accumulators)
+        wait_vmcnt_barrier<0>();
+        issue(kt + 2);
+        read(smem + ((kt + 1) & 1) * STAGE, 0, 0);
+        mfma((KS - 1) & 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, FR, 1);
+#pragma unroll
+        for (int r = 0; r < MF; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x020, (NI + MF - 1) / MF, 1);
+        }
+    }
+    wait_vmcnt_barrier<0>();  // the zero copies have landed before anyone reuses LDS
 }
 
 // ---------------------------------------------------------------- gate epilogue
@@ -499,8 +779,12 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkIte
 }
 
 // ---------------------------------------------------------------- kernel
+// Four-wave workgroups hold 256 accumulators per lane and run one wave per
+// SIMD: telling the compiler so lets it keep fragments in flight instead of
+// minimising registers for an occupancy the LDS use rules out anyway.
 template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH>
-__global__ __launch_bounds__(WI* WJ * 64) void gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(WI* WJ * 64) __attribute__((amdgpu_waves_per_eu(WI * WJ == 4 ? 1 : 2, WI * WJ == 4 ? 1 : 2)))
+void gemm_kernel(GemmParams p) {
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     extern __shared__ u32x4 smem[];
     const int tiles_i = (p.I + BI - 1) / BI, tiles_j = (p.J + BJ - 1) / BJ;
@@ -513,7 +797,12 @@ __global__ __launch_bounds__(WI* WJ * 64) void gemm_kernel(GemmParams p) {
         kend = min(p.K, kbeg + chunk);
     }
     f32x16 acc[S::MI][S::NJ];
-    gemm_mainloop<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
+    if constexpr (LA::kDma && DEPTH == 2)
+        gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ>(p, i0, j0, kbeg, kend, smem, acc);
+    else if constexpr (LA::kDma)
+        gemm_mainloop_dma<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
+    else
+        gemm_mainloop<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
 
     if constexpr (EPI == EPI_STORE) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -534,9 +823,9 @@ __global__ __launch_bounds__(WI* WJ * 64) void gemm_kernel(GemmParams p) {
     }
 }
 
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI>
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH>
 constexpr size_t gemm_lds_bytes() {
-    constexpr size_t main = StageLds<LA, LB>::BYTES;
+    constexpr size_t main = StageLds<LA, LB, DEPTH>::BYTES;
     constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16;
     return EPI == EPI_GATE && gate > main ? gate : main;
 }
@@ -545,7 +834,8 @@ template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, i
 static hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
     if (p.I <= 0 || p.J <= 0) return hipSuccess;
     auto kern = gemm_kernel<LA, LB, BI, BJ, BK, WI, WJ, EPI, DEPTH>;
-    constexpr size_t lds = gemm_lds_bytes<LA, LB, BI, BJ, BK, WI, WJ, EPI>();
+    constexpr size_t lds = gemm_lds_bytes<LA, LB, BI, BJ, BK, WI, WJ, EPI, DEPTH>();
+    static_assert(lds <= 160 * 1024, "exceeds the 160 KiB of LDS per workgroup");
     static bool attr_set = false;  // per instantiation
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
