@@ -166,7 +166,9 @@ int vq_gated_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int6
 
 int64_t vq_gated_linear_bwd_workspace(int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff) {
     if (m < 0 || n <= 0 || d <= 0 || ncand < 1 || m > INT32_MAX || n > INT32_MAX || d > INT32_MAX) return -1;
+    // [gate partials][dX split-tail partial tiles][re-mixed W_eff]
     int64_t bytes = align256(vq::gate_partial_count((int)m, (int)n, (int)d) * ncand * (int64_t)sizeof(float));
+    bytes += align256(vq::dx_tail_bytes((int)m, (int)n, (int)d));
     if (need_w_eff) bytes += align256(n * d_pad * 2);
     return bytes;
 }
@@ -193,23 +195,37 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
                     (long long)(workspace ? ws_bytes : 0));
     if (workspace && !aligned16(workspace)) return fail(VQ_ERR_ALIGN, "workspace not 16-byte aligned");
     float* partials = static_cast<float*>(workspace);
+    const int64_t tail_bytes = align256(vq::dx_tail_bytes((int)m, (int)n, (int)d));
+    // dX splits its tail tiles along K only with room for their partials
+    float* tail_ws = nullptr;
+    if (workspace && tail_bytes > 0 && ws_bytes >= part_bytes + tail_bytes)
+        tail_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
     if (dx) {
         const uint16_t* w = w_eff;
         if (remix) {
             if (!probs) return fail(VQ_ERR_NULL, "probs is NULL");
-            uint16_t* wbuf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes);
+            uint16_t* wbuf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes + tail_bytes);
             rc = hip_check(vq::launch_mix(cs, probs, wbuf, n * d_pad / 256, s), "mix launch");
             if (rc != VQ_OK) return rc;
             w = wbuf;
         }
-        if (m > 0) {
-            rc = hip_check(vq::launch_gemm_dx(dy, w, d_pad, dx, (int)m, (int)n, (int)d, s), "dX GEMM launch");
+        if (m > 0 && dprobs) {
+            // both products in one launch: each fills the other's last round
+            rc = hip_check(vq::launch_gemm_dx_gate(dy, w, d_pad, dx, x, cs, partials, (int)m, (int)n, (int)d,
+                                                   tail_ws, s),
+                           "dX + gate GEMM launch");
+            if (rc != VQ_OK) return rc;
+        } else if (m > 0) {
+            rc = hip_check(vq::launch_gemm_dx(dy, w, d_pad, dx, (int)m, (int)n, (int)d, tail_ws, s),
+                           "dX GEMM launch");
             if (rc != VQ_OK) return rc;
         }
     }
     if (dprobs) {
-        rc = hip_check(vq::launch_gemm_gate(dy, x, cs, partials, (int)m, (int)n, (int)d, s), "gate GEMM launch");
-        if (rc != VQ_OK) return rc;
+        if (!dx) {
+            rc = hip_check(vq::launch_gemm_gate(dy, x, cs, partials, (int)m, (int)n, (int)d, s), "gate GEMM launch");
+            if (rc != VQ_OK) return rc;
+        }
         rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, s),
                        "gate reduce launch");
         if (rc != VQ_OK) return rc;

@@ -213,22 +213,28 @@ __device__ __forceinline__ float dot_run(const uint8_t* __restrict__ g, int p, c
 
 // <v, W> over the 16 weights p0 + 4h + 8u + t (u, t in 0..3) of the 32-weight
 // sub-block starting at p0 (a multiple of 32), with v[4u + t] their values:
-// the per-lane footprint of a 32x32 MFMA accumulator block.  Scales and mins
-// are decoded once per 16-weight half; codes are read 4 bytes at a time.
+// the per-lane footprint of a 32x32 MFMA accumulator block.  sv[hf] is the sum
+// of v over half hf (v[0..7] and v[8..15], weights 0..15 and 16..31 of the
+// sub-block); it is the same for every candidate, so the caller computes it
+// once.  Codes are unpacked four at a time (one shift and mask per 32-bit
+// word, then v_cvt_f32_ubyteN per weight) as unsigned values u; a format's
+// constant offset (Q8_0's sign via u = q ^ 0x80, Q6_K's -32, Q3_K's -4) and
+// K-quant mins are applied once per half through sv:
+//   sum v (dl (u - o) - ml) = dl (sum v u - o sv) - ml sv.
 template <int QT>
-__device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0, int h, const float* __restrict__ v) {
-    float s1[2] = {0.0f, 0.0f}, s0[2] = {0.0f, 0.0f};
-    float dl[2], ml[2] = {0.0f, 0.0f};
-    uint32_t cw[4], xw[4];  // code words (and 5th/high-bit words) of the 4 runs
-    int shift = 0, xshift = 0;
+__device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0, int h, const float* __restrict__ v,
+                                           const float (&sv)[2]) {
+    uint32_t uw[4];  // four unsigned code bytes per word, weights 4u .. 4u + 3 of the lane
+    float dl[2], ml[2] = {0.0f, 0.0f}, off = 0.0f;
     if constexpr (QT == Q8_0) {
         const uint8_t* b = g + 34 * (p0 >> 5);
         dl[0] = dl[1] = h2f(*reinterpret_cast<const uint16_t*>(b));
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + 4 * h + 8 * u);
-            cw[u] = (uint32_t)q[0] | ((uint32_t)q[1] << 16);
+            uw[u] = ((uint32_t)q[0] | ((uint32_t)q[1] << 16)) ^ 0x80808080u;
         }
+        off = 128.0f;
     } else if constexpr (QT == Q4_K || QT == Q5_K) {
         const uint32_t dd = *reinterpret_cast<const uint32_t*>(g);
         const int c = p0 >> 6, nib = (p0 >> 5) & 1;
@@ -238,12 +244,14 @@ __device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0
         ml[0] = ml[1] = h2f(dd >> 16) * (float)m;
         const uint8_t* qs = g + (QT == Q5_K ? 48 : 16) + 32 * c + 4 * h;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) cw[u] = *reinterpret_cast<const uint32_t*>(qs + 8 * u);
-        shift = 4 * nib;
+        for (int u = 0; u < 4; ++u) uw[u] = (*reinterpret_cast<const uint32_t*>(qs + 8 * u) >> (4 * nib)) & 0x0F0F0F0Fu;
         if constexpr (QT == Q5_K) {
+            const int xs = 2 * c + nib;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) xw[u] = *reinterpret_cast<const uint32_t*>(g + 16 + 4 * h + 8 * u);
-            xshift = 2 * c + nib;
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t x = *reinterpret_cast<const uint32_t*>(g + 16 + 4 * h + 8 * u);
+                uw[u] |= ((x >> xs) & 0x01010101u) << 4;
+            }
         }
     } else if constexpr (QT == Q6_K) {
         const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 208));
@@ -256,11 +264,11 @@ __device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0
         for (int u = 0; u < 4; ++u) {
             const uint16_t* a = reinterpret_cast<const uint16_t*>(ql + 8 * u);
             const uint16_t* b = reinterpret_cast<const uint16_t*>(qh + 8 * u);
-            cw[u] = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
-            xw[u] = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+            const uint32_t lw = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
+            const uint32_t hw = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+            uw[u] = ((lw >> (4 * (t4 >> 1))) & 0x0F0F0F0Fu) | (((hw >> (2 * t4)) & 0x03030303u) << 4);
         }
-        shift = 4 * (t4 >> 1);
-        xshift = 2 * t4;
+        off = 32.0f;
     } else if constexpr (QT == Q3_K) {
         const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 108));
         const int n = p0 >> 7, j = (p0 >> 5) & 3;
@@ -272,16 +280,18 @@ __device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0
             const uint32_t hi2 = (sb[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
             dl[hf] = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
         }
+        const int xs = 4 * n + j;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int o = 16 * (u >> 1) + 4 * h + 8 * (u & 1);  // 16 * half + l within the 32-run
             const uint16_t* a = reinterpret_cast<const uint16_t*>(g + 32 + 32 * n + o);
             const uint16_t* b = reinterpret_cast<const uint16_t*>(g + o);
-            cw[u] = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
-            xw[u] = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+            const uint32_t lw = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
+            const uint32_t hw = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+            // q = low2 - (hmask bit ? 0 : 4) = (low2 | bit << 2) - 4
+            uw[u] = ((lw >> (2 * j)) & 0x03030303u) | (((hw >> xs) & 0x01010101u) << 2);
         }
-        shift = 2 * j;
-        xshift = 4 * n + j;
+        off = 4.0f;
     } else {  // Q2_K
         const uint32_t dd = *reinterpret_cast<const uint32_t*>(g + 80);
         const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
@@ -295,36 +305,16 @@ __device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int o = 16 * (u >> 1) + 4 * h + 8 * (u & 1);
-            cw[u] = *reinterpret_cast<const uint32_t*>(g + 16 + 32 * n + o);
-        }
-        shift = 2 * j;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int hf = u >> 1;  // runs 0,1 are weights 0..15 of the sub-block, runs 2,3 are 16..31
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t byte = (cw[u] >> (8 * t)) & 0xffu;
-            float q;
-            if constexpr (QT == Q8_0) {
-                q = (float)(int8_t)byte;
-            } else if constexpr (QT == Q4_K) {
-                q = (float)((byte >> shift) & 0xFu);
-            } else if constexpr (QT == Q5_K) {
-                q = (float)(((byte >> shift) & 0xFu) | ((((xw[u] >> (8 * t)) >> xshift) & 1u) << 4));
-            } else if constexpr (QT == Q6_K) {
-                q = (float)((int)(((byte >> shift) & 0xFu) | ((((xw[u] >> (8 * t)) >> xshift) & 3u) << 4)) - 32);
-            } else if constexpr (QT == Q3_K) {
-                q = (float)((int)((byte >> shift) & 3u) - ((((xw[u] >> (8 * t)) >> xshift) & 1u) ? 0 : 4));
-            } else {
-                q = (float)((byte >> shift) & 3u);
-            }
-            s1[hf] = fmaf(v[4 * u + t], q, s1[hf]);
-            if constexpr (HasMin<QT>::value) s0[hf] += v[4 * u + t];
+            uw[u] = (*reinterpret_cast<const uint32_t*>(g + 16 + 32 * n + o) >> (2 * j)) & 0x03030303u;
         }
     }
-    float r = dl[0] * s1[0] + dl[1] * s1[1];
-    if constexpr (HasMin<QT>::value) r -= ml[0] * s0[0] + ml[1] * s0[1];
+    float s1[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) s1[u >> 1] = fmaf(v[4 * u + t], (float)((uw[u] >> (8 * t)) & 0xffu), s1[u >> 1]);
+    float r = dl[0] * (s1[0] - off * sv[0]) + dl[1] * (s1[1] - off * sv[1]);
+    if constexpr (HasMin<QT>::value) r -= ml[0] * sv[0] + ml[1] * sv[1];
     return r;
 }
 

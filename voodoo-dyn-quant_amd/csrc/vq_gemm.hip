@@ -18,7 +18,7 @@ using DxLB = DmaN<256, 64, 256>;
 using GateL = DmaN<256, 32, 256>;
 constexpr int kGateBI = 256, kGateBJ = 256;
 
-static int device_cus() {
+int device_cus() {
     static int cus = 0;
     if (cus == 0) {
         int dev = 0;
@@ -31,51 +31,66 @@ static int device_cus() {
     return cus;
 }
 
-// Reduction splits of the gate product: more work items shorten the last
-// round of tiles, each split repeats the epilogue (measured: about as long
-// as 1200 rows of the reduction).
-int gate_splits(int M, int N, int D) {
-    const int tiles = ((D + kGateBI - 1) / kGateBI) * ((N + kGateBJ - 1) / kGateBJ);
-    const int cus = device_cus();
-    int best = 1;
-    double best_t = 1e30;
-    for (int s = 1; s <= 4; ++s) {
-        if (s > 1 && M / s < 1024) break;
-        const int64_t rounds = ((int64_t)tiles * s + cus - 1) / cus;
-        const double t = (double)rounds * (1.0 / s + 1200.0 / (M > 0 ? M : 1));
-        if (t < best_t - 1e-9) {
-            best_t = t;
-            best = s;
-        }
-    }
-    return best;
+using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 2, 2, EPI_STORE, 2>;
+using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 2, 2, EPI_STORE, 2>;
+using GateCfg = GemmCfg<GateL, GateL, kGateBI, kGateBJ, 32, 2, 2, EPI_GATE, 2>;
+
+static GemmParams fwd_params(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D) {
+    GemmParams p{};
+    p.A = X; p.lda = D; p.B = W; p.ldb = ldw; p.I = M; p.J = N; p.K = D; p.C = Y; p.ldc = N;
+    return p;
 }
 
+static GemmParams dx_params(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D) {
+    GemmParams p{};
+    p.A = dY; p.lda = N; p.B = W; p.ldb = ldw; p.I = M; p.J = D; p.K = N; p.C = dX; p.ldc = D;
+    return p;
+}
+
+static GemmParams gate_params(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
+                              int D) {
+    GemmParams p{};
+    p.A = X; p.lda = D; p.B = dY; p.ldb = N; p.I = D; p.J = N; p.K = M;
+    p.cs = cs; p.dlimit = D; p.partials = partials;
+    return p;
+}
+
+// One partial per gate grid block (split tail parts and idle padding blocks
+// included; the latter write zeros).
 int64_t gate_partial_count(int M, int N, int D) {
-    return (int64_t)((D + kGateBI - 1) / kGateBI) * ((N + kGateBJ - 1) / kGateBJ) * gate_splits(M, N, D);
+    GemmParams p = gate_params(nullptr, nullptr, CandSet{}, nullptr, M, N, D);
+    return GateCfg::plan(p, device_cus(), true);
+}
+
+// fp32 workspace for the K parts of dX's split tail tiles.
+int64_t dx_tail_bytes(int M, int N, int D) {
+    GemmParams p = dx_params(nullptr, nullptr, 0, nullptr, M, N, D);
+    DxCfg::plan(p, device_cus(), true);
+    return DxCfg::tail_bytes(p);
 }
 
 hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D,
                            hipStream_t s) {
-    GemmParams p{};
-    p.A = X; p.lda = D; p.B = W; p.ldb = ldw; p.I = M; p.J = N; p.K = D; p.splits = 1; p.C = Y; p.ldc = N;
-    return launch_gemm<FwdLA, FwdLB, 256, 256, 64, 2, 2, EPI_STORE, 2>(p, s);
+    return launch_gemm_cfg<FwdCfg>(fwd_params(X, W, ldw, Y, M, N, D), device_cus(), nullptr, s);
 }
 
 hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,
-                          hipStream_t s) {
-    GemmParams p{};
-    p.A = dY; p.lda = N; p.B = W; p.ldb = ldw; p.I = M; p.J = D; p.K = N; p.splits = 1; p.C = dX; p.ldc = D;
-    return launch_gemm<DxLA, DxLB, 256, 256, 64, 2, 2, EPI_STORE, 2>(p, s);
+                          float* tail_ws, hipStream_t s) {
+    return launch_gemm_cfg<DxCfg>(dx_params(dY, W, ldw, dX, M, N, D), device_cus(), tail_ws, s);
 }
 
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
                             int D, hipStream_t s) {
-    GemmParams p{};
-    p.A = X; p.lda = D; p.B = dY; p.ldb = N; p.I = D; p.J = N; p.K = M;
-    p.splits = gate_splits(M, N, D);
-    p.cs = cs; p.dlimit = D; p.partials = partials;
-    return launch_gemm<GateL, GateL, kGateBI, kGateBJ, 32, 2, 2, EPI_GATE, 2>(p, s);
+    return launch_gemm_cfg<GateCfg>(gate_params(dY, X, cs, partials, M, N, D), device_cus(), nullptr, s);
+}
+
+// dX and gate products of one backward in a single launch (dX work items,
+// the longer ones, first).
+hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
+                               const CandSet& cs, float* partials, int M, int N, int D, float* tail_ws,
+                               hipStream_t s) {
+    return launch_gemm_dual<DxCfg, GateCfg>(dx_params(dY, W, ldw, dX, M, N, D),
+                                            gate_params(dY, X, cs, partials, M, N, D), device_cus(), tail_ws, s);
 }
 
 // Fixed-order fp64 sum of the work-item partials: dprobs[k] = sum_t partials[t][k].

@@ -309,29 +309,77 @@ struct DmaN {
 
 // ---------------------------------------------------------------- work order
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on
-// XCD w % 8).  Remap so that each XCD works through a contiguous run of the
-// grouped tile order: tiles sharing A rows and B rows then meet in the same L2.
-struct WorkItem {
-    int tm, tn, split, logical;
+// XCD w % 8, its local index w / 8).  The tiles, in grouped order (group_m
+// tile-rows at a time, so tiles sharing A rows and B rows meet in one L2), are
+// dealt to the XCDs in contiguous ranges.  An XCD with C CUs runs R = tiles/C
+// whole rounds of whole tiles; its last `tail` tiles are each split along K
+// into s parts (s = C / tail, each part keeping at least 4 k-steps), so the
+// final round takes a fraction of a tile's time instead of leaving CUs idle.
+struct XcdPlan {
+    int t0, tiles;  // the XCD's tile range
+    int full;       // tiles run whole
+    int tail, s;    // tiles split along K, and parts per tile
+    __host__ __device__ int items() const { return full + tail * s; }
 };
 
-__device__ __forceinline__ WorkItem map_work(int tiles_m, int tiles_n, int splits, int group_m) {
-    const int total = tiles_m * tiles_n * splits;
-    const int w = blockIdx.x;
-    const int per = total / 8, rem = total % 8;
-    const int xcd = w % 8, local = w / 8;
-    const int logical = xcd * per + min(xcd, rem) + local;
-    const int tile = logical / splits;
+__host__ __device__ inline XcdPlan xcd_plan(int x, int total_tiles, int cus_per_xcd, int ksteps, bool split_ok) {
+    const int base = total_tiles / 8, rem = total_tiles % 8;
+    XcdPlan pl;
+    pl.tiles = base + (x < rem ? 1 : 0);
+    pl.t0 = x * base + (x < rem ? x : rem);
+    const int c = cus_per_xcd > 0 ? cus_per_xcd : 1;
+    const int t = pl.tiles % c;
+    int sp = t > 0 ? c / t : 1;
+    if (sp > 8) sp = 8;
+    if (sp > ksteps / 4) sp = ksteps / 4;
+    if (!split_ok || t == 0 || sp < 2) {
+        pl.full = pl.tiles;
+        pl.tail = 0;
+        pl.s = 1;
+    } else {
+        pl.full = pl.tiles - t;
+        pl.tail = t;
+        pl.s = sp;
+    }
+    return pl;
+}
+
+struct WorkItem {
+    int tm, tn;      // tile coordinates
+    int split, ns;   // K part and parts of this tile (ns = 1: whole)
+    int tail_slot;   // split tiles: x * tail_max + tail index, else -1
+    bool idle;       // padding block of a shorter XCD
+};
+
+__device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
     const int group_size = group_m * tiles_n;
     const int group = tile / group_size;
     const int first_m = group * group_m;
     const int gm = min(tiles_m - first_m, group_m);
     const int in_group = tile % group_size;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+}
+
+__device__ __forceinline__ WorkItem map_work(int w, int tiles_m, int tiles_n, int ksteps, int cus_per_xcd,
+                                             bool split_ok, int tail_max, int group_m) {
+    const int x = w % 8, local = w / 8;
+    const XcdPlan pl = xcd_plan(x, tiles_m * tiles_n, cus_per_xcd, ksteps, split_ok);
     WorkItem wi;
-    wi.tm = first_m + in_group % gm;
-    wi.tn = in_group / gm;
-    wi.split = logical % splits;
-    wi.logical = logical;
+    wi.idle = local >= pl.items();
+    wi.split = 0;
+    wi.ns = 1;
+    wi.tail_slot = -1;
+    int tile = pl.t0 + local;
+    if (!wi.idle && local >= pl.full) {
+        const int q = local - pl.full, tt = q / pl.s;
+        tile = pl.t0 + pl.full + tt;
+        wi.split = q % pl.s;
+        wi.ns = pl.s;
+        wi.tail_slot = x * tail_max + tt;
+    }
+    if (wi.idle) tile = 0;
+    tile_coords(tile, tiles_m, tiles_n, group_m, wi.tm, wi.tn);
     return wi;
 }
 
@@ -343,13 +391,19 @@ struct GemmParams {
     const bf16_t* B;
     int64_t ldb;
     int I, J, K;  // C is I x J, reduction length K
-    int splits;   // reduction splits (gate epilogue only)
     bf16_t* C;
     int64_t ldc;
+    // work decomposition (set by the launcher): CUs per XCD, whether tail
+    // tiles may be split along K, and the largest per-XCD tail and split
+    int cus_per_xcd;
+    int split_ok;
+    int tail_max, s_max;
     // gate epilogue: i indexes d (< dlimit), j indexes n; candidates are rows n
     CandSet cs;
     int dlimit;
-    float* partials;  // [work items][ncand]
+    // gate epilogue: [grid blocks][ncand] partial sums; store epilogue with
+    // split tails: [8 * tail_max][s_max][BI * BJ] fp32 partial tiles
+    float* partials;
 };
 
 template <int BI, int BJ, int BK, int WI, int WJ>
@@ -709,8 +763,9 @@ __device__ __forceinline__ void gate_stage_lds(u32x4* __restrict__ buf, const ui
 // n = 32 b + lane%32, the 16 weights 32 a + 4 (lane/32) + 8 u + t of one
 // 32-weight sub-block (relative to the wave's tile origin).
 template <int QT, int MI, int NJ, int WTI, int WTJ>
-__device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const uint8_t* __restrict__ buf,
-                                              int64_t row_groups, int j0, int group, int wi, int wj, int lane, int J) {
+__device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const float (&sv)[MI][NJ][2],
+                                              const uint8_t* __restrict__ buf, int64_t row_groups, int j0, int group,
+                                              int wi, int wj, int lane, int J) {
     constexpr int GB = group_bytes(QT);
     constexpr int PITCH = 16 * ((GB + 15 + 15) / 16);  // bytes per staged row span
     float s = 0.0f;
@@ -726,14 +781,14 @@ __device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const
             float v[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) v[r] = acc[a][b][r];
-            s += dot_sub32<QT>(g, wi * WTI + 32 * a, lane >> 5, v);
+            s += dot_sub32<QT>(g, wi * WTI + 32 * a, lane >> 5, v, sv[a][b]);
         }
     }
     return s;
 }
 
 template <int BI, int BJ, int BK, int WI, int WJ>
-__device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkItem& w, int i0, int j0,
+__device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, int i0, int j0,
                                               u32x4* __restrict__ smem,
                                               const f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
                                                                  [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
@@ -742,10 +797,24 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkIte
     constexpr int NW = WI * WJ;
     constexpr int BUF_CH = BJ * kGateMaxChunks;  // 16-byte chunks per candidate buffer
     __shared__ float red[NW][kMaxCand];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scale fields index by it
     const int wi = wave / WJ, wj = wave % WJ;
     const int group = i0 / 256;
     const int64_t rg = p.cs.row_groups;
+    // candidate-independent half sums of each accumulator block
+    float sv[S::MI][S::NJ][2];
+#pragma unroll
+    for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+        for (int b = 0; b < S::NJ; ++b)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                float t = 0.0f;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) t += acc[a][b][8 * hf + r];
+                sv[a][b][hf] = t;
+            }
     __syncthreads();  // every wave is past its last main-loop LDS read
     gate_stage_regs<BJ, S::THREADS>(smem, p.cs.qbytes[0], p.cs.qtype[0], rg, j0, group, p.J);
     for (int k = 0; k < p.cs.ncand; ++k) {
@@ -759,12 +828,12 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkIte
         const uint8_t* buf = reinterpret_cast<const uint8_t*>(smem + (k & 1) * BUF_CH);
         float sum;
         switch (p.cs.qtype[k]) {
-        case Q8_0: sum = gate_dot_lds<Q8_0, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q2_K: sum = gate_dot_lds<Q2_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q8_0: sum = gate_dot_lds<Q8_0, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q2_K: sum = gate_dot_lds<Q2_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
@@ -774,25 +843,68 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, const WorkIte
     if ((int)threadIdx.x < p.cs.ncand) {
         float s = 0.0f;
         for (int wv = 0; wv < NW; ++wv) s += red[wv][threadIdx.x];
-        p.partials[(int64_t)w.logical * p.cs.ncand + threadIdx.x] = s;
+        p.partials[(int64_t)block * p.cs.ncand + threadIdx.x] = s;
     }
 }
 
-// ---------------------------------------------------------------- kernel
-// Four-wave workgroups hold 256 accumulators per lane and run one wave per
-// SIMD: telling the compiler so lets it keep fragments in flight instead of
-// minimising registers for an occupancy the LDS use rules out anyway.
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH>
-__global__ __launch_bounds__(WI* WJ * 64) __attribute__((amdgpu_waves_per_eu(WI * WJ == 4 ? 1 : 2, WI * WJ == 4 ? 1 : 2)))
-void gemm_kernel(GemmParams p) {
+// ---------------------------------------------------------------- kernels
+// One GEMM configuration: loaders, tile, wave layout, epilogue, pipeline depth.
+template <class LA_, class LB_, int BI_, int BJ_, int BK_, int WI_, int WJ_, int EPI_, int DEPTH_>
+struct GemmCfg {
+    using LA = LA_;
+    using LB = LB_;
+    static constexpr int BI = BI_, BJ = BJ_, BK = BK_, WI = WI_, WJ = WJ_, EPI = EPI_, DEPTH = DEPTH_;
+    static constexpr int THREADS = WI * WJ * 64;
+    static constexpr size_t main_lds() { return StageLds<LA, LB, DEPTH>::BYTES; }
+    static constexpr size_t lds() {
+        constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16;
+        return EPI == EPI_GATE && gate > main_lds() ? gate : main_lds();
+    }
+    static int tiles_i(const GemmParams& p) { return (p.I + BI - 1) / BI; }
+    static int tiles_j(const GemmParams& p) { return (p.J + BJ - 1) / BJ; }
+    static __host__ __device__ int ksteps(const GemmParams& p) { return (p.K + BK - 1) / BK; }
+    // Fill in the work decomposition; returns the grid size (8 * blocks per XCD).
+    static int plan(GemmParams& p, int cus, bool split_ok) {
+        if (p.I <= 0 || p.J <= 0) return 0;
+        p.cus_per_xcd = cus / 8 > 0 ? cus / 8 : 1;
+        p.split_ok = split_ok ? 1 : 0;
+        const int tiles = tiles_i(p) * tiles_j(p);
+        int items = 0;
+        p.tail_max = 0;
+        p.s_max = 1;
+        for (int x = 0; x < 8; ++x) {
+            const XcdPlan pl = xcd_plan(x, tiles, p.cus_per_xcd, ksteps(p), split_ok);
+            items = pl.items() > items ? pl.items() : items;
+            p.tail_max = pl.tail > p.tail_max ? pl.tail : p.tail_max;
+            p.s_max = pl.s > p.s_max ? pl.s : p.s_max;
+        }
+        return 8 * items;
+    }
+    // fp32 workspace the split tails of a store epilogue need
+    static int64_t tail_bytes(const GemmParams& p) {
+        return p.tail_max > 0 ? (int64_t)8 * p.tail_max * p.s_max * BI * BJ * 4 : 0;
+    }
+};
+
+// Work item `block` of problem p.
+template <class C>
+__device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4* __restrict__ smem) {
+    using LA = typename C::LA;
+    using LB = typename C::LB;
+    constexpr int BI = C::BI, BJ = C::BJ, BK = C::BK, WI = C::WI, WJ = C::WJ, EPI = C::EPI, DEPTH = C::DEPTH;
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
-    extern __shared__ u32x4 smem[];
     const int tiles_i = (p.I + BI - 1) / BI, tiles_j = (p.J + BJ - 1) / BJ;
-    const WorkItem w = map_work(tiles_i, tiles_j, EPI == EPI_GATE ? p.splits : 1, 8);
+    const int ksteps = (p.K + BK - 1) / BK;
+    const WorkItem w = map_work(block, tiles_i, tiles_j, ksteps, p.cus_per_xcd, p.split_ok != 0, p.tail_max, 8);
+    if (w.idle) {
+        if constexpr (EPI == EPI_GATE)
+            if ((int)threadIdx.x < p.cs.ncand) p.partials[(int64_t)block * p.cs.ncand + threadIdx.x] = 0.0f;
+        return;
+    }
     const int i0 = w.tm * BI, j0 = w.tn * BJ;
     int kbeg = 0, kend = p.K;
-    if (EPI == EPI_GATE && p.splits > 1) {
-        const int chunk = ((p.K + p.splits - 1) / p.splits + BK - 1) / BK * BK;
+    if (w.ns > 1) {
+        const int chunk = (ksteps + w.ns - 1) / w.ns * BK;
         kbeg = min(p.K, w.split * chunk);
         kend = min(p.K, kbeg + chunk);
     }
@@ -807,6 +919,18 @@ void gemm_kernel(GemmParams p) {
     if constexpr (EPI == EPI_STORE) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
         const int wi = wave / WJ, wj = wave % WJ;
+        if (w.ns > 1) {
+            // K part of a split tail tile: fp32 partial, [element][thread]
+            float* slot = p.partials + ((int64_t)w.tail_slot * p.s_max + w.split) * (BI * BJ);
+#pragma unroll
+            for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+                for (int b = 0; b < S::NJ; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        slot[((a * S::NJ + b) * 16 + r) * S::THREADS + threadIdx.x] = acc[a][b][r];
+            return;
+        }
 #pragma unroll
         for (int a = 0; a < S::MI; ++a)
 #pragma unroll
@@ -819,32 +943,133 @@ void gemm_kernel(GemmParams p) {
                 }
             }
     } else {
-        gate_epilogue<BI, BJ, BK, WI, WJ>(p, w, i0, j0, smem, acc);
+        gate_epilogue<BI, BJ, BK, WI, WJ>(p, block, i0, j0, smem, acc);
     }
 }
 
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH>
-constexpr size_t gemm_lds_bytes() {
-    constexpr size_t main = StageLds<LA, LB, DEPTH>::BYTES;
-    constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16;
-    return EPI == EPI_GATE && gate > main ? gate : main;
+// Sum of the K parts of each split tail tile of a store epilogue, in part
+// order, rounded to bf16 into C.  One block per (XCD tail slot, accumulator
+// block (a, b)): every thread loads its 16 values of each part at once.
+template <class C>
+__global__ __launch_bounds__(C::THREADS) void gemm_tail_fixup_kernel(GemmParams p) {
+    using S = GemmShape<C::BI, C::BJ, C::BK, C::WI, C::WJ>;
+    constexpr int BLOCKS = S::MI * S::NJ;
+    constexpr int TILE = C::BI * C::BJ;
+    const int slot = blockIdx.x / BLOCKS, ab = blockIdx.x % BLOCKS;
+    const int a = ab / S::NJ, b = ab % S::NJ;
+    const int x = slot / p.tail_max, tt = slot % p.tail_max;
+    const int tiles_i = (p.I + C::BI - 1) / C::BI, tiles_j = (p.J + C::BJ - 1) / C::BJ;
+    const XcdPlan pl = xcd_plan(x, tiles_i * tiles_j, p.cus_per_xcd, C::ksteps(p), p.split_ok != 0);
+    if (tt >= pl.tail) return;
+    int tm, tn;
+    tile_coords(pl.t0 + pl.full + tt, tiles_i, tiles_j, 8, tm, tn);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wi = wave / C::WJ, wj = wave % C::WJ;
+    const float* base = p.partials + (int64_t)slot * p.s_max * TILE + (ab * 16) * S::THREADS + threadIdx.x;
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = base[r * S::THREADS];
+#pragma unroll
+    for (int sp = 1; sp < 8; ++sp) {
+        if (sp < pl.s) {
+            float t[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) t[r] = base[(int64_t)sp * TILE + r * S::THREADS];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] += t[r];
+        }
+    }
+    const int gj = tn * C::BJ + wj * S::WTJ + 32 * b + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int gi = tm * C::BI + wi * S::WTI + 32 * a + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (gi < p.I && gj < p.J) p.C[(int64_t)gi * p.ldc + gj] = f2bf(v[r]);
+    }
+}
+
+// Four-wave workgroups hold 256 accumulators per lane and run one wave per
+// SIMD: telling the compiler so lets it keep fragments in flight instead of
+// minimising registers for an occupancy the LDS use rules out anyway.
+template <class C>
+__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::THREADS == 256 ? 1 : 2, C::THREADS == 256 ? 1 : 2)))
+void gemm_kernel(GemmParams p) {
+    extern __shared__ u32x4 smem[];
+    gemm_body<C>(p, blockIdx.x, smem);
+}
+
+// Two independent products in one launch: blocks [0, n1) run problem 1,
+// blocks [n1, ...) problem 2 (n1 is a multiple of 8, so both keep the XCD
+// mapping of map_work; blocks past problem 1's items exit).  One grid lets
+// the second product's work items fill the last, partial round of the first
+// instead of each launch idling CUs in its own tail.
+template <class C1, class C2>
+__global__ __launch_bounds__(C1::THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_dual_kernel(GemmParams p1, int items1, int n1, GemmParams p2) {
+    static_assert(C1::THREADS == 256 && C2::THREADS == 256, "both problems use four-wave workgroups");
+    extern __shared__ u32x4 smem[];
+    const int b = blockIdx.x;
+    if (b < n1) {
+        if (b < items1) gemm_body<C1>(p1, b, smem);
+    } else {
+        gemm_body<C2>(p2, b - n1, smem);
+    }
+}
+
+template <class C>
+static hipError_t set_lds_attr(const void* kern, size_t lds, bool& done) {
+    if (done) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e == hipSuccess) done = true;
+    return e;
+}
+
+// Launch of one product.  `cus` is the device's CU count; a store epilogue
+// splits tail tiles only when `tail_ws` (tail_bytes of the plan) is given.
+template <class C>
+static hipError_t launch_gemm_cfg(GemmParams p, int cus, float* tail_ws, hipStream_t s) {
+    const bool split_ok = C::EPI == EPI_GATE || tail_ws != nullptr;
+    const int grid = C::plan(p, cus, split_ok);
+    if (grid == 0) return hipSuccess;
+    if (C::EPI == EPI_STORE) p.partials = tail_ws;
+    constexpr size_t lds = C::lds();
+    static_assert(lds <= 160 * 1024, "exceeds the 160 KiB of LDS per workgroup");
+    static bool attr_set = false;  // per instantiation
+    auto kern = gemm_kernel<C>;
+    hipError_t e = set_lds_attr<C>((const void*)kern, lds, attr_set);
+    if (e != hipSuccess) return e;
+    kern<<<dim3(grid), dim3(C::THREADS), lds, s>>>(p);
+    e = hipGetLastError();
+    if (e != hipSuccess || C::EPI != EPI_STORE || p.tail_max == 0) return e;
+    constexpr int FIX_BLOCKS = GemmShape<C::BI, C::BJ, C::BK, C::WI, C::WJ>::MI * GemmShape<C::BI, C::BJ, C::BK, C::WI, C::WJ>::NJ;
+    gemm_tail_fixup_kernel<C><<<dim3(8 * p.tail_max * FIX_BLOCKS), dim3(C::THREADS), 0, s>>>(p);
+    return hipGetLastError();
 }
 
 template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH = 1>
 static hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
-    if (p.I <= 0 || p.J <= 0) return hipSuccess;
-    auto kern = gemm_kernel<LA, LB, BI, BJ, BK, WI, WJ, EPI, DEPTH>;
-    constexpr size_t lds = gemm_lds_bytes<LA, LB, BI, BJ, BK, WI, WJ, EPI, DEPTH>();
+    return launch_gemm_cfg<GemmCfg<LA, LB, BI, BJ, BK, WI, WJ, EPI, DEPTH>>(p, 256, nullptr, s);
+}
+
+// Two products in one launch (see gemm_dual_kernel); problem 1 may be a store
+// product with split tails (tail_ws1), problem 2 a gate product.
+template <class C1, class C2>
+static hipError_t launch_gemm_dual(GemmParams p1, GemmParams p2, int cus, float* tail_ws1, hipStream_t s) {
+    const int grid1 = C1::plan(p1, cus, C1::EPI == EPI_GATE || tail_ws1 != nullptr);
+    const int grid2 = C2::plan(p2, cus, true);
+    if (C1::EPI == EPI_STORE) p1.partials = tail_ws1;
+    if (grid1 == 0) return launch_gemm_cfg<C2>(p2, cus, nullptr, s);
+    if (grid2 == 0) return launch_gemm_cfg<C1>(p1, cus, tail_ws1, s);
+    constexpr size_t lds = C1::lds() > C2::lds() ? C1::lds() : C2::lds();
     static_assert(lds <= 160 * 1024, "exceeds the 160 KiB of LDS per workgroup");
-    static bool attr_set = false;  // per instantiation
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
-    const int splits = EPI == EPI_GATE ? p.splits : 1;
-    const int items = ((p.I + BI - 1) / BI) * ((p.J + BJ - 1) / BJ) * splits;
-    kern<<<dim3(items), dim3(WI * WJ * 64), lds, s>>>(p);
+    static bool attr_set = false;
+    auto kern = gemm_dual_kernel<C1, C2>;
+    hipError_t e = set_lds_attr<C1>((const void*)kern, lds, attr_set);
+    if (e != hipSuccess) return e;
+    kern<<<dim3(grid1 + grid2), dim3(C1::THREADS), lds, s>>>(p1, grid1, grid1, p2);
+    e = hipGetLastError();
+    if (e != hipSuccess || C1::EPI != EPI_STORE || p1.tail_max == 0) return e;
+    constexpr int FIX_BLOCKS = GemmShape<C1::BI, C1::BJ, C1::BK, C1::WI, C1::WJ>::MI * GemmShape<C1::BI, C1::BJ, C1::BK, C1::WI, C1::WJ>::NJ;
+    gemm_tail_fixup_kernel<C1><<<dim3(8 * p1.tail_max * FIX_BLOCKS), dim3(C1::THREADS), 0, s>>>(p1);
     return hipGetLastError();
 }
 

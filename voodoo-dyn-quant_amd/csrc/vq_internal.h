@@ -24,12 +24,17 @@ hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int6
 //   gate: part[t][k] = sum over tile t of (dY^T X)[n][d] * W_k[n][d]
 hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D,
                            hipStream_t s);
+// tail_ws: dx_tail_bytes(M, N, D) of fp32 workspace (NULL: no K-split tail tiles)
 hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,
-                          hipStream_t s);
-int gate_splits(int M, int N, int D);       // reduction splits of the gate product
-int64_t gate_partial_count(int M, int N, int D);  // work-item partials per candidate
+                          float* tail_ws, hipStream_t s);
+int device_cus();
+int64_t gate_partial_count(int M, int N, int D);  // gate partials per candidate (one per grid block)
+int64_t dx_tail_bytes(int M, int N, int D);       // dX split-tail workspace bytes
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
                             int D, hipStream_t s);
+hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
+                               const CandSet& cs, float* partials, int M, int N, int D, float* tail_ws,
+                               hipStream_t s);
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
 
 }  // namespace vq
