@@ -857,8 +857,10 @@ struct GemmCfg {
     static constexpr int THREADS = WI * WJ * 64;
     static constexpr size_t main_lds() { return StageLds<LA, LB, DEPTH>::BYTES; }
     static constexpr size_t lds() {
-        constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16;
-        return EPI == EPI_GATE && gate > main_lds() ? gate : main_lds();
+        constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16;  // two candidate buffers
+        constexpr size_t store = (size_t)BI * (BJ + 8) * 2;            // bf16 staging of the tile
+        constexpr size_t epi = EPI == EPI_GATE ? gate : store;
+        return epi > main_lds() ? epi : main_lds();
     }
     static int tiles_i(const GemmParams& p) { return (p.I + BI - 1) / BI; }
     static int tiles_j(const GemmParams& p) { return (p.J + BJ - 1) / BJ; }
@@ -885,6 +887,45 @@ struct GemmCfg {
         return p.tail_max > 0 ? (int64_t)8 * p.tail_max * p.s_max * BI * BJ * 4 : 0;
     }
 };
+
+// Store epilogue: the tile goes through LDS as bf16 ([BI][BJ + 8], the pad
+// puts the two row halves of an MFMA write on different banks), then out with
+// 16-byte stores, 32 consecutive threads per 512-byte row segment, so C is
+// written in whole cache lines.  C's row length J is a multiple of 8.
+template <int BI, int BJ, int BK, int WI, int WJ>
+__device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int j0, u32x4* __restrict__ smem,
+                                               const f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
+                                                                  [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
+    using S = GemmShape<BI, BJ, BK, WI, WJ>;
+    constexpr int PITCH = BJ + 8;  // bf16 per LDS row
+    static_assert((size_t)BI * PITCH * 2 <= 160 * 1024, "tile fits in LDS");
+    bf16_t* t = reinterpret_cast<bf16_t*>(smem);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wi = wave / WJ, wj = wave % WJ;
+    __syncthreads();  // every wave is past its last main-loop LDS read
+#pragma unroll
+    for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+        for (int b = 0; b < S::NJ; ++b) {
+            const int jl = wj * S::WTJ + 32 * b + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int il = wi * S::WTI + 32 * a + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                t[il * PITCH + jl] = f2bf(acc[a][b][r]);
+            }
+        }
+    __syncthreads();
+    constexpr int CPR = BJ / 8;  // 16-byte chunks per tile row
+    const int rows = min(BI, p.I - i0), cols = min(BJ, p.J - j0);
+#pragma unroll 4
+    for (int c = threadIdx.x; c < BI * CPR; c += S::THREADS) {
+        const int il = c / CPR, jc = c % CPR;
+        if (il < rows && 8 * jc < cols) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(t + il * PITCH + 8 * jc);
+            *reinterpret_cast<u32x4*>(p.C + (int64_t)(i0 + il) * p.ldc + j0 + 8 * jc) = v;
+        }
+    }
+}
 
 // Work item `block` of problem p.
 template <class C>
@@ -917,8 +958,6 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
         gemm_mainloop<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
 
     if constexpr (EPI == EPI_STORE) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const int wi = wave / WJ, wj = wave % WJ;
         if (w.ns > 1) {
             // K part of a split tail tile: fp32 partial, [element][thread]
             float* slot = p.partials + ((int64_t)w.tail_slot * p.s_max + w.split) * (BI * BJ);
@@ -931,17 +970,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
                         slot[((a * S::NJ + b) * 16 + r) * S::THREADS + threadIdx.x] = acc[a][b][r];
             return;
         }
-#pragma unroll
-        for (int a = 0; a < S::MI; ++a)
-#pragma unroll
-            for (int b = 0; b < S::NJ; ++b) {
-                const int gj = j0 + wj * S::WTJ + 32 * b + (lane & 31);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int gi = i0 + wi * S::WTI + 32 * a + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (gi < p.I && gj < p.J) p.C[(int64_t)gi * p.ldc + gj] = f2bf(acc[a][b][r]);
-                }
-            }
+        store_tile_lds<BI, BJ, BK, WI, WJ>(p, i0, j0, smem, acc);
     } else {
         gate_epilogue<BI, BJ, BK, WI, WJ>(p, block, i0, j0, smem, acc);
     }
