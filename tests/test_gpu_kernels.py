@@ -144,6 +144,32 @@ def test_mix_weight_bit_exact(hip, types):
     assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
 
 
+@pytest.mark.parametrize("qt", SIX)
+def test_mix_weight_bit_exact_edge_scales(hip, qt):
+    """Full finite fp16 scale range (subnormal, negative, huge) plus all-0x00
+    and all-0xFF payloads: the mixture decodes candidates with a single
+    rounding per weight and a hardware fp16 conversion, so every exactly
+    representable ggml value must come out identical."""
+    rng = np.random.default_rng(23)
+    n, d_pad = 48, 512
+    per_group = 8 if qt == "Q8_0" else 1
+    nb = n * d_pad // 256 * per_group
+    a = blocks.random_blocks(qt, nb, rng)  # any finite scale, subnormals included
+    a[: nb // 8, :] = 0
+    a[nb // 8: nb // 4, :] = 0xFF
+    for off in blocks.F16_OFFSETS[qt]:  # keep fields finite after the fills
+        h = a[:, off].astype(np.uint16) | (a[:, off + 1].astype(np.uint16) << 8)
+        h = np.where(((h >> 10) & 0x1F) == 0x1F, h ^ np.uint16(0x4000), h).astype(np.uint16)
+        a[:, off], a[:, off + 1] = (h & 0xFF).astype(np.uint8), (h >> 8).astype(np.uint8)
+    b = blocks.random_blocks(qt, nb, rng, allow_subnormal=False)
+    ws = [torch.from_numpy(cdequant.oracle_dequant(qt, q, n * d_pad).reshape(n, d_pad)) for q in (a, b)]
+    probs = torch.tensor([0.3, 0.7])
+    ref = mixture.mix_weight(ws, probs).to(torch.bfloat16)
+    got = hip.mix_weight([GGML[qt]] * 2, [_dev(q.reshape(-1)) for q in (a, b)], probs.cuda(), n, d_pad)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
+
+
 def _run_fwd_bwd(hip, types, m, n, d, d_pad, qbs, probs, x, dy):
     dev_q = [_dev(q.reshape(-1)) for q in qbs]
     ids = [GGML[t] for t in types]

@@ -40,12 +40,31 @@ __device__ __forceinline__ float h2f(uint32_t h) {
     return __uint_as_float(sign | __float_as_uint((float)em * 5.9604644775390625e-8f));
 }
 
+// Hardware fp16 -> fp32 (v_cvt_f32_f16): exact for normals, subnormals and
+// infinities; a NaN stays a NaN but its payload may be quieted, so only paths
+// whose output does not carry NaN payloads (the bf16 mixture) use it.
+__device__ __forceinline__ float h2f_hw(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
 // fp32 -> bf16 exactly as torch's Float->BFloat16 cast: NaN -> 0x7FC0, else
 // round to nearest, ties to even.
 __device__ __forceinline__ bf16_t f2bf(float f) {
     const uint32_t u = __float_as_uint(f);
     if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
     return (bf16_t)((u + (((u >> 16) & 1u) + 0x7fffu)) >> 16);
+}
+
+// Two values -> packed bf16 pair (a in the low half), the same bits as f2bf:
+// gfx950's v_cvt_pk_bf16_f32 rounds to nearest even; NaNs become 0x7fc0.
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+    typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    const f2_t v = {a, b};
+    uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2_t));
+    if (a != a) r = (r & 0xffff0000u) | 0x7fc0u;
+    if (b != b) r = (r & 0x0000ffffu) | 0x7fc00000u;
+    return r;
 }
 
 __device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32_t)b << 16); }
@@ -316,6 +335,82 @@ __device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0
     float r = dl[0] * (s1[0] - off * sv[0]) + dl[1] * (s1[1] - off * sv[1]);
     if constexpr (HasMin<QT>::value) r -= ml[0] * sv[0] + ml[1] * sv[1];
     return r;
+}
+
+// Exact values of the 8 weights p .. p + 7 (p a multiple of 8) of a group,
+// for the mixture: the same real numbers as ggml's dequantize_row_*, computed
+// as y = dl * u + c with u the unsigned code (unpacked four per 32-bit word
+// and converted by v_cvt_f32_ubyteN) and c folding the format's offset and
+// min.  dl * u is exact and each y is rounded once, like ggml's; only the sign
+// of a zero may differ, which the mixture cannot see (+0 + (+-0) = +0).
+template <int QT>
+__device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p, float (&y)[8]) {
+    uint32_t uw[2];
+    float dl, c;
+    if constexpr (QT == Q8_0) {
+        const uint8_t* b = g + 34 * (p >> 5);
+        const float d = h2f_hw(*reinterpret_cast<const uint16_t*>(b));
+        load_run<2, 8>(b + 2 + (p & 31), uw);
+        uw[0] ^= 0x80808080u;  // q + 128
+        uw[1] ^= 0x80808080u;
+        dl = d;
+        c = -128.0f * d;
+    } else if constexpr (QT == Q4_K || QT == Q5_K) {
+        const uint32_t dd = *reinterpret_cast<const uint32_t*>(g);
+        const int ch = p >> 6, hi = (p >> 5) & 1;
+        uint32_t sc, m;
+        scale_min_k4(g + 4, 2 * ch + hi, sc, m);
+        dl = h2f_hw(dd & 0xffffu) * (float)sc;
+        c = -(h2f_hw(dd >> 16) * (float)m);
+        load_run<8, 8>(g + (QT == Q5_K ? 48 : 16) + 32 * ch + (p & 31), uw);
+        uw[0] = (uw[0] >> (4 * hi)) & 0x0F0F0F0Fu;
+        uw[1] = (uw[1] >> (4 * hi)) & 0x0F0F0F0Fu;
+        if constexpr (QT == Q5_K) {
+            uint32_t xw[2];
+            load_run<8, 8>(g + 16 + (p & 31), xw);
+            const int xs = 2 * ch + hi;
+            uw[0] |= ((xw[0] >> xs) & 0x01010101u) << 4;
+            uw[1] |= ((xw[1] >> xs) & 0x01010101u) << 4;
+        }
+    } else if constexpr (QT == Q6_K) {
+        const float d = h2f_hw(*reinterpret_cast<const uint16_t*>(g + 208));
+        const int n = p >> 7, t = (p >> 5) & 3, l = p & 31;
+        dl = d * (float)(int8_t)g[192 + 8 * n + (l >> 4) + 2 * t];
+        c = -32.0f * dl;
+        uint32_t hw[2];
+        load_run<2, 8>(g + 64 * n + 32 * (t & 1) + l, uw);
+        load_run<2, 8>(g + 128 + 32 * n + l, hw);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            uw[i] = ((uw[i] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) | (((hw[i] >> (2 * t)) & 0x03030303u) << 4);
+    } else if constexpr (QT == Q3_K) {
+        const float d = h2f_hw(*reinterpret_cast<const uint16_t*>(g + 108));
+        const int n = p >> 7, j = (p >> 5) & 3, half = (p >> 4) & 1, l = p & 15;
+        const int is = 8 * n + 2 * j + half;
+        const uint8_t* sb = g + 96;
+        const uint32_t lo4 = is < 8 ? (sb[is] & 0xFu) : (uint32_t)(sb[is - 8] >> 4);
+        const uint32_t hi2 = (sb[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
+        dl = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
+        c = -4.0f * dl;
+        uint32_t hw[2];
+        load_run<2, 8>(g + 32 + 32 * n + 16 * half + l, uw);
+        load_run<2, 8>(g + 16 * half + l, hw);
+        const int xs = 4 * n + j;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            uw[i] = ((uw[i] >> (2 * j)) & 0x03030303u) | (((hw[i] >> xs) & 0x01010101u) << 2);
+    } else {  // Q2_K
+        const uint32_t dd = *reinterpret_cast<const uint32_t*>(g + 80);
+        const int n = p >> 7, j = (p >> 5) & 3, half = (p >> 4) & 1, l = p & 15;
+        const uint32_t sc = g[8 * n + 2 * j + half];
+        dl = h2f_hw(dd & 0xffffu) * (float)(sc & 0xFu);
+        c = -(h2f_hw(dd >> 16) * (float)(sc >> 4));
+        load_run<4, 8>(g + 16 + 32 * n + 16 * half + l, uw);
+        uw[0] = (uw[0] >> (2 * j)) & 0x03030303u;
+        uw[1] = (uw[1] >> (2 * j)) & 0x03030303u;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) y[r] = fmaf(dl, (float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu), c);
 }
 
 // Runtime-type dispatch (the type is uniform across a wave).

@@ -92,7 +92,16 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(CandSet cs, const f
             const int qt = cs.qtype[k];
             const int gb = group_bytes(qt);
             float w[8];
-            decode_run_rt<8>(qt, lds + off + j * gb, 8 * (t & 31), w);
+            const uint8_t* g = lds + off + j * gb;
+            const int p = 8 * (t & 31);
+            switch (qt) {
+            case Q8_0: decode8_mix<Q8_0>(g, p, w); break;
+            case Q2_K: decode8_mix<Q2_K>(g, p, w); break;
+            case Q3_K: decode8_mix<Q3_K>(g, p, w); break;
+            case Q4_K: decode8_mix<Q4_K>(g, p, w); break;
+            case Q5_K: decode8_mix<Q5_K>(g, p, w); break;
+            default: decode8_mix<Q6_K>(g, p, w); break;
+            }
             off += (kGroupsPerBlock * gb + 15) & ~15;
             const float pk = probs[k];
             {
@@ -103,10 +112,10 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(CandSet cs, const f
             }
         }
         uint4 v;
-        v.x = (uint32_t)f2bf(mixed[0]) | ((uint32_t)f2bf(mixed[1]) << 16);
-        v.y = (uint32_t)f2bf(mixed[2]) | ((uint32_t)f2bf(mixed[3]) << 16);
-        v.z = (uint32_t)f2bf(mixed[4]) | ((uint32_t)f2bf(mixed[5]) << 16);
-        v.w = (uint32_t)f2bf(mixed[6]) | ((uint32_t)f2bf(mixed[7]) << 16);
+        v.x = f2bf2(mixed[0], mixed[1]);
+        v.y = f2bf2(mixed[2], mixed[3]);
+        v.z = f2bf2(mixed[4], mixed[5]);
+        v.w = f2bf2(mixed[6], mixed[7]);
         *reinterpret_cast<uint4*>(w_eff + (g0 + j) * 256 + 8 * (t & 31)) = v;
     }
 }
