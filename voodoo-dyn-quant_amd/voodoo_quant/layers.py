@@ -181,7 +181,7 @@ class GatedLinearFunction(Function):
         dx = torch.empty_like(x2) if need_dx else None
         dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device) if need_dp else None
         ws = None
-        if need_dp:
+        if need_dx or need_dp:  # gate partials and the K-split parts of dX's last tiles
             nbytes = _hip.bwd_workspace_bytes(x2.shape[0], n, x2.shape[1], d_pad, len(types), False)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
         if need_dx or need_dp:
