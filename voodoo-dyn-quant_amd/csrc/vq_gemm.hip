@@ -6,16 +6,16 @@ namespace vq {
 
 // 256x256 output tiles, 4 waves of 128x128 (256 fp32 accumulators per lane,
 // held in AGPRs), operands copied global -> LDS by direct-to-LDS loads into two
-// padded LDS stages with the stage switch inside the MFMA stream.  BK = 64 for
-// the forward and dX products, 32 for the gate product (its epilogue, not the
-// main loop, sets the LDS size; measured on MI355X at 8192 x 5120 x 17408).
+// padded LDS stages with the stage switch inside the MFMA stream, BK = 64; the
+// stage-switch order is chosen per product (measured on MI355X at
+// 8192 x 5120 x 17408).
 // Operands stored [K][rows] (dX's W, both gate operands) keep that orientation
 // in LDS and are read with ds_read_b64_tr_b16.
 using FwdLA = DmaK<256, 64, 256>;
 using FwdLB = DmaK<256, 64, 256>;
 using DxLA = DmaK<256, 64, 256>;
 using DxLB = DmaN<256, 64, 256>;
-using GateL = DmaN<256, 32, 256>;
+using GateL = DmaN<256, 64, 256>;
 constexpr int kGateBI = 256, kGateBJ = 256;
 
 int device_cus() {
@@ -31,9 +31,9 @@ int device_cus() {
     return cus;
 }
 
-using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 2, 2, EPI_STORE, 2>;
-using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 2, 2, EPI_STORE, 2>;
-using GateCfg = GemmCfg<GateL, GateL, kGateBI, kGateBJ, 32, 2, 2, EPI_GATE, 2>;
+using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED>;
+using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 2, 2, EPI_STORE, 2, SWITCH_COPY_FIRST>;
+using GateCfg = GemmCfg<GateL, GateL, kGateBI, kGateBJ, 64, 2, 2, EPI_GATE, 2, SWITCH_READ_FIRST>;
 
 static GemmParams fwd_params(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D) {
     GemmParams p{};

@@ -564,63 +564,28 @@ __device__ __forceinline__ void wait_vmcnt_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int NS>
-__device__ __forceinline__ void gemm_mainloop_dma(const GemmParams& p, int i0, int j0, int kbeg, int kend,
-                                                  u32x4* __restrict__ smem,
-                                                  f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
-                                                               [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
-    static_assert(NS >= 2 && NS <= 4, "2 to 4 LDS stages");
-    using S = GemmShape<BI, BJ, BK, WI, WJ>;
-    constexpr int STAGE = LA::CHUNKS + LB::CHUNKS;
-    constexpr int NI = LA::NI + LB::NI;  // copies per wave per stage
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wi = wave / WJ, wj = wave % WJ;
-    LA la;
-    LB lb;
-    la.init(p.lda, i0, p.I);
-    lb.init(p.ldb, j0, p.J);
-#pragma unroll
-    for (int a = 0; a < S::MI; ++a)
-#pragma unroll
-        for (int b = 0; b < S::NJ; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+// Main loop over direct-to-LDS stages: NS LDS stages, NS - 1 of them in
+// flight while one is multiplied.  The stage switch sits inside the MFMA
+// stream: the wait for stage kt + 1 and the barrier come after the last
+// k-step's fragments of stage kt are in registers, so the next stage's first
+// fragment reads and the copies of stage kt + NS (into the buffer stage kt just
+// vacated) are issued among the last k-step's MFMAs instead of in front of an
+// idle matrix pipe.  Each wave waits (vmcnt) only for its own copies; the
+// barrier then covers everyone's.
+// Order of the stage switch, measured per product on MI355X (operand layout
+// and tile count change which one keeps the matrix pipe busiest):
+//   SWITCH_COPY_FIRST   copies of stage kt + NS, then reads of stage kt + 1
+//   SWITCH_READ_FIRST   reads first, so the copies can interleave the MFMAs
+//   SWITCH_FENCED       reads first, and the barrier fenced with
+//                       sched_barrier so no MFMA or read crosses it
+enum StageSwitch : int { SWITCH_COPY_FIRST = 0, SWITCH_READ_FIRST = 1, SWITCH_FENCED = 2 };
 
-    const int nk = (kend - kbeg + BK - 1) / BK;
-    auto issue = [&](int kt) {
-        u32x4* st = smem + (kt % NS) * STAGE;
-        const int k0 = kbeg + kt * BK;
-        const int kvalid = min(BK, kend - k0);
-        la.issue(st, p.A, p.lda, i0, k0, kvalid);
-        lb.issue(st + LA::CHUNKS, p.B, p.ldb, j0, k0, kvalid);
-    };
-#pragma unroll
-    for (int s = 0; s < NS - 1; ++s)
-        if (s < nk) issue(s);
-    for (int kt = 0; kt < nk; ++kt) {
-        // stages issued after kt and still allowed in flight
-        // then every wave's copies of stage kt have landed and stage kt - 1 is
-        // no longer read
-        const int newer = min(NS - 2, nk - 1 - kt);
-        if (NS >= 4 && newer >= 2) wait_vmcnt_barrier<(NS >= 4 ? 2 : 0) * NI>();
-        else if (NS >= 3 && newer >= 1) wait_vmcnt_barrier<(NS >= 3 ? 1 : 0) * NI>();
-        else wait_vmcnt_barrier<0>();
-        if (kt + NS - 1 < nk) issue(kt + NS - 1);
-        const u32x4* st = smem + (kt % NS) * STAGE;
-        gemm_stage_mfma<LA, LB, BI, BJ, BK, WI, WJ, true>(st, st + LA::CHUNKS, wi, wj, lane, acc);
-    }
-}
-
-// Two-stage variant with the stage switch inside the MFMA stream: the wait
-// for stage kt + 1 and the barrier come after the last k-step's fragments of
-// stage kt are in registers, so the next stage's first fragment reads and the
-// copies of stage kt + 2 (into the buffer stage kt just vacated) are issued
-// among the last k-step's MFMAs instead of in front of an idle matrix pipe.
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ>
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int NS, int SWITCH>
 __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, int j0, int kbeg, int kend,
                                                  u32x4* __restrict__ smem,
                                                  f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
                                                               [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 LDS stages");
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     constexpr int STAGE = LA::CHUNKS + LB::CHUNKS;
     constexpr int KS = BK / 16;
@@ -644,7 +609,7 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
     const int nk = (kend - kbeg + BK - 1) / BK;
     // stage kt past the end copies nothing (zeros into a free buffer)
     auto issue = [&](int kt) {
-        u32x4* st = smem + (kt & 1) * STAGE;
+        u32x4* st = smem + (kt % NS) * STAGE;
         const int k0 = min(kbeg + kt * BK, kend);
         const int kvalid = min(BK, kend - k0);
         la.issue(st, p.A, p.lda, i0, k0, kvalid);
@@ -666,12 +631,12 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
     };
 
     if (nk <= 0) return;
-    issue(0);
-    wait_vmcnt_barrier<0>();
-    issue(1);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) issue(s);
+    wait_vmcnt_barrier<(NS - 1) * NI>();
     read(smem, 0, 0);
     for (int kt = 0; kt < nk; ++kt) {
-        const u32x4* st = smem + (kt & 1) * STAGE;
+        const u32x4* st = smem + (kt % NS) * STAGE;
 #pragma unroll
         for (int ks = 0; ks + 1 < KS; ++ks) {
             read(st, ks + 1, (ks + 1) & 1);
@@ -687,12 +652,25 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
             }
         }
         __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
-        // all of stage kt is in registers: wait for stage kt + 1, then stage
-        // kt's buffer is free for stage kt + 2 (past the end: harmless zeros
-        // and reads, so the body has no branch and one set of accumulators)
-        wait_vmcnt_barrier<0>();
-        issue(kt + 2);
-        read(smem + ((kt + 1) & 1) * STAGE, 0, 0);
+        // all of stage kt is in registers: wait for stage kt + 1 (stages
+        // kt + 2 .. kt + NS - 1 may still be in flight), then stage kt's
+        // buffer is free for stage kt + NS (past the end: harmless zeros and
+        // reads, so the body has no branch and one set of accumulators)
+        // SWITCH_FENCED: the barrier becomes a hard scheduling boundary (the
+        // scheduler otherwise moves register-only MFMAs from above past it and
+        // fragment reads from below ahead of it)
+        if constexpr (SWITCH == SWITCH_FENCED) __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt_barrier<(NS - 2) * NI>();
+        if constexpr (SWITCH == SWITCH_FENCED) __builtin_amdgcn_sched_barrier(0);
+        // reads first: the compiler cannot tell stage buffers apart, so copies
+        // issued first stay ahead of every later read (and MFMA)
+        if constexpr (SWITCH == SWITCH_COPY_FIRST) {
+            issue(kt + NS);
+            read(smem + ((kt + 1) % NS) * STAGE, 0, 0);
+        } else {
+            read(smem + ((kt + 1) % NS) * STAGE, 0, 0);
+            issue(kt + NS);
+        }
         mfma((KS - 1) & 1);
         __builtin_amdgcn_sched_group_barrier(0x100, FR, 1);
 #pragma unroll
@@ -849,11 +827,13 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
 
 // ---------------------------------------------------------------- kernels
 // One GEMM configuration: loaders, tile, wave layout, epilogue, pipeline depth.
-template <class LA_, class LB_, int BI_, int BJ_, int BK_, int WI_, int WJ_, int EPI_, int DEPTH_>
+template <class LA_, class LB_, int BI_, int BJ_, int BK_, int WI_, int WJ_, int EPI_, int DEPTH_,
+          int SWITCH_ = SWITCH_FENCED>
 struct GemmCfg {
     using LA = LA_;
     using LB = LB_;
     static constexpr int BI = BI_, BJ = BJ_, BK = BK_, WI = WI_, WJ = WJ_, EPI = EPI_, DEPTH = DEPTH_;
+    static constexpr int SWITCH = SWITCH_;
     static constexpr int THREADS = WI * WJ * 64;
     static constexpr size_t main_lds() { return StageLds<LA, LB, DEPTH>::BYTES; }
     static constexpr size_t lds() {
@@ -950,10 +930,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
         kend = min(p.K, kbeg + chunk);
     }
     f32x16 acc[S::MI][S::NJ];
-    if constexpr (LA::kDma && DEPTH == 2)
-        gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ>(p, i0, j0, kbeg, kend, smem, acc);
-    else if constexpr (LA::kDma)
-        gemm_mainloop_dma<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
+    if constexpr (LA::kDma)
+        gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, DEPTH, C::SWITCH>(p, i0, j0, kbeg, kend, smem, acc);
     else
         gemm_mainloop<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
 
@@ -1048,7 +1026,10 @@ template <class C>
 static hipError_t set_lds_attr(const void* kern, size_t lds, bool& done) {
     if (done) return hipSuccess;
     hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e == hipSuccess) done = true;
+    if (e == hipSuccess)
+        done = true;
+    else
+        (void)hipGetLastError();  // report it once, here, not again at the caller's next launch
     return e;
 }
 
