@@ -152,9 +152,10 @@ def main() -> int:
     dx = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
     dp = torch.empty(len(TYPES), dtype=torch.float32, device=dev)
     ws = torch.empty(_hip.bwd_workspace_bytes(m, n, d, d_pad, len(TYPES), False), dtype=torch.uint8, device=dev)
+    fws = torch.empty(max(_hip.fwd_workspace_bytes(m, n, d), 256), dtype=torch.uint8, device=dev)
 
     def fwd():
-        _hip.gated_linear_fwd(x, ids, qbytes, probs, n, d_pad, w_eff, y)
+        _hip.gated_linear_fwd(x, ids, qbytes, probs, n, d_pad, w_eff, y, fws)
 
     def bwd():
         _hip.gated_linear_bwd(dy, x, ids, qbytes, probs, n, d_pad, w_eff, dx, dp, ws)

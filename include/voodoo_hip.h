@@ -67,13 +67,19 @@ int vq_dequant(int qtype, const void *qbytes, float *out, int64_t nrows, int64_t
 int vq_mix_weight(int ncand, const int *qtypes, const void *const *qbytes, const float *probs, int64_t n,
                   int64_t d_pad, uint16_t *w_eff, void *stream);
 
+/* Workspace bytes vq_gated_linear_fwd can use: fp32 partial tiles for the
+ * K-split parts of the GEMM's last tiles (0 when the shape needs none). */
+int64_t vq_gated_linear_fwd_workspace(int64_t m, int64_t n, int64_t d);
+
 /* Forward of the gated Linear: mixes W_eff into `w_eff` ([n][d_pad] bf16,
  * caller-owned, kept for the backward) and writes y[m][n] = x[m][d] . W_eff^T.
+ * `workspace` (optional, ws_bytes >= vq_gated_linear_fwd_workspace) lets the
+ * GEMM split its last round of tiles along K; NULL runs them whole.
  * Replaces get_mixed_weight + F.linear in MixedQuantLinear.forward
  * (voodoo_quant/layers.py:1729-1731). */
 int vq_gated_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
                         const int *qtypes, const void *const *qbytes, const float *probs, uint16_t *w_eff,
-                        uint16_t *y, void *stream);
+                        uint16_t *y, void *workspace, int64_t ws_bytes, void *stream);
 
 /* Workspace bytes vq_gated_linear_bwd needs (gate partials; plus the W_eff
  * buffer when it will be called with w_eff == NULL and dx != NULL). */

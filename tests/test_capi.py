@@ -68,7 +68,17 @@ def test_null_pointers_rejected_before_any_gpu_work():
     assert lib.vq_dequant(8, None, None, 4, 256, None) == _hip.VQ_ERR_NULL
     assert lib.vq_dequant(99, None, None, 4, 256, None) == _hip.VQ_ERR_QTYPE
     assert lib.vq_mix_weight(1, types, None, None, 8, 256, None, None) == _hip.VQ_ERR_NULL
-    assert lib.vq_gated_linear_fwd(None, 4, 8, 256, 256, 1, types, None, None, None, None, None) == _hip.VQ_ERR_NULL
+    assert lib.vq_gated_linear_fwd(None, 4, 8, 256, 256, 1, types, None, None, None, None, None, 0,
+                                   None) == _hip.VQ_ERR_NULL
+
+
+def test_forward_workspace_size():
+    # 8192 x 17408 tiles: 2176 over 8 XCDs of 32 CUs -> each XCD splits its last 16 tiles in 2
+    n = _hip.fwd_workspace_bytes(8192, 17408, 5120)
+    assert n == 8 * 16 * 2 * 256 * 256 * 4
+    assert _hip.fwd_workspace_bytes(8192, 8192, 4096) == 0  # 1024 tiles: whole rounds only
+    with pytest.raises(ValueError):
+        _hip.fwd_workspace_bytes(-1, 64, 256)
 
 
 def test_workspace_size():

@@ -176,7 +176,8 @@ def _run_fwd_bwd(hip, types, m, n, d, d_pad, qbs, probs, x, dy):
     xd, dyd, pd = x.cuda(), dy.cuda(), probs.cuda()
     w_eff = torch.empty(n, d_pad, dtype=torch.bfloat16, device="cuda")
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-    hip.gated_linear_fwd(xd, ids, dev_q, pd, n, d_pad, w_eff, y)
+    fws = torch.empty(max(hip.fwd_workspace_bytes(m, n, d), 16), dtype=torch.uint8, device="cuda")
+    hip.gated_linear_fwd(xd, ids, dev_q, pd, n, d_pad, w_eff, y, fws)
     dx = torch.empty(m, d, dtype=torch.bfloat16, device="cuda")
     dp = torch.empty(len(types), dtype=torch.float32, device="cuda")
     ws = torch.empty(hip.bwd_workspace_bytes(m, n, d, d_pad, len(types), False), dtype=torch.uint8, device="cuda")

@@ -146,9 +146,14 @@ int vq_mix_weight(int ncand, const int* qtypes, const void* const* qbytes, const
     return rc == VQ_OK ? ok() : rc;
 }
 
+int64_t vq_gated_linear_fwd_workspace(int64_t m, int64_t n, int64_t d) {
+    if (m < 0 || n <= 0 || d <= 0 || m > INT32_MAX || n > INT32_MAX || d > INT32_MAX) return -1;
+    return align256(vq::fwd_tail_bytes((int)m, (int)n, (int)d));
+}
+
 int vq_gated_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
                         const int* qtypes, const void* const* qbytes, const float* probs, uint16_t* w_eff,
-                        uint16_t* y, void* stream) {
+                        uint16_t* y, void* workspace, int64_t ws_bytes, void* stream) {
     int rc = check_candidates(ncand, qtypes, qbytes, n, d, d_pad, true);
     if (rc != VQ_OK) return rc;
     if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
@@ -160,7 +165,11 @@ int vq_gated_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int6
     rc = hip_check(vq::launch_mix(cs, probs, w_eff, n * d_pad / 256, s), "mix launch");
     if (rc != VQ_OK) return rc;
     if (m == 0) return ok();
-    rc = hip_check(vq::launch_gemm_fwd(x, w_eff, d_pad, y, (int)m, (int)n, (int)d, s), "forward GEMM launch");
+    if (workspace && !aligned16(workspace)) return fail(VQ_ERR_ALIGN, "workspace not 16-byte aligned");
+    const int64_t tail_bytes = vq::fwd_tail_bytes((int)m, (int)n, (int)d);
+    float* tail_ws = workspace && tail_bytes > 0 && ws_bytes >= tail_bytes ? static_cast<float*>(workspace) : nullptr;
+    rc = hip_check(vq::launch_gemm_fwd(x, w_eff, d_pad, y, (int)m, (int)n, (int)d, tail_ws, s),
+                   "forward GEMM launch");
     return rc == VQ_OK ? ok() : rc;
 }
 

@@ -69,9 +69,16 @@ int64_t dx_tail_bytes(int M, int N, int D) {
     return DxCfg::tail_bytes(p);
 }
 
+// fp32 workspace for the K parts of the forward's split tail tiles.
+int64_t fwd_tail_bytes(int M, int N, int D) {
+    GemmParams p = fwd_params(nullptr, nullptr, 0, nullptr, M, N, D);
+    FwdCfg::plan(p, device_cus(), true);
+    return FwdCfg::tail_bytes(p);
+}
+
 hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D,
-                           hipStream_t s) {
-    return launch_gemm_cfg<FwdCfg>(fwd_params(X, W, ldw, Y, M, N, D), device_cus(), nullptr, s);
+                           float* tail_ws, hipStream_t s) {
+    return launch_gemm_cfg<FwdCfg>(fwd_params(X, W, ldw, Y, M, N, D), device_cus(), tail_ws, s);
 }
 
 hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,

@@ -22,8 +22,10 @@ hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int6
 //   fwd:  Y[M][N]  = X[M][D] . W[N][D]^T          (W row stride ldw)
 //   dx:   dX[M][D] = dY[M][N] . W[N][D]
 //   gate: part[t][k] = sum over tile t of (dY^T X)[n][d] * W_k[n][d]
+// tail_ws: fwd_tail_bytes(M, N, D) of fp32 workspace (NULL: no K-split tail tiles)
 hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D,
-                           hipStream_t s);
+                           float* tail_ws, hipStream_t s);
+int64_t fwd_tail_bytes(int M, int N, int D);      // forward split-tail workspace bytes
 // tail_ws: dx_tail_bytes(M, N, D) of fp32 workspace (NULL: no K-split tail tiles)
 hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,
                           float* tail_ws, hipStream_t s);

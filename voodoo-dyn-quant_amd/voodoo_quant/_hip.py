@@ -28,7 +28,8 @@ _SIGNATURES = [
     ("vq_validate_candidates", _i, [_i, _p, _i64, _i64, _i64]),
     ("vq_dequant", _i, [_i, _p, _p, _i64, _i64, _p]),
     ("vq_mix_weight", _i, [_i, _p, _p, _p, _i64, _i64, _p, _p]),
-    ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p]),
+    ("vq_gated_linear_fwd_workspace", _i64, [_i64, _i64, _i64]),
+    ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
     ("vq_gated_linear_bwd", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
 ]
@@ -134,12 +135,23 @@ def mix_weight(ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int, out:
     return out
 
 
+def fwd_workspace_bytes(m: int, n: int, d: int) -> int:
+    v = int(lib().vq_gated_linear_fwd_workspace(m, n, d))
+    if v < 0:
+        raise ValueError(f"invalid forward sizes m={m} n={n} d={d}")
+    return v
+
+
 def gated_linear_fwd(x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int,
-                     w_eff: torch.Tensor, y: torch.Tensor) -> None:
+                     w_eff: torch.Tensor, y: torch.Tensor, workspace: torch.Tensor | None = None) -> None:
+    """workspace: optional uint8 tensor of fwd_workspace_bytes(m, n, d) (lets the
+    GEMM split its last round of tiles along K)."""
     m, d = x.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(lib().vq_gated_linear_fwd(_dev_ptr(x, "x"), m, n, d, d_pad, len(ggml_types), _int_array(ggml_types),
                                      _ptr_array(qbytes, "qbytes"), _dev_ptr(probs, "probs"),
-                                     _dev_ptr(w_eff, "w_eff"), _dev_ptr(y, "y"), _stream(x.device)),
+                                     _dev_ptr(w_eff, "w_eff"), _dev_ptr(y, "y"), _dev_ptr(workspace, "workspace"),
+                                     ws_bytes, _stream(x.device)),
            "vq_gated_linear_fwd")
 
 

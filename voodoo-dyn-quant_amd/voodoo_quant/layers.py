@@ -165,7 +165,9 @@ class GatedLinearFunction(Function):
         p = probs.detach().to(device=x.device, dtype=torch.float32).contiguous()
         w_eff = torch.empty(n, d_pad, dtype=torch.bfloat16, device=x.device)
         y = torch.empty(x2.shape[0], n, dtype=torch.bfloat16, device=x.device)
-        _hip.gated_linear_fwd(x2, types, qbytes, p, n, d_pad, w_eff, y)
+        nbytes = _hip.fwd_workspace_bytes(x2.shape[0], n, x2.shape[1])
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+        _hip.gated_linear_fwd(x2, types, qbytes, p, n, d_pad, w_eff, y, ws)
         ctx.save_for_backward(x2, p, w_eff)
         ctx.meta = meta
         ctx.qbytes = qbytes
