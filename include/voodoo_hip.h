@@ -61,6 +61,11 @@ int vq_validate_candidates(int ncand, const int *qtypes, int64_t n, int64_t d, i
  * per-type torch decoders (layers.py:62-213). */
 int vq_dequant(int qtype, const void *qbytes, float *out, int64_t nrows, int64_t ncols, void *stream);
 
+/* out[nrows*ncols] bf16 = bf16(ggml dequantize_row_<qtype>(qbytes)) with torch's
+ * rounding: the source-dtype candidate the reference's lazy path decodes
+ * (voodoo_quant/layers.py:298-319, 514-556). */
+int vq_dequant_bf16(int qtype, const void *qbytes, uint16_t *out, int64_t nrows, int64_t ncols, void *stream);
+
 /* w_eff[n][d_pad] bf16 = bf16(sum_k probs[k] * dequant(qbytes[k])), mixed in
  * fp32 in k order with separately rounded products and sums.  Replaces
  * _MixedWeightFunction.forward (voodoo_quant/layers.py:336-352). */
@@ -80,6 +85,18 @@ int64_t vq_gated_linear_fwd_workspace(int64_t m, int64_t n, int64_t d);
 int vq_gated_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
                         const int *qtypes, const void *const *qbytes, const float *probs, uint16_t *w_eff,
                         uint16_t *y, void *workspace, int64_t ws_bytes, void *stream);
+
+/* Per-token quant routing (PTQR) forward: y[t] = x[t] . W_{k(t)}^T, every
+ * token through ONE candidate.  perm (device int32 [m]) lists the tokens
+ * grouped by candidate, group_off (device int32 [ncand + 1]) the group bounds
+ * in perm (group_off[0] = 0, group_off[ncand] = m); cand_bf16[k] (device
+ * [n][d_pad]) is candidate k decoded by vq_dequant_bf16.  Entries outside
+ * [0, m) are skipped.  Requires m * d_pad * 2 < 2^31.  Replaces
+ * _RoutedMixedLinear.forward (voodoo_quant/layers.py:383-406); its backward is
+ * vq_gated_linear_bwd (layers.py:408-429 computes the same dX and dL/dp). */
+int vq_routed_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                         const uint16_t *const *cand_bf16, const int32_t *perm, const int32_t *group_off,
+                         uint16_t *y, void *stream);
 
 /* Workspace bytes vq_gated_linear_bwd needs (gate partials; plus the W_eff
  * buffer when it will be called with w_eff == NULL and dx != NULL). */

@@ -253,3 +253,18 @@ def test_trainer_calls():
     p.grad = torch.tensor([1.0, -1.0, 0.0])
     trainer.gate_optimizer_step([p], opt, sched)
     assert float(p[0]) < 0 < float(p[1]) and p.grad is None or float(p.grad.abs().sum()) == 0
+
+
+def test_router_shares():
+    """Port of tests/test_ptqr.py:29-44: token shares track the probabilities,
+    and a seeded draw is reproducible."""
+    torch.manual_seed(0)
+    for pv in ([0.25, 0.75], [0.1, 0.2, 0.3, 0.4], [0.05, 0.05, 0.9]):
+        routing = layers._sample_token_routing(torch.tensor(pv), 200_000)
+        for k, p in enumerate(pv):
+            assert abs(float((routing == k).float().mean()) - p) <= 0.01
+    torch.manual_seed(0)
+    a = layers._sample_token_routing(torch.tensor([0.5, 0.5]), 64)
+    torch.manual_seed(0)
+    b = layers._sample_token_routing(torch.tensor([0.5, 0.5]), 64)
+    assert torch.equal(a, b)

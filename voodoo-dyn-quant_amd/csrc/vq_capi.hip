@@ -134,6 +134,41 @@ int vq_dequant(int qtype, const void* qbytes, float* out, int64_t nrows, int64_t
     return rc == VQ_OK ? ok() : rc;
 }
 
+int vq_dequant_bf16(int qtype, const void* qbytes, uint16_t* out, int64_t nrows, int64_t ncols, void* stream) {
+    if (vq::group_bytes(qtype) == 0) return fail(VQ_ERR_QTYPE, "unsupported ggml type %d", qtype);
+    if (!qbytes || !out) return fail(VQ_ERR_NULL, "qbytes/out is NULL");
+    if (nrows < 0 || ncols < 0) return fail(VQ_ERR_SHAPE, "negative size");
+    if (ncols % 256 != 0) return fail(VQ_ERR_ALIGN, "ncols=%lld is not a multiple of 256", (long long)ncols);
+    if (!aligned16(qbytes) || !aligned16(out)) return fail(VQ_ERR_ALIGN, "qbytes/out not 16-byte aligned");
+    const int64_t total = nrows * ncols;
+    int rc = hip_check(vq::launch_dequant_bf16(qtype, static_cast<const uint8_t*>(qbytes), out, total / 256,
+                                               static_cast<hipStream_t>(stream)),
+                       "dequant launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_routed_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                         const uint16_t* const* cand_bf16, const int32_t* perm, const int32_t* group_off,
+                         uint16_t* y, void* stream) {
+    if (ncand < 1 || ncand > vq::kMaxCand) return fail(VQ_ERR_SHAPE, "ncand=%d out of [1, %d]", ncand, vq::kMaxCand);
+    if (n <= 0 || d <= 0 || d > d_pad || n > (1 << 21) || d_pad > (1 << 21))
+        return fail(VQ_ERR_SHAPE, "sizes n=%lld d=%lld d_pad=%lld", (long long)n, (long long)d, (long long)d_pad);
+    if (n % 8 || d % 8 || d_pad % 256) return fail(VQ_ERR_ALIGN, "n, d need multiples of 8 and d_pad of 256");
+    if (m < 0 || m * d_pad * 2 >= ((int64_t)1 << 31))
+        return fail(VQ_ERR_SHAPE, "m=%lld: m * d_pad * 2 must stay below 2^31", (long long)m);
+    if (!x || !y || !perm || !group_off || !cand_bf16) return fail(VQ_ERR_NULL, "x/y/perm/group_off/cand is NULL");
+    if (!aligned16(x) || !aligned16(y)) return fail(VQ_ERR_ALIGN, "x/y not 16-byte aligned");
+    for (int k = 0; k < ncand; ++k) {
+        if (!cand_bf16[k]) return fail(VQ_ERR_NULL, "cand_bf16[%d] is NULL", k);
+        if (!aligned16(cand_bf16[k])) return fail(VQ_ERR_ALIGN, "cand_bf16[%d] not 16-byte aligned", k);
+    }
+    if (m == 0) return ok();
+    int rc = hip_check(vq::launch_routed_fwd(x, (int)m, (int)d, cand_bf16, d_pad, (int)n, ncand, perm, group_off, y,
+                                             static_cast<hipStream_t>(stream)),
+                       "routed GEMM launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int vq_mix_weight(int ncand, const int* qtypes, const void* const* qbytes, const float* probs, int64_t n,
                   int64_t d_pad, uint16_t* w_eff, void* stream) {
     int rc = check_candidates(ncand, qtypes, qbytes, n, d_pad, d_pad, true);

@@ -25,9 +25,12 @@ __device__ __forceinline__ void stage_bytes(uint8_t* __restrict__ dst, const uin
     if ((int)threadIdx.x < tail) dst[(nvec << 4) + threadIdx.x] = src[(nvec << 4) + threadIdx.x];
 }
 
-template <int QT>
+// OUT = float: ggml's fp32 values bit for bit; OUT = bf16_t: those values
+// rounded to bf16 (torch's rounding), the source-dtype candidate the
+// reference's lazy path holds.
+template <int QT, class OUT>
 __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* __restrict__ q,
-                                                                 float* __restrict__ out, int64_t ngroups) {
+                                                                 OUT* __restrict__ out, int64_t ngroups) {
     constexpr int GB = group_bytes(QT);
     __shared__ __attribute__((aligned(16))) uint8_t lds[kGroupsPerBlock * GB + 16];
     const int64_t g0 = (int64_t)blockIdx.x * kGroupsPerBlock;
@@ -41,26 +44,44 @@ __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* 
         if (j < ng) {
             float y[8];
             decode_run<QT, 8>(lds + j * GB, 8 * (t & 31), y);
-            float4* o = reinterpret_cast<float4*>(out + (g0 + j) * 256 + 8 * (t & 31));
-            o[0] = make_float4(y[0], y[1], y[2], y[3]);
-            o[1] = make_float4(y[4], y[5], y[6], y[7]);
+            if constexpr (sizeof(OUT) == 4) {
+                float4* o = reinterpret_cast<float4*>(out + (g0 + j) * 256 + 8 * (t & 31));
+                o[0] = make_float4(y[0], y[1], y[2], y[3]);
+                o[1] = make_float4(y[4], y[5], y[6], y[7]);
+            } else {
+                uint4 v;
+                v.x = f2bf2(y[0], y[1]);
+                v.y = f2bf2(y[2], y[3]);
+                v.z = f2bf2(y[4], y[5]);
+                v.w = f2bf2(y[6], y[7]);
+                *reinterpret_cast<uint4*>(out + (g0 + j) * 256 + 8 * (t & 31)) = v;
+            }
         }
     }
 }
 
-hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s) {
+template <class OUT>
+static hipError_t launch_dequant_t(int qtype, const uint8_t* q, OUT* out, int64_t ngroups, hipStream_t s) {
     if (ngroups <= 0) return hipSuccess;
     const dim3 grid((unsigned)((ngroups + kGroupsPerBlock - 1) / kGroupsPerBlock));
     switch (qtype) {
-    case Q8_0: dequant_kernel<Q8_0><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q2_K: dequant_kernel<Q2_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q3_K: dequant_kernel<Q3_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q4_K: dequant_kernel<Q4_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q5_K: dequant_kernel<Q5_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q6_K: dequant_kernel<Q6_K><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q8_0: dequant_kernel<Q8_0, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q2_K: dequant_kernel<Q2_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q3_K: dequant_kernel<Q3_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q4_K: dequant_kernel<Q4_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q5_K: dequant_kernel<Q5_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q6_K: dequant_kernel<Q6_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s) {
+    return launch_dequant_t<float>(qtype, q, out, ngroups, s);
+}
+
+hipError_t launch_dequant_bf16(int qtype, const uint8_t* q, bf16_t* out, int64_t ngroups, hipStream_t s) {
+    return launch_dequant_t<bf16_t>(qtype, q, out, ngroups, s);
 }
 
 // ---------------------------------------------------------------------------

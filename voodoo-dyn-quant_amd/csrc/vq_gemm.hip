@@ -100,6 +100,22 @@ hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, b
                                             gate_params(dY, X, cs, partials, M, N, D), device_cus(), tail_ws, s);
 }
 
+// PTQR forward: token rows grouped by candidate, each group multiplied by its
+// candidate's bf16 decode (the mainloop and store of the forward product, with
+// A rows gathered and Y rows scattered through perm).
+using RoutedCfg = GemmCfg<DmaKG<256, 64, 256>, DmaK<256, 64, 256>, 256, 256, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED>;
+
+hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const* cand_bf16, int64_t ldw, int N,
+                             int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s) {
+    GemmParams p = fwd_params(X, nullptr, ldw, Y, M, N, D);
+    p.rowmap = perm;
+    p.group_off = group_off;
+    p.ngroups = ncand;
+    p.map_rows = M;
+    for (int k = 0; k < ncand; ++k) p.bk[k] = cand_bf16[k];
+    return launch_routed_gemm<RoutedCfg>(p, M, device_cus(), s);
+}
+
 // Fixed-order fp64 sum of the work-item partials: dprobs[k] = sum_t partials[t][k].
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ partials, int64_t ntiles,
                                                           int ncand, float* __restrict__ dprobs) {

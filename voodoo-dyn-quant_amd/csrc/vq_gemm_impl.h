@@ -241,7 +241,7 @@ struct DmaK {
     int kpos[NI];
 
     // tile rows [r0, r0 + ROWS) of src[row * ld + k]
-    __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* = nullptr, int = 0) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -282,7 +282,7 @@ struct DmaN {
     int kpos[NI];
 
     // tile rows [r0, r0 + ROWS) of src[k * ld + row]
-    __device__ __forceinline__ void init(int64_t ld, int r0, int rows) {
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* = nullptr, int = 0) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -304,6 +304,41 @@ struct DmaN {
     }
     static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
         return LoaderN<ROWS, BK, THREADS>::read_frag(lds, row, ks, lane);
+    }
+};
+
+// DmaK with gathered rows: tile row r is source row map[r0 + r] (rows
+// r0 + r >= rows are zeros).  The per-lane offsets carry the whole row offset,
+// so the descriptor base moves with k only; the host bounds m * ld * 2 < 2^31.
+template <int ROWS, int BK, int THREADS>
+struct DmaKG : DmaK<ROWS, BK, THREADS> {
+    using Base = DmaK<ROWS, BK, THREADS>;
+    using Base::CPR;
+    using Base::NI;
+    using Base::NW;
+    using Base::PCH;
+    // map_rows: valid source rows; an entry outside [0, map_rows) reads zeros
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* map, int map_rows) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int L = (i * NW + wave) * 64 + lane;
+            const int row = L / PCH, c = L % PCH;
+            const bool in_tile = c < CPR && row < ROWS && r0 + row < rows;
+            const int src = in_tile ? map[r0 + row] : -1;
+            const bool ok = in_tile && (unsigned)src < (unsigned)map_rows;
+            this->voff[i] = ok ? (uint32_t)(((int64_t)src * ld + 8 * c) * 2) : kOOB;
+            this->kpos[i] = 8 * c + 8;
+        }
+    }
+    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t, int, int k0,
+                                          int kvalid) const {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + k0);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
+                                                     this->kpos[i] <= kvalid ? this->voff[i] : kOOB, 0, 0, 0);
     }
 };
 
@@ -404,6 +439,14 @@ struct GemmParams {
     // gate epilogue: [grid blocks][ncand] partial sums; store epilogue with
     // split tails: [8 * tail_max][s_max][BI * BJ] fp32 partial tiles
     float* partials;
+    // routed product: A rows gathered and C rows scattered through rowmap;
+    // group g owns rowmap[group_off[g] .. group_off[g + 1]) and multiplies
+    // by bk[g]
+    const int* rowmap;
+    const int* group_off;
+    int ngroups;
+    int map_rows;  // rows of A and C (entries of rowmap outside [0, map_rows) are skipped)
+    const bf16_t* bk[kMaxCand];
 };
 
 template <int BI, int BJ, int BK, int WI, int WJ>
@@ -597,7 +640,7 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
     const int wi = wave / WJ, wj = wave % WJ;
     LA la;
     LB lb;
-    la.init(p.lda, i0, p.I);
+    la.init(p.lda, i0, p.I, p.rowmap, p.map_rows);
     lb.init(p.ldb, j0, p.J);
 #pragma unroll
     for (int a = 0; a < S::MI; ++a)
@@ -902,7 +945,9 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int 
         const int il = c / CPR, jc = c % CPR;
         if (il < rows && 8 * jc < cols) {
             const u32x4 v = *reinterpret_cast<const u32x4*>(t + il * PITCH + 8 * jc);
-            *reinterpret_cast<u32x4*>(p.C + (int64_t)(i0 + il) * p.ldc + j0 + 8 * jc) = v;
+            const int64_t gi = p.rowmap ? p.rowmap[i0 + il] : i0 + il;  // routed: scatter rows
+            if (!p.rowmap || (uint64_t)gi < (uint64_t)p.map_rows)
+                *reinterpret_cast<u32x4*>(p.C + gi * p.ldc + j0 + 8 * jc) = v;
         }
     }
 }
@@ -1080,6 +1125,64 @@ static hipError_t launch_gemm_dual(GemmParams p1, GemmParams p2, int cus, float*
     if (e != hipSuccess || C1::EPI != EPI_STORE || p1.tail_max == 0) return e;
     constexpr int FIX_BLOCKS = GemmShape<C1::BI, C1::BJ, C1::BK, C1::WI, C1::WJ>::MI * GemmShape<C1::BI, C1::BJ, C1::BK, C1::WI, C1::WJ>::NJ;
     gemm_tail_fixup_kernel<C1><<<dim3(8 * p1.tail_max * FIX_BLOCKS), dim3(C1::THREADS), 0, s>>>(p1);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- routed product
+// Grouped GEMM: C[rowmap[r]] = A[rowmap[r]] . bk[g]^T for the rows r of each
+// group g (group_off on the device, so the host never waits for the counts).
+// The grid covers ceil(m / BI) + ngroups - 1 tile-rows, the most the groups can
+// need; a block maps to a (tile-row, tile-column) pair as in map_work, finds
+// its group by walking the group sizes, and exits past the last group's rows.
+template <class C>
+__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void routed_gemm_kernel(GemmParams p, int tile_rows) {
+    using LA = typename C::LA;
+    using LB = typename C::LB;
+    constexpr int BI = C::BI, BJ = C::BJ, BK = C::BK, WI = C::WI, WJ = C::WJ;
+    using S = GemmShape<BI, BJ, BK, WI, WJ>;
+    extern __shared__ u32x4 smem[];
+    const int tiles_j = (p.J + BJ - 1) / BJ;
+    const WorkItem w = map_work(blockIdx.x, tile_rows, tiles_j, 0, p.cus_per_xcd, false, 0, 8);
+    if (w.idle) return;
+    // group bounds clamped to [0, map_rows] and made monotonic, so bad
+    // offsets cannot index rowmap out of range
+    int tm = w.tm, g = 0, lo = 0, hi = 0;
+    for (; g < p.ngroups; ++g) {
+        lo = min(max(p.group_off[g], hi), p.map_rows);
+        hi = min(max(p.group_off[g + 1], lo), p.map_rows);
+        const int nt = (hi - lo + BI - 1) / BI;
+        if (tm < nt) break;
+        tm -= nt;
+    }
+    if (g >= p.ngroups) return;
+    GemmParams q = p;
+    q.B = p.bk[g];
+    q.I = hi;  // end of the group's rows in rowmap
+    const int i0 = lo + tm * BI, j0 = w.tn * BJ;
+    f32x16 acc[S::MI][S::NJ];
+    gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, C::DEPTH, C::SWITCH>(q, i0, j0, 0, q.K, smem, acc);
+    store_tile_lds<BI, BJ, BK, WI, WJ>(q, i0, j0, smem, acc);
+}
+
+template <class C>
+static hipError_t launch_routed_gemm(GemmParams p, int m, int cus, hipStream_t s) {
+    if (m <= 0 || p.J <= 0 || p.ngroups <= 0) return hipSuccess;
+    const int tile_rows = (m + C::BI - 1) / C::BI + p.ngroups - 1;
+    const int tiles = tile_rows * ((p.J + C::BJ - 1) / C::BJ);
+    p.cus_per_xcd = cus / 8 > 0 ? cus / 8 : 1;
+    p.split_ok = 0;
+    int items = 0;
+    for (int x = 0; x < 8; ++x) {
+        const XcdPlan pl = xcd_plan(x, tiles, p.cus_per_xcd, C::ksteps(p), false);
+        items = pl.items() > items ? pl.items() : items;
+    }
+    constexpr size_t lds = C::lds();
+    static bool attr_set = false;
+    auto kern = routed_gemm_kernel<C>;
+    hipError_t e = set_lds_attr<C>((const void*)kern, lds, attr_set);
+    if (e != hipSuccess) return e;
+    kern<<<dim3(8 * items), dim3(C::THREADS), lds, s>>>(p, tile_rows);
     return hipGetLastError();
 }
 

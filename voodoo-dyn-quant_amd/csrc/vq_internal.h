@@ -16,6 +16,7 @@ constexpr int kRunsPerThread = 2;
 constexpr int kGroupsPerBlock = kStreamThreads * 8 * kRunsPerThread / 256;  // 16
 
 hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s);
+hipError_t launch_dequant_bf16(int qtype, const uint8_t* q, bf16_t* out, int64_t ngroups, hipStream_t s);
 hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int64_t ngroups, hipStream_t s);
 
 // Gated-Linear GEMMs (vq_gemm.hip).  All matrices are row-major bf16.
@@ -37,6 +38,9 @@ hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs
 hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
                                const CandSet& cs, float* partials, int M, int N, int D, float* tail_ws,
                                hipStream_t s);
+// PTQR: Y[perm[r]] = X[perm[r]] . W_g^T for r in [group_off[g], group_off[g+1])
+hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const* cand_bf16, int64_t ldw, int N,
+                             int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s);
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
 
 }  // namespace vq

@@ -27,7 +27,9 @@ _SIGNATURES = [
     ("vq_qbytes_size", _i64, [_i, _i64, _i64]),
     ("vq_validate_candidates", _i, [_i, _p, _i64, _i64, _i64]),
     ("vq_dequant", _i, [_i, _p, _p, _i64, _i64, _p]),
+    ("vq_dequant_bf16", _i, [_i, _p, _p, _i64, _i64, _p]),
     ("vq_mix_weight", _i, [_i, _p, _p, _p, _i64, _i64, _p, _p]),
+    ("vq_routed_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p]),
     ("vq_gated_linear_fwd_workspace", _i64, [_i64, _i64, _i64]),
     ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
@@ -122,6 +124,27 @@ def dequant(ggml_type: int, qbytes: torch.Tensor, nrows: int, ncols: int, out: t
     _check(lib().vq_dequant(ggml_type, _dev_ptr(qbytes, "qbytes"), _dev_ptr(out, "out"), nrows, ncols,
                             _stream(qbytes.device)), "vq_dequant")
     return out
+
+
+def dequant_bf16(ggml_type: int, qbytes: torch.Tensor, nrows: int, ncols: int, out: torch.Tensor | None = None):
+    """bf16 [nrows, ncols] of ggml's values (torch's rounding)."""
+    if out is None:
+        out = torch.empty(nrows, ncols, dtype=torch.bfloat16, device=qbytes.device)
+    _check(lib().vq_dequant_bf16(ggml_type, _dev_ptr(qbytes, "qbytes"), _dev_ptr(out, "out"), nrows, ncols,
+                                 _stream(qbytes.device)), "vq_dequant_bf16")
+    return out
+
+
+def routed_linear_fwd(x: torch.Tensor, cand_bf16, perm: torch.Tensor, group_off: torch.Tensor, n: int, d_pad: int,
+                      y: torch.Tensor) -> None:
+    """PTQR forward: y[perm[r]] = x[perm[r]] . cand_bf16[g]^T for the rows r of group g."""
+    m, d = x.shape
+    if perm.dtype != torch.int32 or group_off.dtype != torch.int32:
+        raise ValueError("perm and group_off must be int32")
+    _check(lib().vq_routed_linear_fwd(_dev_ptr(x, "x"), m, n, d, d_pad, len(cand_bf16),
+                                      _ptr_array(cand_bf16, "cand_bf16"), _dev_ptr(perm, "perm"),
+                                      _dev_ptr(group_off, "group_off"), _dev_ptr(y, "y"), _stream(x.device)),
+           "vq_routed_linear_fwd")
 
 
 def mix_weight(ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int, out: torch.Tensor | None = None):

@@ -95,10 +95,21 @@ _PTQR_STATE = _PTQRState()
 
 
 def set_ptqr(enabled: bool) -> None:
-    """Per-token routing switch (reference ``layers.py:864-865``).  The routed
-    forward is not implemented on the HIP path yet; enabling it makes the
-    gated Linear forward raise rather than silently run the soft mixture."""
+    """Per-token quant routing switch (reference ``layers.py:864-865``): every
+    token of every gated Linear runs through ONE candidate, sampled from the
+    gate probabilities."""
     _PTQR_STATE.enabled = bool(enabled)
+
+
+def _sample_token_routing(probs: torch.Tensor, num_tokens: int) -> torch.Tensor:
+    """k(t) ~ Categorical(probs) for each token by the Gumbel-argmax trick
+    (reference ``layers.py:868-881``): one uniform draw of [K, tokens] on
+    probs' device, Gumbel noise -log(-log u) with the reference's 1e-9 clamps,
+    argmax of log p + noise over the candidates.  The same draws give the same
+    routing as the reference."""
+    u = torch.rand(probs.shape[0], num_tokens, device=probs.device)
+    noise = -torch.log((-torch.log(u.clamp_min(1e-9))).clamp_min(1e-9))
+    return (torch.log(probs.clamp_min(1e-9)).unsqueeze(1) + noise).argmax(dim=0)
 
 
 # ---------------------------------------------------------------------------
@@ -191,6 +202,53 @@ class GatedLinearFunction(Function):
         if dprobs is not None:
             dprobs = dprobs.to(ctx.probs_device)
         return (dx, dprobs, None) + (None,) * len(ctx.qbytes)
+
+
+class RoutedLinearFunction(Function):
+    """PTQR forward on libvoodoo_hip: y[t] = x[t] W_{k(t)}^T, tokens grouped by
+    their routed candidate (reference ``_RoutedMixedLinear``,
+    ``layers.py:366-429``).
+
+    forward(ctx, x [M, D] bf16, probs [K] fp32, routing [M] int, meta,
+    cand_bf16 (list of [N, D_pad] bf16 decodes), *qbytes) -> y [M, N] bf16.
+    The backward is the straight-through mixture gradient at the routed point,
+    the same as the gated Linear's: dX = dY W_eff and dL/dp_k = <dY^T X, W_k>,
+    with W_eff re-mixed from the packed candidates."""
+
+    @staticmethod
+    def forward(ctx, x, probs, routing, meta, cand_bf16, *qbytes):
+        types, n, d_pad = meta
+        x2 = _aligned(x)
+        k = len(types)
+        r = routing.to(device=x2.device, dtype=torch.int64)
+        perm = torch.argsort(r, stable=True).to(torch.int32)
+        group_off = torch.zeros(k + 1, dtype=torch.int32, device=x2.device)
+        group_off[1:] = torch.cumsum(torch.bincount(r, minlength=k), 0).to(torch.int32)
+        y = torch.empty(x2.shape[0], n, dtype=torch.bfloat16, device=x2.device)
+        _hip.routed_linear_fwd(x2, cand_bf16, perm, group_off, n, d_pad, y)
+        p = probs.detach().to(device=x2.device, dtype=torch.float32).contiguous()
+        ctx.save_for_backward(x2, p)
+        ctx.meta = meta
+        ctx.qbytes = qbytes
+        ctx.probs_device = probs.device
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, p = ctx.saved_tensors
+        types, n, d_pad = ctx.meta
+        need_dx, need_dp = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dy2 = _aligned(dy.to(torch.bfloat16))
+        dx = torch.empty_like(x2) if need_dx else None
+        dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device) if need_dp else None
+        if need_dx or need_dp:
+            # no W_eff from the forward: the library re-mixes it into the workspace
+            nbytes = _hip.bwd_workspace_bytes(x2.shape[0], n, x2.shape[1], d_pad, len(types), need_dx)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
+            _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, None, dx, dprobs, ws)
+        if dprobs is not None:
+            dprobs = dprobs.to(ctx.probs_device)
+        return (dx, dprobs, None, None, None) + (None,) * len(ctx.qbytes)
 
 
 class MixedWeightFunction(Function):
@@ -323,9 +381,24 @@ class _MixedQuantBase(nn.Module):
         return w[:, : self.in_features].to(self.source_dtype)
 
     def invalidate_candidate_cache(self):
-        """Kept for the trainer's calls (``trainer.py:2502-2506``).  Nothing is
-        cached between steps: candidates are decoded inside the kernels."""
-        return None
+        """Drop the bf16 decodes the routed (PTQR) forward keeps (the trainer
+        calls this, ``trainer.py:2502-2506``).  The mixture path caches
+        nothing: its kernels decode the packed bytes directly."""
+        self.__dict__["_bf16_cache"] = None
+
+    def _bf16_candidates(self, device) -> list[torch.Tensor]:
+        """bf16 [N, D_pad] decode of every candidate, kept until invalidated:
+        candidates are constant, so the routed forward decodes them once (the
+        reference's lazy path keeps the same per-candidate decodes)."""
+        cache = self.__dict__.get("_bf16_cache")
+        device = torch.device(device)
+        if cache is None or cache[0].device != device:
+            self._move_qbytes(device)
+            cache = [_hip.dequant_bf16(_ggml_id(qt), getattr(self, f"_qweight_{k}"), self.out_features,
+                                       self.padded_in_features)
+                     for k, qt in enumerate(self.candidate_types)]
+            self.__dict__["_bf16_cache"] = cache
+        return cache
 
     # -- gates ----------------------------------------------------------------
     def set_temperature(self, temperature: float):
@@ -390,6 +463,7 @@ class _MixedQuantBase(nn.Module):
             setattr(self, f"_qweight_{k}", torch.cat([q2d[s:e] for s, e in row_ranges], 0).reshape(-1).contiguous())
         self._full_out_features = self.out_features
         self.out_features = shard_out
+        self.invalidate_candidate_cache()
 
     def shard_cols(self, col_range: tuple[int, int]) -> None:
         if getattr(self, "_full_out_features", None) is not None or getattr(self, "_full_in_features", None):
@@ -409,6 +483,7 @@ class _MixedQuantBase(nn.Module):
         self._full_in_features = self.in_features
         self.in_features = e - s
         self.padded_in_features = e - s
+        self.invalidate_candidate_cache()
 
 
 def _quantize_candidates(padded: torch.Tensor, padded_imatrix: torch.Tensor | None,
@@ -442,8 +517,6 @@ class MixedQuantLinear(_MixedQuantBase):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.device.type != "cuda":
             raise RuntimeError(f"{self._tensor_name}: MixedQuantLinear runs on a ROCm device only (got {x.device})")
-        if _PTQR_STATE.enabled:
-            raise NotImplementedError("per-token quant routing (set_ptqr) has no HIP forward yet")
         self._move_qbytes(x.device)
         probs = self.get_probs()
         if probs.device != x.device:
@@ -453,7 +526,12 @@ class MixedQuantLinear(_MixedQuantBase):
         if x2.dtype != torch.bfloat16:
             x2 = x2.to(torch.bfloat16)
         meta = (self._ggml_types(), self.out_features, self.padded_in_features)
-        y = GatedLinearFunction.apply(x2, probs, meta, *self._qbytes())
+        if _PTQR_STATE.enabled:
+            routing = _sample_token_routing(probs.detach(), x2.shape[0])
+            y = RoutedLinearFunction.apply(x2, probs, routing, meta, self._bf16_candidates(x.device),
+                                           *self._qbytes())
+        else:
+            y = GatedLinearFunction.apply(x2, probs, meta, *self._qbytes())
         if x.dtype != torch.bfloat16:
             y = y.to(x.dtype)
         out = y.reshape(*lead, self.out_features)
