@@ -202,6 +202,23 @@ def main() -> int:
         traffic = json.loads(tfile.read_text()).get(dom)
     log("kernels ms: " + ", ".join(f"{k} {v:.3f}" for k, v in kernels.items()))
 
+    # PTQR routed forward at the same shape: tokens Gumbel-routed from probs,
+    # one grouped GEMM over the cached bf16 candidate decodes
+    from voodoo_quant import layers
+
+    cand_bf16 = [_hip.dequant_bf16(GGML[qt], qb, n, d_pad) for qt, qb in zip(TYPES, qbytes)]
+    t_dec = time_events(torch, lambda: [_hip.dequant_bf16(GGML[qt], qb, n, d_pad, c)
+                                        for qt, qb, c in zip(TYPES, qbytes, cand_bf16)], 3)
+    routing = layers._sample_token_routing(probs, m)
+    perm = torch.argsort(routing, stable=True).to(torch.int32)
+    goff = torch.zeros(len(TYPES) + 1, dtype=torch.int32, device=dev)
+    goff[1:] = torch.cumsum(torch.bincount(routing, minlength=len(TYPES)), 0).to(torch.int32)
+    t_routed = time_events(torch, lambda: _hip.routed_linear_fwd(x, cand_bf16, perm, goff, n, d_pad, y), reps)
+    ptqr = {"routed_fwd_ms": round(t_routed, 4), "routed_fwd_TFLOPs": round(gemm_flops / (t_routed * 1e-3) / 1e12, 1),
+            "bf16_decode_all_candidates_ms": round(t_dec, 4)}
+    del cand_bf16
+    log(f"ptqr: routed fwd {t_routed:.3f} ms, bf16 decode of {len(TYPES)} candidates {t_dec:.3f} ms")
+
     # dequant microbench, 4096 x 14336
     dq = {}
     nr, nc = 4096, 14336
@@ -253,6 +270,7 @@ def main() -> int:
         },
         "kernels_ms": {k: round(v, 4) for k, v in kernels.items()},
         "dequant_gbps": dq,
+        "ptqr": ptqr,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -1132,8 +1132,9 @@ static hipError_t launch_gemm_dual(GemmParams p1, GemmParams p2, int cus, float*
 // Grouped GEMM: C[rowmap[r]] = A[rowmap[r]] . bk[g]^T for the rows r of each
 // group g (group_off on the device, so the host never waits for the counts).
 // The grid covers ceil(m / BI) + ngroups - 1 tile-rows, the most the groups can
-// need; a block maps to a (tile-row, tile-column) pair as in map_work, finds
-// its group by walking the group sizes, and exits past the last group's rows.
+// need; every block counts the tile-rows the groups do need, maps itself onto
+// those as in map_work (so the XCDs share the work evenly and the spare blocks
+// spread over all of them), then finds its group by walking the group sizes.
 template <class C>
 __global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void routed_gemm_kernel(GemmParams p, int tile_rows) {
@@ -1143,10 +1144,18 @@ void routed_gemm_kernel(GemmParams p, int tile_rows) {
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     extern __shared__ u32x4 smem[];
     const int tiles_j = (p.J + BJ - 1) / BJ;
-    const WorkItem w = map_work(blockIdx.x, tile_rows, tiles_j, 0, p.cus_per_xcd, false, 0, 8);
-    if (w.idle) return;
     // group bounds clamped to [0, map_rows] and made monotonic, so bad
-    // offsets cannot index rowmap out of range
+    // offsets cannot index rowmap out of range; the work is spread over the
+    // tile-rows the groups actually have (the grid covers the most they can)
+    int used_rows = 0;
+    for (int g = 0, h = 0; g < p.ngroups; ++g) {
+        const int l = min(max(p.group_off[g], h), p.map_rows);
+        h = min(max(p.group_off[g + 1], l), p.map_rows);
+        used_rows += (h - l + BI - 1) / BI;
+    }
+    used_rows = min(used_rows, tile_rows);
+    const WorkItem w = map_work(blockIdx.x, used_rows, tiles_j, 0, p.cus_per_xcd, false, 0, 8);
+    if (w.idle) return;
     int tm = w.tm, g = 0, lo = 0, hi = 0;
     for (; g < p.ngroups; ++g) {
         lo = min(max(p.group_off[g], hi), p.map_rows);
