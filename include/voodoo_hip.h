@@ -98,6 +98,39 @@ int vq_routed_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int
                          const uint16_t *const *cand_bf16, const int32_t *perm, const int32_t *group_off,
                          uint16_t *y, void *stream);
 
+/* Embedding rows of the packed candidates (vocabulary [num_embeddings][d_pad],
+ * every candidate's rows stored as d_pad/256 consecutive groups):
+ *   routing == NULL: out[r][0:dim] = row ids[r] of
+ *       sum_k probs[k] * dequant(qbytes[k]) mixed in fp32 in k order with
+ *       separately rounded products and sums; as bf16 it is bit-identical to
+ *       the same row of vq_mix_weight's W_eff;
+ *   routing != NULL (device int64 [nids], PTQR): out[r] = row ids[r] of
+ *       candidate routing[r] (probs unused): ggml's value, bf16-rounded as
+ *       vq_dequant_bf16 does or exact in fp32.
+ * ids: device int64 [nids].  An id outside [0, num_embeddings), or a route
+ * outside [0, ncand), gives a zero row.  dim % 8 == 0; out is [nids][dim],
+ * bf16 (out_f32 == 0) or fp32 (out_f32 != 0), 16-byte aligned.
+ * Replaces the row-select lookup of _MixedEmbeddingRowFunctionLazy.forward
+ * (voodoo_quant/layers.py:684-728), _RoutedEmbeddingRowFunction.forward
+ * (layers.py:764-779) and, with one Q8_0 candidate and probs = {1},
+ * Q8Embedding.forward (voodoo_quant/training/q8_teacher.py:155-173). */
+int vq_embedding_rows_fwd(int ncand, const int *qtypes, const void *const *qbytes, const float *probs,
+                          const int64_t *routing, const int64_t *ids, int64_t nids, int64_t num_embeddings,
+                          int64_t dim, int64_t d_pad, void *out, int out_f32, void *stream);
+
+/* Workspace bytes vq_embedding_rows_bwd needs (one fp32 partial per
+ * workgroup and candidate). */
+int64_t vq_embedding_rows_bwd_workspace(int64_t nids, int64_t dim, int ncand);
+
+/* dprobs[k] = sum_r <grad[r][0:dim], W_k[ids[r]][0:dim]> (fp32 [ncand]; the
+ * candidates decoded exactly, partials reduced in a fixed order in fp64).
+ * grad: device [nids][dim], bf16 (grad_f32 == 0) or fp32.  Replaces _MixedEmbeddingRowFunctionLazy.backward
+ * (voodoo_quant/layers.py:730-750) and _RoutedEmbeddingRowFunction.backward
+ * (layers.py:781-790). */
+int vq_embedding_rows_bwd(int ncand, const int *qtypes, const void *const *qbytes, const int64_t *ids,
+                          int64_t nids, int64_t num_embeddings, int64_t dim, int64_t d_pad, const void *grad,
+                          int grad_f32, float *dprobs, void *workspace, int64_t ws_bytes, void *stream);
+
 /* Workspace bytes vq_gated_linear_bwd needs (gate partials; plus the W_eff
  * buffer when it will be called with w_eff == NULL and dx != NULL). */
 int64_t vq_gated_linear_bwd_workspace(int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff);

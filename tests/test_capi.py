@@ -72,6 +72,31 @@ def test_null_pointers_rejected_before_any_gpu_work():
                                    None) == _hip.VQ_ERR_NULL
 
 
+def test_embedding_rows_argument_checks():
+    lib = _hip.lib()
+    types = (ctypes.c_int * 1)(12)
+    ptrs = (ctypes.c_void_p * 1)(None)
+    # a NULL candidate pointer, an unsupported type and bad sizes fail before any GPU work
+    assert lib.vq_embedding_rows_fwd(1, types, ptrs, None, None, None, 4, 10, 256, 256, None, 0,
+                                     None) == _hip.VQ_ERR_NULL
+    bad = (ctypes.c_int * 1)(9)
+    assert lib.vq_embedding_rows_fwd(1, bad, ptrs, None, None, None, 4, 10, 256, 256, None, 0,
+                                     None) == _hip.VQ_ERR_QTYPE
+    fake = (ctypes.c_void_p * 1)(4096)  # never dereferenced: the checks fail first
+    assert lib.vq_embedding_rows_fwd(1, types, fake, None, None, None, 4, 10, 100, 256, None, 0,
+                                     None) == _hip.VQ_ERR_ALIGN
+    assert lib.vq_embedding_rows_fwd(1, types, fake, None, None, None, 4, 10, 512, 256, None, 0,
+                                     None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_embedding_rows_fwd(1, types, fake, None, None, None, 4, 10, 256, 256, None, 0,
+                                     None) == _hip.VQ_ERR_NULL  # ids
+    assert lib.vq_embedding_rows_bwd(1, types, fake, None, 0, 10, 256, 256, None, 0, None, None, 0,
+                                     None) == _hip.VQ_ERR_NULL  # dprobs
+    # workspace: one fp32 partial per (row, segment of <= 16 groups) and candidate
+    assert lib.vq_embedding_rows_bwd_workspace(100, 5120, 6) == 100 * 2 * 6 * 4 + 64
+    assert lib.vq_embedding_rows_bwd_workspace(0, 256, 1) == 0
+    assert lib.vq_embedding_rows_bwd_workspace(4, 256, 13) == -1
+
+
 def test_forward_workspace_size():
     # 8192 x 17408 tiles: 2176 over 8 XCDs of 32 CUs -> each XCD splits its last 16 tiles in 2
     n = _hip.fwd_workspace_bytes(8192, 17408, 5120)

@@ -268,3 +268,101 @@ def test_router_shares():
     torch.manual_seed(0)
     b = layers._sample_token_routing(torch.tensor([0.5, 0.5]), 64)
     assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ gated embedding and the Q8_0 teacher (host side)
+def test_embedding_module_construction(isolated_cache):
+    g = torch.Generator().manual_seed(3)
+    emb = layers.MixedQuantEmbedding(100, 1000, ["Q2_K", "Q8_0"], torch.randn(100, 1000, generator=g) * 0.02,
+                                     tensor_name="tok_embeddings")
+    assert emb.num_embeddings == 100 and emb.embedding_dim == 1000 and emb.padded_in_features == 1024
+    assert emb.out_features == 100 and emb.in_features == 1000
+    for k, qt in enumerate(["Q2_K", "Q8_0"]):
+        info = ggml.get_quant_info(qt)
+        assert getattr(emb, f"_qweight_{k}").numel() == 100 * 1024 // info.block_size * info.block_bytes
+    expect = 0.5 * (ggml.bytes_per_weight("Q2_K") + ggml.bytes_per_weight("Q8_0")) * 100 * 1000
+    assert float(emb.effective_bytes().detach()) == pytest.approx(expect, rel=1e-6)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        emb(torch.tensor([1, 2]))
+
+
+def test_replace_embedding_walker(isolated_cache):
+    net = torch.nn.Module()
+    net.embed_tokens = torch.nn.Embedding(50, 256)
+    net.inner = torch.nn.Sequential(torch.nn.Embedding(20, 512), torch.nn.Linear(512, 8))
+    net.skipme = torch.nn.Embedding(10, 256)
+    replaced = layers.replace_embedding_with_mixed_quant(net, ["Q4_K", "Q8_0"], skip_names={"skipme"})
+    assert set(replaced) == {"embed_tokens", "inner.0"}
+    assert isinstance(net.embed_tokens, layers.MixedQuantEmbedding)
+    assert isinstance(net.inner[1], torch.nn.Linear) and isinstance(net.skipme, torch.nn.Embedding)
+    assert replaced["inner.0"].candidate_types == ["Q4_K", "Q8_0"]
+
+
+def _q8_teacher_checkpoint():
+    """A tiny HF-style model and a checkpoint with stripped names, Q8_0 bytes
+    for its Linears/Embedding and plain tensors for the rest."""
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.up = torch.nn.Linear(64, 32, bias=True)
+            self.norm = torch.nn.LayerNorm(64)
+
+    class Body(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.embed_tokens = torch.nn.Embedding(40, 64)
+            self.layers = torch.nn.ModuleList([Block(), Block()])
+
+    class Model(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.model = Body()
+            self.lm_head = torch.nn.Linear(64, 40, bias=False)
+
+    g = torch.Generator().manual_seed(9)
+    sd, meta = {}, {}
+    for name, (o, i) in {"embed_tokens": (40, 64), "layers.0.up": (32, 64), "layers.1.up": (32, 64),
+                         "lm_head": (40, 64)}.items():
+        sd[name + ".weight"] = rtn.rtn_quantize_tensor(torch.randn(o, i, generator=g), "Q8_0")
+        meta[name + ".weight"] = {"out_features": o, "in_features": i}
+    for li in range(2):
+        sd[f"layers.{li}.up.bias"] = torch.randn(32, generator=g)
+        sd[f"layers.{li}.norm.weight"] = torch.full((64,), 2.0 + li)
+        sd[f"layers.{li}.norm.bias"] = torch.zeros(64)
+    return Model(), sd, meta
+
+
+def test_wrap_q8_teacher():
+    from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear, wrap_q8_teacher
+
+    model, sd, meta = _q8_teacher_checkpoint()
+    wrap_q8_teacher(model, sd, meta)
+    assert isinstance(model.model.embed_tokens, Q8Embedding) and isinstance(model.lm_head, Q8Linear)
+    assert all(isinstance(blk.up, Q8Linear) for blk in model.model.layers)
+    up = model.model.layers[0].up
+    assert torch.equal(up.qweight, sd["layers.0.up.weight"])
+    assert up.out_features == 32 and up.in_features == 64
+    assert torch.equal(up.bias.detach(), sd["layers.0.up.bias"])  # carried over the constructor's copy
+    assert torch.equal(up._voodoo_qb_src[0], sd["layers.0.up.weight"])
+    # non-Q8 tensors are carried over under the model's names
+    assert torch.equal(model.model.layers[1].norm.weight, torch.full((64,), 3.0))
+    assert model.model.embed_tokens.num_embeddings == 40
+    with pytest.raises(RuntimeError, match="ROCm"):
+        model.lm_head(torch.randn(2, 64))
+
+
+def test_q8_padding_repacks_rows():
+    from voodoo_quant.training.q8_teacher import _padded_q8
+
+    w = torch.randn(8, 96)
+    qb = rtn.rtn_quantize_tensor(w, "Q8_0").reshape(-1)
+    padded, d_pad = _padded_q8(qb, 8, 96, 16)
+    assert d_pad == 256 and padded.numel() == 16 * 8 * 34
+    vals = cdequant.oracle_dequant("Q8_0", padded.numpy(), 16 * 256).reshape(16, 256)
+    ref = cdequant.oracle_dequant("Q8_0", qb.numpy(), 8 * 96).reshape(8, 96)
+    assert np.array_equal(vals[:8, :96], ref)
+    assert not vals[8:].any() and not vals[:, 96:].any()
+    same, d = _padded_q8(rtn.rtn_quantize_tensor(torch.randn(8, 256), "Q8_0"), 8, 256, 8)
+    assert d == 256 and same.numel() == 8 * 8 * 34
+    with pytest.raises(ValueError):
+        _padded_q8(qb, 8, 80, 8)

@@ -47,8 +47,7 @@ const char* qtype_name(int qt) {
 
 int block_size(int qt) { return qt == vq::Q8_0 ? 32 : 256; }
 
-int check_candidates(int ncand, const int* qtypes, const void* const* qbytes, int64_t n, int64_t d, int64_t d_pad,
-                     bool need_ptrs) {
+int check_types(int ncand, const int* qtypes, const void* const* qbytes, bool need_ptrs) {
     if (ncand < 1 || ncand > vq::kMaxCand)
         return fail(VQ_ERR_SHAPE, "ncand=%d outside [1, %d]", ncand, vq::kMaxCand);
     if (!qtypes) return fail(VQ_ERR_NULL, "qtypes is NULL");
@@ -63,6 +62,13 @@ int check_candidates(int ncand, const int* qtypes, const void* const* qbytes, in
                 return fail(VQ_ERR_ALIGN, "candidate %d (%s): qbytes not 16-byte aligned", k, qtype_name(qtypes[k]));
         }
     }
+    return VQ_OK;
+}
+
+int check_candidates(int ncand, const int* qtypes, const void* const* qbytes, int64_t n, int64_t d, int64_t d_pad,
+                     bool need_ptrs) {
+    const int rc = check_types(ncand, qtypes, qbytes, need_ptrs);
+    if (rc != VQ_OK) return rc;
     if (n <= 0 || d <= 0 || d_pad <= 0) return fail(VQ_ERR_SHAPE, "n=%lld d=%lld d_pad=%lld must be positive",
                                                    (long long)n, (long long)d, (long long)d_pad);
     if (d_pad % 256 != 0) return fail(VQ_ERR_ALIGN, "d_pad=%lld is not a multiple of 256", (long long)d_pad);
@@ -89,6 +95,25 @@ vq::CandSet make_set(int ncand, const int* qtypes, const void* const* qbytes, in
 }
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+// Shared checks of the embedding-row entry points.
+int check_embed(int ncand, const int* qtypes, const void* const* qbytes, const int64_t* ids, int64_t nids,
+                int64_t vocab, int64_t dim, int64_t d_pad) {
+    int rc = check_types(ncand, qtypes, qbytes, true);
+    if (rc != VQ_OK) return rc;
+    if (vocab <= 0 || dim <= 0 || d_pad <= 0 || nids < 0)
+        return fail(VQ_ERR_SHAPE, "num_embeddings=%lld dim=%lld d_pad=%lld nids=%lld", (long long)vocab,
+                    (long long)dim, (long long)d_pad, (long long)nids);
+    if (d_pad % 256 != 0) return fail(VQ_ERR_ALIGN, "d_pad=%lld is not a multiple of 256", (long long)d_pad);
+    if (dim > d_pad) return fail(VQ_ERR_SHAPE, "embedding_dim=%lld exceeds d_pad=%lld", (long long)dim, (long long)d_pad);
+    if (dim % 8 != 0) return fail(VQ_ERR_ALIGN, "embedding_dim=%lld must be a multiple of 8", (long long)dim);
+    if (d_pad > (1 << 21)) return fail(VQ_ERR_SHAPE, "d_pad=%lld exceeds 2^21", (long long)d_pad);
+    if (vq::embed_plan(nids, dim).blocks >= ((int64_t)1 << 31))
+        return fail(VQ_ERR_SHAPE, "nids=%lld: too many rows for one launch", (long long)nids);
+    if (nids > 0 && !ids) return fail(VQ_ERR_NULL, "ids is NULL");
+    return VQ_OK;
+}
+
 
 }  // namespace
 
@@ -169,10 +194,55 @@ int vq_routed_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int
     return rc == VQ_OK ? ok() : rc;
 }
 
+int vq_embedding_rows_fwd(int ncand, const int* qtypes, const void* const* qbytes, const float* probs,
+                          const int64_t* routing, const int64_t* ids, int64_t nids, int64_t num_embeddings,
+                          int64_t dim, int64_t d_pad, void* out, int out_f32, void* stream) {
+    int rc = check_embed(ncand, qtypes, qbytes, ids, nids, num_embeddings, dim, d_pad);
+    if (rc != VQ_OK) return rc;
+    if (nids == 0) return ok();
+    if (!out) return fail(VQ_ERR_NULL, "out is NULL");
+    if (!routing && !probs) return fail(VQ_ERR_NULL, "probs is NULL (needed without routing)");
+    if (!aligned16(out)) return fail(VQ_ERR_ALIGN, "out not 16-byte aligned");
+    const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);
+    rc = hip_check(vq::launch_embed_rows(cs, probs, routing, ids, nids, num_embeddings, dim, out, out_f32 != 0,
+                                         static_cast<hipStream_t>(stream)),
+                   "embedding rows launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int64_t vq_embedding_rows_bwd_workspace(int64_t nids, int64_t dim, int ncand) {
+    if (nids < 0 || dim <= 0 || ncand < 1 || ncand > vq::kMaxCand) return -1;
+    return align256(vq::embed_plan(nids, dim).blocks * ncand * (int64_t)sizeof(float));
+}
+
+int vq_embedding_rows_bwd(int ncand, const int* qtypes, const void* const* qbytes, const int64_t* ids,
+                          int64_t nids, int64_t num_embeddings, int64_t dim, int64_t d_pad, const void* grad,
+                          int grad_f32, float* dprobs, void* workspace, int64_t ws_bytes, void* stream) {
+    int rc = check_embed(ncand, qtypes, qbytes, ids, nids, num_embeddings, dim, d_pad);
+    if (rc != VQ_OK) return rc;
+    if (!dprobs) return fail(VQ_ERR_NULL, "dprobs is NULL");
+    if (nids > 0 && !grad) return fail(VQ_ERR_NULL, "grad is NULL");
+    if (nids > 0 && !aligned16(grad)) return fail(VQ_ERR_ALIGN, "grad not 16-byte aligned");
+    const int64_t need = vq::embed_plan(nids, dim).blocks * ncand * (int64_t)sizeof(float);
+    if (need > 0 && (!workspace || ws_bytes < need))
+        return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes needed, %lld given", (long long)need,
+                    (long long)ws_bytes);
+    const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);
+    rc = hip_check(vq::launch_embed_rows_bwd(cs, ids, nids, num_embeddings, dim, grad, grad_f32 != 0,
+                                             static_cast<float*>(workspace), dprobs,
+                                             static_cast<hipStream_t>(stream)),
+                   "embedding rows backward launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int vq_mix_weight(int ncand, const int* qtypes, const void* const* qbytes, const float* probs, int64_t n,
                   int64_t d_pad, uint16_t* w_eff, void* stream) {
-    int rc = check_candidates(ncand, qtypes, qbytes, n, d_pad, d_pad, true);
+    // the mix streams whole 256-weight groups: any row count (a vocabulary, say) works
+    int rc = check_types(ncand, qtypes, qbytes, true);
     if (rc != VQ_OK) return rc;
+    if (n <= 0 || d_pad <= 0) return fail(VQ_ERR_SHAPE, "n=%lld d_pad=%lld must be positive", (long long)n,
+                                         (long long)d_pad);
+    if (d_pad % 256 != 0) return fail(VQ_ERR_ALIGN, "d_pad=%lld is not a multiple of 256", (long long)d_pad);
     if (!probs || !w_eff) return fail(VQ_ERR_NULL, "probs/w_eff is NULL");
     if (!aligned16(w_eff)) return fail(VQ_ERR_ALIGN, "w_eff not 16-byte aligned");
     const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);

@@ -43,4 +43,20 @@ hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const*
                              int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s);
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
 
+// Embedding rows (vq_embed.hip): one workgroup per (requested row, segment of
+// at most kGroupsPerBlock groups); gused = groups covering dim.
+struct EmbedPlan {
+    int gused, nseg, seg;
+    int64_t blocks;  // nids * nseg; also the backward's partials per candidate
+};
+EmbedPlan embed_plan(int64_t nids, int64_t dim);
+// out[r][0:dim] (bf16, or fp32 when out_f32) = row ids[r] of the mixture
+// (routing NULL) or of candidate routing[r]
+hipError_t launch_embed_rows(const CandSet& cs, const float* probs, const int64_t* routing, const int64_t* ids,
+                             int64_t nids, int64_t vocab, int64_t dim, void* out, bool out_f32, hipStream_t s);
+// dprobs[k] = sum_r <grad[r][0:dim], W_k[ids[r]][0:dim]> (grad bf16, or fp32
+// when grad_f32); partials: embed_plan(...).blocks * ncand floats
+hipError_t launch_embed_rows_bwd(const CandSet& cs, const int64_t* ids, int64_t nids, int64_t vocab, int64_t dim,
+                                 const void* grad, bool grad_f32, float* partials, float* dprobs, hipStream_t s);
+
 }  // namespace vq

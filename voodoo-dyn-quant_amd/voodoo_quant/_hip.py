@@ -30,6 +30,9 @@ _SIGNATURES = [
     ("vq_dequant_bf16", _i, [_i, _p, _p, _i64, _i64, _p]),
     ("vq_mix_weight", _i, [_i, _p, _p, _p, _i64, _i64, _p, _p]),
     ("vq_routed_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p]),
+    ("vq_embedding_rows_fwd", _i, [_i, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i, _p]),
+    ("vq_embedding_rows_bwd_workspace", _i64, [_i64, _i64, _i]),
+    ("vq_embedding_rows_bwd", _i, [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i, _p, _p, _i64, _p]),
     ("vq_gated_linear_fwd_workspace", _i64, [_i64, _i64, _i64]),
     ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
@@ -145,6 +148,59 @@ def routed_linear_fwd(x: torch.Tensor, cand_bf16, perm: torch.Tensor, group_off:
                                       _ptr_array(cand_bf16, "cand_bf16"), _dev_ptr(perm, "perm"),
                                       _dev_ptr(group_off, "group_off"), _dev_ptr(y, "y"), _stream(x.device)),
            "vq_routed_linear_fwd")
+
+
+def _ids(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int64:
+        raise ValueError(f"{name} must be int64, got {t.dtype}")
+    return t
+
+
+def embedding_rows_fwd(ggml_types, qbytes, probs: torch.Tensor | None, routing: torch.Tensor | None,
+                       ids: torch.Tensor, num_embeddings: int, dim: int, d_pad: int,
+                       dtype: torch.dtype = torch.bfloat16, out: torch.Tensor | None = None) -> torch.Tensor:
+    """[len(ids), dim] in `dtype` (bf16 or fp32): rows `ids` of the mixture
+    (routing None) or, per row r, of candidate routing[r] (PTQR)."""
+    ids = _ids(ids, "ids")
+    if routing is not None:
+        routing = _ids(routing, "routing")
+        if routing.numel() != ids.numel():
+            raise ValueError(f"routing has {routing.numel()} entries for {ids.numel()} ids")
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"embedding rows come as bf16 or fp32, not {dtype}")
+    dev = ids.device
+    if out is None:
+        out = torch.empty(ids.numel(), dim, dtype=dtype, device=dev)
+    elif out.dtype != dtype:
+        raise ValueError(f"out is {out.dtype}, expected {dtype}")
+    _check(lib().vq_embedding_rows_fwd(len(ggml_types), _int_array(ggml_types), _ptr_array(qbytes, "qbytes"),
+                                       _dev_ptr(probs, "probs"), _dev_ptr(routing, "routing"), _dev_ptr(ids, "ids"),
+                                       ids.numel(), num_embeddings, dim, d_pad, _dev_ptr(out, "out"),
+                                       int(dtype == torch.float32), _stream(dev)),
+           "vq_embedding_rows_fwd")
+    return out
+
+
+def embedding_rows_bwd(ggml_types, qbytes, ids: torch.Tensor, num_embeddings: int, dim: int, d_pad: int,
+                       grad: torch.Tensor, dprobs: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [K]: dprobs[k] = sum_r <grad[r], W_k[ids[r]][:dim]> (grad bf16 or fp32)."""
+    ids = _ids(ids, "ids")
+    dev = ids.device
+    k = len(ggml_types)
+    if grad.dtype not in (torch.bfloat16, torch.float32) or tuple(grad.shape) != (ids.numel(), dim):
+        raise ValueError(f"grad must be bf16 or fp32 [{ids.numel()}, {dim}], got {grad.dtype} {tuple(grad.shape)}")
+    if dprobs is None:
+        dprobs = torch.empty(k, dtype=torch.float32, device=dev)
+    nbytes = int(lib().vq_embedding_rows_bwd_workspace(ids.numel(), dim, k))
+    if nbytes < 0:
+        raise ValueError(f"invalid embedding sizes nids={ids.numel()} dim={dim} ncand={k}")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    _check(lib().vq_embedding_rows_bwd(k, _int_array(ggml_types), _ptr_array(qbytes, "qbytes"), _dev_ptr(ids, "ids"),
+                                       ids.numel(), num_embeddings, dim, d_pad, _dev_ptr(grad, "grad"),
+                                       int(grad.dtype == torch.float32), _dev_ptr(dprobs, "dprobs"), _dev_ptr(ws, "workspace"), ws.numel(),
+                                       _stream(dev)),
+           "vq_embedding_rows_bwd")
+    return dprobs
 
 
 def mix_weight(ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int, out: torch.Tensor | None = None):

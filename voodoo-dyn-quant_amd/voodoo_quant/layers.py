@@ -277,6 +277,43 @@ class MixedWeightFunction(Function):
         return (gp, None) + (None,) * len(ctx.qbytes)
 
 
+class EmbeddingRowsFunction(Function):
+    """Row lookup of a gated embedding on libvoodoo_hip: only the requested
+    rows of each packed candidate are decoded (reference
+    ``_MixedEmbeddingRowFunctionLazy``, ``layers.py:670-750``; with a routing,
+    its PTQR row selection, ``layers.py:712-716``).
+
+    forward(ctx, probs [K] fp32, routing [R] int64 or None, row_ids [R] int64,
+    meta, *qbytes) -> [R, dim] in meta's dtype (bf16 or fp32), where
+    meta = (ggml type ids, num_embeddings, dim, d_pad, dtype).  Without a
+    routing a row is the fp32 k-ordered mixture of the candidates' rows; with
+    one, row r is candidate routing[r]'s row.  The backward is the full
+    mixture gradient in both cases (straight-through under PTQR):
+    dL/dp_k = sum_r <G[r], W_k[row_ids[r]]>."""
+
+    @staticmethod
+    def forward(ctx, probs, routing, row_ids, meta, *qbytes):
+        types, vocab, dim, d_pad, dtype = meta
+        p = probs.detach().to(device=row_ids.device, dtype=torch.float32).contiguous()
+        out = _hip.embedding_rows_fwd(types, qbytes, p, routing, row_ids, vocab, dim, d_pad, dtype)
+        ctx.save_for_backward(row_ids)
+        ctx.meta = meta
+        ctx.qbytes = qbytes
+        ctx.probs_device = probs.device
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        (row_ids,) = ctx.saved_tensors
+        types, vocab, dim, d_pad, dtype = ctx.meta
+        dprobs = None
+        if ctx.needs_input_grad[0]:
+            g = _aligned(grad.to(dtype))
+            dprobs = _hip.embedding_rows_bwd(types, ctx.qbytes, row_ids, vocab, dim, d_pad, g)
+            dprobs = dprobs.to(ctx.probs_device)
+        return (dprobs, None, None, None) + (None,) * len(ctx.qbytes)
+
+
 # ---------------------------------------------------------------------------
 # gated modules
 # ---------------------------------------------------------------------------
@@ -545,6 +582,72 @@ class MixedQuantLinear(_MixedQuantBase):
                 f"candidates={self.candidate_types}, source={self.candidate_source}")
 
 
+class MixedQuantEmbedding(_MixedQuantBase):
+    """Embedding whose weight is a softmax mixture of K packed candidates
+    (reference ``layers.py:1743-1842``): the weight is the [num_embeddings,
+    embedding_dim] matrix, padded along embedding_dim to a multiple of 256.
+
+    Every lookup takes the reference's row-select route (``layers.py:1805-1828``):
+    the batch's unique ids are looked up once, decoding only those rows of the
+    candidates, and the rows are scattered back to the positions.  Under PTQR
+    each unique row takes one candidate, sampled per row as there.  Rows come
+    in fp32 when the source weight is fp32 (the mixture before the reference's
+    final cast, and exact candidate values when routed) and as bf16 otherwise
+    (then cast to the source dtype)."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int, candidate_types: list[str],
+                 source_weight: torch.Tensor, imatrix: torch.Tensor | None = None, device=None, lazy: bool = False,
+                 tensor_name: str = "unknown", qbytes_device=None, shard_spec=None,
+                 full_source_weight: torch.Tensor | None = None):
+        super().__init__(candidate_types=candidate_types, source_weight=source_weight, out_features=num_embeddings,
+                         in_features=embedding_dim, imatrix=imatrix, device=device, lazy=lazy,
+                         tensor_name=tensor_name, qbytes_device=qbytes_device, shard_spec=shard_spec,
+                         full_source_weight=full_source_weight)
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+        if shard_spec is not None and getattr(shard_spec, "vocab_start", None) is not None:
+            self.tp_vocab_start = shard_spec.vocab_start
+            self.tp_vocab_end = shard_spec.vocab_start + num_embeddings
+
+    def forward(self, input: torch.Tensor) -> torch.Tensor:
+        spec = self.shard_spec
+        if spec is not None and getattr(spec, "vocab_start", None) is not None:
+            raise NotImplementedError("vocab-parallel gated embedding needs the TP all-reduce")
+        return self._embedding_lookup(input)
+
+    def _row_dtype(self) -> torch.dtype:
+        return torch.float32 if self.source_dtype == torch.float32 else torch.bfloat16
+
+    def _embedding_lookup(self, input: torch.Tensor) -> torch.Tensor:
+        if input.device.type != "cuda":
+            raise RuntimeError(f"{self._tensor_name}: MixedQuantEmbedding runs on a ROCm device only "
+                               f"(got {input.device})")
+        dev = input.device
+        self._move_qbytes(dev)
+        rows, inverse = torch.unique(input.reshape(-1), return_inverse=True)
+        rows = rows.to(torch.int64)
+        if rows.numel():
+            lo, hi = torch.stack([rows[0], rows[-1]]).tolist()
+            if lo < 0 or hi >= self.num_embeddings:
+                raise IndexError(f"{self._tensor_name}: index out of range in self "
+                                 f"(ids span [{lo}, {hi}], num_embeddings={self.num_embeddings})")
+        probs = self.get_probs()
+        if probs.device != dev:
+            probs = probs.to(dev)
+        routing = _sample_token_routing(probs.detach(), rows.numel()) if _PTQR_STATE.enabled else None
+        dim8 = (self.embedding_dim + 7) // 8 * 8  # the kernels store whole 8-weight runs
+        meta = (self._ggml_types(), self.num_embeddings, dim8, self.padded_in_features, self._row_dtype())
+        row_vals = EmbeddingRowsFunction.apply(probs, routing, rows, meta, *self._qbytes())
+        if dim8 != self.embedding_dim:
+            row_vals = row_vals[:, : self.embedding_dim]
+        out = row_vals[inverse].reshape(*input.shape, self.embedding_dim)
+        return out if out.dtype == self.source_dtype else out.to(self.source_dtype)
+
+    def extra_repr(self) -> str:
+        return (f"num_embeddings={self.num_embeddings}, embedding_dim={self.embedding_dim}, "
+                f"candidates={self.candidate_types}, source={self.candidate_source}")
+
+
 # ---------------------------------------------------------------------------
 # module walkers (reference layers.py:1845-2160)
 # ---------------------------------------------------------------------------
@@ -625,6 +728,46 @@ def replace_linear_with_mixed_quant(module: nn.Module, candidate_types: list[str
                 skip_names=skip_names, imatrix_dict=imatrix_dict, device=device, lazy=lazy,
                 attention_candidates=attention_candidates, non_attention_candidates=non_attention_candidates,
                 qbytes_device=qbytes_device))
+    return replaced
+
+
+def replace_embedding_with_mixed_quant(module: nn.Module, candidate_types: list[str] | None, prefix: str = "",
+                                       skip_names: Optional[set[str]] = None,
+                                       imatrix_dict: Optional[dict[str, torch.Tensor]] = None, device=None,
+                                       lazy: bool = False, qbytes_device=None,
+                                       attention_candidates: Optional[list[str]] = None,
+                                       non_attention_candidates: Optional[list[str]] = None
+                                       ) -> dict[str, MixedQuantEmbedding]:
+    """Replace every selected ``nn.Embedding`` below ``module`` by a
+    :class:`MixedQuantEmbedding` (reference ``layers.py:2085-2153``)."""
+    if candidate_types is None:
+        candidate_types = list(HIP_TYPES)
+    skip_names = set() if skip_names is None else skip_names
+    imatrix_dict = {} if imatrix_dict is None else imatrix_dict
+    replaced: dict[str, MixedQuantEmbedding] = {}
+    for name, child in list(module.named_children()):
+        full_name = f"{prefix}.{name}" if prefix else name
+        if name in skip_names:
+            continue
+        if isinstance(child, nn.Embedding):
+            imatrix = imatrix_dict.get(full_name)
+            if imatrix is None:
+                imatrix = imatrix_dict.get(full_name + ".weight")
+            types = resolve_candidate_types(full_name, candidate_types, attention_candidates,
+                                            non_attention_candidates)
+            new = MixedQuantEmbedding(child.num_embeddings, child.embedding_dim, types, child.weight.data,
+                                      imatrix=imatrix, device=device, lazy=lazy, tensor_name=full_name,
+                                      qbytes_device=qbytes_device,
+                                      shard_spec=getattr(child, "tp_shard_spec", None),
+                                      full_source_weight=getattr(child, "tp_full_weight", None))
+            setattr(module, name, new)
+            replaced[full_name] = new
+            print(f"  MixedQuantEmbedding init: {full_name} replaced", flush=True)
+        else:
+            replaced.update(replace_embedding_with_mixed_quant(
+                child, candidate_types, prefix=full_name, skip_names=skip_names, imatrix_dict=imatrix_dict,
+                device=device, lazy=lazy, qbytes_device=qbytes_device, attention_candidates=attention_candidates,
+                non_attention_candidates=non_attention_candidates))
     return replaced
 
 

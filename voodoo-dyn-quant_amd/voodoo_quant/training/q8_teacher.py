@@ -1,0 +1,265 @@
+"""Q8_0 teacher modules on the MI355X kernels.
+
+Drop-in for the reference's ``voodoo_quant/training/q8_teacher.py``: the
+teacher keeps every Linear/Embedding weight as llama.cpp Q8_0 bytes on the
+device and decodes them when it runs.
+
+* :class:`Q8Linear` (reference ``q8_teacher.py:62-139``) is the gated Linear
+  with one candidate and probability 1: ``vq_gated_linear_fwd`` writes the
+  bf16 decode of the bytes (``bf16(0 + 1 * w)``, the reference's
+  ``dequantize_tensor_gpu`` value) and runs the MFMA GEMM on it, then the bias
+  is added as in ``F.linear``.  The reference's row-blocked path for
+  vocabulary-scale heads (``q8_teacher.py:36-58, 103-122``) exists to bound
+  transients on 32 GB cards; here the whole bf16 weight is one transient
+  buffer (2.5 GB for 248320 x 5120, against 288 GB of HBM).
+* :class:`Q8Embedding` (``q8_teacher.py:142-173``) looks up the batch's unique
+  rows with ``vq_embedding_rows_fwd`` routed to the one candidate, which gives
+  ggml's values rounded to bf16 exactly as the reference's row decode.
+* :func:`wrap_q8_teacher` (``q8_teacher.py:176-294``) swaps them into a model
+  built from a Q8_0 teacher checkpoint.
+
+Q8_0 stores 32-weight blocks; the kernels read rows as whole 256-weight groups
+and the GEMM wants out_features % 8 == 0, so a tensor whose in_features is not
+a multiple of 256 (or whose out_features is not a multiple of 8) is repacked
+once into zero-padded rows (zero blocks decode to 0).  Inputs run in bf16, the
+teacher's dtype in the reference's training runs; fp32 inputs are cast to bf16
+for the GEMM and the result cast back.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from voodoo_quant import _hip
+
+_Q8_0 = 8            # ggml type id
+_Q8_BLOCK = 32       # weights per block
+_Q8_BLOCK_BYTES = 34  # fp16 scale + 32 int8
+
+
+def _padded_q8(qbytes: torch.Tensor, rows: int, cols: int, rows_to: int) -> tuple[torch.Tensor, int]:
+    """Q8_0 bytes of [rows, cols] as [rows_pad, d_pad] with d_pad = cols rounded
+    up to 256 and rows_pad = rows rounded up to `rows_to` (zero blocks added)."""
+    if cols % _Q8_BLOCK:
+        raise ValueError(f"Q8_0 needs in_features % 32 == 0, got {cols}")
+    nb = cols // _Q8_BLOCK
+    if qbytes.numel() != rows * nb * _Q8_BLOCK_BYTES:
+        raise ValueError(f"Q8_0 [{rows}, {cols}] holds {rows * nb * _Q8_BLOCK_BYTES} bytes, got {qbytes.numel()}")
+    d_pad = (cols + 255) // 256 * 256
+    rows_pad = (rows + rows_to - 1) // rows_to * rows_to
+    flat = qbytes.reshape(-1)
+    if d_pad == cols and rows_pad == rows:
+        return (flat if flat.is_contiguous() else flat.contiguous()), d_pad
+    out = torch.zeros(rows_pad, d_pad // _Q8_BLOCK, _Q8_BLOCK_BYTES, dtype=torch.uint8, device=qbytes.device)
+    out[:rows, :nb] = flat.view(rows, nb, _Q8_BLOCK_BYTES)
+    return out.reshape(-1), d_pad
+
+
+class Q8Linear(nn.Module):
+    """nn.Linear stand-in keeping Q8_0 bytes on the device (``qweight``),
+    decoded on every forward (reference ``q8_teacher.py:62-139``)."""
+
+    def __init__(self, qbytes: torch.Tensor, out_features: int, in_features: int,
+                 bias: torch.Tensor | None = None, device: torch.device | None = None):
+        super().__init__()
+        self.out_features = out_features
+        self.in_features = in_features
+        dev = torch.device(device) if device is not None else qbytes.device
+        self.register_buffer("qweight", qbytes.to(dev) if qbytes.device != dev else qbytes)
+        self._w: torch.Tensor | None = None
+        if bias is not None:
+            self.bias = nn.Parameter(bias.to(dev).to(torch.bfloat16), requires_grad=False)
+        else:
+            self.register_parameter("bias", None)
+
+    def _packed(self) -> tuple[torch.Tensor, int, int]:
+        """(bytes in the kernels' row layout, rows, d_pad), repacked once if needed."""
+        key = (self.qweight.data_ptr(), self.qweight.device)
+        cached = self.__dict__.get("_pack")
+        if cached is None or cached[0] != key:
+            qb, d_pad = _padded_q8(self.qweight, self.out_features, self.in_features, 8)
+            rows = qb.numel() // (d_pad // _Q8_BLOCK * _Q8_BLOCK_BYTES)
+            cached = (key, qb, rows, d_pad)
+            self.__dict__["_pack"] = cached
+        return cached[1], cached[2], cached[3]
+
+    def _weight(self) -> torch.Tensor:
+        """bf16 [out, in] decode (the reference's dequant cache)."""
+        if self.qweight.numel() == 0:
+            raise RuntimeError(f"Q8Linear empty qweight: {self.out_features}x{self.in_features} "
+                               "(offloaded, never reloaded)")
+        if self._w is None or self._w.device != self.qweight.device:
+            qb, rows, d_pad = self._packed()
+            self._w = _hip.dequant_bf16(_Q8_0, qb, rows, d_pad)[: self.out_features, : self.in_features]
+        return self._w
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.device.type != "cuda":
+            raise RuntimeError(f"Q8Linear runs on a ROCm device only (got {x.device})")
+        if self.qweight.numel() == 0:
+            raise RuntimeError(f"Q8Linear empty qweight: {self.out_features}x{self.in_features} "
+                               "(offloaded, never reloaded)")
+        qb, rows, d_pad = self._packed()
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if x2.dtype != torch.bfloat16:
+            x2 = x2.to(torch.bfloat16)
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.contiguous().clone()
+        m = x2.shape[0]
+        dev = x2.device
+        y = torch.empty(m, rows, dtype=torch.bfloat16, device=dev)
+        if m:
+            w = torch.empty(rows, d_pad, dtype=torch.bfloat16, device=dev)
+            one = torch.ones(1, dtype=torch.float32, device=dev)
+            nbytes = _hip.fwd_workspace_bytes(m, rows, self.in_features)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
+            _hip.gated_linear_fwd(x2, (_Q8_0,), [qb], one, rows, d_pad, w, y, ws)
+        if rows != self.out_features:
+            y = y[:, : self.out_features]
+        if self.bias is not None:
+            y = y + self.bias.to(y.dtype)
+        self._w = None  # one-shot, as the reference's teacher forward
+        out = y.reshape(*lead, self.out_features)
+        return out if out.dtype == x.dtype else out.to(x.dtype)
+
+
+class Q8Embedding(nn.Module):
+    """nn.Embedding stand-in keeping Q8_0 bytes on the device; a forward
+    decodes only the batch's rows (reference ``q8_teacher.py:142-173``)."""
+
+    def __init__(self, qbytes: torch.Tensor, num_embeddings: int, embedding_dim: int,
+                 device: torch.device | None = None):
+        super().__init__()
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+        dev = torch.device(device) if device is not None else qbytes.device
+        self.register_buffer("qweight", qbytes.to(dev) if qbytes.device != dev else qbytes)
+        self._w: torch.Tensor | None = None
+
+    def _packed(self) -> tuple[torch.Tensor, int]:
+        key = (self.qweight.data_ptr(), self.qweight.device)
+        cached = self.__dict__.get("_pack")
+        if cached is None or cached[0] != key:
+            qb, d_pad = _padded_q8(self.qweight, self.num_embeddings, self.embedding_dim, 1)
+            cached = (key, qb, d_pad)
+            self.__dict__["_pack"] = cached
+        return cached[1], cached[2]
+
+    def _weight(self) -> torch.Tensor:
+        """bf16 [num_embeddings, embedding_dim] decode of the whole table."""
+        if self._w is None or self._w.device != self.qweight.device:
+            qb, d_pad = self._packed()
+            self._w = _hip.dequant_bf16(_Q8_0, qb, self.num_embeddings, d_pad)[:, : self.embedding_dim]
+        return self._w
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.device.type != "cuda":
+            raise RuntimeError(f"Q8Embedding runs on a ROCm device only (got {x.device})")
+        qb, d_pad = self._packed()
+        rows, inverse = torch.unique(x.reshape(-1), return_inverse=True)
+        rows = rows.to(device=qb.device, dtype=torch.int64)
+        if rows.numel():
+            lo, hi = torch.stack([rows[0], rows[-1]]).tolist()
+            if lo < 0 or hi >= self.num_embeddings:
+                raise IndexError(f"Q8Embedding: index out of range in self (ids span [{lo}, {hi}], "
+                                 f"num_embeddings={self.num_embeddings})")
+        dim8 = (self.embedding_dim + 7) // 8 * 8
+        routing = torch.zeros_like(rows)  # every row from the one candidate: exact decode
+        w_rows = _hip.embedding_rows_fwd((_Q8_0,), [qb], None, routing, rows, self.num_embeddings, dim8, d_pad)
+        if dim8 != self.embedding_dim:
+            w_rows = w_rows[:, : self.embedding_dim]
+        return w_rows[inverse.to(w_rows.device)].reshape(*x.shape, self.embedding_dim)
+
+
+def _layer_index(name: str) -> int | None:
+    parts = name.split(".")
+    if len(parts) >= 2 and parts[-2] == "layers":
+        try:
+            return int(parts[-1])
+        except ValueError:
+            return None
+    return None
+
+
+def wrap_q8_teacher(model: nn.Module, teacher_state_dict: dict, quant_meta: dict,
+                    layer_devices: dict[int, torch.device] | None = None) -> nn.Module:
+    """Replace the model's Linears/Embeddings whose ``<name>.weight`` is a 2-D
+    uint8 (Q8_0) tensor of the checkpoint with :class:`Q8Linear` /
+    :class:`Q8Embedding`, and load every other checkpoint tensor as-is
+    (reference ``q8_teacher.py:176-294``).
+
+    Lookups try the module's own name and the name without a leading
+    ``model.`` (the checkpoint stores the stripped names); shapes come from
+    ``quant_meta[...]["out_features"/"in_features"]``.  ``layer_devices``
+    ({layer index: device}) places each decoder layer's modules and tensors on
+    its device."""
+    if layer_devices:
+        for name, module in model.named_modules():
+            idx = _layer_index(name)
+            dev = layer_devices.get(idx) if idx is not None else None
+            if dev is not None and name.count(".") <= 2:
+                module._q8_target_device = dev
+
+    def lookup(key: str):
+        for k in (key, key.removeprefix("model.")):
+            if k in teacher_state_dict:
+                return teacher_state_dict[k]
+        return None
+
+    def meta_for(full: str, weight_key: str):
+        for k in (weight_key, weight_key.removeprefix("model."), full, full.removeprefix("model.")):
+            if k in quant_meta:
+                return quant_meta[k]
+        return None
+
+    replaced = 0
+    wrapped: set[str] = set()
+    for name, module in list(model.named_modules()):
+        for child_name, child in list(module.named_children()):
+            full = f"{name}.{child_name}" if name else child_name
+            weight_key = full + ".weight"
+            qb = lookup(weight_key)
+            if qb is None or qb.dim() != 2 or qb.dtype != torch.uint8:
+                continue
+            meta = meta_for(full, weight_key)
+            if meta is None:
+                print(f"  q8 teacher WARNING: no quant_meta for {full}; skipping", flush=True)
+                continue
+            dev = getattr(module, "_q8_target_device", None)
+            if isinstance(child, nn.Linear):
+                new = Q8Linear(qb, meta["out_features"], meta["in_features"],
+                               child.bias.detach() if child.bias is not None else None, device=dev)
+            elif isinstance(child, nn.Embedding):
+                new = Q8Embedding(qb, child.num_embeddings, child.embedding_dim, device=dev)
+            else:
+                continue
+            # the host source of the bytes and the full-tensor shard descriptor,
+            # for a trainer that drops and re-creates teacher buffers per step
+            new._voodoo_qb_src = (qb,)
+            new._voodoo_qb_shard = (qb, meta["out_features"], meta["in_features"], {})
+            setattr(module, child_name, new)
+            replaced += 1
+            wrapped.add(weight_key)
+            wrapped.add(weight_key.removeprefix("model."))
+
+    def carry_key(k: str) -> str:
+        # the teacher nests its text stack as `model.`; the checkpoint strips it
+        return k if (k.startswith("model.") or k == "lm_head.weight") else "model." + k
+
+    carry = {carry_key(k): v for k, v in teacher_state_dict.items()
+             if carry_key(k) not in wrapped and k not in wrapped}
+    missing, unexpected = model.load_state_dict(carry, strict=False, assign=True)
+    print(f"  q8 teacher: wrapped {replaced} Q8_0 tensors; carried {len(carry)} as-is "
+          f"({len(missing)} missing, {len(unexpected)} unexpected)", flush=True)
+    if unexpected:
+        print(f"  q8 teacher WARNING: {len(unexpected)} unexpected keys (e.g. {unexpected[:3]})", flush=True)
+    if layer_devices:
+        # the reference's rule, applied to the tensor's own name
+        for name, t in list(model.named_parameters()) + list(model.named_buffers()):
+            idx = _layer_index(name)
+            dev = layer_devices.get(idx) if idx is not None else None
+            if dev is not None and t.device.type == "cpu":
+                t.data = t.data.to(dev)
+    return model
