@@ -118,12 +118,56 @@ def cpu_baseline(torch, m: int, n_total: int, d: int, budget_s: float = 12.0) ->
     }
 
 
+def train_step_bench(torch, dev, steps: int, warmup: int) -> dict:
+    """Gate-training steps of the 0.8B-class decoder (24 layers, hidden 1024,
+    16x64 query heads, 4 KV heads, SwiGLU 3072, vocabulary 151936 tied; every
+    Linear and the embedding gated over 6 candidates; Q8_0 teacher), batch
+    4 x 2048 uniform-random token ids: tokens per second of the whole step
+    (forwards, CE + KL + size loss, backward, clip, AdamW)."""
+    from voodoo_quant.training import step as st
+
+    cfg = st.DecoderConfig()
+    t0 = time.perf_counter()
+    student, teacher, replaced = st.build_models(cfg, TYPES, dev, seed=0, packed=True)
+    torch.cuda.synchronize()
+    log(f"train: decoder built in {time.perf_counter() - t0:.1f} s ({len(replaced)} gated tensors)")
+    b, s = 4, 2048
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randint(0, cfg.vocab, (b, s), device=dev, generator=g)
+    y = torch.randint(0, cfg.vocab, (b, s), device=dev, generator=g)
+    tr = st.GateTrainer(student, teacher, replaced, st.StepConfig(max_steps=max(steps + warmup, 2)),
+                        total_8bit_bytes=float(cfg.gated_weights()))
+    for _ in range(warmup):
+        tr.step(x, y)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = tr.step(x, y)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / max(steps, 1) * 1e3
+    tokens = b * s
+    fl = st.step_flops(cfg, tokens, s)
+    rec = {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "steps": steps,
+           "warmup": warmup, "model_TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
+           "loss": {k: round(float(v), 4) for k, v in out.items()},
+           "workload": "0.8B-class decoder gate-training step: 24 layers, hidden 1024, 16x64 q heads, 4 KV heads, "
+                       "SwiGLU 3072, vocab 151936 tied; 168 gated Linears + gated embedding, K=6; Q8_0 teacher; "
+                       "batch 4x2048 uniform-random ids; CE + KL + dead-zone size loss at 45% of 8-bit",
+           "candidate_bytes": "random valid GGUF blocks, scales sized for N(0, 0.02)-like weights"}
+    log(f"train: {ms:.1f} ms/step -> {rec['tokens_per_s']:.0f} tokens/s ({rec['model_TFLOPs']} model TFLOP/s)")
+    del student, teacher, replaced, tr
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train", action="store_true", help="skip the decoder gate-training step measurement")
+    ap.add_argument("--train-steps", type=int, default=5)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -232,6 +276,12 @@ def main() -> int:
         del qb
     log("dequant GB/s: " + ", ".join(f"{k} {v['GBps']}" for k, v in dq.items()))
 
+    train = None
+    if not args.no_train:
+        del qbytes, w_eff, y, dx, ws, fws, out
+        torch.cuda.empty_cache()
+        train = train_step_bench(torch, dev, args.train_steps, 2)
+
     if args.copy_calibration:
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -271,6 +321,7 @@ def main() -> int:
         "kernels_ms": {k: round(v, 4) for k, v in kernels.items()},
         "dequant_gbps": dq,
         "ptqr": ptqr,
+        "train": train,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -1,0 +1,89 @@
+"""The training-step losses on the CPU, on a small decoder of plain torch
+modules: the full-logits losses against their closed forms, and the chunked
+path (reference ``trainer.py:751-832``) against the full-logits path
+(``trainer.py:2566-2603``), which it must reproduce exactly when the
+distillation weight is 1 (the chunk backward omits it, as in the reference)."""
+
+import pytest
+import torch
+import torch.nn as nn
+
+from voodoo_quant.training import step as st
+from voodoo_quant.training import trainer
+
+CFG = st.DecoderConfig(layers=2, hidden=64, heads=2, kv_heads=1, head_dim=32, mlp=96, vocab=50)
+
+
+def _plain_decoder(seed, trainable=True):
+    g = torch.Generator().manual_seed(seed)
+
+    def lin(o, i):
+        m = nn.Linear(i, o, bias=False)
+        with torch.no_grad():
+            m.weight.copy_(torch.randn(o, i, generator=g) * 0.1)
+        m.to(torch.bfloat16).requires_grad_(trainable)
+        return m
+
+    layers = [{n: lin(o, i) for n, (o, i) in CFG.linear_shapes().items()} for _ in range(CFG.layers)]
+    emb = nn.Embedding(CFG.vocab, CFG.hidden)
+    with torch.no_grad():
+        emb.weight.copy_(torch.randn(CFG.vocab, CFG.hidden, generator=g) * 0.5)
+    emb.requires_grad_(False)
+    head = st._TiedHead(emb.weight.detach().to(torch.bfloat16).clone())
+    return st.Decoder(st._Body(CFG, emb, layers, "cpu"), head)
+
+
+def _batch():
+    g = torch.Generator().manual_seed(7)
+    return torch.randint(0, CFG.vocab, (2, 12), generator=g), torch.randint(0, CFG.vocab, (2, 12), generator=g)
+
+
+def test_full_logits_losses_closed_form():
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn(3, 5, 11, generator=g, dtype=torch.float64)
+    t_logits = torch.randn(3, 5, 11, generator=g, dtype=torch.float64)
+    y = torch.randint(0, 11, (3, 5), generator=g)
+    temp = 1.7
+    ce, kl = trainer.distill_losses(logits, t_logits, y, temp)
+    lp = torch.log_softmax(logits.reshape(-1, 11), -1)
+    assert float(ce) == pytest.approx(float(-lp[torch.arange(15), y.reshape(-1)].mean()), rel=1e-12)
+    sp = torch.log_softmax(logits.reshape(-1, 11) / temp, -1)
+    tp = torch.softmax(t_logits.reshape(-1, 11) / temp, -1)
+    ref = (tp * (tp.log() - sp)).sum(-1).mean() * temp * temp
+    assert float(kl) == pytest.approx(float(ref), rel=1e-10)
+    # a planted sign error in the closed form must not pass
+    assert float(kl) != pytest.approx(float((tp * (tp.log() + sp)).sum(-1).mean() * temp * temp), rel=1e-3)
+
+
+def test_chunked_loss_matches_full_logits():
+    x, y = _batch()
+    temp = 1.3
+    student, teacher = _plain_decoder(0), _plain_decoder(1, trainable=False)
+    ce, kl = trainer.distill_losses(student(x), teacher(x), y, temp)
+    (ce + kl).backward()
+    full = {n: p.grad.clone() for n, p in student.named_parameters() if p.requires_grad}
+    student.zero_grad()
+    ce_c, kl_c = trainer.chunked_forward_loss(student, teacher, x, y, temp, chunk=5)
+    chunked = {n: p.grad.clone() for n, p in student.named_parameters() if p.requires_grad}
+    assert ce_c == pytest.approx(float(ce.detach()), rel=1e-2) and kl_c == pytest.approx(float(kl.detach()), rel=2e-2)
+    for n, g in full.items():
+        rel = float((chunked[n].float() - g.float()).norm() / g.float().norm())
+        assert rel < 5e-2, (n, rel)
+
+
+def test_step_flops_and_gated_weights():
+    cfg = st.DecoderConfig()
+    assert cfg.gated_weights() == 24 * 12_058_624 + 151936 * 1024
+    fl = st.step_flops(cfg, 8192, 2048)
+    assert 25e12 < fl < 35e12
+
+
+def test_synthetic_candidates_are_valid_and_centred():
+    from oracle import cdequant
+
+    g = torch.Generator().manual_seed(0)
+    for qt in ("Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"):
+        qb = st.synthetic_candidate_bytes(qt, 16, 512, "cpu", g)
+        w = torch.from_numpy(cdequant.oracle_dequant(qt, qb.numpy(), 16 * 512))
+        assert torch.isfinite(w).all()
+        assert abs(float(w.mean())) < 0.01 and 0.01 < float(w.std()) < 0.08 and float(w.abs().max()) < 0.2

@@ -326,27 +326,10 @@ class _MixedQuantBase(nn.Module):
                  tensor_name: str = "unknown", qbytes_device=None, shard_spec=None,
                  full_source_weight: torch.Tensor | None = None):
         super().__init__()
-        self.candidate_types = list(candidate_types)
-        bad = [qt for qt in self.candidate_types if qt not in HIP_TYPES]
-        if bad:
-            raise ValueError(f"{tensor_name}: candidate types {bad} have no HIP decoder (supported: {HIP_TYPES})")
-        if not self.candidate_types:
-            raise ValueError(f"{tensor_name}: empty candidate list")
-        self.num_candidates = len(self.candidate_types)
-        self.out_features = out_features
-        self.in_features = in_features
-        self.lazy = lazy
-        self._tensor_name = tensor_name
-        self._qbytes_device = torch.device(qbytes_device) if qbytes_device is not None else None
-        self.shard_spec = shard_spec
         if shard_spec is not None and full_source_weight is None:
             raise ValueError(f"{tensor_name}: shard_spec requires full_source_weight")
-        if device is None:
-            device = source_weight.device
-        self._device = torch.device(device)
-        self.gates = nn.Parameter(torch.zeros(self.num_candidates, device=self._device))
-        self.temperature = 1.0
-        self.source_dtype = source_weight.dtype
+        self._setup(candidate_types, out_features, in_features, lazy, tensor_name, qbytes_device, shard_spec,
+                    source_weight.device if device is None else device, source_weight.dtype)
 
         src = (full_source_weight if shard_spec is not None else source_weight).detach().to("cpu").contiguous()
         if imatrix is not None:
@@ -381,6 +364,51 @@ class _MixedQuantBase(nn.Module):
         self.imatrix = imatrix
         if self._qbytes_device is not None:
             self._move_qbytes(self._qbytes_device)
+
+    def _setup(self, candidate_types, out_features, in_features, lazy, tensor_name, qbytes_device, shard_spec,
+               device, source_dtype) -> None:
+        self.candidate_types = list(candidate_types)
+        bad = [qt for qt in self.candidate_types if qt not in HIP_TYPES]
+        if bad:
+            raise ValueError(f"{tensor_name}: candidate types {bad} have no HIP decoder (supported: {HIP_TYPES})")
+        if not self.candidate_types:
+            raise ValueError(f"{tensor_name}: empty candidate list")
+        self.num_candidates = len(self.candidate_types)
+        self.out_features = out_features
+        self.in_features = in_features
+        self.lazy = lazy
+        self._tensor_name = tensor_name
+        self._qbytes_device = torch.device(qbytes_device) if qbytes_device is not None else None
+        self.shard_spec = shard_spec
+        self._device = torch.device(device)
+        self.gates = nn.Parameter(torch.zeros(self.num_candidates, device=self._device))
+        self.temperature = 1.0
+        self.source_dtype = source_dtype
+
+    @classmethod
+    def _from_packed(cls, candidate_types: list[str], qbytes: list[torch.Tensor], out_features: int,
+                     in_features: int, source_dtype: torch.dtype, tensor_name: str, device=None):
+        """A layer over candidate bytes that already exist (one packed
+        [out_features, in_features rounded up to 256] stream per type): no
+        quantization, no cache.  The bytes stay where they are."""
+        obj = cls.__new__(cls)
+        nn.Module.__init__(obj)
+        dev = qbytes[0].device if device is None else device
+        obj._setup(candidate_types, out_features, in_features, True, tensor_name, None, None, dev, source_dtype)
+        if len(qbytes) != obj.num_candidates:
+            raise ValueError(f"{tensor_name}: {len(qbytes)} byte streams for {obj.num_candidates} candidates")
+        obj.padded_in_features = (in_features + 255) // 256 * 256
+        obj._full_padded_in_features = obj.padded_in_features
+        obj.candidate_source = "packed"
+        for k, qt in enumerate(obj.candidate_types):
+            info = get_quant_info(qt)
+            expect = out_features * (obj.padded_in_features // info.block_size) * info.block_bytes
+            qb = qbytes[k].reshape(-1)
+            if qb.dtype != torch.uint8 or qb.numel() != expect:
+                raise ValueError(f"{tensor_name}: {qt} bytes must be uint8 x {expect}, got {qb.dtype} x {qb.numel()}")
+            obj.register_buffer(f"_qweight_{k}", qb.contiguous(), persistent=False)
+        obj.imatrix = None
+        return obj
 
     # -- candidate storage ----------------------------------------------------
     def _qbytes(self) -> list[torch.Tensor]:
@@ -551,6 +579,15 @@ class MixedQuantLinear(_MixedQuantBase):
             self.tp_vocab_start = shard_spec.vocab_start
             self.tp_vocab_end = shard_spec.vocab_start + out_features
 
+    @classmethod
+    def from_packed(cls, in_features: int, out_features: int, candidate_types: list[str],
+                    qbytes: list[torch.Tensor], source_dtype: torch.dtype = torch.bfloat16,
+                    tensor_name: str = "unknown", device=None) -> "MixedQuantLinear":
+        """A gated Linear over existing candidate bytes (a candidate cache
+        entry, another process's quantization, synthetic blocks)."""
+        return cls._from_packed(candidate_types, qbytes, out_features, in_features, source_dtype, tensor_name,
+                                device)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.device.type != "cuda":
             raise RuntimeError(f"{self._tensor_name}: MixedQuantLinear runs on a ROCm device only (got {x.device})")
@@ -608,6 +645,17 @@ class MixedQuantEmbedding(_MixedQuantBase):
         if shard_spec is not None and getattr(shard_spec, "vocab_start", None) is not None:
             self.tp_vocab_start = shard_spec.vocab_start
             self.tp_vocab_end = shard_spec.vocab_start + num_embeddings
+
+    @classmethod
+    def from_packed(cls, num_embeddings: int, embedding_dim: int, candidate_types: list[str],
+                    qbytes: list[torch.Tensor], source_dtype: torch.dtype = torch.bfloat16,
+                    tensor_name: str = "unknown", device=None) -> "MixedQuantEmbedding":
+        """A gated embedding over existing candidate bytes."""
+        obj = cls._from_packed(candidate_types, qbytes, num_embeddings, embedding_dim, source_dtype, tensor_name,
+                               device)
+        obj.num_embeddings = num_embeddings
+        obj.embedding_dim = embedding_dim
+        return obj
 
     def forward(self, input: torch.Tensor) -> torch.Tensor:
         spec = self.shard_spec

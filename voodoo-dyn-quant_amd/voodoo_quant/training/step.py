@@ -1,0 +1,329 @@
+"""Gate-training step of a decoder whose Linears and embedding are gated.
+
+The step the reference's trainer runs per batch (``trainer.py:2498-2616``),
+on a Llama/Qwen-style decoder (RMSNorm, RoPE, grouped-query attention,
+SwiGLU MLP, tied embeddings):
+
+* the student's seven Linears per layer are :class:`MixedQuantLinear` and its
+  embedding a :class:`MixedQuantEmbedding`; with tied embeddings the student's
+  lm_head stays a plain Linear over the source embedding weight, as in the
+  reference (``trainer.py:2098-2101``);
+* the teacher is the same architecture over Q8_0 bytes
+  (:class:`Q8Linear`/:class:`Q8Embedding`, its tied lm_head a Q8Linear over the
+  embedding's bytes) and runs without gradients;
+* loss = CE + distill_weight * KL(teacher || student) + size_weight *
+  dead-zone size penalty, backward, global clip 1.0, AdamW + cosine step on
+  the gates only (every other weight is frozen), temperature annealed per step.
+
+Only the gates train, so the backward runs dX through every layer and the
+gate gradients of every gated tensor; no weight gradient is formed.  Attention
+uses torch's fused scaled-dot-product kernels (flash or memory-efficient);
+without one of them it runs the math path in fp32.
+"""
+
+from __future__ import annotations
+
+import warnings
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from voodoo_quant import layers
+from voodoo_quant.ggml import get_quant_info
+from voodoo_quant.training import trainer
+from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear
+
+
+@dataclass
+class DecoderConfig:
+    layers: int = 24
+    hidden: int = 1024
+    heads: int = 16
+    kv_heads: int = 4
+    head_dim: int = 64
+    mlp: int = 3072
+    vocab: int = 151936
+    rope_theta: float = 1.0e6
+    eps: float = 1.0e-6
+
+    def linear_shapes(self) -> dict[str, tuple[int, int]]:
+        """{name: (out_features, in_features)} of one layer's Linears."""
+        h, q, kv, m = self.hidden, self.heads * self.head_dim, self.kv_heads * self.head_dim, self.mlp
+        return {"self_attn.q_proj": (q, h), "self_attn.k_proj": (kv, h), "self_attn.v_proj": (kv, h),
+                "self_attn.o_proj": (h, q), "mlp.gate_proj": (m, h), "mlp.up_proj": (m, h),
+                "mlp.down_proj": (h, m)}
+
+    def gated_weights(self) -> int:
+        per_layer = sum(o * i for o, i in self.linear_shapes().values())
+        return self.layers * per_layer + self.vocab * self.hidden  # tied: the embedding counted once
+
+
+def _rope(s: int, head_dim: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim))
+    ang = torch.outer(torch.arange(s, dtype=torch.float32, device=device), inv)
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+
+
+def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+    return x * cos + rot * sin
+
+
+_SDPA_FUSED: bool | None = None
+
+
+def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Causal attention, q [B, Hq, S, d], k/v [B, Hkv, S, d] (KV heads repeated)."""
+    global _SDPA_FUSED
+    rep = q.shape[1] // k.shape[1]
+    if rep > 1:
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    if _SDPA_FUSED is not False:
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            _SDPA_FUSED = True
+            return out
+        except RuntimeError as e:
+            if _SDPA_FUSED:
+                raise
+            warnings.warn(f"no fused attention kernel ({e}); using the fp32 math path")
+            _SDPA_FUSED = False
+    with sdpa_kernel([SDPBackend.MATH]):
+        out = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
+    return out.to(q.dtype)
+
+
+class _Attention(nn.Module):
+    def __init__(self, cfg: DecoderConfig, lin: dict[str, nn.Module]):
+        super().__init__()
+        self.cfg = cfg
+        self.q_proj, self.k_proj = lin["self_attn.q_proj"], lin["self_attn.k_proj"]
+        self.v_proj, self.o_proj = lin["self_attn.v_proj"], lin["self_attn.o_proj"]
+
+    def forward(self, x, cos, sin):
+        b, s, _ = x.shape
+        c = self.cfg
+        q = self.q_proj(x).view(b, s, c.heads, c.head_dim).transpose(1, 2)
+        k = self.k_proj(x).view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
+        v = self.v_proj(x).view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
+        q, k = _apply_rope(q, cos, sin), _apply_rope(k, cos, sin)
+        a = _attention(q, k, v).transpose(1, 2).reshape(b, s, c.heads * c.head_dim)
+        return self.o_proj(a)
+
+
+class _MLP(nn.Module):
+    def __init__(self, lin: dict[str, nn.Module]):
+        super().__init__()
+        self.gate_proj, self.up_proj, self.down_proj = lin["mlp.gate_proj"], lin["mlp.up_proj"], lin["mlp.down_proj"]
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class _Layer(nn.Module):
+    def __init__(self, cfg: DecoderConfig, lin: dict[str, nn.Module], device):
+        super().__init__()
+        self.eps = cfg.eps
+        self.self_attn = _Attention(cfg, lin)
+        self.mlp = _MLP(lin)
+        self.input_layernorm = nn.Parameter(torch.ones(cfg.hidden, dtype=torch.bfloat16, device=device),
+                                            requires_grad=False)
+        self.post_attention_layernorm = nn.Parameter(torch.ones(cfg.hidden, dtype=torch.bfloat16, device=device),
+                                                     requires_grad=False)
+
+    def forward(self, h, cos, sin):
+        h = h + self.self_attn(F.rms_norm(h, (h.shape[-1],), self.input_layernorm, self.eps), cos, sin)
+        return h + self.mlp(F.rms_norm(h, (h.shape[-1],), self.post_attention_layernorm, self.eps))
+
+
+class _Body(nn.Module):
+    def __init__(self, cfg: DecoderConfig, embed: nn.Module, layer_linears: list[dict[str, nn.Module]], device):
+        super().__init__()
+        self.cfg = cfg
+        self.embed_tokens = embed
+        self.layers = nn.ModuleList([_Layer(cfg, lin, device) for lin in layer_linears])
+        self.norm = nn.Parameter(torch.ones(cfg.hidden, dtype=torch.bfloat16, device=device), requires_grad=False)
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        h = self.embed_tokens(input_ids).to(torch.bfloat16)
+        cos, sin = _rope(input_ids.shape[1], self.cfg.head_dim, self.cfg.rope_theta, input_ids.device)
+        for layer in self.layers:
+            h = layer(h, cos, sin)
+        return F.rms_norm(h, (h.shape[-1],), self.norm, self.cfg.eps)
+
+
+class Decoder(nn.Module):
+    """``model`` (the text stack, returning final hidden states) + ``lm_head``."""
+
+    def __init__(self, body: _Body, lm_head: nn.Module):
+        super().__init__()
+        self.model = body
+        self.lm_head = lm_head
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        return self.lm_head(self.model(input_ids))
+
+
+class _TiedHead(nn.Module):
+    """Plain Linear over the (frozen) source embedding weight."""
+
+    def __init__(self, weight: torch.Tensor):
+        super().__init__()
+        self.weight = nn.Parameter(weight, requires_grad=False)
+
+    def forward(self, h):
+        return F.linear(h, self.weight)
+
+
+# Smallest fp16 scale of the synthetic blocks, per format (scales are drawn
+# from [base, 2 base)), chosen so that decoded weights stay within about
+# +-0.2 (standard deviations 0.02-0.06).
+_SYNTH_SCALE_BASE = {"Q8_0": 2.0 ** -11, "Q6_K": 2.0 ** -16, "Q5_K": 2.0 ** -15, "Q4_K": 2.0 ** -14,
+                     "Q3_K": 2.0 ** -11, "Q2_K": 2.0 ** -9}
+_F16_FIELDS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,)}
+# dmin / d of the formats with mins: the mean code, so weights centre on 0
+_SYNTH_MIN_RATIO = {"Q2_K": 1.5, "Q4_K": 7.5, "Q5_K": 15.5}
+
+
+def synthetic_candidate_bytes(qt: str, rows: int, cols: int, device, gen: torch.Generator) -> torch.Tensor:
+    """Random valid blocks of an [rows, cols rounded up to 256] tensor,
+    generated on `device`: random payload bytes and fp16 scale fields drawn
+    uniformly from [base, 2 base) with a per-format base (normal or subnormal
+    fp16, never inf or NaN)."""
+    info = get_quant_info(qt)
+    d_pad = (cols + 255) // 256 * 256
+    nblocks = rows * d_pad // info.block_size
+    q = torch.randint(0, 256, (nblocks, info.block_bytes), dtype=torch.uint8, device=device, generator=gen)
+    for i, off in enumerate(_F16_FIELDS[qt]):
+        base = _SYNTH_SCALE_BASE[qt] * (_SYNTH_MIN_RATIO[qt] if i == 1 else 1.0)
+        d = base * (1.0 + torch.rand(nblocks, device=device, generator=gen))
+        h = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+        q[:, off] = (h & 0xFF).to(torch.uint8)
+        q[:, off + 1] = (h >> 8).to(torch.uint8)
+    return q.reshape(-1)
+
+
+def build_models(cfg: DecoderConfig, types: list[str], device, seed: int = 0, packed: bool = True):
+    """(student, teacher, replaced): the gated student, the Q8_0 teacher and
+    {tensor name: gated module}.
+
+    packed=True takes candidates and teacher bytes from
+    :func:`synthetic_candidate_bytes` (no quantization: the way to build a
+    vocabulary-scale model in seconds); packed=False draws N(0, 0.02) source
+    weights and quantizes them through the module constructors (the
+    reference's path; CPU-bound, for small configurations)."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    cpu_gen = torch.Generator().manual_seed(seed)
+    replaced: dict[str, nn.Module] = {}
+
+    def gated_linear(name, out_f, in_f):
+        if packed:
+            qbs = [synthetic_candidate_bytes(qt, out_f, in_f, device, gen) for qt in types]
+            mod = layers.MixedQuantLinear.from_packed(in_f, out_f, types, qbs, tensor_name=name, device=device)
+        else:
+            w = torch.randn(out_f, in_f, generator=cpu_gen) * 0.02
+            mod = layers.MixedQuantLinear(in_f, out_f, types, w.to(torch.bfloat16), tensor_name=name,
+                                          device=device).to(device)
+        replaced[name] = mod
+        return mod
+
+    def teacher_linear(out_f, in_f):
+        return Q8Linear(synthetic_candidate_bytes("Q8_0", out_f, in_f, device, gen), out_f, in_f)
+
+    shapes = cfg.linear_shapes()
+    s_layers, t_layers = [], []
+    for li in range(cfg.layers):
+        s_layers.append({n: gated_linear(f"model.layers.{li}.{n}", o, i) for n, (o, i) in shapes.items()})
+        t_layers.append({n: teacher_linear(o, i) for n, (o, i) in shapes.items()})
+
+    v, h = cfg.vocab, cfg.hidden
+    src = (torch.randn(v, h, device=device, generator=gen) * 0.02).to(torch.bfloat16)
+    if packed:
+        qbs = [synthetic_candidate_bytes(qt, v, h, device, gen) for qt in types]
+        emb = layers.MixedQuantEmbedding.from_packed(v, h, types, qbs, tensor_name="model.embed_tokens",
+                                                     device=device)
+    else:
+        emb = layers.MixedQuantEmbedding(v, h, types, src.cpu(), tensor_name="model.embed_tokens",
+                                         device=device).to(device)
+    replaced["model.embed_tokens"] = emb
+    student = Decoder(_Body(cfg, emb, s_layers, device), _TiedHead(src))
+
+    t_bytes = synthetic_candidate_bytes("Q8_0", v, h, device, gen)
+    t_emb = Q8Embedding(t_bytes, v, h)
+    teacher = Decoder(_Body(cfg, t_emb, t_layers, device), Q8Linear(t_bytes, v, h))
+    teacher.requires_grad_(False)
+    return student, teacher, replaced
+
+
+@dataclass
+class StepConfig:
+    max_steps: int = 200
+    lr: float = 0.05
+    temp_start: float = 1.0
+    temp_end: float = 0.1
+    distill_weight: float = 1.0
+    distill_temperature: float = 1.0
+    size_weight: float = 10.0
+    size_tolerance: float = 0.02
+    target_fraction: float = 0.45   # of 8-bit bytes
+    logits_chunk: int = 0
+
+
+class GateTrainer:
+    """Runs the reference's per-batch gate-training step (``trainer.py:2498-2616``)."""
+
+    def __init__(self, student: Decoder, teacher: Decoder, replaced: dict[str, nn.Module], cfg: StepConfig,
+                 total_8bit_bytes: float, non_targeted_bytes: float = 0.0):
+        self.student, self.teacher, self.replaced, self.cfg = student, teacher, replaced, cfg
+        self.trainable = [m.gates for m in replaced.values()]
+        self.opt, self.sched = trainer.build_gate_optimizer(self.trainable, cfg.lr, cfg.max_steps)
+        self.target_bytes = cfg.target_fraction * total_8bit_bytes
+        self.non_targeted_bytes = non_targeted_bytes
+        self.step_index = 0
+
+    def step(self, x: torch.Tensor, y: torch.Tensor) -> dict[str, torch.Tensor]:
+        """One optimizer step on batch (x, y); returns the detached losses (no host sync)."""
+        c = self.cfg
+        tau = trainer.anneal_temperature(self.step_index, c.max_steps, c.temp_start, c.temp_end)
+        trainer.set_temperature_all(self.replaced, tau)
+        dev = x.device
+        t = c.distill_temperature
+        if c.logits_chunk > 0:
+            lm, kl = trainer.chunked_forward_loss(self.student, self.teacher, x, y, t, c.logits_chunk)
+            lm_loss, distill = torch.tensor(lm), torch.tensor(kl)
+        else:
+            logits = self.student(x)
+            with torch.no_grad():
+                t_logits = self.teacher(x)
+            lm_loss, distill = trainer.distill_losses(logits, t_logits, y, t)
+        current = layers.total_effective_bytes(self.replaced).to(dev) + self.non_targeted_bytes
+        size = trainer.size_loss(current, self.target_bytes, c.size_tolerance)
+        if c.logits_chunk > 0:
+            (c.size_weight * size).backward()
+        else:
+            loss = lm_loss + c.distill_weight * distill + c.size_weight * size
+            loss.backward()
+        trainer.gate_optimizer_step(self.trainable, self.opt, self.sched, max_norm=1.0)
+        self.step_index += 1
+        return {"lm": lm_loss.detach(), "kl": distill.detach(), "size": size.detach(), "tau": tau}
+
+
+def step_flops(cfg: DecoderConfig, tokens: int, seq: int) -> float:
+    """Model FLOPs of one step: student gated Linears 6 M N D, its lm_head
+    4 M V H (forward + dX), the teacher 2 M N D over all its Linears and head,
+    and causal attention (QK^T and PV, forward 2 M S d per head halved by the
+    mask, backward 2x the forward; the teacher forward once)."""
+    per_layer = sum(o * i for o, i in cfg.linear_shapes().values())
+    lin = cfg.layers * per_layer
+    head = cfg.vocab * cfg.hidden
+    attn_fwd = cfg.layers * 2 * 2 * tokens * seq * cfg.heads * cfg.head_dim / 2
+    return 6 * tokens * lin + 4 * tokens * head + 2 * tokens * (lin + head) + attn_fwd * 3 + attn_fwd

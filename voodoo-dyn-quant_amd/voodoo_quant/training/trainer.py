@@ -64,3 +64,68 @@ def gate_optimizer_step(trainable, opt, sched, max_norm: float = 1.0) -> None:
     opt.step()
     sched.step()
     opt.zero_grad()
+
+
+# ---------------------------------------------------------------------------
+# losses over logits (reference trainer.py:2566-2575, 751-832)
+# ---------------------------------------------------------------------------
+def distill_losses(logits: torch.Tensor, teacher_logits: torch.Tensor, y: torch.Tensor, temperature: float):
+    """(CE, KL): mean token cross-entropy against `y`, and the mean per-token
+    KL(teacher || student) of the temperature-softened distributions times T^2
+    (the reference's full-logits path, ``trainer.py:2566-2575``)."""
+    import torch.nn.functional as F
+
+    v = logits.size(-1)
+    t = temperature
+    lm_loss = F.cross_entropy(logits.view(-1, v), y.view(-1))
+    student_log_probs = F.log_softmax(logits / t, dim=-1)
+    teacher_probs = F.softmax(teacher_logits / t, dim=-1)
+    per_token_kl = F.kl_div(student_log_probs.view(-1, v), teacher_probs.view(-1, v),
+                            reduction="none").sum(dim=-1) * (t * t)
+    return lm_loss, per_token_kl.mean()
+
+
+def _hidden(out) -> torch.Tensor:
+    return out.last_hidden_state if hasattr(out, "last_hidden_state") else out
+
+
+def chunked_forward_loss(student, teacher, x: torch.Tensor, y: torch.Tensor, temperature: float, chunk: int):
+    """Token-chunked CE + KL with one backward through the student's text
+    stack (reference ``_chunked_forward_loss``, ``trainer.py:751-832``).
+
+    Each chunk's head forward, losses and head backward run on a detached copy
+    of the final hidden states, and its input gradient is collected; one
+    backward of the collected gradient then runs through the stack.  As in the
+    reference, the chunk backward differentiates (CE + KL) / tokens, so the
+    distillation weight is not applied on this path.  Returns (CE, KL) as
+    floats, each a mean over tokens."""
+    import torch.nn.functional as F
+
+    hidden = _hidden(student.model(input_ids=x))
+    with torch.no_grad():
+        t_hidden = _hidden(teacher.model(input_ids=x))
+    h = hidden.shape[-1]
+    s_flat, t_flat, y_flat = hidden.reshape(-1, h), t_hidden.reshape(-1, h), y.reshape(-1)
+    n_tok = s_flat.shape[0]
+    t = temperature
+    h_grad = torch.zeros_like(s_flat)
+    lm_total = torch.zeros((), dtype=torch.float64, device=s_flat.device)
+    kl_total = torch.zeros((), dtype=torch.float64, device=s_flat.device)
+    for i in range(0, n_tok, chunk):
+        h_c = s_flat[i:i + chunk].detach().requires_grad_(True)
+        logits_c = student.lm_head(h_c)
+        lm_c = F.cross_entropy(logits_c, y_flat[i:i + chunk], reduction="sum")
+        student_log_probs = F.log_softmax(logits_c / t, dim=-1)
+        del logits_c
+        with torch.no_grad():
+            teacher_probs = F.softmax(teacher.lm_head(t_flat[i:i + chunk]) / t, dim=-1)
+        kl_c = F.kl_div(student_log_probs, teacher_probs, reduction="none").sum() * (t * t)
+        del student_log_probs, teacher_probs
+        ((lm_c + kl_c) / n_tok).backward()
+        with torch.no_grad():
+            if h_c.grad is not None:
+                h_grad[i:i + chunk] = h_c.grad
+        lm_total += lm_c.detach().double() / n_tok
+        kl_total += kl_c.detach().double() / n_tok
+    hidden.backward(h_grad.reshape(hidden.shape))
+    return float(lm_total), float(kl_total)
