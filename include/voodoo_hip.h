@@ -76,6 +76,14 @@ int vq_mix_weight(int ncand, const int *qtypes, const void *const *qbytes, const
  * K-split parts of the GEMM's last tiles (0 when the shape needs none). */
 int64_t vq_gated_linear_fwd_workspace(int64_t m, int64_t n, int64_t d);
 
+/* y[m][n] = x[m][d] . w^T for a bf16 weight w[n][ldw] already in memory (the
+ * forward GEMM of vq_gated_linear_fwd without the mix).  `workspace` is
+ * optional as there (vq_gated_linear_fwd_workspace bytes).  Replaces the
+ * F.linear of Q8Linear.forward over its decoded weight
+ * (voodoo_quant/training/q8_teacher.py:121-122). */
+int vq_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, const uint16_t *w, int64_t ldw, uint16_t *y,
+                  void *workspace, int64_t ws_bytes, void *stream);
+
 /* Forward of the gated Linear: mixes W_eff into `w_eff` ([n][d_pad] bf16,
  * caller-owned, kept for the backward) and writes y[m][n] = x[m][d] . W_eff^T.
  * `workspace` (optional, ws_bytes >= vq_gated_linear_fwd_workspace) lets the
@@ -113,7 +121,7 @@ int vq_routed_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int
  * Replaces the row-select lookup of _MixedEmbeddingRowFunctionLazy.forward
  * (voodoo_quant/layers.py:684-728), _RoutedEmbeddingRowFunction.forward
  * (layers.py:764-779) and, with one Q8_0 candidate and probs = {1},
- * Q8Embedding.forward (voodoo_quant/training/q8_teacher.py:155-173). */
+ * Q8Embedding.forward (voodoo_quant/training/q8_teacher.py:156-173). */
 int vq_embedding_rows_fwd(int ncand, const int *qtypes, const void *const *qbytes, const float *probs,
                           const int64_t *routing, const int64_t *ids, int64_t nids, int64_t num_embeddings,
                           int64_t dim, int64_t d_pad, void *out, int out_f32, void *stream);

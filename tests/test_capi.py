@@ -97,6 +97,13 @@ def test_embedding_rows_argument_checks():
     assert lib.vq_embedding_rows_bwd_workspace(4, 256, 13) == -1
 
 
+def test_linear_fwd_argument_checks():
+    lib = _hip.lib()
+    assert lib.vq_linear_fwd(None, 4, 8, 256, None, 256, None, None, 0, None) == _hip.VQ_ERR_NULL
+    assert lib.vq_linear_fwd(None, 4, 12, 256, None, 256, None, None, 0, None) == _hip.VQ_ERR_ALIGN
+    assert lib.vq_linear_fwd(None, 4, 8, 256, None, 128, None, None, 0, None) == _hip.VQ_ERR_SHAPE  # ldw < d
+
+
 def test_forward_workspace_size():
     # 8192 x 17408 tiles: 2176 over 8 XCDs of 32 CUs -> each XCD splits its last 16 tiles in 2
     n = _hip.fwd_workspace_bytes(8192, 17408, 5120)

@@ -287,8 +287,9 @@ def _q8_bytes(rows, cols, seed):
 
 @pytest.mark.parametrize("out_f,in_f,bias", [(13, 160, True), (512, 1024, False), (264, 5120, True)])
 def test_q8_linear(hip, out_f, in_f, bias):
-    from voodoo_quant.training.q8_teacher import Q8Linear
+    from voodoo_quant.training.q8_teacher import Q8Linear, set_keep_decoded
 
+    set_keep_decoded(False)
     print(f"[q8 linear] out={out_f} in={in_f} bias={bias}", flush=True)
     qb, dec = _q8_bytes(out_f, in_f, seed=out_f)
     g = torch.Generator().manual_seed(in_f)
@@ -307,6 +308,15 @@ def test_q8_linear(hip, out_f, in_f, bias):
     assert torch.equal(_bits(lin._weight().cpu()), _bits(dec.to(torch.bfloat16)))
     yf = lin(x.float().cuda())
     assert yf.dtype == torch.float32
+    # the decode kept between forwards (vq_linear_fwd on it) gives the same output
+    from voodoo_quant.training import q8_teacher
+
+    q8_teacher.set_keep_decoded(True)
+    try:
+        y1, y2 = lin(x.cuda()), lin(x.cuda())
+    finally:
+        q8_teacher.set_keep_decoded(False)
+    assert torch.equal(_bits(y1), _bits(y)) and torch.equal(_bits(y2), _bits(y))
 
 
 @pytest.mark.parametrize("vocab,dim", [(100, 160), (57, 512)])

@@ -366,3 +366,22 @@ def test_q8_padding_repacks_rows():
     assert d == 256 and same.numel() == 8 * 8 * 34
     with pytest.raises(ValueError):
         _padded_q8(qb, 8, 80, 8)
+
+
+def test_total_effective_bytes_batches_like_the_per_layer_sum(isolated_cache):
+    mods = {f"l{i}": _lin(types=t, out_f=16, in_f=256, name=f"eb.{i}", seed=i)
+            for i, t in enumerate([("Q2_K", "Q4_K", "Q8_0"), ("Q3_K", "Q6_K"), ("Q2_K", "Q5_K", "Q8_0")])}
+    g = torch.Generator().manual_seed(4)
+    for i, m in enumerate(mods.values()):
+        with torch.no_grad():
+            m.gates.copy_(torch.randn(m.num_candidates, generator=g))
+        m.set_temperature(0.5 + i)
+    total = layers.total_effective_bytes(mods)
+    ref = sum(float(m.effective_bytes()) for m in mods.values())
+    assert float(total) == pytest.approx(ref, rel=1e-6)
+    total.backward()
+    for m in mods.values():
+        p = m.soft_probs().detach().double()
+        c = torch.tensor(m._bytes_per_candidate(), dtype=torch.float64)
+        grad_ref = (torch.diag(p) - torch.outer(p, p)) @ c / m.temperature
+        assert torch.allclose(m.gates.grad.double(), grad_ref, rtol=1e-4)

@@ -251,6 +251,25 @@ int vq_mix_weight(int ncand, const int* qtypes, const void* const* qbytes, const
     return rc == VQ_OK ? ok() : rc;
 }
 
+int vq_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, const uint16_t* w, int64_t ldw, uint16_t* y,
+                  void* workspace, int64_t ws_bytes, void* stream) {
+    if (n <= 0 || d <= 0 || m < 0 || n > (1 << 21) || d > (1 << 21) || ldw < d || ldw > (1 << 21))
+        return fail(VQ_ERR_SHAPE, "sizes m=%lld n=%lld d=%lld ldw=%lld", (long long)m, (long long)n, (long long)d,
+                    (long long)ldw);
+    if (n % 8 || d % 8 || ldw % 8) return fail(VQ_ERR_ALIGN, "n, d and ldw must be multiples of 8");
+    if (m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld exceeds 2^31 - 1", (long long)m);
+    if (!x || !w || !y) return fail(VQ_ERR_NULL, "x/w/y is NULL");
+    if (!aligned16(x) || !aligned16(w) || !aligned16(y)) return fail(VQ_ERR_ALIGN, "x/w/y not 16-byte aligned");
+    if (m == 0) return ok();
+    const int64_t need = vq::fwd_tail_bytes((int)m, (int)n, (int)d);
+    float* tail = (workspace && ws_bytes >= need && need > 0) ? static_cast<float*>(workspace) : nullptr;
+    int rc = hip_check(vq::launch_gemm_fwd(reinterpret_cast<const vq::bf16_t*>(x),
+                                           reinterpret_cast<const vq::bf16_t*>(w), ldw, reinterpret_cast<vq::bf16_t*>(y),
+                                           (int)m, (int)n, (int)d, tail, static_cast<hipStream_t>(stream)),
+                       "GEMM launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int64_t vq_gated_linear_fwd_workspace(int64_t m, int64_t n, int64_t d) {
     if (m < 0 || n <= 0 || d <= 0 || m > INT32_MAX || n > INT32_MAX || d > INT32_MAX) return -1;
     return align256(vq::fwd_tail_bytes((int)m, (int)n, (int)d));

@@ -1,6 +1,6 @@
 // Embedding rows straight from the packed candidates: the row-select lookup of
 // a gated embedding (reference layers.py:670-750, 753-790) and the Q8_0
-// teacher's embedding (training/q8_teacher.py:142-173).
+// teacher's embedding (training/q8_teacher.py:131-173).
 //
 // Every supported format stores a weight row as row_groups consecutive
 // 256-weight groups, so row `id` of candidate k is the byte span

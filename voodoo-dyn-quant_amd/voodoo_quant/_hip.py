@@ -33,6 +33,7 @@ _SIGNATURES = [
     ("vq_embedding_rows_fwd", _i, [_i, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i, _p]),
     ("vq_embedding_rows_bwd_workspace", _i64, [_i64, _i64, _i]),
     ("vq_embedding_rows_bwd", _i, [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i, _p, _p, _i64, _p]),
+    ("vq_linear_fwd", _i, [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p]),
     ("vq_gated_linear_fwd_workspace", _i64, [_i64, _i64, _i64]),
     ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
@@ -219,6 +220,16 @@ def fwd_workspace_bytes(m: int, n: int, d: int) -> int:
     if v < 0:
         raise ValueError(f"invalid forward sizes m={m} n={n} d={d}")
     return v
+
+
+def linear_fwd(x: torch.Tensor, w: torch.Tensor, n: int, y: torch.Tensor,
+               workspace: torch.Tensor | None = None) -> None:
+    """y[m, :n] = x @ w[:n, :d]^T for a bf16 w with row stride w.shape[1]."""
+    m, d = x.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().vq_linear_fwd(_dev_ptr(x, "x"), m, n, d, _dev_ptr(w, "w"), w.shape[1], _dev_ptr(y, "y"),
+                               _dev_ptr(workspace, "workspace"), ws_bytes, _stream(x.device)),
+           "vq_linear_fwd")
 
 
 def gated_linear_fwd(x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int,

@@ -499,15 +499,17 @@ class _MixedQuantBase(nn.Module):
             raise RuntimeError(f"{self._tensor_name}: the gated layers run on ROCm devices only")
         return torch.device("cuda", torch.cuda.current_device())
 
-    def effective_bytes(self) -> torch.Tensor:
-        probs = self.soft_probs()
+    def _bytes_per_candidate(self) -> list[float]:
+        """bpw_k * N * D with the full (unsharded) dims."""
         out_eff = getattr(self, "_full_out_features", None) or self.out_features
         in_eff = getattr(self, "_full_in_features", None) or self.in_features
-        n = in_eff * out_eff
-        total = torch.tensor(0.0, device=probs.device)
-        for k, qt in enumerate(self.candidate_types):
-            total = total + probs[k] * bytes_per_weight(qt) * n
-        return total
+        return [bytes_per_weight(qt) * in_eff * out_eff for qt in self.candidate_types]
+
+    def effective_bytes(self) -> torch.Tensor:
+        """sum_k p_k * bpw_k * N * D (reference ``layers.py:1537-1550``)."""
+        probs = self.soft_probs()
+        coef = torch.tensor(self._bytes_per_candidate(), dtype=probs.dtype).to(probs.device, non_blocking=True)
+        return (probs * coef).sum()
 
     def get_assignment(self) -> str:
         return self.candidate_types[self.gates.argmax().item()]
@@ -819,8 +821,28 @@ def replace_embedding_with_mixed_quant(module: nn.Module, candidate_types: list[
     return replaced
 
 
+_BYTES_TABLES: dict[tuple, torch.Tensor] = {}
+
+
 def total_effective_bytes(replaced: dict[str, _MixedQuantBase]) -> torch.Tensor:
-    total = torch.tensor(0.0)
+    """sum over layers of effective_bytes() (reference ``layers.py:2156-2160``).
+
+    Layers with the same candidate count, device and temperature are batched:
+    one stack of their gates, one softmax and one weighted sum, instead of a
+    handful of tiny launches per layer."""
+    groups: dict[tuple, list[_MixedQuantBase]] = {}
     for layer in replaced.values():
-        total = total + layer.effective_bytes()
+        key = (layer.num_candidates, layer.gates.device, float(layer.temperature))
+        groups.setdefault(key, []).append(layer)
+    total = torch.tensor(0.0)
+    for (_, dev, temp), mods in groups.items():
+        tkey = (dev, tuple((id(m), tuple(m._bytes_per_candidate())) for m in mods))
+        coef = _BYTES_TABLES.get(tkey)
+        if coef is None:
+            if len(_BYTES_TABLES) > 64:
+                _BYTES_TABLES.clear()
+            coef = torch.tensor([m._bytes_per_candidate() for m in mods], dtype=torch.float32).to(dev)
+            _BYTES_TABLES[tkey] = coef
+        probs = F.softmax(torch.stack([m.gates for m in mods]) / temp, dim=1)
+        total = total + (probs * coef).sum()
     return total

@@ -4,15 +4,15 @@ Drop-in for the reference's ``voodoo_quant/training/q8_teacher.py``: the
 teacher keeps every Linear/Embedding weight as llama.cpp Q8_0 bytes on the
 device and decodes them when it runs.
 
-* :class:`Q8Linear` (reference ``q8_teacher.py:62-139``) is the gated Linear
+* :class:`Q8Linear` (reference ``q8_teacher.py:62-128``) is the gated Linear
   with one candidate and probability 1: ``vq_gated_linear_fwd`` writes the
   bf16 decode of the bytes (``bf16(0 + 1 * w)``, the reference's
   ``dequantize_tensor_gpu`` value) and runs the MFMA GEMM on it, then the bias
   is added as in ``F.linear``.  The reference's row-blocked path for
-  vocabulary-scale heads (``q8_teacher.py:36-58, 103-122``) exists to bound
+  vocabulary-scale heads (``q8_teacher.py:39-59, 102-120``) exists to bound
   transients on 32 GB cards; here the whole bf16 weight is one transient
   buffer (2.5 GB for 248320 x 5120, against 288 GB of HBM).
-* :class:`Q8Embedding` (``q8_teacher.py:142-173``) looks up the batch's unique
+* :class:`Q8Embedding` (``q8_teacher.py:131-173``) looks up the batch's unique
   rows with ``vq_embedding_rows_fwd`` routed to the one candidate, which gives
   ggml's values rounded to bf16 exactly as the reference's row decode.
 * :func:`wrap_q8_teacher` (``q8_teacher.py:176-294``) swaps them into a model
@@ -37,6 +37,19 @@ _Q8_0 = 8            # ggml type id
 _Q8_BLOCK = 32       # weights per block
 _Q8_BLOCK_BYTES = 34  # fp16 scale + 32 int8
 
+_KEEP_DECODED = False
+
+
+def set_keep_decoded(enabled: bool) -> None:
+    """Keep each Q8Linear's bf16 decode from one forward to the next.
+
+    Off (the default, the reference's behaviour) every forward decodes the
+    bytes and drops the result, bounding the teacher's memory to its Q8_0
+    bytes.  On, the decode is made once and every later forward is only the
+    GEMM: on a 288 GB device the decoded 0.8B-class teacher is 0.9 GB."""
+    global _KEEP_DECODED
+    _KEEP_DECODED = bool(enabled)
+
 
 def _padded_q8(qbytes: torch.Tensor, rows: int, cols: int, rows_to: int) -> tuple[torch.Tensor, int]:
     """Q8_0 bytes of [rows, cols] as [rows_pad, d_pad] with d_pad = cols rounded
@@ -58,7 +71,7 @@ def _padded_q8(qbytes: torch.Tensor, rows: int, cols: int, rows_to: int) -> tupl
 
 class Q8Linear(nn.Module):
     """nn.Linear stand-in keeping Q8_0 bytes on the device (``qweight``),
-    decoded on every forward (reference ``q8_teacher.py:62-139``)."""
+    decoded on every forward (reference ``q8_teacher.py:62-128``)."""
 
     def __init__(self, qbytes: torch.Tensor, out_features: int, in_features: int,
                  bias: torch.Tensor | None = None, device: torch.device | None = None):
@@ -84,14 +97,23 @@ class Q8Linear(nn.Module):
             self.__dict__["_pack"] = cached
         return cached[1], cached[2], cached[3]
 
+    def _decoded(self) -> torch.Tensor:
+        """bf16 [rows, d_pad] decode of the (padded) bytes, kept in ``_w``'s storage."""
+        qb, rows, d_pad = self._packed()
+        full = self.__dict__.get("_w_full")
+        if full is None or self._w is None or full.device != self.qweight.device:
+            full = _hip.dequant_bf16(_Q8_0, qb, rows, d_pad)
+            self.__dict__["_w_full"] = full
+            self._w = full[: self.out_features, : self.in_features]
+        return full
+
     def _weight(self) -> torch.Tensor:
         """bf16 [out, in] decode (the reference's dequant cache)."""
         if self.qweight.numel() == 0:
             raise RuntimeError(f"Q8Linear empty qweight: {self.out_features}x{self.in_features} "
                                "(offloaded, never reloaded)")
         if self._w is None or self._w.device != self.qweight.device:
-            qb, rows, d_pad = self._packed()
-            self._w = _hip.dequant_bf16(_Q8_0, qb, rows, d_pad)[: self.out_features, : self.in_features]
+            self._decoded()
         return self._w
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -111,23 +133,28 @@ class Q8Linear(nn.Module):
         dev = x2.device
         y = torch.empty(m, rows, dtype=torch.bfloat16, device=dev)
         if m:
-            w = torch.empty(rows, d_pad, dtype=torch.bfloat16, device=dev)
-            one = torch.ones(1, dtype=torch.float32, device=dev)
             nbytes = _hip.fwd_workspace_bytes(m, rows, self.in_features)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
-            _hip.gated_linear_fwd(x2, (_Q8_0,), [qb], one, rows, d_pad, w, y, ws)
+            if _KEEP_DECODED:
+                _hip.linear_fwd(x2, self._decoded(), rows, y, ws)
+            else:
+                w = torch.empty(rows, d_pad, dtype=torch.bfloat16, device=dev)
+                one = torch.ones(1, dtype=torch.float32, device=dev)
+                _hip.gated_linear_fwd(x2, (_Q8_0,), [qb], one, rows, d_pad, w, y, ws)
         if rows != self.out_features:
             y = y[:, : self.out_features]
         if self.bias is not None:
             y = y + self.bias.to(y.dtype)
-        self._w = None  # one-shot, as the reference's teacher forward
+        if not _KEEP_DECODED:
+            self._w = None  # one-shot, as the reference's teacher forward
+            self.__dict__["_w_full"] = None
         out = y.reshape(*lead, self.out_features)
         return out if out.dtype == x.dtype else out.to(x.dtype)
 
 
 class Q8Embedding(nn.Module):
     """nn.Embedding stand-in keeping Q8_0 bytes on the device; a forward
-    decodes only the batch's rows (reference ``q8_teacher.py:142-173``)."""
+    decodes only the batch's rows (reference ``q8_teacher.py:131-173``)."""
 
     def __init__(self, qbytes: torch.Tensor, num_embeddings: int, embedding_dim: int,
                  device: torch.device | None = None):

@@ -33,7 +33,7 @@ import torch.nn.functional as F
 from voodoo_quant import layers
 from voodoo_quant.ggml import get_quant_info
 from voodoo_quant.training import trainer
-from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear
+from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear, set_keep_decoded
 
 
 @dataclass
@@ -257,6 +257,7 @@ def build_models(cfg: DecoderConfig, types: list[str], device, seed: int = 0, pa
     replaced["model.embed_tokens"] = emb
     student = Decoder(_Body(cfg, emb, s_layers, device), _TiedHead(src))
 
+    set_keep_decoded(True)  # the teacher's weights never change: decode them once
     t_bytes = synthetic_candidate_bytes("Q8_0", v, h, device, gen)
     t_emb = Q8Embedding(t_bytes, v, h)
     teacher = Decoder(_Body(cfg, t_emb, t_layers, device), Q8Linear(t_bytes, v, h))
