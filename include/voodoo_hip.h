@@ -139,6 +139,27 @@ int vq_embedding_rows_bwd(int ncand, const int *qtypes, const void *const *qbyte
                           int64_t nids, int64_t num_embeddings, int64_t dim, int64_t d_pad, const void *grad,
                           int grad_f32, float *dprobs, void *workspace, int64_t ws_bytes, void *stream);
 
+/* Workspace bytes of the distillation loss (per-row log-sum-exps and losses;
+ * written by vq_distill_loss_fwd, read by vq_distill_loss_bwd). */
+int64_t vq_distill_loss_workspace(int64_t rows);
+
+/* out[0] = mean over rows with labels != -100 of cross-entropy(logits, labels);
+ * out[1] = mean over rows of T^2 KL(softmax(teacher / T) || softmax(logits / T)).
+ * logits, teacher_logits: device bf16 [rows][vocab], vocab % 8 == 0; labels:
+ * device int64 [rows] (a label outside [0, vocab) other than -100 gives a NaN
+ * cross-entropy).  Sums run in fp64 in a fixed order.  Replaces the
+ * full-logits losses of the trainer (voodoo_quant/training/trainer.py:2566-2575:
+ * F.cross_entropy, F.log_softmax, F.softmax, F.kl_div ... .sum(-1) * T^2, .mean()). */
+int vq_distill_loss_fwd(const uint16_t *logits, const uint16_t *teacher_logits, const int64_t *labels, int64_t rows,
+                        int64_t vocab, float temperature, float *out, void *workspace, int64_t ws_bytes, void *stream);
+
+/* grad_logits (bf16 [rows][vocab]) = grad_out[0] d out[0] / d logits + grad_out[1] d out[1] / d logits,
+ * with grad_out a device fp32 [2] and the forward's workspace.  Replaces the
+ * autograd backward of those losses. */
+int vq_distill_loss_bwd(const uint16_t *logits, const uint16_t *teacher_logits, const int64_t *labels, int64_t rows,
+                        int64_t vocab, float temperature, const float *grad_out, uint16_t *grad_logits,
+                        const void *workspace, int64_t ws_bytes, void *stream);
+
 /* Workspace bytes vq_gated_linear_bwd needs (gate partials; plus the W_eff
  * buffer when it will be called with w_eff == NULL and dx != NULL). */
 int64_t vq_gated_linear_bwd_workspace(int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff);

@@ -270,6 +270,55 @@ int vq_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, const uint
     return rc == VQ_OK ? ok() : rc;
 }
 
+int64_t vq_distill_loss_workspace(int64_t rows) {
+    if (rows < 0) return -1;
+    return align256((5 * rows + 2) * (int64_t)sizeof(float));
+}
+
+namespace {
+int check_distill(const uint16_t* logits, const uint16_t* teacher_logits, const int64_t* labels, int64_t rows,
+                  int64_t vocab, float temperature, const void* ws, int64_t ws_bytes) {
+    if (rows <= 0 || vocab <= 0 || rows > INT32_MAX)
+        return fail(VQ_ERR_SHAPE, "rows=%lld vocab=%lld", (long long)rows, (long long)vocab);
+    if (vocab % 8) return fail(VQ_ERR_ALIGN, "vocab=%lld must be a multiple of 8", (long long)vocab);
+    if (!(temperature > 0.0f)) return fail(VQ_ERR_SHAPE, "temperature must be positive");
+    if (!logits || !teacher_logits || !labels) return fail(VQ_ERR_NULL, "logits/teacher_logits/labels is NULL");
+    if (!aligned16(logits) || !aligned16(teacher_logits)) return fail(VQ_ERR_ALIGN, "logits not 16-byte aligned");
+    if (!ws || ws_bytes < (5 * rows + 2) * (int64_t)sizeof(float))
+        return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes needed", (long long)((5 * rows + 2) * 4));
+    return VQ_OK;
+}
+}  // namespace
+
+int vq_distill_loss_fwd(const uint16_t* logits, const uint16_t* teacher_logits, const int64_t* labels, int64_t rows,
+                        int64_t vocab, float temperature, float* out, void* workspace, int64_t ws_bytes,
+                        void* stream) {
+    int rc = check_distill(logits, teacher_logits, labels, rows, vocab, temperature, workspace, ws_bytes);
+    if (rc != VQ_OK) return rc;
+    if (!out) return fail(VQ_ERR_NULL, "out is NULL");
+    rc = hip_check(vq::launch_distill_fwd(reinterpret_cast<const vq::bf16_t*>(logits),
+                                          reinterpret_cast<const vq::bf16_t*>(teacher_logits), labels, rows, vocab,
+                                          temperature, out, static_cast<float*>(workspace),
+                                          static_cast<hipStream_t>(stream)),
+                   "distillation loss launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_distill_loss_bwd(const uint16_t* logits, const uint16_t* teacher_logits, const int64_t* labels, int64_t rows,
+                        int64_t vocab, float temperature, const float* grad_out, uint16_t* grad_logits,
+                        const void* workspace, int64_t ws_bytes, void* stream) {
+    int rc = check_distill(logits, teacher_logits, labels, rows, vocab, temperature, workspace, ws_bytes);
+    if (rc != VQ_OK) return rc;
+    if (!grad_out || !grad_logits) return fail(VQ_ERR_NULL, "grad_out/grad_logits is NULL");
+    if (!aligned16(grad_logits)) return fail(VQ_ERR_ALIGN, "grad_logits not 16-byte aligned");
+    rc = hip_check(vq::launch_distill_bwd(reinterpret_cast<const vq::bf16_t*>(logits),
+                                          reinterpret_cast<const vq::bf16_t*>(teacher_logits), labels, rows, vocab,
+                                          temperature, grad_out, reinterpret_cast<vq::bf16_t*>(grad_logits),
+                                          static_cast<const float*>(workspace), static_cast<hipStream_t>(stream)),
+                   "distillation loss backward launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int64_t vq_gated_linear_fwd_workspace(int64_t m, int64_t n, int64_t d) {
     if (m < 0 || n <= 0 || d <= 0 || m > INT32_MAX || n > INT32_MAX || d > INT32_MAX) return -1;
     return align256(vq::fwd_tail_bytes((int)m, (int)n, (int)d));

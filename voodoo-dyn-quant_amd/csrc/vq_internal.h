@@ -59,4 +59,12 @@ hipError_t launch_embed_rows(const CandSet& cs, const float* probs, const int64_
 hipError_t launch_embed_rows_bwd(const CandSet& cs, const int64_t* ids, int64_t nids, int64_t vocab, int64_t dim,
                                  const void* grad, bool grad_f32, float* partials, float* dprobs, hipStream_t s);
 
+// Distillation loss over full logits (vq_loss.hip).  ws: 5 * rows + 2 floats
+// (per-row log-sum-exps and losses, then 1/N_ce and 1/N), written by the
+// forward and read by the backward.
+hipError_t launch_distill_fwd(const bf16_t* S, const bf16_t* T, const int64_t* labels, int64_t rows, int64_t V,
+                              float temperature, float* out, float* ws, hipStream_t s);
+hipError_t launch_distill_bwd(const bf16_t* S, const bf16_t* T, const int64_t* labels, int64_t rows, int64_t V,
+                              float temperature, const float* grad_out, bf16_t* dS, const float* ws, hipStream_t s);
+
 }  // namespace vq

@@ -34,6 +34,9 @@ _SIGNATURES = [
     ("vq_embedding_rows_bwd_workspace", _i64, [_i64, _i64, _i]),
     ("vq_embedding_rows_bwd", _i, [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i, _p, _p, _i64, _p]),
     ("vq_linear_fwd", _i, [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p]),
+    ("vq_distill_loss_workspace", _i64, [_i64]),
+    ("vq_distill_loss_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _i64, _p]),
+    ("vq_distill_loss_bwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_fwd_workspace", _i64, [_i64, _i64, _i64]),
     ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
@@ -230,6 +233,37 @@ def linear_fwd(x: torch.Tensor, w: torch.Tensor, n: int, y: torch.Tensor,
     _check(lib().vq_linear_fwd(_dev_ptr(x, "x"), m, n, d, _dev_ptr(w, "w"), w.shape[1], _dev_ptr(y, "y"),
                                _dev_ptr(workspace, "workspace"), ws_bytes, _stream(x.device)),
            "vq_linear_fwd")
+
+
+def distill_loss_fwd(logits: torch.Tensor, teacher_logits: torch.Tensor, labels: torch.Tensor,
+                     temperature: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(out fp32 [2] = (CE mean, KL mean), workspace for the backward)."""
+    rows, vocab = logits.shape
+    if logits.dtype != torch.bfloat16 or teacher_logits.dtype != torch.bfloat16:
+        raise ValueError("logits must be bf16")
+    if tuple(teacher_logits.shape) != (rows, vocab) or labels.numel() != rows or labels.dtype != torch.int64:
+        raise ValueError("teacher_logits [rows, vocab] bf16 and labels [rows] int64 expected")
+    dev = logits.device
+    ws = torch.empty(max(int(lib().vq_distill_loss_workspace(rows)), 1), dtype=torch.uint8, device=dev)
+    out = torch.empty(2, dtype=torch.float32, device=dev)
+    _check(lib().vq_distill_loss_fwd(_dev_ptr(logits, "logits"), _dev_ptr(teacher_logits, "teacher_logits"),
+                                     _dev_ptr(labels, "labels"), rows, vocab, float(temperature), _dev_ptr(out, "out"),
+                                     _dev_ptr(ws, "workspace"), ws.numel(), _stream(dev)),
+           "vq_distill_loss_fwd")
+    return out, ws
+
+
+def distill_loss_bwd(logits: torch.Tensor, teacher_logits: torch.Tensor, labels: torch.Tensor, temperature: float,
+                     grad_out: torch.Tensor, ws: torch.Tensor) -> torch.Tensor:
+    rows, vocab = logits.shape
+    dev = logits.device
+    g = torch.empty_like(logits)
+    _check(lib().vq_distill_loss_bwd(_dev_ptr(logits, "logits"), _dev_ptr(teacher_logits, "teacher_logits"),
+                                     _dev_ptr(labels, "labels"), rows, vocab, float(temperature),
+                                     _dev_ptr(grad_out, "grad_out"), _dev_ptr(g, "grad_logits"),
+                                     _dev_ptr(ws, "workspace"), ws.numel(), _stream(dev)),
+           "vq_distill_loss_bwd")
+    return g
 
 
 def gated_linear_fwd(x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int,

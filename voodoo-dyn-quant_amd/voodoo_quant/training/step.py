@@ -277,6 +277,7 @@ class StepConfig:
     size_tolerance: float = 0.02
     target_fraction: float = 0.45   # of 8-bit bytes
     logits_chunk: int = 0
+    fused_loss: bool = True         # CE + KL on the HIP kernels (full-logits path)
 
 
 class GateTrainer:
@@ -305,7 +306,9 @@ class GateTrainer:
             logits = self.student(x)
             with torch.no_grad():
                 t_logits = self.teacher(x)
-            lm_loss, distill = trainer.distill_losses(logits, t_logits, y, t)
+            fused = c.fused_loss and logits.is_cuda and logits.dtype == torch.bfloat16 and logits.size(-1) % 8 == 0
+            losses = trainer.distill_losses_fused if fused else trainer.distill_losses
+            lm_loss, distill = losses(logits, t_logits, y, t)
         current = layers.total_effective_bytes(self.replaced).to(dev) + self.non_targeted_bytes
         size = trainer.size_loss(current, self.target_bytes, c.size_tolerance)
         if c.logits_chunk > 0:

@@ -85,6 +85,43 @@ def distill_losses(logits: torch.Tensor, teacher_logits: torch.Tensor, y: torch.
     return lm_loss, per_token_kl.mean()
 
 
+class DistillLossFunction(torch.autograd.Function):
+    """(CE, KL) of :func:`distill_losses` as one HIP pass over the logits and
+    one for the gradient (``vq_distill_loss_fwd/bwd``).
+
+    forward(ctx, logits [T, V] bf16, teacher_logits [T, V] bf16, labels [T]
+    int64, temperature) -> fp32 [2] = (CE mean, KL mean); the backward gives
+    the gradient of the logits only (the teacher runs without gradients)."""
+
+    @staticmethod
+    def forward(ctx, logits, teacher_logits, labels, temperature):
+        from voodoo_quant import _hip
+
+        out, ws = _hip.distill_loss_fwd(logits, teacher_logits, labels, temperature)
+        ctx.save_for_backward(logits, teacher_logits, labels, ws)
+        ctx.temperature = temperature
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        from voodoo_quant import _hip
+
+        logits, teacher_logits, labels, ws = ctx.saved_tensors
+        g = _hip.distill_loss_bwd(logits, teacher_logits, labels, ctx.temperature,
+                                  grad_out.to(torch.float32).contiguous(), ws)
+        return g, None, None, None
+
+
+def distill_losses_fused(logits: torch.Tensor, teacher_logits: torch.Tensor, y: torch.Tensor, temperature: float):
+    """:func:`distill_losses` on the GPU kernels: bf16 logits, vocabulary a
+    multiple of 8.  The exponentials and sums run in fp32 (the per-token sums
+    of the reference's bf16 tensors run in bf16) and the means in fp64."""
+    v = logits.size(-1)
+    out = DistillLossFunction.apply(logits.reshape(-1, v).contiguous(), teacher_logits.reshape(-1, v).contiguous(),
+                                    y.reshape(-1).to(torch.int64).contiguous(), float(temperature))
+    return out[0], out[1]
+
+
 def _hidden(out) -> torch.Tensor:
     return out.last_hidden_state if hasattr(out, "last_hidden_state") else out
 
