@@ -139,6 +139,35 @@ int vq_embedding_rows_bwd(int ncand, const int *qtypes, const void *const *qbyte
                           int64_t nids, int64_t num_embeddings, int64_t dim, int64_t d_pad, const void *grad,
                           int grad_f32, float *dprobs, void *workspace, int64_t ws_bytes, void *stream);
 
+/* Gated tensors that read the same input (q/k/v, gate/up), stacked along N:
+ * member i has n[i] rows (a multiple of 256 when nmembers > 1), ncand[i]
+ * candidates whose types and byte pointers follow the previous members' in
+ * qtypes/qbytes, and probs[i] (device fp32 [ncand[i]]).  Mixes every member
+ * into its rows of w_eff ([sum n][d_pad] bf16) and runs ONE GEMM:
+ * y[m][sum n] = x . w_eff^T (member i's outputs are columns
+ * [n[0] + ... + n[i-1], ... + n[i]) of y).  1 <= nmembers <= 4.  Replaces the
+ * separate forwards of MixedQuantLinear (voodoo_quant/layers.py:1729-1731)
+ * for projections of one input; no counterpart entry in the reference. */
+int vq_gated_linear_group_fwd(const uint16_t *x, int64_t m, int64_t d, int64_t d_pad, int nmembers, const int64_t *n,
+                              const int *ncand, const int *qtypes, const void *const *qbytes,
+                              const float *const *probs, uint16_t *w_eff, uint16_t *y, void *workspace,
+                              int64_t ws_bytes, void *stream);
+
+/* Workspace bytes of vq_gated_linear_group_bwd (gate partials of every member
+ * and dX's split tail tiles). */
+int64_t vq_gated_linear_group_bwd_workspace(int64_t m, int64_t d, int nmembers, const int64_t *n, const int *ncand);
+
+/* Backward of the stacked group: dx = dy . w_eff (one GEMM over the stacked
+ * rows, which also sums the members' input gradients) and, for each member,
+ * dprobs[i][k] = <dy_i^T x, W_ik> (device fp32 [ncand[i]]), all in one
+ * launch.  dy: [m][sum n] bf16; w_eff: the forward's.  dprobs may be NULL
+ * (no gate gradients), dx may be NULL.  Replaces the members' F.linear
+ * backwards and _MixedWeightFunction.backward (voodoo_quant/layers.py:354-363). */
+int vq_gated_linear_group_bwd(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t d, int64_t d_pad, int nmembers,
+                              const int64_t *n, const int *ncand, const int *qtypes, const void *const *qbytes,
+                              const uint16_t *w_eff, uint16_t *dx, float *const *dprobs, void *workspace,
+                              int64_t ws_bytes, void *stream);
+
 /* Workspace bytes of the distillation loss (per-row log-sum-exps and losses;
  * written by vq_distill_loss_fwd, read by vq_distill_loss_bwd). */
 int64_t vq_distill_loss_workspace(int64_t rows);

@@ -96,6 +96,44 @@ vq::CandSet make_set(int ncand, const int* qtypes, const void* const* qbytes, in
 
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
+// One gated tensor as a group of one.
+vq::CandGroup group_of(const vq::CandSet& cs, int64_t n) {
+    vq::CandGroup g{};
+    g.nsets = 1;
+    g.kstride = cs.ncand;
+    g.set_j0[0] = 0;
+    g.set_j0[1] = (int)n;
+    g.sets[0] = cs;
+    return g;
+}
+
+// Checks of a stacked group of gated tensors sharing one input; fills cg and
+// the total row count.
+int check_group(int nmembers, const int64_t* n, const int* ncand, const int* qtypes, const void* const* qbytes,
+                int64_t d, int64_t d_pad, vq::CandGroup& cg, int64_t& n_total) {
+    if (nmembers < 1 || nmembers > vq::kMaxSets)
+        return fail(VQ_ERR_SHAPE, "nmembers=%d outside [1, %d]", nmembers, vq::kMaxSets);
+    if (!n || !ncand || !qtypes || !qbytes) return fail(VQ_ERR_NULL, "n/ncand/qtypes/qbytes is NULL");
+    cg = vq::CandGroup{};
+    cg.nsets = nmembers;
+    n_total = 0;
+    int off = 0;
+    for (int i = 0; i < nmembers; ++i) {
+        int rc = check_candidates(ncand[i], qtypes + off, qbytes + off, n[i], d, d_pad, true);
+        if (rc != VQ_OK) return rc;
+        if (nmembers > 1 && n[i] % 256 != 0)
+            return fail(VQ_ERR_ALIGN, "member %d: n=%lld must be a multiple of 256 in a group", i, (long long)n[i]);
+        cg.sets[i] = make_set(ncand[i], qtypes + off, qbytes + off, d_pad);
+        cg.set_j0[i] = (int)n_total;
+        cg.kstride = ncand[i] > cg.kstride ? ncand[i] : cg.kstride;
+        n_total += n[i];
+        off += ncand[i];
+    }
+    if (n_total > (1 << 21)) return fail(VQ_ERR_SHAPE, "stacked n=%lld exceeds 2^21", (long long)n_total);
+    cg.set_j0[nmembers] = (int)n_total;
+    return VQ_OK;
+}
+
 // Shared checks of the embedding-row entry points.
 int check_embed(int ncand, const int* qtypes, const void* const* qbytes, const int64_t* ids, int64_t nids,
                 int64_t vocab, int64_t dim, int64_t d_pad) {
@@ -393,8 +431,8 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
         }
         if (m > 0 && dprobs) {
             // both products in one launch: each fills the other's last round
-            rc = hip_check(vq::launch_gemm_dx_gate(dy, w, d_pad, dx, x, cs, partials, (int)m, (int)n, (int)d,
-                                                   tail_ws, s),
+            rc = hip_check(vq::launch_gemm_dx_gate(dy, w, d_pad, dx, x, group_of(cs, n), partials, (int)m, (int)n,
+                                                   (int)d, tail_ws, s),
                            "dX + gate GEMM launch");
             if (rc != VQ_OK) return rc;
         } else if (m > 0) {
@@ -404,13 +442,122 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
         }
     }
     if (dprobs) {
+        if (m == 0) {
+            // no tokens: dL/dp = 0 (written by the reduce over zero partials)
+            rc = hip_check(vq::launch_gate_reduce(partials, 0, ncand, dprobs, s), "gate reduce launch");
+            return rc == VQ_OK ? ok() : rc;
+        }
         if (!dx) {
-            rc = hip_check(vq::launch_gemm_gate(dy, x, cs, partials, (int)m, (int)n, (int)d, s), "gate GEMM launch");
+            rc = hip_check(vq::launch_gemm_gate(dy, x, group_of(cs, n), partials, (int)m, (int)n, (int)d, s),
+                           "gate GEMM launch");
             if (rc != VQ_OK) return rc;
         }
         rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, s),
                        "gate reduce launch");
         if (rc != VQ_OK) return rc;
+    }
+    return ok();
+}
+
+int vq_gated_linear_group_fwd(const uint16_t* x, int64_t m, int64_t d, int64_t d_pad, int nmembers, const int64_t* n,
+                              const int* ncand, const int* qtypes, const void* const* qbytes,
+                              const float* const* probs, uint16_t* w_eff, uint16_t* y, void* workspace,
+                              int64_t ws_bytes, void* stream) {
+    vq::CandGroup cg;
+    int64_t n_total = 0;
+    int rc = check_group(nmembers, n, ncand, qtypes, qbytes, d, d_pad, cg, n_total);
+    if (rc != VQ_OK) return rc;
+    if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
+    if (!x || !probs || !w_eff || !y) return fail(VQ_ERR_NULL, "x/probs/w_eff/y is NULL");
+    if (!aligned16(x) || !aligned16(w_eff) || !aligned16(y))
+        return fail(VQ_ERR_ALIGN, "x/w_eff/y not 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < nmembers; ++i) {
+        if (!probs[i]) return fail(VQ_ERR_NULL, "probs[%d] is NULL", i);
+        rc = hip_check(vq::launch_mix(cg.sets[i], probs[i], w_eff + (int64_t)cg.set_j0[i] * d_pad, n[i] * d_pad / 256,
+                                      s),
+                       "mix launch");
+        if (rc != VQ_OK) return rc;
+    }
+    if (m == 0) return ok();
+    if (workspace && !aligned16(workspace)) return fail(VQ_ERR_ALIGN, "workspace not 16-byte aligned");
+    const int64_t tail_bytes = vq::fwd_tail_bytes((int)m, (int)n_total, (int)d);
+    float* tail_ws = workspace && tail_bytes > 0 && ws_bytes >= tail_bytes ? static_cast<float*>(workspace) : nullptr;
+    rc = hip_check(vq::launch_gemm_fwd(x, w_eff, d_pad, y, (int)m, (int)n_total, (int)d, tail_ws, s),
+                   "forward GEMM launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int64_t vq_gated_linear_group_bwd_workspace(int64_t m, int64_t d, int nmembers, const int64_t* n, const int* ncand) {
+    if (m < 0 || d <= 0 || m > INT32_MAX || d > INT32_MAX || nmembers < 1 || nmembers > vq::kMaxSets || !n || !ncand)
+        return -1;
+    int64_t n_total = 0;
+    int kstride = 0;
+    for (int i = 0; i < nmembers; ++i) {
+        if (n[i] <= 0 || ncand[i] < 1 || ncand[i] > vq::kMaxCand) return -1;
+        n_total += n[i];
+        kstride = ncand[i] > kstride ? ncand[i] : kstride;
+    }
+    if (n_total > INT32_MAX) return -1;
+    int64_t bytes =
+        align256(vq::gate_partial_count((int)m, (int)n_total, (int)d) * nmembers * kstride * (int64_t)sizeof(float));
+    bytes += align256(vq::dx_tail_bytes((int)m, (int)n_total, (int)d));
+    return bytes;
+}
+
+int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t d, int64_t d_pad, int nmembers,
+                              const int64_t* n, const int* ncand, const int* qtypes, const void* const* qbytes,
+                              const uint16_t* w_eff, uint16_t* dx, float* const* dprobs, void* workspace,
+                              int64_t ws_bytes, void* stream) {
+    vq::CandGroup cg;
+    int64_t n_total = 0;
+    int rc = check_group(nmembers, n, ncand, qtypes, qbytes, d, d_pad, cg, n_total);
+    if (rc != VQ_OK) return rc;
+    if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
+    if (!dy || !x) return fail(VQ_ERR_NULL, "dy/x is NULL");
+    if (!aligned16(dy) || !aligned16(x)) return fail(VQ_ERR_ALIGN, "dy/x not 16-byte aligned");
+    if (dx && (!w_eff || !aligned16(dx) || !aligned16(w_eff)))
+        return fail(w_eff ? VQ_ERR_ALIGN : VQ_ERR_NULL, "dx needs the forward's 16-byte aligned w_eff");
+    if (dprobs)
+        for (int i = 0; i < nmembers; ++i)
+            if (!dprobs[i]) return fail(VQ_ERR_NULL, "dprobs[%d] is NULL", i);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t need = vq_gated_linear_group_bwd_workspace(m, d, nmembers, n, ncand);
+    const int64_t nparts = vq::gate_partial_count((int)m, (int)n_total, (int)d);
+    const int nslot = nmembers * cg.kstride;
+    const int64_t part_bytes = align256(nparts * nslot * (int64_t)sizeof(float));
+    if (dprobs && (!workspace || ws_bytes < need))
+        return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
+                    (long long)(workspace ? ws_bytes : 0));
+    if (workspace && !aligned16(workspace)) return fail(VQ_ERR_ALIGN, "workspace not 16-byte aligned");
+    float* partials = static_cast<float*>(workspace);
+    const int64_t tail_bytes = align256(vq::dx_tail_bytes((int)m, (int)n_total, (int)d));
+    float* tail_ws = nullptr;
+    if (workspace && tail_bytes > 0 && ws_bytes >= part_bytes + tail_bytes)
+        tail_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
+    if (dx && m > 0) {
+        if (dprobs)
+            rc = hip_check(vq::launch_gemm_dx_gate(dy, w_eff, d_pad, dx, x, cg, partials, (int)m, (int)n_total, (int)d,
+                                                   tail_ws, s),
+                           "dX + gate GEMM launch");
+        else
+            rc = hip_check(vq::launch_gemm_dx(dy, w_eff, d_pad, dx, (int)m, (int)n_total, (int)d, tail_ws, s),
+                           "dX GEMM launch");
+        if (rc != VQ_OK) return rc;
+    }
+    if (dprobs) {
+        if (!dx && m > 0) {
+            rc = hip_check(vq::launch_gemm_gate(dy, x, cg, partials, (int)m, (int)n_total, (int)d, s),
+                           "gate GEMM launch");
+            if (rc != VQ_OK) return rc;
+        }
+        for (int i = 0; i < nmembers; ++i) {
+            // no tokens: a reduce over zero partials writes dL/dp = 0
+            rc = hip_check(vq::launch_gate_reduce_strided(partials + i * cg.kstride, m > 0 ? nparts : 0, nslot,
+                                                          ncand[i], dprobs[i], s),
+                           "gate reduce launch");
+            if (rc != VQ_OK) return rc;
+        }
     }
     return ok();
 }

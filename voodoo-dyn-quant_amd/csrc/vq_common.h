@@ -437,4 +437,16 @@ struct CandSet {
     int64_t row_groups;  // D_pad / 256
 };
 
+// Gated tensors that share one input, stacked along N: set g owns rows
+// [set_j0[g], set_j0[g + 1]) of the stacked weight (boundaries on 256-row
+// tiles).  Gate partials are [grid block][nsets * kstride], set g's candidate
+// k at g * kstride + k.
+constexpr int kMaxSets = 4;
+struct CandGroup {
+    int nsets;
+    int kstride;
+    int set_j0[kMaxSets + 1];
+    CandSet sets[kMaxSets];
+};
+
 }  // namespace vq

@@ -47,18 +47,18 @@ static GemmParams dx_params(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16
     return p;
 }
 
-static GemmParams gate_params(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
+static GemmParams gate_params(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
                               int D) {
     GemmParams p{};
     p.A = X; p.lda = D; p.B = dY; p.ldb = N; p.I = D; p.J = N; p.K = M;
-    p.cs = cs; p.dlimit = D; p.partials = partials;
+    p.cg = cg; p.dlimit = D; p.partials = partials;
     return p;
 }
 
 // One partial per gate grid block (split tail parts and idle padding blocks
 // included; the latter write zeros).
 int64_t gate_partial_count(int M, int N, int D) {
-    GemmParams p = gate_params(nullptr, nullptr, CandSet{}, nullptr, M, N, D);
+    GemmParams p = gate_params(nullptr, nullptr, CandGroup{}, nullptr, M, N, D);
     return GateCfg::plan(p, device_cus(), true);
 }
 
@@ -86,18 +86,18 @@ hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t
     return launch_gemm_cfg<DxCfg>(dx_params(dY, W, ldw, dX, M, N, D), device_cus(), tail_ws, s);
 }
 
-hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
+hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
                             int D, hipStream_t s) {
-    return launch_gemm_cfg<GateCfg>(gate_params(dY, X, cs, partials, M, N, D), device_cus(), nullptr, s);
+    return launch_gemm_cfg<GateCfg>(gate_params(dY, X, cg, partials, M, N, D), device_cus(), nullptr, s);
 }
 
 // dX and gate products of one backward in a single launch (dX work items,
 // the longer ones, first).
 hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
-                               const CandSet& cs, float* partials, int M, int N, int D, float* tail_ws,
+                               const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
                                hipStream_t s) {
     return launch_gemm_dual<DxCfg, GateCfg>(dx_params(dY, W, ldw, dX, M, N, D),
-                                            gate_params(dY, X, cs, partials, M, N, D), device_cus(), tail_ws, s);
+                                            gate_params(dY, X, cg, partials, M, N, D), device_cus(), tail_ws, s);
 }
 
 // PTQR forward: token rows grouped by candidate, each group multiplied by its
@@ -116,13 +116,13 @@ hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const*
     return launch_routed_gemm<RoutedCfg>(p, M, device_cus(), s);
 }
 
-// Fixed-order fp64 sum of the work-item partials: dprobs[k] = sum_t partials[t][k].
+// Fixed-order fp64 sum of the work-item partials: dprobs[k] = sum_t partials[t * stride + k].
 __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ partials, int64_t ntiles,
-                                                          int ncand, float* __restrict__ dprobs) {
+                                                          int stride, float* __restrict__ dprobs) {
     __shared__ double sh[256];
     const int k = blockIdx.x;
     double s = 0.0;
-    for (int64_t t = threadIdx.x; t < ntiles; t += 256) s += (double)partials[t * ncand + k];
+    for (int64_t t = threadIdx.x; t < ntiles; t += 256) s += (double)partials[t * stride + k];
     sh[threadIdx.x] = s;
     __syncthreads();
     for (int w = 128; w >= 1; w >>= 1) {
@@ -133,7 +133,12 @@ __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restric
 }
 
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s) {
-    gate_reduce_kernel<<<dim3(ncand), dim3(256), 0, s>>>(partials, ntiles, ncand, dprobs);
+    return launch_gate_reduce_strided(partials, ntiles, ncand, ncand, dprobs, s);
+}
+
+hipError_t launch_gate_reduce_strided(const float* partials, int64_t ntiles, int stride, int ncand, float* dprobs,
+                                      hipStream_t s) {
+    gate_reduce_kernel<<<dim3(ncand), dim3(256), 0, s>>>(partials, ntiles, stride, dprobs);
     return hipGetLastError();
 }
 

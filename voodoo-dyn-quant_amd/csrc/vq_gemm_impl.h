@@ -434,9 +434,9 @@ struct GemmParams {
     int split_ok;
     int tail_max, s_max;
     // gate epilogue: i indexes d (< dlimit), j indexes n; candidates are rows n
-    CandSet cs;
+    CandGroup cg;
     int dlimit;
-    // gate epilogue: [grid blocks][ncand] partial sums; store epilogue with
+    // gate epilogue: [grid blocks][nsets * kstride] partial sums; store epilogue with
     // split tails: [8 * tail_max][s_max][BI * BJ] fp32 partial tiles
     float* partials;
     // routed product: A rows gathered and C rows scattered through rowmap;
@@ -822,7 +822,15 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scale fields index by it
     const int wi = wave / WJ, wj = wave % WJ;
     const int group = i0 / 256;
-    const int64_t rg = p.cs.row_groups;
+    // the gated tensor this tile's rows belong to (uniform per block)
+    int g = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxSets; ++q)
+        if (q < p.cg.nsets && j0 >= p.cg.set_j0[q]) g = q;
+    const CandSet& cs = p.cg.sets[g];
+    const int jl0 = j0 - p.cg.set_j0[g];                 // first row within the tensor
+    const int jn = p.cg.set_j0[g + 1] - p.cg.set_j0[g];  // the tensor's rows
+    const int64_t rg = cs.row_groups;
     // candidate-independent half sums of each accumulator block
     float sv[S::MI][S::NJ][2];
 #pragma unroll
@@ -837,34 +845,38 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
                 sv[a][b][hf] = t;
             }
     __syncthreads();  // every wave is past its last main-loop LDS read
-    gate_stage_regs<BJ, S::THREADS>(smem, p.cs.qbytes[0], p.cs.qtype[0], rg, j0, group, p.J);
-    for (int k = 0; k < p.cs.ncand; ++k) {
+    gate_stage_regs<BJ, S::THREADS>(smem, cs.qbytes[0], cs.qtype[0], rg, jl0, group, jn);
+    for (int k = 0; k < cs.ncand; ++k) {
         // this wave's direct-to-LDS copies of candidate k have landed, then
         // everyone's have; buffer (k+1) % 2 is no longer read
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __syncthreads();
-        if (k + 1 < p.cs.ncand)
-            gate_stage_lds<BJ, S::THREADS>(smem + ((k + 1) & 1) * BUF_CH, p.cs.qbytes[k + 1], p.cs.qtype[k + 1], rg, j0,
-                                           group, p.J);
+        if (k + 1 < cs.ncand)
+            gate_stage_lds<BJ, S::THREADS>(smem + ((k + 1) & 1) * BUF_CH, cs.qbytes[k + 1], cs.qtype[k + 1], rg, jl0,
+                                           group, jn);
         const uint8_t* buf = reinterpret_cast<const uint8_t*>(smem + (k & 1) * BUF_CH);
         float sum;
-        switch (p.cs.qtype[k]) {
-        case Q8_0: sum = gate_dot_lds<Q8_0, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q2_K: sum = gate_dot_lds<Q2_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
-        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, j0, group, wi, wj, lane, p.J); break;
+        switch (cs.qtype[k]) {
+        case Q8_0: sum = gate_dot_lds<Q8_0, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
+        case Q2_K: sum = gate_dot_lds<Q2_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
+        case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
+        case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
+        case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
+        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
         if (lane == 0) red[wave][k] = sum;
     }
     __syncthreads();
-    if ((int)threadIdx.x < p.cs.ncand) {
+    // this block's slots of every tensor: its own sums, zeros for the others
+    const int nslot = p.cg.nsets * p.cg.kstride;
+    if ((int)threadIdx.x < nslot) {
+        const int k = (int)threadIdx.x - g * p.cg.kstride;
         float s = 0.0f;
-        for (int wv = 0; wv < NW; ++wv) s += red[wv][threadIdx.x];
-        p.partials[(int64_t)block * p.cs.ncand + threadIdx.x] = s;
+        if (k >= 0 && k < cs.ncand)
+            for (int wv = 0; wv < NW; ++wv) s += red[wv][k];
+        p.partials[(int64_t)block * nslot + threadIdx.x] = s;
     }
 }
 
@@ -963,8 +975,10 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
     const int ksteps = (p.K + BK - 1) / BK;
     const WorkItem w = map_work(block, tiles_i, tiles_j, ksteps, p.cus_per_xcd, p.split_ok != 0, p.tail_max, 8);
     if (w.idle) {
-        if constexpr (EPI == EPI_GATE)
-            if ((int)threadIdx.x < p.cs.ncand) p.partials[(int64_t)block * p.cs.ncand + threadIdx.x] = 0.0f;
+        if constexpr (EPI == EPI_GATE) {
+            const int nslot = p.cg.nsets * p.cg.kstride;
+            if ((int)threadIdx.x < nslot) p.partials[(int64_t)block * nslot + threadIdx.x] = 0.0f;
+        }
         return;
     }
     const int i0 = w.tm * BI, j0 = w.tn * BJ;

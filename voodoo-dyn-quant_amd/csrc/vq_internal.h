@@ -33,15 +33,18 @@ hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t
 int device_cus();
 int64_t gate_partial_count(int M, int N, int D);  // gate partials per candidate (one per grid block)
 int64_t dx_tail_bytes(int M, int N, int D);       // dX split-tail workspace bytes
-hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandSet& cs, float* partials, int M, int N,
+hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
                             int D, hipStream_t s);
 hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
-                               const CandSet& cs, float* partials, int M, int N, int D, float* tail_ws,
+                               const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
                                hipStream_t s);
 // PTQR: Y[perm[r]] = X[perm[r]] . W_g^T for r in [group_off[g], group_off[g+1])
 hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const* cand_bf16, int64_t ldw, int N,
                              int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s);
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
+// dprobs[k] = sum_t partials[t * stride + k], k < ncand
+hipError_t launch_gate_reduce_strided(const float* partials, int64_t ntiles, int stride, int ncand, float* dprobs,
+                                      hipStream_t s);
 
 // Embedding rows (vq_embed.hip): one workgroup per (requested row, segment of
 // at most kGroupsPerBlock groups); gused = groups covering dim.

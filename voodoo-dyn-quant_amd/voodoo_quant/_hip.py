@@ -34,6 +34,9 @@ _SIGNATURES = [
     ("vq_embedding_rows_bwd_workspace", _i64, [_i64, _i64, _i]),
     ("vq_embedding_rows_bwd", _i, [_i, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _i, _p, _p, _i64, _p]),
     ("vq_linear_fwd", _i, [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p]),
+    ("vq_gated_linear_group_fwd", _i, [_p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    ("vq_gated_linear_group_bwd_workspace", _i64, [_i64, _i64, _i, _p, _p]),
+    ("vq_gated_linear_group_bwd", _i, [_p, _p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_distill_loss_workspace", _i64, [_i64]),
     ("vq_distill_loss_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _i64, _p]),
     ("vq_distill_loss_bwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _i64, _p]),
@@ -233,6 +236,51 @@ def linear_fwd(x: torch.Tensor, w: torch.Tensor, n: int, y: torch.Tensor,
     _check(lib().vq_linear_fwd(_dev_ptr(x, "x"), m, n, d, _dev_ptr(w, "w"), w.shape[1], _dev_ptr(y, "y"),
                                _dev_ptr(workspace, "workspace"), ws_bytes, _stream(x.device)),
            "vq_linear_fwd")
+
+
+def _group_arrays(members):
+    """members: [(ggml_types, qbytes, n)] -> ctypes arrays (n, ncand, qtypes, qbytes)."""
+    ns = (ctypes.c_int64 * len(members))(*[int(mb[2]) for mb in members])
+    nc = (ctypes.c_int * len(members))(*[len(mb[0]) for mb in members])
+    types = [t for mb in members for t in mb[0]]
+    qbs = [q for mb in members for q in mb[1]]
+    return ns, nc, _int_array(types), _ptr_array(qbs, "qbytes")
+
+
+def gated_linear_group_fwd(x: torch.Tensor, members, probs, d_pad: int, w_eff: torch.Tensor, y: torch.Tensor,
+                           workspace: torch.Tensor | None = None) -> None:
+    """members: [(ggml_types, qbytes, n)]; probs: fp32 [K_i] per member.
+    Writes w_eff [sum n, d_pad] and y [m, sum n]."""
+    m, d = x.shape
+    ns, nc, types, qbs = _group_arrays(members)
+    pp = (ctypes.c_void_p * len(members))(*[_dev_ptr(p, f"probs[{i}]") for i, p in enumerate(probs)])
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().vq_gated_linear_group_fwd(_dev_ptr(x, "x"), m, d, d_pad, len(members), ns, nc, types, qbs, pp,
+                                           _dev_ptr(w_eff, "w_eff"), _dev_ptr(y, "y"), _dev_ptr(workspace, "workspace"),
+                                           ws_bytes, _stream(x.device)),
+           "vq_gated_linear_group_fwd")
+
+
+def group_bwd_workspace_bytes(m: int, d: int, members) -> int:
+    ns, nc, _, _ = _group_arrays([(mb[0], [], mb[2]) for mb in members])
+    v = int(lib().vq_gated_linear_group_bwd_workspace(m, d, len(members), ns, nc))
+    if v < 0:
+        raise ValueError(f"invalid group backward sizes m={m} d={d}")
+    return v
+
+
+def gated_linear_group_bwd(dy: torch.Tensor, x: torch.Tensor, members, d_pad: int, w_eff: torch.Tensor | None,
+                           dx: torch.Tensor | None, dprobs: list | None, workspace: torch.Tensor | None) -> None:
+    m, d = x.shape
+    ns, nc, types, qbs = _group_arrays(members)
+    dp = None
+    if dprobs is not None:
+        dp = (ctypes.c_void_p * len(members))(*[_dev_ptr(t, f"dprobs[{i}]") for i, t in enumerate(dprobs)])
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().vq_gated_linear_group_bwd(_dev_ptr(dy, "dy"), _dev_ptr(x, "x"), m, d, d_pad, len(members), ns, nc,
+                                           types, qbs, _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"), dp,
+                                           _dev_ptr(workspace, "workspace"), ws_bytes, _stream(dy.device)),
+           "vq_gated_linear_group_bwd")
 
 
 def distill_loss_fwd(logits: torch.Tensor, teacher_logits: torch.Tensor, labels: torch.Tensor,

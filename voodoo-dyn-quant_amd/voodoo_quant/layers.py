@@ -204,6 +204,95 @@ class GatedLinearFunction(Function):
         return (dx, dprobs, None) + (None,) * len(ctx.qbytes)
 
 
+class GatedLinearGroupFunction(Function):
+    """Gated Linears that read the same input (q/k/v, gate/up) as ONE stacked
+    product on libvoodoo_hip: every member's W_eff is mixed into its rows of a
+    stacked [sum N, D_pad] weight, then one GEMM gives [M, sum N]; the
+    backward is one launch for dX (which also sums the members' input
+    gradients) and every member's gate gradients.
+
+    forward(ctx, x [M, D] bf16, meta, *probs_then_qbytes) -> y [M, sum N] bf16
+    with meta = (((ggml types, N) per member), D_pad), then each member's probs
+    [K_i] and finally every member's qbytes in order."""
+
+    @staticmethod
+    def forward(ctx, x, meta, *tensors):
+        members, d_pad = meta
+        nm = len(members)
+        probs, qbytes = tensors[:nm], tensors[nm:]
+        x2 = _aligned(x)
+        dev = x2.device
+        ps = [p.detach().to(device=dev, dtype=torch.float32).contiguous() for p in probs]
+        spec, off = [], 0
+        for types, n in members:
+            spec.append((types, qbytes[off:off + len(types)], n))
+            off += len(types)
+        n_total = sum(n for _, n in members)
+        w_eff = torch.empty(n_total, d_pad, dtype=torch.bfloat16, device=dev)
+        y = torch.empty(x2.shape[0], n_total, dtype=torch.bfloat16, device=dev)
+        nbytes = _hip.fwd_workspace_bytes(x2.shape[0], n_total, x2.shape[1])
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
+        _hip.gated_linear_group_fwd(x2, spec, ps, d_pad, w_eff, y, ws)
+        ctx.save_for_backward(x2, w_eff)
+        ctx.spec = spec
+        ctx.meta = meta
+        ctx.probs_devices = [p.device for p in probs]
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w_eff = ctx.saved_tensors
+        members, d_pad = ctx.meta
+        nm = len(members)
+        need_dx = ctx.needs_input_grad[0]
+        need_dp = any(ctx.needs_input_grad[2:2 + nm])
+        dx = torch.empty_like(x2) if need_dx else None
+        dprobs = None
+        if need_dp:
+            dprobs = [torch.empty(len(t), dtype=torch.float32, device=x2.device) for t, _ in members]
+        if need_dx or need_dp:
+            dy2 = _aligned(dy.to(torch.bfloat16))
+            nbytes = _hip.group_bwd_workspace_bytes(x2.shape[0], x2.shape[1], ctx.spec)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x2.device)
+            _hip.gated_linear_group_bwd(dy2, x2, ctx.spec, d_pad, w_eff if need_dx else None, dx, dprobs, ws)
+        grads_p = [None] * nm if dprobs is None else [g.to(d) for g, d in zip(dprobs, ctx.probs_devices)]
+        n_q = sum(len(t) for t, _ in members)
+        return (dx, None, *grads_p) + (None,) * n_q
+
+
+def gated_linear_group(x: torch.Tensor, modules: list) -> list[torch.Tensor]:
+    """Outputs of gated Linears that all read `x`, as one stacked product when
+    they allow it: 2 to 4 :class:`MixedQuantLinear` modules with the same
+    input width, out_features multiples of 256 and PTQR off.  Otherwise each
+    module runs its own forward.  The outputs equal the modules' own forwards
+    up to the GEMM's summation order."""
+    groupable = (2 <= len(modules) <= 4 and not _PTQR_STATE.enabled and x.device.type == "cuda"
+                 and all(isinstance(m, MixedQuantLinear) for m in modules)
+                 and len({(m.in_features, m.padded_in_features) for m in modules}) == 1
+                 and all(m.out_features % 256 == 0 and m.shard_spec is None for m in modules))
+    if not groupable:
+        return [m(x) for m in modules]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    probs, qbytes, members = [], [], []
+    for m in modules:
+        m._move_qbytes(x.device)
+        p = m.get_probs()
+        probs.append(p if p.device == x.device else p.to(x.device))
+        qbytes.extend(m._qbytes())
+        members.append((m._ggml_types(), m.out_features))
+    meta = (tuple(members), modules[0].padded_in_features)
+    y = GatedLinearGroupFunction.apply(x2, meta, *probs, *qbytes)
+    outs = torch.split(y, [m.out_features for m in modules], dim=1)
+    res = []
+    for m, o in zip(modules, outs):
+        o = o.reshape(*lead, m.out_features)
+        res.append(o if x.dtype == torch.bfloat16 else o.to(x.dtype))
+    return res
+
+
 class RoutedLinearFunction(Function):
     """PTQR forward on libvoodoo_hip: y[t] = x[t] W_{k(t)}^T, tokens grouped by
     their routed candidate (reference ``_RoutedMixedLinear``,

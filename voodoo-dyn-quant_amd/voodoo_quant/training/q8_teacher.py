@@ -200,6 +200,39 @@ class Q8Embedding(nn.Module):
         return w_rows[inverse.to(w_rows.device)].reshape(*x.shape, self.embedding_dim)
 
 
+_GROUP_DECODES: dict[tuple, torch.Tensor] = {}
+
+
+def q8_linear_group(x: torch.Tensor, modules: list) -> list[torch.Tensor]:
+    """Outputs of Q8Linears that all read `x`.  With kept decodes and no
+    biases, their decodes are stacked once and the outputs come from ONE GEMM
+    (``vq_linear_fwd``); otherwise each module runs its own forward."""
+    ok = (_KEEP_DECODED and len(modules) >= 2 and x.device.type == "cuda"
+          and all(isinstance(m, Q8Linear) and m.bias is None and m.out_features % 8 == 0 for m in modules)
+          and len({m.in_features for m in modules}) == 1)
+    if not ok:
+        return [m(x) for m in modules]
+    key = tuple((id(m), m.qweight.data_ptr()) for m in modules)
+    w = _GROUP_DECODES.get(key)
+    if w is None:
+        w = torch.cat([m._decoded()[: m.out_features] for m in modules], 0).contiguous()
+        _GROUP_DECODES[key] = w
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, modules[0].in_features)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous().clone()
+    m_rows, n_total = x2.shape[0], w.shape[0]
+    y = torch.empty(m_rows, n_total, dtype=torch.bfloat16, device=x2.device)
+    if m_rows:
+        nbytes = _hip.fwd_workspace_bytes(m_rows, n_total, modules[0].in_features)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device) if nbytes > 0 else None
+        _hip.linear_fwd(x2, w, n_total, y, ws)
+    outs = torch.split(y, [m.out_features for m in modules], dim=1)
+    return [o.reshape(*lead, m.out_features).to(x.dtype) for m, o in zip(modules, outs)]
+
+
 def _layer_index(name: str) -> int | None:
     parts = name.split(".")
     if len(parts) >= 2 and parts[-2] == "layers":

@@ -33,7 +33,7 @@ import torch.nn.functional as F
 from voodoo_quant import layers
 from voodoo_quant.ggml import get_quant_info
 from voodoo_quant.training import trainer
-from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear, set_keep_decoded
+from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear, q8_linear_group, set_keep_decoded
 
 
 @dataclass
@@ -101,6 +101,17 @@ def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tenso
     return out.to(q.dtype)
 
 
+GROUP_PROJECTIONS = True  # stack the projections that read one input into one product
+
+
+def _project(x: torch.Tensor, mods: list[nn.Module]) -> list[torch.Tensor]:
+    if GROUP_PROJECTIONS and all(isinstance(m, layers.MixedQuantLinear) for m in mods):
+        return layers.gated_linear_group(x, mods)
+    if GROUP_PROJECTIONS and all(isinstance(m, Q8Linear) for m in mods):
+        return q8_linear_group(x, mods)
+    return [m(x) for m in mods]
+
+
 class _Attention(nn.Module):
     def __init__(self, cfg: DecoderConfig, lin: dict[str, nn.Module]):
         super().__init__()
@@ -111,9 +122,10 @@ class _Attention(nn.Module):
     def forward(self, x, cos, sin):
         b, s, _ = x.shape
         c = self.cfg
-        q = self.q_proj(x).view(b, s, c.heads, c.head_dim).transpose(1, 2)
-        k = self.k_proj(x).view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
-        v = self.v_proj(x).view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
+        q, k, v = _project(x, [self.q_proj, self.k_proj, self.v_proj])
+        q = q.view(b, s, c.heads, c.head_dim).transpose(1, 2)
+        k = k.view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
+        v = v.view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
         q, k = _apply_rope(q, cos, sin), _apply_rope(k, cos, sin)
         a = _attention(q, k, v).transpose(1, 2).reshape(b, s, c.heads * c.head_dim)
         return self.o_proj(a)
@@ -125,7 +137,8 @@ class _MLP(nn.Module):
         self.gate_proj, self.up_proj, self.down_proj = lin["mlp.gate_proj"], lin["mlp.up_proj"], lin["mlp.down_proj"]
 
     def forward(self, x):
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        g, u = _project(x, [self.gate_proj, self.up_proj])
+        return self.down_proj(F.silu(g) * u)
 
 
 class _Layer(nn.Module):
