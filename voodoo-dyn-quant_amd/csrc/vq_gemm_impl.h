@@ -357,7 +357,10 @@ struct XcdPlan {
     __host__ __device__ int items() const { return full + tail * s; }
 };
 
-__host__ __device__ inline XcdPlan xcd_plan(int x, int total_tiles, int cus_per_xcd, int ksteps, bool split_ok) {
+// min_saved: split only when a part is at least this many K steps shorter
+// than the whole tile (a split store tile pays a fixup launch).
+__host__ __device__ inline XcdPlan xcd_plan(int x, int total_tiles, int cus_per_xcd, int ksteps, bool split_ok,
+                                            int min_saved = 0) {
     const int base = total_tiles / 8, rem = total_tiles % 8;
     XcdPlan pl;
     pl.tiles = base + (x < rem ? 1 : 0);
@@ -367,6 +370,7 @@ __host__ __device__ inline XcdPlan xcd_plan(int x, int total_tiles, int cus_per_
     int sp = t > 0 ? c / t : 1;
     if (sp > 8) sp = 8;
     if (sp > ksteps / 4) sp = ksteps / 4;
+    if (sp >= 2 && ksteps - (ksteps + sp - 1) / sp < min_saved) sp = 1;
     if (!split_ok || t == 0 || sp < 2) {
         pl.full = pl.tiles;
         pl.tail = 0;
@@ -397,9 +401,9 @@ __device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, 
 }
 
 __device__ __forceinline__ WorkItem map_work(int w, int tiles_m, int tiles_n, int ksteps, int cus_per_xcd,
-                                             bool split_ok, int tail_max, int group_m) {
+                                             bool split_ok, int tail_max, int group_m, int min_saved = 0) {
     const int x = w % 8, local = w / 8;
-    const XcdPlan pl = xcd_plan(x, tiles_m * tiles_n, cus_per_xcd, ksteps, split_ok);
+    const XcdPlan pl = xcd_plan(x, tiles_m * tiles_n, cus_per_xcd, ksteps, split_ok, min_saved);
     WorkItem wi;
     wi.idle = local >= pl.items();
     wi.split = 0;
@@ -432,6 +436,7 @@ struct GemmParams {
     // tiles may be split along K, and the largest per-XCD tail and split
     int cus_per_xcd;
     int split_ok;
+    int split_min_saved;  // see xcd_plan
     int tail_max, s_max;
     // gate epilogue: i indexes d (< dlimit), j indexes n; candidates are rows n
     CandGroup cg;
@@ -882,6 +887,8 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
 
 // ---------------------------------------------------------------- kernels
 // One GEMM configuration: loaders, tile, wave layout, epilogue, pipeline depth.
+constexpr int kMinSavedSplitSteps = 10;  // see GemmCfg::plan
+
 template <class LA_, class LB_, int BI_, int BJ_, int BK_, int WI_, int WJ_, int EPI_, int DEPTH_,
           int SWITCH_ = SWITCH_FENCED>
 struct GemmCfg {
@@ -903,6 +910,9 @@ struct GemmCfg {
     // Fill in the work decomposition; returns the grid size (8 * blocks per XCD).
     static int plan(GemmParams& p, int cus, bool split_ok) {
         if (p.I <= 0 || p.J <= 0) return 0;
+        // a split store tile pays a fixup launch (about 6-8 K steps of one
+        // tile on MI355X): split only when a part saves more than that
+        p.split_min_saved = EPI == EPI_STORE ? kMinSavedSplitSteps : 0;
         p.cus_per_xcd = cus / 8 > 0 ? cus / 8 : 1;
         p.split_ok = split_ok ? 1 : 0;
         const int tiles = tiles_i(p) * tiles_j(p);
@@ -910,7 +920,7 @@ struct GemmCfg {
         p.tail_max = 0;
         p.s_max = 1;
         for (int x = 0; x < 8; ++x) {
-            const XcdPlan pl = xcd_plan(x, tiles, p.cus_per_xcd, ksteps(p), split_ok);
+            const XcdPlan pl = xcd_plan(x, tiles, p.cus_per_xcd, ksteps(p), split_ok, p.split_min_saved);
             items = pl.items() > items ? pl.items() : items;
             p.tail_max = pl.tail > p.tail_max ? pl.tail : p.tail_max;
             p.s_max = pl.s > p.s_max ? pl.s : p.s_max;
@@ -973,7 +983,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     const int tiles_i = (p.I + BI - 1) / BI, tiles_j = (p.J + BJ - 1) / BJ;
     const int ksteps = (p.K + BK - 1) / BK;
-    const WorkItem w = map_work(block, tiles_i, tiles_j, ksteps, p.cus_per_xcd, p.split_ok != 0, p.tail_max, 8);
+    const WorkItem w = map_work(block, tiles_i, tiles_j, ksteps, p.cus_per_xcd, p.split_ok != 0, p.tail_max, 8,
+                                p.split_min_saved);
     if (w.idle) {
         if constexpr (EPI == EPI_GATE) {
             const int nslot = p.cg.nsets * p.cg.kstride;
@@ -1025,7 +1036,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_tail_fixup_kernel(GemmParams 
     const int a = ab / S::NJ, b = ab % S::NJ;
     const int x = slot / p.tail_max, tt = slot % p.tail_max;
     const int tiles_i = (p.I + C::BI - 1) / C::BI, tiles_j = (p.J + C::BJ - 1) / C::BJ;
-    const XcdPlan pl = xcd_plan(x, tiles_i * tiles_j, p.cus_per_xcd, C::ksteps(p), p.split_ok != 0);
+    const XcdPlan pl = xcd_plan(x, tiles_i * tiles_j, p.cus_per_xcd, C::ksteps(p), p.split_ok != 0, p.split_min_saved);
     if (tt >= pl.tail) return;
     int tm, tn;
     tile_coords(pl.t0 + pl.full + tt, tiles_i, tiles_j, 8, tm, tn);
