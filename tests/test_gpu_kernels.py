@@ -189,6 +189,8 @@ def _run_fwd_bwd(hip, types, m, n, d, d_pad, qbs, probs, x, dy):
 CASES = [
     # (name, types, m, n, d, d_pad)
     ("cfg1", ["Q8_0", "Q6_K", "Q4_K", "Q3_K"], 512, 1024, 1024, 1024),
+    # 512 tiles of 256x256: the large-product tile configuration and split tails
+    ("large-tiles", ["Q4_K", "Q8_0"], 4096, 8192, 512, 512),
     ("ragged", ["Q2_K", "Q5_K", "Q8_0"], 37, 136, 264, 512),
     ("single-token", ["Q6_K", "Q4_K"], 1, 256, 256, 256),
     ("multi-tile", SIX, 300, 520, 1000, 1024),

@@ -32,6 +32,17 @@ int device_cus() {
 }
 
 using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED>;
+// Products with fewer than two rounds of 256x256 tiles (the 0.8B decoder's
+// projections at 8192 tokens) fill the chip better with 128x128 tiles, four
+// waves of 64x64 and two workgroups per CU (measured on MI355X: 8192 x 1024 x
+// 3072 67 vs 78 us, 8192 x 1024 -> 1536 38 vs 41 us, 8192 x 3072 -> 1024
+// 56 vs 90 us).
+using FwdSmallCfg = GemmCfg<DmaK<128, 64, 256>, DmaK<128, 64, 256>, 128, 128, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED, 2>;
+
+static bool small_product(int M, int N) {
+    const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    return tiles < 2 * (int64_t)device_cus();
+}
 using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 2, 2, EPI_STORE, 2, SWITCH_COPY_FIRST>;
 using GateCfg = GemmCfg<GateL, GateL, kGateBI, kGateBJ, 64, 2, 2, EPI_GATE, 2, SWITCH_READ_FIRST>;
 
@@ -72,12 +83,18 @@ int64_t dx_tail_bytes(int M, int N, int D) {
 // fp32 workspace for the K parts of the forward's split tail tiles.
 int64_t fwd_tail_bytes(int M, int N, int D) {
     GemmParams p = fwd_params(nullptr, nullptr, 0, nullptr, M, N, D);
+    if (small_product(M, N)) {
+        FwdSmallCfg::plan(p, device_cus(), true);
+        return FwdSmallCfg::tail_bytes(p);
+    }
     FwdCfg::plan(p, device_cus(), true);
     return FwdCfg::tail_bytes(p);
 }
 
 hipError_t launch_gemm_fwd(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D,
                            float* tail_ws, hipStream_t s) {
+    if (small_product(M, N))
+        return launch_gemm_cfg<FwdSmallCfg>(fwd_params(X, W, ldw, Y, M, N, D), device_cus(), tail_ws, s);
     return launch_gemm_cfg<FwdCfg>(fwd_params(X, W, ldw, Y, M, N, D), device_cus(), tail_ws, s);
 }
 

@@ -360,7 +360,7 @@ struct XcdPlan {
 // min_saved: split only when a part is at least this many K steps shorter
 // than the whole tile (a split store tile pays a fixup launch).
 __host__ __device__ inline XcdPlan xcd_plan(int x, int total_tiles, int cus_per_xcd, int ksteps, bool split_ok,
-                                            int min_saved = 0) {
+                                            int min_saved = 0, int max_split = 8) {
     const int base = total_tiles / 8, rem = total_tiles % 8;
     XcdPlan pl;
     pl.tiles = base + (x < rem ? 1 : 0);
@@ -368,7 +368,7 @@ __host__ __device__ inline XcdPlan xcd_plan(int x, int total_tiles, int cus_per_
     const int c = cus_per_xcd > 0 ? cus_per_xcd : 1;
     const int t = pl.tiles % c;
     int sp = t > 0 ? c / t : 1;
-    if (sp > 8) sp = 8;
+    if (sp > max_split) sp = max_split;
     if (sp > ksteps / 4) sp = ksteps / 4;
     if (sp >= 2 && ksteps - (ksteps + sp - 1) / sp < min_saved) sp = 1;
     if (!split_ok || t == 0 || sp < 2) {
@@ -401,9 +401,10 @@ __device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, 
 }
 
 __device__ __forceinline__ WorkItem map_work(int w, int tiles_m, int tiles_n, int ksteps, int cus_per_xcd,
-                                             bool split_ok, int tail_max, int group_m, int min_saved = 0) {
+                                             bool split_ok, int tail_max, int group_m, int min_saved = 0,
+                                             int max_split = 8) {
     const int x = w % 8, local = w / 8;
-    const XcdPlan pl = xcd_plan(x, tiles_m * tiles_n, cus_per_xcd, ksteps, split_ok, min_saved);
+    const XcdPlan pl = xcd_plan(x, tiles_m * tiles_n, cus_per_xcd, ksteps, split_ok, min_saved, max_split);
     WorkItem wi;
     wi.idle = local >= pl.items();
     wi.split = 0;
@@ -437,6 +438,7 @@ struct GemmParams {
     int cus_per_xcd;
     int split_ok;
     int split_min_saved;  // see xcd_plan
+    int split_max;        // most K parts of one tile
     int tail_max, s_max;
     // gate epilogue: i indexes d (< dlimit), j indexes n; candidates are rows n
     CandGroup cg;
@@ -890,12 +892,13 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
 constexpr int kMinSavedSplitSteps = 10;  // see GemmCfg::plan
 
 template <class LA_, class LB_, int BI_, int BJ_, int BK_, int WI_, int WJ_, int EPI_, int DEPTH_,
-          int SWITCH_ = SWITCH_FENCED>
+          int SWITCH_ = SWITCH_FENCED, int OCC_ = 1>
 struct GemmCfg {
     using LA = LA_;
     using LB = LB_;
     static constexpr int BI = BI_, BJ = BJ_, BK = BK_, WI = WI_, WJ = WJ_, EPI = EPI_, DEPTH = DEPTH_;
     static constexpr int SWITCH = SWITCH_;
+    static constexpr int OCC = OCC_;  // waves per SIMD the registers are budgeted for
     static constexpr int THREADS = WI * WJ * 64;
     static constexpr size_t main_lds() { return StageLds<LA, LB, DEPTH>::BYTES; }
     static constexpr size_t lds() {
@@ -913,6 +916,9 @@ struct GemmCfg {
         // a split store tile pays a fixup launch (about 6-8 K steps of one
         // tile on MI355X): split only when a part saves more than that
         p.split_min_saved = EPI == EPI_STORE ? kMinSavedSplitSteps : 0;
+        // more than 8 parts (tried for the gate at 1024 x 1024) loses: the
+        // parts of a dual launch then overflow one round of the CUs
+        p.split_max = 8;
         p.cus_per_xcd = cus / 8 > 0 ? cus / 8 : 1;
         p.split_ok = split_ok ? 1 : 0;
         const int tiles = tiles_i(p) * tiles_j(p);
@@ -920,7 +926,7 @@ struct GemmCfg {
         p.tail_max = 0;
         p.s_max = 1;
         for (int x = 0; x < 8; ++x) {
-            const XcdPlan pl = xcd_plan(x, tiles, p.cus_per_xcd, ksteps(p), split_ok, p.split_min_saved);
+            const XcdPlan pl = xcd_plan(x, tiles, p.cus_per_xcd, ksteps(p), split_ok, p.split_min_saved, p.split_max);
             items = pl.items() > items ? pl.items() : items;
             p.tail_max = pl.tail > p.tail_max ? pl.tail : p.tail_max;
             p.s_max = pl.s > p.s_max ? pl.s : p.s_max;
@@ -984,7 +990,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
     const int tiles_i = (p.I + BI - 1) / BI, tiles_j = (p.J + BJ - 1) / BJ;
     const int ksteps = (p.K + BK - 1) / BK;
     const WorkItem w = map_work(block, tiles_i, tiles_j, ksteps, p.cus_per_xcd, p.split_ok != 0, p.tail_max, 8,
-                                p.split_min_saved);
+                                p.split_min_saved, p.split_max);
     if (w.idle) {
         if constexpr (EPI == EPI_GATE) {
             const int nslot = p.cg.nsets * p.cg.kstride;
@@ -1036,7 +1042,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_tail_fixup_kernel(GemmParams 
     const int a = ab / S::NJ, b = ab % S::NJ;
     const int x = slot / p.tail_max, tt = slot % p.tail_max;
     const int tiles_i = (p.I + C::BI - 1) / C::BI, tiles_j = (p.J + C::BJ - 1) / C::BJ;
-    const XcdPlan pl = xcd_plan(x, tiles_i * tiles_j, p.cus_per_xcd, C::ksteps(p), p.split_ok != 0, p.split_min_saved);
+    const XcdPlan pl = xcd_plan(x, tiles_i * tiles_j, p.cus_per_xcd, C::ksteps(p), p.split_ok != 0, p.split_min_saved,
+                                p.split_max);
     if (tt >= pl.tail) return;
     int tm, tn;
     tile_coords(pl.t0 + pl.full + tt, tiles_i, tiles_j, 8, tm, tn);
@@ -1068,7 +1075,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_tail_fixup_kernel(GemmParams 
 // SIMD: telling the compiler so lets it keep fragments in flight instead of
 // minimising registers for an occupancy the LDS use rules out anyway.
 template <class C>
-__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::THREADS == 256 ? 1 : 2, C::THREADS == 256 ? 1 : 2)))
+__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::OCC, C::OCC)))
 void gemm_kernel(GemmParams p) {
     extern __shared__ u32x4 smem[];
     gemm_body<C>(p, blockIdx.x, smem);
