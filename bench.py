@@ -168,6 +168,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-train", action="store_true", help="skip the decoder gate-training step measurement")
     ap.add_argument("--train-steps", type=int, default=5)
+    ap.add_argument("--only-train", action="store_true",
+                    help="measure only the decoder gate-training step and print its record")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -182,6 +184,9 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.only_train:
+        print(json.dumps({"train": train_step_bench(torch, dev, args.train_steps, 2)}), flush=True)
+        return 0
     m, n, d = 8192, 17408, 5120
     d_pad = d
     ids = [GGML[t] for t in TYPES]
