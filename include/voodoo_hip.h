@@ -168,6 +168,28 @@ int vq_gated_linear_group_bwd(const uint16_t *dy, const uint16_t *x, int64_t m, 
                               const uint16_t *w_eff, uint16_t *dx, float *const *dprobs, void *workspace,
                               int64_t ws_bytes, void *stream);
 
+/* Decoder-layer glue of the gate-training step (the model the trainer runs
+ * around the gated projections; no counterpart in voodoo_quant itself).
+ * vq_rope_qkv_fwd: qkv [B*S][(Hq + 2 Hkv) D] bf16 (stacked q/k/v projection
+ * output) -> q, k, v, each [B*S][Hq][D] bf16: rotary embedding on q and k
+ * (y = x cos + [-x2, x1] sin with cos/sin fp32 [S][D]), K/V heads repeated
+ * Hq / Hkv times.  D % 16 == 0, Hq % Hkv == 0. */
+int vq_rope_qkv_fwd(const uint16_t *qkv, int64_t B, int64_t S, int Hq, int Hkv, int D, const float *cosb,
+                    const float *sinb, uint16_t *q, uint16_t *k, uint16_t *v, void *stream);
+
+/* Backward of vq_rope_qkv_fwd: dq, dk, dv [B][Hq][S][D] with element strides
+ * (stride_b, stride_h, stride_s; multiples of 8; unit stride along D) ->
+ * dqkv [B*S][(Hq + 2 Hkv) D] (inverse rotation, repeated heads summed). */
+int vq_rope_qkv_bwd(const uint16_t *dq, const uint16_t *dk, const uint16_t *dv, int64_t stride_b, int64_t stride_h,
+                    int64_t stride_s, int64_t B, int64_t S, int Hq, int Hkv, int D, const float *cosb,
+                    const float *sinb, uint16_t *dqkv, void *stream);
+
+/* out [tokens][F] = silu(gu[:, :F]) * gu[:, F:] for the stacked gate/up
+ * projection output gu [tokens][2F] (F % 8 == 0), and its backward
+ * dgu [tokens][2F] from dy [tokens][F]. */
+int vq_swiglu_fwd(const uint16_t *gu, int64_t tokens, int64_t F, uint16_t *out, void *stream);
+int vq_swiglu_bwd(const uint16_t *gu, const uint16_t *dy, int64_t tokens, int64_t F, uint16_t *dgu, void *stream);
+
 /* Workspace bytes of the distillation loss (per-row log-sum-exps and losses;
  * written by vq_distill_loss_fwd, read by vq_distill_loss_bwd). */
 int64_t vq_distill_loss_workspace(int64_t rows);

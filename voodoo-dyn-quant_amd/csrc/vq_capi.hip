@@ -308,6 +308,77 @@ int vq_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, const uint
     return rc == VQ_OK ? ok() : rc;
 }
 
+namespace {
+int check_rope(int64_t B, int64_t S, int Hq, int Hkv, int D, const void* cosb, const void* sinb) {
+    if (B < 0 || S <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || B * S > INT32_MAX)
+        return fail(VQ_ERR_SHAPE, "B=%lld S=%lld Hq=%d Hkv=%d D=%d", (long long)B, (long long)S, Hq, Hkv, D);
+    if (Hq % Hkv) return fail(VQ_ERR_SHAPE, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+    if (D % 16) return fail(VQ_ERR_ALIGN, "head dim %d must be a multiple of 16", D);
+    if (!cosb || !sinb) return fail(VQ_ERR_NULL, "cos/sin is NULL");
+    if (!aligned16(cosb) || !aligned16(sinb)) return fail(VQ_ERR_ALIGN, "cos/sin not 16-byte aligned");
+    return VQ_OK;
+}
+}  // namespace
+
+int vq_rope_qkv_fwd(const uint16_t* qkv, int64_t B, int64_t S, int Hq, int Hkv, int D, const float* cosb,
+                    const float* sinb, uint16_t* q, uint16_t* k, uint16_t* v, void* stream) {
+    int rc = check_rope(B, S, Hq, Hkv, D, cosb, sinb);
+    if (rc != VQ_OK) return rc;
+    if (B == 0) return ok();
+    if (!qkv || !q || !k || !v) return fail(VQ_ERR_NULL, "qkv/q/k/v is NULL");
+    if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v))
+        return fail(VQ_ERR_ALIGN, "qkv/q/k/v not 16-byte aligned");
+    rc = hip_check(vq::launch_rope_qkv_fwd(reinterpret_cast<const vq::bf16_t*>(qkv), B * S, (int)S, Hq, Hkv, D, cosb,
+                                           sinb, reinterpret_cast<vq::bf16_t*>(q), reinterpret_cast<vq::bf16_t*>(k),
+                                           reinterpret_cast<vq::bf16_t*>(v), static_cast<hipStream_t>(stream)),
+                   "rope launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_rope_qkv_bwd(const uint16_t* dq, const uint16_t* dk, const uint16_t* dv, int64_t stride_b, int64_t stride_h,
+                    int64_t stride_s, int64_t B, int64_t S, int Hq, int Hkv, int D, const float* cosb,
+                    const float* sinb, uint16_t* dqkv, void* stream) {
+    int rc = check_rope(B, S, Hq, Hkv, D, cosb, sinb);
+    if (rc != VQ_OK) return rc;
+    if (B == 0) return ok();
+    if (!dq || !dk || !dv || !dqkv) return fail(VQ_ERR_NULL, "dq/dk/dv/dqkv is NULL");
+    if (!aligned16(dq) || !aligned16(dk) || !aligned16(dv) || !aligned16(dqkv) || stride_b % 8 || stride_h % 8 ||
+        stride_s % 8)
+        return fail(VQ_ERR_ALIGN, "gradients not 16-byte aligned (pointers and strides)");
+    rc = hip_check(vq::launch_rope_qkv_bwd(reinterpret_cast<const vq::bf16_t*>(dq),
+                                           reinterpret_cast<const vq::bf16_t*>(dk),
+                                           reinterpret_cast<const vq::bf16_t*>(dv), stride_b, stride_h, stride_s,
+                                           B * S, (int)S, Hq, Hkv, D, cosb, sinb, reinterpret_cast<vq::bf16_t*>(dqkv),
+                                           static_cast<hipStream_t>(stream)),
+                   "rope backward launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_swiglu_fwd(const uint16_t* gu, int64_t tokens, int64_t F, uint16_t* out, void* stream) {
+    if (tokens < 0 || F <= 0 || F > INT32_MAX) return fail(VQ_ERR_SHAPE, "tokens=%lld F=%lld", (long long)tokens, (long long)F);
+    if (F % 8) return fail(VQ_ERR_ALIGN, "F=%lld must be a multiple of 8", (long long)F);
+    if (tokens == 0) return ok();
+    if (!gu || !out) return fail(VQ_ERR_NULL, "gu/out is NULL");
+    if (!aligned16(gu) || !aligned16(out)) return fail(VQ_ERR_ALIGN, "gu/out not 16-byte aligned");
+    int rc = hip_check(vq::launch_swiglu_fwd(reinterpret_cast<const vq::bf16_t*>(gu), tokens, (int)F,
+                                             reinterpret_cast<vq::bf16_t*>(out), static_cast<hipStream_t>(stream)),
+                       "swiglu launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_swiglu_bwd(const uint16_t* gu, const uint16_t* dy, int64_t tokens, int64_t F, uint16_t* dgu, void* stream) {
+    if (tokens < 0 || F <= 0 || F > INT32_MAX) return fail(VQ_ERR_SHAPE, "tokens=%lld F=%lld", (long long)tokens, (long long)F);
+    if (F % 8) return fail(VQ_ERR_ALIGN, "F=%lld must be a multiple of 8", (long long)F);
+    if (tokens == 0) return ok();
+    if (!gu || !dy || !dgu) return fail(VQ_ERR_NULL, "gu/dy/dgu is NULL");
+    if (!aligned16(gu) || !aligned16(dy) || !aligned16(dgu)) return fail(VQ_ERR_ALIGN, "gu/dy/dgu not 16-byte aligned");
+    int rc = hip_check(vq::launch_swiglu_bwd(reinterpret_cast<const vq::bf16_t*>(gu),
+                                             reinterpret_cast<const vq::bf16_t*>(dy), tokens, (int)F,
+                                             reinterpret_cast<vq::bf16_t*>(dgu), static_cast<hipStream_t>(stream)),
+                       "swiglu backward launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int64_t vq_distill_loss_workspace(int64_t rows) {
     if (rows < 0) return -1;
     return align256((5 * rows + 2) * (int64_t)sizeof(float));

@@ -62,6 +62,15 @@ hipError_t launch_embed_rows(const CandSet& cs, const float* probs, const int64_
 hipError_t launch_embed_rows_bwd(const CandSet& cs, const int64_t* ids, int64_t nids, int64_t vocab, int64_t dim,
                                  const void* grad, bool grad_f32, float* partials, float* dprobs, hipStream_t s);
 
+// Decoder glue (vq_decoder.hip).
+hipError_t launch_rope_qkv_fwd(const bf16_t* qkv, int64_t tokens, int S, int Hq, int Hkv, int D, const float* cosb,
+                               const float* sinb, bf16_t* q, bf16_t* k, bf16_t* v, hipStream_t s);
+hipError_t launch_rope_qkv_bwd(const bf16_t* dq, const bf16_t* dk, const bf16_t* dv, int64_t sb, int64_t sh,
+                               int64_t ss, int64_t tokens, int S, int Hq, int Hkv, int D, const float* cosb,
+                               const float* sinb, bf16_t* dqkv, hipStream_t s);
+hipError_t launch_swiglu_fwd(const bf16_t* gu, int64_t tokens, int F, bf16_t* out, hipStream_t s);
+hipError_t launch_swiglu_bwd(const bf16_t* gu, const bf16_t* dy, int64_t tokens, int F, bf16_t* dgu, hipStream_t s);
+
 // Distillation loss over full logits (vq_loss.hip).  ws: 5 * rows + 2 floats
 // (per-row log-sum-exps and losses, then 1/N_ce and 1/N), written by the
 // forward and read by the backward.

@@ -37,6 +37,10 @@ _SIGNATURES = [
     ("vq_gated_linear_group_fwd", _i, [_p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_group_bwd_workspace", _i64, [_i64, _i64, _i, _p, _p]),
     ("vq_gated_linear_group_bwd", _i, [_p, _p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    ("vq_rope_qkv_fwd", _i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p]),
+    ("vq_rope_qkv_bwd", _i, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _p, _p, _p]),
+    ("vq_swiglu_fwd", _i, [_p, _i64, _i64, _p, _p]),
+    ("vq_swiglu_bwd", _i, [_p, _p, _i64, _i64, _p, _p]),
     ("vq_distill_loss_workspace", _i64, [_i64]),
     ("vq_distill_loss_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _i64, _p]),
     ("vq_distill_loss_bwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _i64, _p]),
@@ -281,6 +285,49 @@ def gated_linear_group_bwd(dy: torch.Tensor, x: torch.Tensor, members, d_pad: in
                                            types, qbs, _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"), dp,
                                            _dev_ptr(workspace, "workspace"), ws_bytes, _stream(dy.device)),
            "vq_gated_linear_group_bwd")
+
+
+def rope_qkv_fwd(qkv: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, D: int, cos: torch.Tensor, sin: torch.Tensor):
+    """(q, k, v), each bf16 [B*S, Hq, D], from the stacked projection output."""
+    dev = qkv.device
+    q, k, v = (torch.empty(B * S, Hq, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    _check(lib().vq_rope_qkv_fwd(_dev_ptr(qkv, "qkv"), B, S, Hq, Hkv, D, _dev_ptr(cos, "cos"), _dev_ptr(sin, "sin"),
+                                 _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _stream(dev)),
+           "vq_rope_qkv_fwd")
+    return q, k, v
+
+
+def rope_qkv_bwd(dq, dk, dv, B: int, S: int, Hq: int, Hkv: int, D: int, cos, sin) -> torch.Tensor:
+    """dqkv bf16 [B*S, (Hq + 2 Hkv) D] from gradients shaped [B, Hq, S, D]
+    (any strides with a unit stride along D; the three share them)."""
+    dev = dq.device
+    grads = [dq, dk, dv]
+    if any(g.stride() != dq.stride() or g.stride(-1) != 1 for g in grads):
+        grads = [g.contiguous() for g in grads]
+    sb, sh, ss, _ = grads[0].stride()
+    out = torch.empty(B * S, (Hq + 2 * Hkv) * D, dtype=torch.bfloat16, device=dev)
+    ptr = [g.data_ptr() for g in grads]
+    _check(lib().vq_rope_qkv_bwd(ptr[0], ptr[1], ptr[2], sb, sh, ss, B, S, Hq, Hkv, D, _dev_ptr(cos, "cos"),
+                                 _dev_ptr(sin, "sin"), _dev_ptr(out, "dqkv"), _stream(dev)),
+           "vq_rope_qkv_bwd")
+    return out
+
+
+def swiglu_fwd(gu: torch.Tensor) -> torch.Tensor:
+    t, f2 = gu.shape
+    out = torch.empty(t, f2 // 2, dtype=torch.bfloat16, device=gu.device)
+    _check(lib().vq_swiglu_fwd(_dev_ptr(gu, "gu"), t, f2 // 2, _dev_ptr(out, "out"), _stream(gu.device)),
+           "vq_swiglu_fwd")
+    return out
+
+
+def swiglu_bwd(gu: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
+    t, f2 = gu.shape
+    dgu = torch.empty_like(gu)
+    _check(lib().vq_swiglu_bwd(_dev_ptr(gu, "gu"), _dev_ptr(dy, "dy"), t, f2 // 2, _dev_ptr(dgu, "dgu"),
+                               _stream(gu.device)),
+           "vq_swiglu_bwd")
+    return dgu
 
 
 def distill_loss_fwd(logits: torch.Tensor, teacher_logits: torch.Tensor, labels: torch.Tensor,

@@ -260,18 +260,21 @@ class GatedLinearGroupFunction(Function):
         return (dx, None, *grads_p) + (None,) * n_q
 
 
-def gated_linear_group(x: torch.Tensor, modules: list) -> list[torch.Tensor]:
+def gated_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
     """Outputs of gated Linears that all read `x`, as one stacked product when
     they allow it: 2 to 4 :class:`MixedQuantLinear` modules with the same
     input width, out_features multiples of 256 and PTQR off.  Otherwise each
     module runs its own forward.  The outputs equal the modules' own forwards
-    up to the GEMM's summation order."""
+    up to the GEMM's summation order.
+
+    stacked=True returns the stacked output [tokens, sum out_features] itself
+    (None when the modules cannot be stacked)."""
     groupable = (2 <= len(modules) <= 4 and not _PTQR_STATE.enabled and x.device.type == "cuda"
                  and all(isinstance(m, MixedQuantLinear) for m in modules)
                  and len({(m.in_features, m.padded_in_features) for m in modules}) == 1
                  and all(m.out_features % 256 == 0 and m.shard_spec is None for m in modules))
     if not groupable:
-        return [m(x) for m in modules]
+        return None if stacked else [m(x) for m in modules]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype != torch.bfloat16:
@@ -285,6 +288,8 @@ def gated_linear_group(x: torch.Tensor, modules: list) -> list[torch.Tensor]:
         members.append((m._ggml_types(), m.out_features))
     meta = (tuple(members), modules[0].padded_in_features)
     y = GatedLinearGroupFunction.apply(x2, meta, *probs, *qbytes)
+    if stacked:
+        return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     outs = torch.split(y, [m.out_features for m in modules], dim=1)
     res = []
     for m, o in zip(modules, outs):

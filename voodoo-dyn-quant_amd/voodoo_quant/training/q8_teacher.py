@@ -203,18 +203,22 @@ class Q8Embedding(nn.Module):
 _GROUP_DECODES: dict[tuple, torch.Tensor] = {}
 
 
-def q8_linear_group(x: torch.Tensor, modules: list) -> list[torch.Tensor]:
+def q8_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
     """Outputs of Q8Linears that all read `x`.  With kept decodes and no
     biases, their decodes are stacked once and the outputs come from ONE GEMM
-    (``vq_linear_fwd``); otherwise each module runs its own forward."""
+    (``vq_linear_fwd``); otherwise each module runs its own forward.
+    stacked=True returns the stacked output [tokens, sum out_features] (None
+    when the modules cannot be stacked)."""
     ok = (_KEEP_DECODED and len(modules) >= 2 and x.device.type == "cuda"
           and all(isinstance(m, Q8Linear) and m.bias is None and m.out_features % 8 == 0 for m in modules)
           and len({m.in_features for m in modules}) == 1)
     if not ok:
-        return [m(x) for m in modules]
+        return None if stacked else [m(x) for m in modules]
     key = tuple((id(m), m.qweight.data_ptr()) for m in modules)
     w = _GROUP_DECODES.get(key)
     if w is None:
+        if len(_GROUP_DECODES) > 1024:
+            _GROUP_DECODES.clear()
         w = torch.cat([m._decoded()[: m.out_features] for m in modules], 0).contiguous()
         _GROUP_DECODES[key] = w
     lead = x.shape[:-1]
@@ -229,6 +233,8 @@ def q8_linear_group(x: torch.Tensor, modules: list) -> list[torch.Tensor]:
         nbytes = _hip.fwd_workspace_bytes(m_rows, n_total, modules[0].in_features)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device) if nbytes > 0 else None
         _hip.linear_fwd(x2, w, n_total, y, ws)
+    if stacked:
+        return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     outs = torch.split(y, [m.out_features for m in modules], dim=1)
     return [o.reshape(*lead, m.out_features).to(x.dtype) for m, o in zip(modules, outs)]
 

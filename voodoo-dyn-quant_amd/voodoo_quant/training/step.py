@@ -30,7 +30,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from voodoo_quant import layers
+from voodoo_quant import _hip, layers
 from voodoo_quant.ggml import get_quant_info
 from voodoo_quant.training import trainer
 from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear, q8_linear_group, set_keep_decoded
@@ -102,6 +102,7 @@ def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tenso
 
 
 GROUP_PROJECTIONS = True  # stack the projections that read one input into one product
+FUSED_GLUE = True         # rotary embedding / SwiGLU on the stacked outputs in one kernel each
 
 
 def _project(x: torch.Tensor, mods: list[nn.Module]) -> list[torch.Tensor]:
@@ -110,6 +111,74 @@ def _project(x: torch.Tensor, mods: list[nn.Module]) -> list[torch.Tensor]:
     if GROUP_PROJECTIONS and all(isinstance(m, Q8Linear) for m in mods):
         return q8_linear_group(x, mods)
     return [m(x) for m in mods]
+
+
+def _project_stacked(x: torch.Tensor, mods: list[nn.Module]) -> torch.Tensor | None:
+    """The stacked output [tokens, sum out] of projections that read x, or None."""
+    if not (GROUP_PROJECTIONS and FUSED_GLUE and x.is_cuda):
+        return None
+    if all(isinstance(m, layers.MixedQuantLinear) for m in mods):
+        return layers.gated_linear_group(x, mods, stacked=True)
+    if all(isinstance(m, Q8Linear) for m in mods):
+        return q8_linear_group(x, mods, stacked=True)
+    return None
+
+
+class _RopeQKV(torch.autograd.Function):
+    """Stacked q/k/v projection output -> (q, k, v) as [B, Hq, S, D] views of
+    [B, S, Hq, D] memory: rotary embedding on q and k, K/V heads repeated for
+    grouped-query attention (``vq_rope_qkv_fwd/bwd``)."""
+
+    @staticmethod
+    def forward(ctx, qkv, cos, sin, shape):
+        b, s_, hq, hkv, d = shape
+        q, k, v = _hip.rope_qkv_fwd(qkv.contiguous(), b, s_, hq, hkv, d, cos, sin)
+        ctx.save_for_backward(cos, sin)
+        ctx.shape = shape
+        return tuple(t.view(b, s_, hq, d).transpose(1, 2) for t in (q, k, v))
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        cos, sin = ctx.saved_tensors
+        b, s_, hq, hkv, d = ctx.shape
+        zeros = None
+        grads = []
+        for g in (dq, dk, dv):
+            if g is None:
+                zeros = zeros if zeros is not None else torch.zeros(b, hq, s_, d, dtype=torch.bfloat16, device=cos.device)
+                g = zeros
+            grads.append(g.to(torch.bfloat16))
+        return _hip.rope_qkv_bwd(*grads, b, s_, hq, hkv, d, cos, sin), None, None, None
+
+
+class _SwiGLU(torch.autograd.Function):
+    """silu(gate) * up from the stacked gate/up output [tokens, 2F] (``vq_swiglu_fwd/bwd``)."""
+
+    @staticmethod
+    def forward(ctx, gu):
+        gu = gu.contiguous()
+        ctx.save_for_backward(gu)
+        return _hip.swiglu_fwd(gu)
+
+    @staticmethod
+    def backward(ctx, dy):
+        (gu,) = ctx.saved_tensors
+        return _hip.swiglu_bwd(gu, dy.to(torch.bfloat16).contiguous())
+
+
+_ROPE_F32: dict[tuple, tuple[torch.Tensor, torch.Tensor]] = {}
+
+
+def _rope_tables_f32(s: int, head_dim: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    key = (s, head_dim, theta, str(device))
+    t = _ROPE_F32.get(key)
+    if t is None:
+        inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64, device=device) / head_dim))
+        ang = torch.outer(torch.arange(s, dtype=torch.float64, device=device), inv)
+        ang = torch.cat([ang, ang], dim=-1)
+        t = (ang.cos().float().contiguous(), ang.sin().float().contiguous())
+        _ROPE_F32[key] = t
+    return t
 
 
 class _Attention(nn.Module):
@@ -122,11 +191,16 @@ class _Attention(nn.Module):
     def forward(self, x, cos, sin):
         b, s, _ = x.shape
         c = self.cfg
-        q, k, v = _project(x, [self.q_proj, self.k_proj, self.v_proj])
-        q = q.view(b, s, c.heads, c.head_dim).transpose(1, 2)
-        k = k.view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
-        v = v.view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
-        q, k = _apply_rope(q, cos, sin), _apply_rope(k, cos, sin)
+        qkv = _project_stacked(x, [self.q_proj, self.k_proj, self.v_proj])
+        if qkv is not None and c.head_dim % 16 == 0:
+            cos32, sin32 = _rope_tables_f32(s, c.head_dim, c.rope_theta, x.device)
+            q, k, v = _RopeQKV.apply(qkv.reshape(b * s, -1), cos32, sin32, (b, s, c.heads, c.kv_heads, c.head_dim))
+        else:
+            q, k, v = _project(x, [self.q_proj, self.k_proj, self.v_proj])
+            q = q.view(b, s, c.heads, c.head_dim).transpose(1, 2)
+            k = k.view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
+            v = v.view(b, s, c.kv_heads, c.head_dim).transpose(1, 2)
+            q, k = _apply_rope(q, cos, sin), _apply_rope(k, cos, sin)
         a = _attention(q, k, v).transpose(1, 2).reshape(b, s, c.heads * c.head_dim)
         return self.o_proj(a)
 
@@ -137,8 +211,13 @@ class _MLP(nn.Module):
         self.gate_proj, self.up_proj, self.down_proj = lin["mlp.gate_proj"], lin["mlp.up_proj"], lin["mlp.down_proj"]
 
     def forward(self, x):
-        g, u = _project(x, [self.gate_proj, self.up_proj])
-        return self.down_proj(F.silu(g) * u)
+        gu = _project_stacked(x, [self.gate_proj, self.up_proj])
+        if gu is not None and gu.shape[-1] % 16 == 0:
+            h = _SwiGLU.apply(gu.reshape(-1, gu.shape[-1])).view(*x.shape[:-1], gu.shape[-1] // 2)
+        else:
+            g, u = _project(x, [self.gate_proj, self.up_proj])
+            h = F.silu(g) * u
+        return self.down_proj(h)
 
 
 class _Layer(nn.Module):
