@@ -160,6 +160,46 @@ def train_step_bench(torch, dev, steps: int, warmup: int) -> dict:
     return rec
 
 
+def stack_step_bench(torch, dev, steps: int, warmup: int) -> dict:
+    """The long-context, wide-menu stress configuration: 8 SwiGLU blocks at
+    hidden 4096, MLP 14336 (MLP-only blocks), K = 8 candidates per tensor
+    (the six formats, Q4_K and Q6_K twice with their own bytes), 2 x 8192
+    tokens, temperature annealed 2.0 -> 0.1 over 200 steps; tokens per second
+    of the whole step (student, Q8_0 teacher, MSE + size loss, backward,
+    optimizer)."""
+    from voodoo_quant.training import step as st
+
+    cfg = st.StackConfig()
+    types = ["Q2_K", "Q3_K", "Q4_K", "Q4_K", "Q5_K", "Q6_K", "Q6_K", "Q8_0"]
+    student, teacher, replaced = st.build_stack(cfg, types, dev, seed=1)
+    tokens = 2 * 8192
+    g = torch.Generator(device=dev).manual_seed(6)
+    x = torch.randn(tokens, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
+    tr = st.StackTrainer(student, teacher, replaced,
+                         st.StepConfig(max_steps=200, temp_start=2.0, temp_end=0.1),
+                         total_8bit_bytes=float(cfg.gated_weights()))
+    for _ in range(warmup):
+        tr.step(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = tr.step(x)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / max(steps, 1) * 1e3
+    fl = st.stack_flops(cfg, tokens)
+    rec = {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "steps": steps,
+           "warmup": warmup, "model_TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
+           "loss": {k: round(float(v), 5) for k, v in out.items()},
+           "workload": "8 SwiGLU blocks (MLP-only) at hidden 4096, MLP 14336: 24 gated tensors, 1.409e9 weights, "
+                       "K=8 (Q2_K, Q3_K, Q4_K x2, Q5_K, Q6_K x2, Q8_0); 2 x 8192 tokens; T 2.0 -> 0.1 over 200 steps; "
+                       "relative MSE to a Q8_0 teacher + dead-zone size loss at 45% of 8-bit",
+           "candidate_bytes": "random valid GGUF blocks, scales sized for N(0, 0.02)-like weights"}
+    log(f"stack: {ms:.1f} ms/step -> {rec['tokens_per_s']:.0f} tokens/s ({rec['model_TFLOPs']} model TFLOP/s)")
+    del student, teacher, replaced, tr, x
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +210,7 @@ def main() -> int:
     ap.add_argument("--train-steps", type=int, default=5)
     ap.add_argument("--only-train", action="store_true",
                     help="measure only the decoder gate-training step and print its record")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 8-block SwiGLU stress measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -286,6 +327,9 @@ def main() -> int:
         del qbytes, w_eff, y, dx, ws, fws, out
         torch.cuda.empty_cache()
         train = train_step_bench(torch, dev, args.train_steps, 2)
+    stack = None
+    if not args.no_stack:
+        stack = stack_step_bench(torch, dev, 3, 2)
 
     if args.copy_calibration:
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
@@ -327,6 +371,7 @@ def main() -> int:
         "dequant_gbps": dq,
         "ptqr": ptqr,
         "train": train,
+        "stress": stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

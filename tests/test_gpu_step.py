@@ -143,3 +143,24 @@ def test_steps_are_finite_and_move_the_gates(models):
     assert all(torch.isfinite(torch.as_tensor(v)).all() for v in out.values())
     after = torch.cat([m.gates.detach() for m in replaced.values()])
     assert torch.isfinite(after).all() and float((after - before).abs().max()) > 1e-3
+
+
+def test_swiglu_stack_steps_with_repeated_formats():
+    """The stress configuration's model at a small size: K = 8 candidates with
+    two formats repeated (each its own bytes), stacked gate/up, a few steps."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    cfg = st.StackConfig(blocks=2, hidden=512, mlp=1024)
+    types = ["Q2_K", "Q3_K", "Q4_K", "Q4_K", "Q5_K", "Q6_K", "Q6_K", "Q8_0"]
+    student, teacher, replaced = st.build_stack(cfg, types, torch.device("cuda", 0), seed=2)
+    x = torch.randn(300, cfg.hidden, device="cuda").to(torch.bfloat16)
+    tr = st.StackTrainer(student, teacher, replaced, st.StepConfig(max_steps=5, temp_start=2.0, temp_end=0.1),
+                         float(cfg.gated_weights()))
+    before = torch.cat([m.gates.detach().clone() for m in replaced.values()])
+    for _ in range(5):
+        out = tr.step(x)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out["mse"]) and torch.isfinite(out["size"]) and out["tau"] == pytest.approx(0.1)
+    after = torch.cat([m.gates.detach() for m in replaced.values()])
+    assert torch.isfinite(after).all() and float((after - before).abs().max()) > 1e-3
+    assert len(replaced) == 6 and all(m.num_candidates == 8 for m in replaced.values())

@@ -55,12 +55,12 @@ def _losses(ys, targets, total_bytes, target_bytes, with_mse=True):
     return (mse if with_mse else 0.0) + LAMBDA * mixture.size_loss(total_bytes, target_bytes, TOL)
 
 
-def _reference_run(cands, xs, targets, target_bytes, with_mse=True):
+def _reference_run(cands, xs, targets, target_bytes, with_mse=True, steps=STEPS, t0=1.0, t1=0.3):
     gates = [torch.zeros(len(c), requires_grad=True) for c in cands]
-    opt, sched = mixture.make_gate_optimizer(gates, LR, STEPS)
+    opt, sched = mixture.make_gate_optimizer(gates, LR, steps)
     bpw = [[ggml.bytes_per_weight(qt) for qt in types] for _, types, _, _, _ in SPECS]
-    for step in range(STEPS):
-        t = mixture.anneal_temperature(step, STEPS, 1.0, 0.3)
+    for step in range(steps):
+        t = mixture.anneal_temperature(step, steps, t0, t1)
         ys, total = [], 0.0
         for g, c, x, b, (_, _, n, d, _) in zip(gates, cands, xs, bpw, SPECS):
             p = mixture.soft_probs(g, t)
@@ -78,17 +78,17 @@ def _reference_run(cands, xs, targets, target_bytes, with_mse=True):
     return [g.detach() for g in gates]
 
 
-def _hip_run(mods, xs, targets, target_bytes):
+def _hip_run(mods, xs, targets, target_bytes, steps=STEPS, t0=1.0, t1=0.3):
     dev = torch.device("cuda", 0)
     for m in mods:
         m.to(dev)
     xs = [x.to(dev) for x in xs]
     targets = [t.to(dev) for t in targets]
     trainable = [m.gates for m in mods]
-    opt, sched = trainer.build_gate_optimizer(trainable, LR, STEPS)
+    opt, sched = trainer.build_gate_optimizer(trainable, LR, steps)
     replaced = {SPECS[i][0]: m for i, m in enumerate(mods)}
-    for step in range(STEPS):
-        trainer.set_temperature_all(replaced, trainer.anneal_temperature(step, STEPS, 1.0, 0.3))
+    for step in range(steps):
+        trainer.set_temperature_all(replaced, trainer.anneal_temperature(step, steps, t0, t1))
         ys = [m(x) for m, x in zip(mods, xs)]
         total = layers.total_effective_bytes(replaced)
         loss = _losses(ys, targets, total, target_bytes)
@@ -99,11 +99,14 @@ def _hip_run(mods, xs, targets, target_bytes):
 
 
 @pytest.mark.gpu
-def test_gate_argmax_matches_reference_after_short_run():
+@pytest.mark.parametrize("steps,t0,t1", [(STEPS, 1.0, 0.3), (200, 2.0, 0.1)])
+def test_gate_argmax_matches_reference_after_short_run(steps, t0, t1):
+    """40 steps at T 1.0 -> 0.3, and the stress configuration's schedule
+    (200 steps, T 2.0 -> 0.1)."""
     torch.manual_seed(0)
     mods, cands, xs, targets, target_bytes = _problem()
-    ref = _reference_run(cands, xs, targets, target_bytes)
-    got = _hip_run(mods, xs, targets, target_bytes)
+    ref = _reference_run(cands, xs, targets, target_bytes, steps=steps, t0=t0, t1=t1)
+    got = _hip_run(mods, xs, targets, target_bytes, steps=steps, t0=t0, t1=t1)
     for (name, types, *_), r, g in zip(SPECS, ref, got):
         print(f"{name}: reference {types[int(r.argmax())]} {r.numpy().round(3)}  hip {types[int(g.argmax())]} "
               f"{g.numpy().round(3)}")
@@ -113,7 +116,7 @@ def test_gate_argmax_matches_reference_after_short_run():
     # GEMM gradients shape the result (a size-only run ends elsewhere)
     winners = {SPECS[i][1][int(r.argmax())] for i, r in enumerate(ref)}
     assert len(winners) >= 2, winners
-    ctrl = _reference_run(cands, xs, targets, target_bytes, with_mse=False)
+    ctrl = _reference_run(cands, xs, targets, target_bytes, with_mse=False, steps=steps, t0=t0, t1=t1)
     assert max(float((r - c).abs().max()) for r, c in zip(ref, ctrl)) > 0.2
 
 

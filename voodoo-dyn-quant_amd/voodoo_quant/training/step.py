@@ -423,3 +423,102 @@ def step_flops(cfg: DecoderConfig, tokens: int, seq: int) -> float:
     head = cfg.vocab * cfg.hidden
     attn_fwd = cfg.layers * 2 * 2 * tokens * seq * cfg.heads * cfg.head_dim / 2
     return 6 * tokens * lin + 4 * tokens * head + 2 * tokens * (lin + head) + attn_fwd * 3 + attn_fwd
+
+
+# ---------------------------------------------------------------------------
+# the wide-menu stress configuration: a stack of SwiGLU blocks
+# ---------------------------------------------------------------------------
+@dataclass
+class StackConfig:
+    blocks: int = 8
+    hidden: int = 4096
+    mlp: int = 14336
+    eps: float = 1.0e-6
+
+    def gated_weights(self) -> int:
+        return self.blocks * 3 * self.hidden * self.mlp
+
+
+class _SwiGLUBlock(nn.Module):
+    """h + down(silu(gate(rmsnorm h)) * up(rmsnorm h))."""
+
+    def __init__(self, cfg: StackConfig, lin: dict[str, nn.Module], device):
+        super().__init__()
+        self.eps = cfg.eps
+        self.mlp = _MLP(lin)
+        self.norm = nn.Parameter(torch.ones(cfg.hidden, dtype=torch.bfloat16, device=device), requires_grad=False)
+
+    def forward(self, h):
+        return h + self.mlp(F.rms_norm(h, (h.shape[-1],), self.norm, self.eps))
+
+
+class SwiGLUStack(nn.Module):
+    def __init__(self, cfg: StackConfig, block_linears: list[dict[str, nn.Module]], device):
+        super().__init__()
+        self.blocks = nn.ModuleList([_SwiGLUBlock(cfg, lin, device) for lin in block_linears])
+
+    def forward(self, h):
+        for b in self.blocks:
+            h = b(h)
+        return h
+
+
+def build_stack(cfg: StackConfig, types: list[str], device, seed: int = 0):
+    """(student, teacher, replaced) for the SwiGLU stack: every gate/up/down
+    gated over `types` (a type may repeat: each entry is its own candidate),
+    the teacher over Q8_0 bytes with kept decodes; candidates are synthetic
+    valid blocks (see :func:`synthetic_candidate_bytes`)."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    replaced: dict[str, nn.Module] = {}
+    shapes = {"mlp.gate_proj": (cfg.mlp, cfg.hidden), "mlp.up_proj": (cfg.mlp, cfg.hidden),
+              "mlp.down_proj": (cfg.hidden, cfg.mlp)}
+    s_blocks, t_blocks = [], []
+    for bi in range(cfg.blocks):
+        lin = {}
+        for n, (o, i) in shapes.items():
+            name = f"blocks.{bi}.{n}"
+            qbs = [synthetic_candidate_bytes(qt, o, i, device, gen) for qt in types]
+            lin[n] = layers.MixedQuantLinear.from_packed(i, o, types, qbs, tensor_name=name, device=device)
+            replaced[name] = lin[n]
+        s_blocks.append(lin)
+        t_blocks.append({n: Q8Linear(synthetic_candidate_bytes("Q8_0", o, i, device, gen), o, i)
+                         for n, (o, i) in shapes.items()})
+    set_keep_decoded(True)
+    teacher = SwiGLUStack(cfg, t_blocks, device)
+    teacher.requires_grad_(False)
+    return SwiGLUStack(cfg, s_blocks, device), teacher, replaced
+
+
+class StackTrainer:
+    """Gate training of the SwiGLU stack: loss = relative MSE of the output
+    against the Q8_0 teacher's + size_weight * dead-zone size penalty;
+    temperature annealed, clip 1.0, AdamW + cosine on the gates."""
+
+    def __init__(self, student, teacher, replaced, cfg: StepConfig, total_8bit_bytes: float):
+        self.student, self.teacher, self.replaced, self.cfg = student, teacher, replaced, cfg
+        self.trainable = [m.gates for m in replaced.values()]
+        self.opt, self.sched = trainer.build_gate_optimizer(self.trainable, cfg.lr, cfg.max_steps)
+        self.target_bytes = cfg.target_fraction * total_8bit_bytes
+        self.step_index = 0
+
+    def step(self, x: torch.Tensor) -> dict[str, torch.Tensor]:
+        c = self.cfg
+        tau = trainer.anneal_temperature(self.step_index, c.max_steps, c.temp_start, c.temp_end)
+        trainer.set_temperature_all(self.replaced, tau)
+        y = self.student(x)
+        with torch.no_grad():
+            t = self.teacher(x).float()
+        mse = ((y.float() - t) ** 2).mean() / (t ** 2).mean()
+        size = trainer.size_loss(layers.total_effective_bytes(self.replaced).to(x.device), self.target_bytes,
+                                 c.size_tolerance)
+        (mse + c.size_weight * size).backward()
+        trainer.gate_optimizer_step(self.trainable, self.opt, self.sched, max_norm=1.0)
+        self.step_index += 1
+        return {"mse": mse.detach(), "size": size.detach(), "tau": tau}
+
+
+def stack_flops(cfg: StackConfig, tokens: int) -> float:
+    """6 M N D for the student's gated products (forward, dX, dW-gate) plus
+    2 M N D for the teacher's forward."""
+    return 8.0 * tokens * cfg.gated_weights()
