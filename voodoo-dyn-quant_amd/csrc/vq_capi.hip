@@ -543,13 +543,15 @@ int vq_gated_linear_group_fwd(const uint16_t* x, int64_t m, int64_t d, int64_t d
     if (!aligned16(x) || !aligned16(w_eff) || !aligned16(y))
         return fail(VQ_ERR_ALIGN, "x/w_eff/y not 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
+    vq::bf16_t* outs[vq::kMaxSets];
+    int64_t ngroups[vq::kMaxSets];
     for (int i = 0; i < nmembers; ++i) {
         if (!probs[i]) return fail(VQ_ERR_NULL, "probs[%d] is NULL", i);
-        rc = hip_check(vq::launch_mix(cg.sets[i], probs[i], w_eff + (int64_t)cg.set_j0[i] * d_pad, n[i] * d_pad / 256,
-                                      s),
-                       "mix launch");
-        if (rc != VQ_OK) return rc;
+        outs[i] = w_eff + (int64_t)cg.set_j0[i] * d_pad;
+        ngroups[i] = n[i] * d_pad / 256;
     }
+    rc = hip_check(vq::launch_mix_sets(nmembers, cg.sets, probs, outs, ngroups, s), "mix launch");
+    if (rc != VQ_OK) return rc;
     if (m == 0) return ok();
     if (workspace && !aligned16(workspace)) return fail(VQ_ERR_ALIGN, "workspace not 16-byte aligned");
     const int64_t tail_bytes = vq::fwd_tail_bytes((int)m, (int)n_total, (int)d);

@@ -87,22 +87,42 @@ hipError_t launch_dequant_bf16(int qtype, const uint8_t* q, bf16_t* out, int64_t
 // ---------------------------------------------------------------------------
 // Mixture: W_eff = bf16( (((0 + p0 W0) + p1 W1) + ...) ) with every product and
 // sum rounded separately, exactly as the fp32 torch ops of the reference.
+// One launch mixes up to kMaxSets tensors (the members of a stacked
+// product); a workgroup covers RUNS * 8 groups of one tensor, so small
+// tensors get more, shorter workgroups.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kStreamThreads) void mix_kernel(CandSet cs, const float* __restrict__ probs,
-                                                             bf16_t* __restrict__ w_eff, int64_t ngroups) {
+struct MixPlan {
+    int nsets;
+    CandSet sets[kMaxSets];
+    const float* probs[kMaxSets];
+    bf16_t* out[kMaxSets];
+    int64_t ngroups[kMaxSets];
+    int64_t block0[kMaxSets + 1];  // first workgroup of each set
+};
+
+template <int RUNS>
+__global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int64_t g0 = (int64_t)blockIdx.x * kGroupsPerBlock;
-    const int ng = (int)min<int64_t>(kGroupsPerBlock, ngroups - g0);
+    constexpr int GPB = kStreamThreads * 8 * RUNS / 256;  // groups per workgroup
+    int si = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxSets; ++q)
+        if (q < mp.nsets && (int64_t)blockIdx.x >= mp.block0[q]) si = q;
+    const CandSet& cs = mp.sets[si];
+    const int64_t g0 = ((int64_t)blockIdx.x - mp.block0[si]) * GPB;
+    const int ng = (int)min<int64_t>(GPB, mp.ngroups[si] - g0);
     int acc = 0;
     for (int k = 0; k < cs.ncand; ++k) {
         const int gb = group_bytes(cs.qtype[k]);
         stage_bytes(lds + acc, cs.qbytes[k] + g0 * gb, ng * gb);
-        acc += (kGroupsPerBlock * gb + 15) & ~15;
+        acc += (GPB * gb + 15) & ~15;
     }
     __syncthreads();
     const int t = threadIdx.x;
+    const float* probs = mp.probs[si];
+    bf16_t* w_eff = mp.out[si];
 #pragma unroll
-    for (int u = 0; u < kRunsPerThread; ++u) {
+    for (int u = 0; u < RUNS; ++u) {
         const int j = (t >> 5) + 8 * u;
         if (j >= ng) continue;
         float mixed[8];
@@ -123,7 +143,7 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(CandSet cs, const f
             case Q5_K: decode8_mix<Q5_K>(g, p, w); break;
             default: decode8_mix<Q6_K>(g, p, w); break;
             }
-            off += (kGroupsPerBlock * gb + 15) & ~15;
+            off += (GPB * gb + 15) & ~15;
             const float pk = probs[k];
             {
                 // product and sum rounded separately, like the two torch ops
@@ -141,13 +161,39 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(CandSet cs, const f
     }
 }
 
-hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int64_t ngroups, hipStream_t s) {
-    if (ngroups <= 0) return hipSuccess;
+hipError_t launch_mix_sets(int nsets, const CandSet* sets, const float* const* probs, bf16_t* const* out,
+                           const int64_t* ngroups, hipStream_t s) {
+    MixPlan mp{};
+    mp.nsets = nsets;
+    int64_t total = 0;
+    for (int i = 0; i < nsets; ++i) total += ngroups[i];
+    // workgroups of 8 groups when 16-group ones would not give every CU two
+    const bool small = (total + 15) / 16 < 2 * (int64_t)device_cus();
+    const int gpb = small ? 8 : 16;
     size_t lds = 0;
-    for (int k = 0; k < cs.ncand; ++k) lds += (kGroupsPerBlock * group_bytes(cs.qtype[k]) + 15) & ~15;
-    const dim3 grid((unsigned)((ngroups + kGroupsPerBlock - 1) / kGroupsPerBlock));
-    mix_kernel<<<grid, kStreamThreads, lds, s>>>(cs, probs, w_eff, ngroups);
+    int64_t blocks = 0;
+    for (int i = 0; i < nsets; ++i) {
+        mp.sets[i] = sets[i];
+        mp.probs[i] = probs[i];
+        mp.out[i] = out[i];
+        mp.ngroups[i] = ngroups[i];
+        mp.block0[i] = blocks;
+        blocks += (ngroups[i] + gpb - 1) / gpb;
+        size_t l = 0;
+        for (int k = 0; k < sets[i].ncand; ++k) l += (gpb * group_bytes(sets[i].qtype[k]) + 15) & ~15;
+        lds = l > lds ? l : lds;
+    }
+    mp.block0[nsets] = blocks;
+    if (blocks <= 0) return hipSuccess;
+    if (small)
+        mix_kernel<1><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
+    else
+        mix_kernel<2><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
     return hipGetLastError();
+}
+
+hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int64_t ngroups, hipStream_t s) {
+    return launch_mix_sets(1, &cs, &probs, &w_eff, &ngroups, s);
 }
 
 }  // namespace vq

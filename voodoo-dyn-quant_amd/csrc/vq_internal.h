@@ -18,6 +18,9 @@ constexpr int kGroupsPerBlock = kStreamThreads * 8 * kRunsPerThread / 256;  // 1
 hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s);
 hipError_t launch_dequant_bf16(int qtype, const uint8_t* q, bf16_t* out, int64_t ngroups, hipStream_t s);
 hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int64_t ngroups, hipStream_t s);
+// Mixes of up to kMaxSets tensors in one launch (set i: ngroups[i] groups into out[i]).
+hipError_t launch_mix_sets(int nsets, const CandSet* sets, const float* const* probs, bf16_t* const* out,
+                           const int64_t* ngroups, hipStream_t s);
 
 // Gated-Linear GEMMs (vq_gemm.hip).  All matrices are row-major bf16.
 //   fwd:  Y[M][N]  = X[M][D] . W[N][D]^T          (W row stride ldw)
