@@ -824,7 +824,10 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
     static_assert(BI == 256, "the gate tile covers exactly one 256-weight group per row");
     constexpr int NW = WI * WJ;
     constexpr int BUF_CH = BJ * kGateMaxChunks;  // 16-byte chunks per candidate buffer
-    __shared__ float red[NW][kMaxCand];
+    // per-wave candidate sums, after the two candidate buffers (inside the
+    // dynamic allocation: a static array would push an 8-wave workgroup whose
+    // main loop takes all 160 KiB past the limit)
+    float(*red)[kMaxCand] = reinterpret_cast<float(*)[kMaxCand]>(smem + 2 * BUF_CH);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scale fields index by it
     const int wi = wave / WJ, wj = wave % WJ;
@@ -902,7 +905,7 @@ struct GemmCfg {
     static constexpr int THREADS = WI * WJ * 64;
     static constexpr size_t main_lds() { return StageLds<LA, LB, DEPTH>::BYTES; }
     static constexpr size_t lds() {
-        constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16;  // two candidate buffers
+        constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16 + (size_t)WI * WJ * kMaxCand * 4;  // two candidate buffers, wave sums
         constexpr size_t store = (size_t)BI * (BJ + 8) * 2;            // bf16 staging of the tile
         constexpr size_t epi = EPI == EPI_GATE ? gate : store;
         return epi > main_lds() ? epi : main_lds();
@@ -1071,9 +1074,11 @@ __global__ __launch_bounds__(C::THREADS) void gemm_tail_fixup_kernel(GemmParams 
     }
 }
 
-// Four-wave workgroups hold 256 accumulators per lane and run one wave per
-// SIMD: telling the compiler so lets it keep fragments in flight instead of
-// minimising registers for an occupancy the LDS use rules out anyway.
+// The register budget is set by the waves per SIMD the configuration runs at
+// (OCC: one for four-wave 256x256 tiles with 256 accumulators per lane, two
+// for eight-wave ones or two 128x128 workgroups per CU): telling the compiler
+// so lets it keep fragments in flight instead of minimising registers for an
+// occupancy the LDS use rules out anyway.
 template <class C>
 __global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::OCC, C::OCC)))
 void gemm_kernel(GemmParams p) {
@@ -1087,9 +1092,9 @@ void gemm_kernel(GemmParams p) {
 // the second product's work items fill the last, partial round of the first
 // instead of each launch idling CUs in its own tail.
 template <class C1, class C2>
-__global__ __launch_bounds__(C1::THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(C1::THREADS) __attribute__((amdgpu_waves_per_eu(C1::OCC, C1::OCC)))
 void gemm_dual_kernel(GemmParams p1, int items1, int n1, GemmParams p2) {
-    static_assert(C1::THREADS == 256 && C2::THREADS == 256, "both problems use four-wave workgroups");
+    static_assert(C1::THREADS == C2::THREADS && C1::OCC == C2::OCC, "both problems use the same workgroup shape");
     extern __shared__ u32x4 smem[];
     const int b = blockIdx.x;
     if (b < n1) {
