@@ -12,6 +12,8 @@ Also reported in the same JSON line:
                 peak (HIP events on the stream the kernels run on); the backward
                 runs dX and the gate product in one launch
   kernels_ms    per-kernel average durations
+  hipblaslt_ms  torch's bf16 matmul (hipBLASLt) on the same plain products
+                (Y = X W_eff^T, dX = dY W_eff), for scale
   dequant_gbps  dequant microbench (4096 x 14336, each format): algorithmic
                 bytes (packed read + fp32 write) / time, against 8 TB/s
   cpu_baseline  the oracle's fp32 torch restatement of the reference step on
@@ -291,6 +293,13 @@ def main() -> int:
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get(dom)
     log("kernels ms: " + ", ".join(f"{k} {v:.3f}" for k, v in kernels.items()))
+    # the vendor library on the same plain products, for scale: torch's bf16
+    # matmul (hipBLASLt) for Y = X W_eff^T and dX = dY W_eff
+    w_c = w_eff[:, :d].contiguous()
+    lib = {"fwd_gemm": time_events(torch, lambda: torch.nn.functional.linear(x, w_c), reps),
+           "dx_gemm": time_events(torch, lambda: torch.matmul(dy, w_c), reps)}
+    del w_c
+    log("hipBLASLt ms (same shapes, plain bf16 products): " + ", ".join(f"{k} {v:.3f}" for k, v in lib.items()))
 
     # PTQR routed forward at the same shape: tokens Gumbel-routed from probs,
     # one grouped GEMM over the cached bf16 candidate decodes
@@ -368,6 +377,7 @@ def main() -> int:
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
         },
         "kernels_ms": {k: round(v, 4) for k, v in kernels.items()},
+        "hipblaslt_ms": {k: round(v, 4) for k, v in lib.items()},
         "dequant_gbps": dq,
         "ptqr": ptqr,
         "train": train,

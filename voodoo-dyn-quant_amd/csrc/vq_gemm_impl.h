@@ -743,9 +743,13 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
 // is decoded in the accumulator layout.  The descriptor covers exactly the
 // candidate's bytes, so the rounded-out tail of the last span reads zeros;
 // rows past J load row 0 (their dW is zero).
-constexpr int kGateMaxChunks = (272 + 15 + 15) / 16;  // 16-byte chunks per row span, worst type (Q8_0)
+// A staged span takes an odd number of 16-byte chunks: the 32 rows one wave
+// reads at the same offset then fall on 16 distinct 16-byte bank groups
+// instead of 4 or 8 (even pitches repeat after 4 or 8 rows).
+__host__ __device__ constexpr int gate_span_chunks(int gb) { return ((gb + 15 + 15) / 16) | 1; }
+constexpr int kGateMaxChunks = gate_span_chunks(272);  // worst type (Q8_0)
 
-__device__ __forceinline__ int gate_row_chunks(int qt) { return (group_bytes(qt) + 15 + 15) / 16; }
+__device__ __forceinline__ int gate_row_chunks(int qt) { return gate_span_chunks(group_bytes(qt)); }
 
 // Same copy through registers (ordinary loads, then ds_write), for the first
 // candidate, which is consumed right after it is staged.
@@ -795,7 +799,7 @@ __device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const
                                               const uint8_t* __restrict__ buf, int64_t row_groups, int j0, int group,
                                               int wi, int wj, int lane, int J) {
     constexpr int GB = group_bytes(QT);
-    constexpr int PITCH = 16 * ((GB + 15 + 15) / 16);  // bytes per staged row span
+    constexpr int PITCH = 16 * gate_span_chunks(GB);  // bytes per staged row span
     float s = 0.0f;
 #pragma unroll
     for (int b = 0; b < NJ; ++b) {
