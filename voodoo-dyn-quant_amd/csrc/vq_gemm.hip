@@ -16,9 +16,9 @@ namespace vq {
 // Operands stored [K][rows] (dX's W, both gate operands) keep that orientation
 // in LDS and are read with ds_read_b64_tr_b16.
 constexpr int kWaves = 8;
-using FwdLA = DmaK<256, 64, 64 * kWaves>;
-using FwdLB = DmaK<256, 64, 64 * kWaves>;
-using DxLA = DmaK<256, 64, 64 * kWaves>;
+using FwdLA = DmaKS<256, 64, 64 * kWaves>;
+using FwdLB = DmaKS<256, 64, 64 * kWaves>;
+using DxLA = DmaKS<256, 64, 64 * kWaves>;
 using DxLB = DmaN<256, 64, 64 * kWaves>;
 using GateL = DmaN<256, 64, 64 * kWaves>;
 constexpr int kGateBI = 256, kGateBJ = 256;
@@ -42,7 +42,7 @@ using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_RE
 // waves of 64x64 and two workgroups per CU (measured on MI355X: 8192 x 1024 x
 // 3072 67 vs 78 us, 8192 x 1024 -> 1536 38 vs 41 us, 8192 x 3072 -> 1024
 // 56 vs 90 us).
-using FwdSmallCfg = GemmCfg<DmaK<128, 64, 256>, DmaK<128, 64, 256>, 128, 128, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED, 2>;
+using FwdSmallCfg = GemmCfg<DmaKS<128, 64, 256>, DmaKS<128, 64, 256>, 128, 128, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED, 2>;
 
 static bool small_product(int M, int N) {
     const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);

@@ -269,6 +269,63 @@ struct DmaK {
     }
 };
 
+// DmaK without padding: a K-major tile row keeps its CPR = BK/8 data chunks,
+// and chunk c of row r sits in slot c ^ sw(r) of that row.  The copy fills
+// LDS slots in order (lane l of an instruction writes slot M0/16 + l), so a
+// lane fetches the global chunk its slot holds; a fragment read addresses the
+// slot of its chunk.  sw spreads the 8 (16) rows one ds_read_b128 pass serves
+// over distinct 16-byte bank groups with 32 (64) banks of 4 bytes: for CPR = 8,
+// rows r and r + 8 differ through r >> 3; for CPR = 4 (64-byte rows, two rows
+// per 128 bytes), the rows of one parity within 8, and the rows of one residue
+// mod 4 within 16, take distinct slots.  Against DmaK the stage is 1/9 (BK 64)
+// smaller, and no copy lane writes padding.
+template <int ROWS, int BK, int THREADS>
+struct DmaKS {
+    static constexpr bool kDma = true;
+    static constexpr int kFragReads = 1;
+    static constexpr int CPR = BK / 8;
+    static_assert(CPR == 4 || CPR == 8, "BK 32 or 64");
+    static constexpr int NW = THREADS / 64;
+    static constexpr int NI = ROWS * CPR / (64 * NW);  // instructions per wave per stage
+    static_assert(NI * 64 * NW == ROWS * CPR, "the tile splits evenly over the waves");
+    static constexpr int CHUNKS = ROWS * CPR;
+    uint32_t voff[NI];
+    int kpos[NI];
+
+    static __device__ __forceinline__ int sw(int r) {
+        if constexpr (CPR == 4)
+            return ((r >> 1) ^ (r >> 3)) & 3;
+        else
+            return (r ^ (r >> 3)) & 7;
+    }
+    // tile rows [r0, r0 + ROWS) of src[row * ld + k]
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* = nullptr, int = 0) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int L = (i * NW + wave) * 64 + lane;
+            const int row = L / CPR;
+            const int c = (L % CPR) ^ sw(row);
+            voff[i] = r0 + row < rows ? (uint32_t)((row * ld + 8 * c) * 2) : kOOB;
+            kpos[i] = 8 * c + 8;  // k extent this lane's chunk needs
+        }
+    }
+    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t ld, int r0, int k0,
+                                          int kvalid) const {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)r0 * ld + k0);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
+                                                     kpos[i] <= kvalid ? voff[i] : kOOB, 0, 0, 0);
+    }
+    // MFMA fragment: tile row `row + lane%32`, k = 16 ks + 8 (lane/32) .. +7
+    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
+        const int r = row + (lane & 31);
+        return __builtin_bit_cast(bf16x8_t, lds[r * CPR + ((2 * ks + (lane >> 5)) ^ sw(r))]);
+    }
+};
+
 template <int ROWS, int BK, int THREADS>
 struct DmaN {
     static constexpr bool kDma = true;
