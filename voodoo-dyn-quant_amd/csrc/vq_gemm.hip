@@ -19,8 +19,8 @@ constexpr int kWaves = 8;
 using FwdLA = DmaKS<256, 64, 64 * kWaves>;
 using FwdLB = DmaKS<256, 64, 64 * kWaves>;
 using DxLA = DmaKS<256, 64, 64 * kWaves>;
-using DxLB = DmaN<256, 64, 64 * kWaves>;
-using GateL = DmaN<256, 64, 64 * kWaves>;
+using DxLB = DmaNS<256, 64, 64 * kWaves>;
+using GateL = DmaNS<256, 64, 64 * kWaves>;
 constexpr int kGateBI = 256, kGateBJ = 256;
 
 int device_cus() {

@@ -364,6 +364,62 @@ struct DmaN {
     }
 };
 
+// DmaN without padding: k-row kr keeps its RCH = ROWS/8 chunks, chunk c in
+// slot c ^ 4 (kr % 4).  One ds_read_b64_tr_b16 pass reads 4 consecutive
+// k-rows x 32 tile rows (4 chunks, 64 bytes, aligned: fragment rows start at
+// multiples of 32); the XOR moves the 4 k-rows' 64-byte blocks onto distinct
+// quarters of 256 bytes, which the padded layout achieves with its 64-byte
+// pitch.  The read at k + 4 keeps the same XOR.
+template <int ROWS, int BK, int THREADS>
+struct DmaNS {
+    static constexpr bool kDma = true;
+    static constexpr int kFragReads = 2;
+    static constexpr int RCH = ROWS / 8;  // chunks per k-row
+    static_assert(RCH % 16 == 0, "the XOR of up to 12 stays inside the k-row");
+    static constexpr int NW = THREADS / 64;
+    static constexpr int NI = BK * RCH / (64 * NW);
+    static_assert(NI * 64 * NW == BK * RCH, "the tile splits evenly over the waves");
+    static constexpr int CHUNKS = BK * RCH;
+    uint32_t voff[NI];
+    int kpos[NI];
+
+    // tile rows [r0, r0 + ROWS) of src[k * ld + row]
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* = nullptr, int = 0) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int L = (i * NW + wave) * 64 + lane;
+            const int kr = L / RCH;
+            const int c = (L % RCH) ^ (4 * (kr & 3));
+            voff[i] = r0 + 8 * c < rows ? (uint32_t)((kr * ld + 8 * c) * 2) : kOOB;
+            kpos[i] = kr + 1;
+        }
+    }
+    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t ld, int r0, int k0,
+                                          int kvalid) const {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)k0 * ld + r0);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
+                                                     kpos[i] <= kvalid ? voff[i] : kOOB, 0, 0, 0);
+    }
+    // the LoaderN fragment (same lane -> (k, row) map), at swizzled addresses
+    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
+        typedef short v4i16 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+        const int k = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
+        const int r = row + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        const bf16_t* base =
+            reinterpret_cast<const bf16_t*>(lds) + 8 * (k * RCH + ((r >> 3) ^ (4 * (k & 3)))) + (r & 7);
+        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base));
+        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + 8 * 4 * RCH));
+        typedef short v8i16 __attribute__((ext_vector_type(8)));
+        const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        return __builtin_bit_cast(bf16x8_t, v);
+    }
+};
+
 // DmaK with gathered rows: tile row r is source row map[r0 + r] (rows
 // r0 + r >= rows are zeros).  The per-lane offsets carry the whole row offset,
 // so the descriptor base moves with k only; the host bounds m * ld * 2 < 2^31.
