@@ -37,18 +37,19 @@ int device_cus() {
 }
 
 using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_READ_FIRST, 2>;
-// Products with fewer than two rounds of 256x256 tiles (the 0.8B decoder's
-// projections at 8192 tokens) fill the chip better with 128x128 tiles, four
-// waves of 64x64 and two workgroups per CU (measured on MI355X: 8192 x 1024 x
-// 3072 67 vs 78 us, 8192 x 1024 -> 1536 38 vs 41 us, 8192 x 3072 -> 1024
-// 56 vs 90 us).
+// Products with fewer 256x256 tiles than three quarters of the CUs (the 0.8B
+// decoder's 1024-wide projections at 8192 tokens) fill the chip better with
+// 128x128 tiles, four waves of 64x64 and two workgroups per CU (measured on
+// MI355X at 8192 tokens: 1024 -> 1024 25 vs 33 us, 3072 -> 1024 55 vs 67 us);
+// from 192 tiles on the 8-wave 256x256 tiles win (1024 -> 1536 33 vs 39 us,
+// 1024 -> 3072 65 vs 68 us).
 using FwdSmallCfg = GemmCfg<DmaKS<128, 64, 256>, DmaKS<128, 64, 256>, 128, 128, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED, 2>;
 
 static bool small_product(int M, int N) {
     const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    return tiles < 2 * (int64_t)device_cus();
+    return 4 * tiles < 3 * (int64_t)device_cus();
 }
-using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_COPY_FIRST, 2>;
+using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_FENCED, 2>;
 using GateCfg = GemmCfg<GateL, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2, SWITCH_READ_FIRST, 2>;
 
 static GemmParams fwd_params(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D) {
@@ -125,7 +126,7 @@ hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, b
 // PTQR forward: token rows grouped by candidate, each group multiplied by its
 // candidate's bf16 decode (the mainloop and store of the forward product, with
 // A rows gathered and Y rows scattered through perm).
-using RoutedCfg = GemmCfg<DmaKG<256, 64, 256>, DmaK<256, 64, 256>, 256, 256, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED>;
+using RoutedCfg = GemmCfg<DmaKSG<256, 64, 64 * kWaves>, FwdLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_READ_FIRST, 2>;
 
 hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const* cand_bf16, int64_t ldw, int N,
                              int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s) {

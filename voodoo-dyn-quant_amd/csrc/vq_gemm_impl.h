@@ -455,6 +455,38 @@ struct DmaKG : DmaK<ROWS, BK, THREADS> {
     }
 };
 
+// DmaKS with gathered rows, as DmaKG over the swizzled layout.
+template <int ROWS, int BK, int THREADS>
+struct DmaKSG : DmaKS<ROWS, BK, THREADS> {
+    using Base = DmaKS<ROWS, BK, THREADS>;
+    using Base::CPR;
+    using Base::NI;
+    using Base::NW;
+    // map_rows: valid source rows; an entry outside [0, map_rows) reads zeros
+    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* map, int map_rows) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int L = (i * NW + wave) * 64 + lane;
+            const int row = L / CPR;
+            const int c = (L % CPR) ^ Base::sw(row);
+            const int src = r0 + row < rows ? map[r0 + row] : -1;
+            const bool ok = (unsigned)src < (unsigned)map_rows;
+            this->voff[i] = ok ? (uint32_t)(((int64_t)src * ld + 8 * c) * 2) : kOOB;
+            this->kpos[i] = 8 * c + 8;
+        }
+    }
+    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t, int, int k0,
+                                          int kvalid) const {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + k0);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
+                                                     this->kpos[i] <= kvalid ? this->voff[i] : kOOB, 0, 0, 0);
+    }
+};
+
 // ---------------------------------------------------------------- work order
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on
 // XCD w % 8, its local index w / 8).  The tiles, in grouped order (group_m
@@ -1290,7 +1322,7 @@ static hipError_t launch_gemm_dual(GemmParams p1, GemmParams p2, int cus, float*
 // those as in map_work (so the XCDs share the work evenly and the spare blocks
 // spread over all of them), then finds its group by walking the group sizes.
 template <class C>
-__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::OCC, C::OCC)))
 void routed_gemm_kernel(GemmParams p, int tile_rows) {
     using LA = typename C::LA;
     using LB = typename C::LB;
