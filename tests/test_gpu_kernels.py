@@ -144,6 +144,19 @@ def test_mix_weight_bit_exact(hip, types):
     assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
 
 
+def test_mix_weight_bit_exact_large(hip):
+    """A tensor large enough for the mix kernel's 32-group workgroups, with a
+    ragged last workgroup (4104 x 1280 = 20520 groups)."""
+    rng = np.random.default_rng(12)
+    n, d_pad = 4104, 1280
+    qbs, ws = _candidates(SIX, n, d_pad, rng)
+    probs = torch.softmax(torch.randn(len(SIX), generator=torch.Generator().manual_seed(2)), 0)
+    ref = mixture.mix_weight(ws, probs).to(torch.bfloat16)
+    got = hip.mix_weight([GGML[t] for t in SIX], [_dev(q.reshape(-1)) for q in qbs], probs.cuda(), n, d_pad)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
+
+
 @pytest.mark.parametrize("qt", SIX)
 def test_mix_weight_bit_exact_edge_scales(hip, qt):
     """Full finite fp16 scale range (subnormal, negative, huge) plus all-0x00

@@ -97,16 +97,19 @@ __device__ __forceinline__ void scale_min_k4(const uint8_t* __restrict__ s, int 
     }
 }
 
-// Load R (4 or 8) consecutive bytes whose address is a multiple of ALIGN
+// Load R (4, 8 or 16) consecutive bytes whose address is a multiple of ALIGN
 // (a property of the format's layout: group bases are 16-byte aligned in
 // memory and in LDS, so field offsets fix the alignment), with the widest
 // loads that alignment allows.  Byte r is (w[r / 4] >> (8 * (r % 4))) & 0xff.
 template <int ALIGN, int R>
 __device__ __forceinline__ void load_run(const uint8_t* __restrict__ p, uint32_t (&w)[R / 4]) {
-    if constexpr (ALIGN >= 8 && R == 8) {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        w[0] = v.x;
-        w[1] = v.y;
+    if constexpr (ALIGN >= 8 && R % 8 == 0) {
+#pragma unroll
+        for (int i = 0; i < R / 8; ++i) {
+            const uint2 v = *reinterpret_cast<const uint2*>(p + 8 * i);
+            w[2 * i] = v.x;
+            w[2 * i + 1] = v.y;
+        }
     } else if constexpr (ALIGN >= 4) {
 #pragma unroll
         for (int i = 0; i < R / 4; ++i) w[i] = *reinterpret_cast<const uint32_t*>(p + 4 * i);
@@ -337,22 +340,26 @@ __device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0
     return r;
 }
 
-// Exact values of the 8 weights p .. p + 7 (p a multiple of 8) of a group,
-// for the mixture: the same real numbers as ggml's dequantize_row_*, computed
-// as y = dl * u + c with u the unsigned code (unpacked four per 32-bit word
-// and converted by v_cvt_f32_ubyteN) and c folding the format's offset and
-// min.  dl * u is exact and each y is rounded once, like ggml's; only the sign
-// of a zero may differ, which the mixture cannot see (+0 + (+-0) = +0).
-template <int QT>
-__device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p, float (&y)[8]) {
-    uint32_t uw[2];
+// Exact values of the R (8 or 16) weights p .. p + R - 1 (p a multiple of R)
+// of a group, for the mixture: the same real numbers as ggml's
+// dequantize_row_*, computed as y = dl * u + c with u the unsigned code
+// (unpacked four per 32-bit word and converted by v_cvt_f32_ubyteN) and c
+// folding the format's offset and min.  dl * u is exact and each y is rounded
+// once, like ggml's; only the sign of a zero may differ, which the mixture
+// cannot see (+0 + (+-0) = +0).  A run of 16 never crosses a 16-weight scale
+// block, so each run decodes one scale.
+template <int QT, int R = 8>
+__device__ __forceinline__ void decode_mix(const uint8_t* __restrict__ g, int p, float (&y)[R]) {
+    static_assert(R == 8 || R == 16, "runs of 8 or 16 weights");
+    constexpr int W = R / 4;
+    uint32_t uw[W];
     float dl, c;
     if constexpr (QT == Q8_0) {
         const uint8_t* b = g + 34 * (p >> 5);
         const float d = h2f_hw(*reinterpret_cast<const uint16_t*>(b));
-        load_run<2, 8>(b + 2 + (p & 31), uw);
-        uw[0] ^= 0x80808080u;  // q + 128
-        uw[1] ^= 0x80808080u;
+        load_run<2, R>(b + 2 + (p & 31), uw);
+#pragma unroll
+        for (int i = 0; i < W; ++i) uw[i] ^= 0x80808080u;  // q + 128
         dl = d;
         c = -128.0f * d;
     } else if constexpr (QT == Q4_K || QT == Q5_K) {
@@ -362,26 +369,26 @@ __device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p
         scale_min_k4(g + 4, 2 * ch + hi, sc, m);
         dl = h2f_hw(dd & 0xffffu) * (float)sc;
         c = -(h2f_hw(dd >> 16) * (float)m);
-        load_run<8, 8>(g + (QT == Q5_K ? 48 : 16) + 32 * ch + (p & 31), uw);
-        uw[0] = (uw[0] >> (4 * hi)) & 0x0F0F0F0Fu;
-        uw[1] = (uw[1] >> (4 * hi)) & 0x0F0F0F0Fu;
+        load_run<8, R>(g + (QT == Q5_K ? 48 : 16) + 32 * ch + (p & 31), uw);
+#pragma unroll
+        for (int i = 0; i < W; ++i) uw[i] = (uw[i] >> (4 * hi)) & 0x0F0F0F0Fu;
         if constexpr (QT == Q5_K) {
-            uint32_t xw[2];
-            load_run<8, 8>(g + 16 + (p & 31), xw);
+            uint32_t xw[W];
+            load_run<8, R>(g + 16 + (p & 31), xw);
             const int xs = 2 * ch + hi;
-            uw[0] |= ((xw[0] >> xs) & 0x01010101u) << 4;
-            uw[1] |= ((xw[1] >> xs) & 0x01010101u) << 4;
+#pragma unroll
+            for (int i = 0; i < W; ++i) uw[i] |= ((xw[i] >> xs) & 0x01010101u) << 4;
         }
     } else if constexpr (QT == Q6_K) {
         const float d = h2f_hw(*reinterpret_cast<const uint16_t*>(g + 208));
         const int n = p >> 7, t = (p >> 5) & 3, l = p & 31;
         dl = d * (float)(int8_t)g[192 + 8 * n + (l >> 4) + 2 * t];
         c = -32.0f * dl;
-        uint32_t hw[2];
-        load_run<2, 8>(g + 64 * n + 32 * (t & 1) + l, uw);
-        load_run<2, 8>(g + 128 + 32 * n + l, hw);
+        uint32_t hw[W];
+        load_run<2, R>(g + 64 * n + 32 * (t & 1) + l, uw);
+        load_run<2, R>(g + 128 + 32 * n + l, hw);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < W; ++i)
             uw[i] = ((uw[i] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) | (((hw[i] >> (2 * t)) & 0x03030303u) << 4);
     } else if constexpr (QT == Q3_K) {
         const float d = h2f_hw(*reinterpret_cast<const uint16_t*>(g + 108));
@@ -392,12 +399,12 @@ __device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p
         const uint32_t hi2 = (sb[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
         dl = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
         c = -4.0f * dl;
-        uint32_t hw[2];
-        load_run<2, 8>(g + 32 + 32 * n + 16 * half + l, uw);
-        load_run<2, 8>(g + 16 * half + l, hw);
+        uint32_t hw[W];
+        load_run<2, R>(g + 32 + 32 * n + 16 * half + l, uw);
+        load_run<2, R>(g + 16 * half + l, hw);
         const int xs = 4 * n + j;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < W; ++i)
             uw[i] = ((uw[i] >> (2 * j)) & 0x03030303u) | (((hw[i] >> xs) & 0x01010101u) << 2);
     } else {  // Q2_K
         const uint32_t dd = *reinterpret_cast<const uint32_t*>(g + 80);
@@ -405,12 +412,17 @@ __device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p
         const uint32_t sc = g[8 * n + 2 * j + half];
         dl = h2f_hw(dd & 0xffffu) * (float)(sc & 0xFu);
         c = -(h2f_hw(dd >> 16) * (float)(sc >> 4));
-        load_run<4, 8>(g + 16 + 32 * n + 16 * half + l, uw);
-        uw[0] = (uw[0] >> (2 * j)) & 0x03030303u;
-        uw[1] = (uw[1] >> (2 * j)) & 0x03030303u;
+        load_run<4, R>(g + 16 + 32 * n + 16 * half + l, uw);
+#pragma unroll
+        for (int i = 0; i < W; ++i) uw[i] = (uw[i] >> (2 * j)) & 0x03030303u;
     }
 #pragma unroll
-    for (int r = 0; r < 8; ++r) y[r] = fmaf(dl, (float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu), c);
+    for (int r = 0; r < R; ++r) y[r] = fmaf(dl, (float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu), c);
+}
+
+template <int QT>
+__device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p, float (&y)[8]) {
+    decode_mix<QT, 8>(g, p, y);
 }
 
 // Runtime-type dispatch (the type is uniform across a wave).

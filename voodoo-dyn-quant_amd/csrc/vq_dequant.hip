@@ -88,8 +88,9 @@ hipError_t launch_dequant_bf16(int qtype, const uint8_t* q, bf16_t* out, int64_t
 // Mixture: W_eff = bf16( (((0 + p0 W0) + p1 W1) + ...) ) with every product and
 // sum rounded separately, exactly as the fp32 torch ops of the reference.
 // One launch mixes up to kMaxSets tensors (the members of a stacked
-// product); a workgroup covers RUNS * 8 groups of one tensor, so small
-// tensors get more, shorter workgroups.
+// product); a workgroup covers RUNS * 16 groups of one tensor, so small
+// tensors get more, shorter workgroups.  A thread takes 16 consecutive
+// weights of a group per run (one scale decode per candidate and run).
 // ---------------------------------------------------------------------------
 struct MixPlan {
     int nsets;
@@ -100,10 +101,13 @@ struct MixPlan {
     int64_t block0[kMaxSets + 1];  // first workgroup of each set
 };
 
+constexpr int kMixRun = 16;                                     // weights per thread and run
+constexpr int kMixGroupsPerPass = kStreamThreads * kMixRun / 256;  // 16
+
 template <int RUNS>
 __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int GPB = kStreamThreads * 8 * RUNS / 256;  // groups per workgroup
+    constexpr int GPB = kMixGroupsPerPass * RUNS;  // groups per workgroup
     int si = 0;
 #pragma unroll
     for (int q = 1; q < kMaxSets; ++q)
@@ -121,27 +125,27 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
     const int t = threadIdx.x;
     const float* probs = mp.probs[si];
     bf16_t* w_eff = mp.out[si];
+    const int p = kMixRun * (t & 15);
 #pragma unroll
     for (int u = 0; u < RUNS; ++u) {
-        const int j = (t >> 5) + 8 * u;
+        const int j = (t >> 4) + kMixGroupsPerPass * u;
         if (j >= ng) continue;
-        float mixed[8];
+        float mixed[kMixRun];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) mixed[r] = 0.0f;
+        for (int r = 0; r < kMixRun; ++r) mixed[r] = 0.0f;
         int off = 0;
         for (int k = 0; k < cs.ncand; ++k) {
             const int qt = cs.qtype[k];
             const int gb = group_bytes(qt);
-            float w[8];
+            float w[kMixRun];
             const uint8_t* g = lds + off + j * gb;
-            const int p = 8 * (t & 31);
             switch (qt) {
-            case Q8_0: decode8_mix<Q8_0>(g, p, w); break;
-            case Q2_K: decode8_mix<Q2_K>(g, p, w); break;
-            case Q3_K: decode8_mix<Q3_K>(g, p, w); break;
-            case Q4_K: decode8_mix<Q4_K>(g, p, w); break;
-            case Q5_K: decode8_mix<Q5_K>(g, p, w); break;
-            default: decode8_mix<Q6_K>(g, p, w); break;
+            case Q8_0: decode_mix<Q8_0, kMixRun>(g, p, w); break;
+            case Q2_K: decode_mix<Q2_K, kMixRun>(g, p, w); break;
+            case Q3_K: decode_mix<Q3_K, kMixRun>(g, p, w); break;
+            case Q4_K: decode_mix<Q4_K, kMixRun>(g, p, w); break;
+            case Q5_K: decode_mix<Q5_K, kMixRun>(g, p, w); break;
+            default: decode_mix<Q6_K, kMixRun>(g, p, w); break;
             }
             off += (GPB * gb + 15) & ~15;
             const float pk = probs[k];
@@ -149,15 +153,20 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
                 // product and sum rounded separately, like the two torch ops
 #pragma clang fp contract(off)
 #pragma unroll
-                for (int r = 0; r < 8; ++r) mixed[r] = mixed[r] + pk * w[r];
+                for (int r = 0; r < kMixRun; ++r) mixed[r] = mixed[r] + pk * w[r];
             }
         }
-        uint4 v;
-        v.x = f2bf2(mixed[0], mixed[1]);
-        v.y = f2bf2(mixed[2], mixed[3]);
-        v.z = f2bf2(mixed[4], mixed[5]);
-        v.w = f2bf2(mixed[6], mixed[7]);
-        *reinterpret_cast<uint4*>(w_eff + (g0 + j) * 256 + 8 * (t & 31)) = v;
+        uint4 v[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v[h].x = f2bf2(mixed[8 * h + 0], mixed[8 * h + 1]);
+            v[h].y = f2bf2(mixed[8 * h + 2], mixed[8 * h + 3]);
+            v[h].z = f2bf2(mixed[8 * h + 4], mixed[8 * h + 5]);
+            v[h].w = f2bf2(mixed[8 * h + 6], mixed[8 * h + 7]);
+        }
+        uint4* o = reinterpret_cast<uint4*>(w_eff + (g0 + j) * 256 + p);
+        o[0] = v[0];
+        o[1] = v[1];
     }
 }
 
@@ -167,9 +176,17 @@ hipError_t launch_mix_sets(int nsets, const CandSet* sets, const float* const* p
     mp.nsets = nsets;
     int64_t total = 0;
     for (int i = 0; i < nsets; ++i) total += ngroups[i];
-    // workgroups of 8 groups when 16-group ones would not give every CU two
-    const bool small = (total + 15) / 16 < 2 * (int64_t)device_cus();
-    const int gpb = small ? 8 : 16;
+    // 16-group workgroups when 32-group ones would not give every CU two, or
+    // would stage more than 64 KiB (wide menus of large formats)
+    size_t lds32 = 0;
+    for (int i = 0; i < nsets; ++i) {
+        size_t l = 0;
+        for (int k = 0; k < sets[i].ncand; ++k) l += (2 * kMixGroupsPerPass * group_bytes(sets[i].qtype[k]) + 15) & ~15;
+        lds32 = l > lds32 ? l : lds32;
+    }
+    const bool small = (total + 2 * kMixGroupsPerPass - 1) / (2 * kMixGroupsPerPass) < 2 * (int64_t)device_cus() ||
+                       lds32 > 64 * 1024;
+    const int gpb = small ? kMixGroupsPerPass : 2 * kMixGroupsPerPass;
     size_t lds = 0;
     int64_t blocks = 0;
     for (int i = 0; i < nsets; ++i) {
