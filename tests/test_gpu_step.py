@@ -164,3 +164,60 @@ def test_swiglu_stack_steps_with_repeated_formats():
     after = torch.cat([m.gates.detach() for m in replaced.values()])
     assert torch.isfinite(after).all() and float((after - before).abs().max()) > 1e-3
     assert len(replaced) == 6 and all(m.num_candidates == 8 for m in replaced.values())
+
+
+def test_gate_bank_gradients_match_per_module_gates():
+    """GateBank (one softmax for all gates, rows handed to the modules) gives
+    the per-module path's gate gradients and effective bytes, and the
+    trainer's first steps agree."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    base = st.build_models(CFG, TYPES, dev, seed=7, packed=False)
+    a, b = copy.deepcopy(base), copy.deepcopy(base)
+    x, y = _batch(dev)
+    tau = 0.8
+    # per-module gates
+    st_b, te_b, rep_b = b
+    trainer.set_temperature_all(rep_b, tau)
+    bytes_b = layers.total_effective_bytes(rep_b).to(dev)
+    (_loss(st_b, te_b, x, y) + 1e-9 * bytes_b).backward()
+    grad_b = torch.cat([m.gates.grad for m in rep_b.values()])
+    # bank
+    st_a, te_a, rep_a = a
+    trainer.set_temperature_all(rep_a, tau)
+    bank = trainer.GateBank(rep_a.values())
+    assert len(bank.parameters()) == 1 and bank.parameters()[0].shape == (len(rep_a), len(TYPES))
+    bytes_a = bank.begin(tau)
+    (_loss(st_a, te_a, x, y) + 1e-9 * bytes_a).backward()
+    bank.end()
+    grad_a = bank.parameters()[0].grad.reshape(-1)
+    assert float(bytes_a) == pytest.approx(float(bytes_b), rel=1e-6)
+    assert float((grad_a - grad_b).norm() / grad_b.norm()) < 1e-5
+    # the modules' gates read the bank; release gives independent parameters back
+    with torch.no_grad():
+        bank.parameters()[0].add_(1.0)
+    assert float(next(iter(rep_a.values())).gates[0]) == pytest.approx(float(next(iter(rep_b.values())).gates[0]) + 1.0)
+    bank.release()
+    assert all(m.gates.requires_grad and m.gates.grad is None for m in rep_a.values())
+
+
+def test_gate_bank_trainer_matches_per_module_trainer():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    base = st.build_models(CFG, TYPES, dev, seed=8, packed=False)
+    a, b = copy.deepcopy(base), copy.deepcopy(base)
+    x, y = _batch(dev)
+    ta = st.GateTrainer(*a, st.StepConfig(max_steps=3), float(CFG.gated_weights()))
+    tb = st.GateTrainer(*b, st.StepConfig(max_steps=3, gate_bank=False), float(CFG.gated_weights()))
+    assert ta.bank is not None and tb.bank is None
+    for _ in range(3):
+        oa, ob = ta.step(x, y), tb.step(x, y)
+        for k in ("lm", "kl", "size"):
+            assert float(oa[k]) == pytest.approx(float(ob[k]), rel=1e-4, abs=1e-6), k
+    ga = torch.cat([m.gates.detach() for m in a[2].values()])
+    gb = torch.cat([m.gates.detach() for m in b[2].values()])
+    assert float((ga - gb).abs().max()) < 1e-3

@@ -385,3 +385,38 @@ def test_total_effective_bytes_batches_like_the_per_layer_sum(isolated_cache):
         c = torch.tensor(m._bytes_per_candidate(), dtype=torch.float64)
         grad_ref = (torch.diag(p) - torch.outer(p, p)) @ c / m.temperature
         assert torch.allclose(m.gates.grad.double(), grad_ref, rtol=1e-4)
+
+
+def test_gate_bank_rows_bytes_and_release(isolated_cache):
+    """GateBank: one [T, K] parameter per candidate count; each module's
+    soft_probs is its row of one softmax, the bank's bytes equal the
+    per-layer sum, gradients land in the bank, and release() gives each
+    module an independent parameter with the trained values."""
+    from voodoo_quant.training import trainer
+
+    mods = {f"l{i}": _lin(types=t, out_f=16, in_f=256, name=f"gb.{i}", seed=i)
+            for i, t in enumerate([("Q2_K", "Q4_K", "Q8_0"), ("Q3_K", "Q6_K"), ("Q2_K", "Q5_K", "Q8_0")])}
+    g = torch.Generator().manual_seed(5)
+    for m in mods.values():
+        with torch.no_grad():
+            m.gates.copy_(torch.randn(m.num_candidates, generator=g))
+        m.set_temperature(0.7)
+    expect_probs = {n: m.soft_probs().detach().clone() for n, m in mods.items()}
+    expect_bytes = float(layers.total_effective_bytes(mods))
+    bank = trainer.GateBank(mods.values())
+    assert sorted(p.shape for p in bank.parameters()) == [(1, 2), (2, 3)]
+    total = bank.begin(0.7)
+    assert float(total) == pytest.approx(expect_bytes, rel=1e-6)
+    for n, m in mods.items():
+        assert torch.allclose(m.soft_probs(), expect_probs[n], rtol=1e-6, atol=1e-7)
+    total.backward()
+    bank.end()
+    assert all(m.__dict__.get("_probs_override") is None for m in mods.values())
+    assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in bank.parameters())
+    with torch.no_grad():
+        for p in bank.parameters():
+            p.mul_(2.0)
+    doubled = {n: m.gates.detach().clone() for n, m in mods.items()}
+    bank.release()
+    for n, m in mods.items():
+        assert m.gates.requires_grad and torch.equal(m.gates.detach(), doubled[n])

@@ -564,6 +564,11 @@ class _MixedQuantBase(nn.Module):
         self.temperature = max(temperature, 1e-6)
 
     def soft_probs(self) -> torch.Tensor:
+        # a GateBank computes every bank member's softmax in one launch and
+        # hands each module its row for the step
+        override = self.__dict__.get("_probs_override")
+        if override is not None:
+            return override
         return F.softmax(self.gates / self.temperature, dim=0)
 
     def get_probs(self) -> torch.Tensor:

@@ -370,6 +370,7 @@ class StepConfig:
     target_fraction: float = 0.45   # of 8-bit bytes
     logits_chunk: int = 0
     fused_loss: bool = True         # CE + KL on the HIP kernels (full-logits path)
+    gate_bank: bool = True          # one softmax launch for all gates (trainer.GateBank)
 
 
 class GateTrainer:
@@ -378,7 +379,10 @@ class GateTrainer:
     def __init__(self, student: Decoder, teacher: Decoder, replaced: dict[str, nn.Module], cfg: StepConfig,
                  total_8bit_bytes: float, non_targeted_bytes: float = 0.0):
         self.student, self.teacher, self.replaced, self.cfg = student, teacher, replaced, cfg
-        self.trainable = [m.gates for m in replaced.values()]
+        # the chunked loss runs one backward per chunk, so its probabilities
+        # must come from each module's own graph
+        self.bank = trainer.GateBank(replaced.values()) if cfg.gate_bank and cfg.logits_chunk == 0 else None
+        self.trainable = self.bank.parameters() if self.bank else [m.gates for m in replaced.values()]
         self.opt, self.sched = trainer.build_gate_optimizer(self.trainable, cfg.lr, cfg.max_steps)
         self.target_bytes = cfg.target_fraction * total_8bit_bytes
         self.non_targeted_bytes = non_targeted_bytes
@@ -391,23 +395,30 @@ class GateTrainer:
         trainer.set_temperature_all(self.replaced, tau)
         dev = x.device
         t = c.distill_temperature
-        if c.logits_chunk > 0:
-            lm, kl = trainer.chunked_forward_loss(self.student, self.teacher, x, y, t, c.logits_chunk)
-            lm_loss, distill = torch.tensor(lm), torch.tensor(kl)
-        else:
-            logits = self.student(x)
-            with torch.no_grad():
-                t_logits = self.teacher(x)
-            fused = c.fused_loss and logits.is_cuda and logits.dtype == torch.bfloat16 and logits.size(-1) % 8 == 0
-            losses = trainer.distill_losses_fused if fused else trainer.distill_losses
-            lm_loss, distill = losses(logits, t_logits, y, t)
-        current = layers.total_effective_bytes(self.replaced).to(dev) + self.non_targeted_bytes
-        size = trainer.size_loss(current, self.target_bytes, c.size_tolerance)
-        if c.logits_chunk > 0:
-            (c.size_weight * size).backward()
-        else:
-            loss = lm_loss + c.distill_weight * distill + c.size_weight * size
-            loss.backward()
+        bank_bytes = self.bank.begin(tau) if self.bank else None
+        try:
+            if c.logits_chunk > 0:
+                lm, kl = trainer.chunked_forward_loss(self.student, self.teacher, x, y, t, c.logits_chunk)
+                lm_loss, distill = torch.tensor(lm), torch.tensor(kl)
+            else:
+                logits = self.student(x)
+                with torch.no_grad():
+                    t_logits = self.teacher(x)
+                fused = (c.fused_loss and logits.is_cuda and logits.dtype == torch.bfloat16
+                         and logits.size(-1) % 8 == 0)
+                losses = trainer.distill_losses_fused if fused else trainer.distill_losses
+                lm_loss, distill = losses(logits, t_logits, y, t)
+            gated = bank_bytes if bank_bytes is not None else layers.total_effective_bytes(self.replaced)
+            current = gated.to(dev) + self.non_targeted_bytes
+            size = trainer.size_loss(current, self.target_bytes, c.size_tolerance)
+            if c.logits_chunk > 0:
+                (c.size_weight * size).backward()
+            else:
+                loss = lm_loss + c.distill_weight * distill + c.size_weight * size
+                loss.backward()
+        finally:
+            if self.bank:
+                self.bank.end()
         trainer.gate_optimizer_step(self.trainable, self.opt, self.sched, max_norm=1.0)
         self.step_index += 1
         return {"lm": lm_loss.detach(), "kl": distill.detach(), "size": size.detach(), "tau": tau}
@@ -497,7 +508,8 @@ class StackTrainer:
 
     def __init__(self, student, teacher, replaced, cfg: StepConfig, total_8bit_bytes: float):
         self.student, self.teacher, self.replaced, self.cfg = student, teacher, replaced, cfg
-        self.trainable = [m.gates for m in replaced.values()]
+        self.bank = trainer.GateBank(replaced.values()) if cfg.gate_bank else None
+        self.trainable = self.bank.parameters() if self.bank else [m.gates for m in replaced.values()]
         self.opt, self.sched = trainer.build_gate_optimizer(self.trainable, cfg.lr, cfg.max_steps)
         self.target_bytes = cfg.target_fraction * total_8bit_bytes
         self.step_index = 0
@@ -506,13 +518,18 @@ class StackTrainer:
         c = self.cfg
         tau = trainer.anneal_temperature(self.step_index, c.max_steps, c.temp_start, c.temp_end)
         trainer.set_temperature_all(self.replaced, tau)
-        y = self.student(x)
-        with torch.no_grad():
-            t = self.teacher(x).float()
-        mse = ((y.float() - t) ** 2).mean() / (t ** 2).mean()
-        size = trainer.size_loss(layers.total_effective_bytes(self.replaced).to(x.device), self.target_bytes,
-                                 c.size_tolerance)
-        (mse + c.size_weight * size).backward()
+        bank_bytes = self.bank.begin(tau) if self.bank else None
+        try:
+            y = self.student(x)
+            with torch.no_grad():
+                t = self.teacher(x).float()
+            mse = ((y.float() - t) ** 2).mean() / (t ** 2).mean()
+            gated = bank_bytes if bank_bytes is not None else layers.total_effective_bytes(self.replaced)
+            size = trainer.size_loss(gated.to(x.device), self.target_bytes, c.size_tolerance)
+            (mse + c.size_weight * size).backward()
+        finally:
+            if self.bank:
+                self.bank.end()
         trainer.gate_optimizer_step(self.trainable, self.opt, self.sched, max_norm=1.0)
         self.step_index += 1
         return {"mse": mse.detach(), "size": size.detach(), "tau": tau}

@@ -59,6 +59,63 @@ def build_gate_optimizer(trainable: list[torch.nn.Parameter], lr: float, max_ste
     return opt, sched
 
 
+class GateBank:
+    """The gate logits of many gated tensors as one [T, K] parameter per
+    (candidate count, device) group.
+
+    The reference trains one [K] parameter per gated tensor and each layer
+    takes its own softmax (``layers.py:1729-1731``); with ~170 tensors that
+    is ~170 softmaxes forward, ~170 backward and the scale ops around them,
+    each a launch on a few bytes.  Here one softmax per group runs at the
+    start of a step and each module reads its row (``soft_probs``); autograd
+    brings the modules' gate gradients back as one stacked tensor.  The
+    values and the optimizer update are the same elementwise: AdamW, the
+    global-norm clip and the dead-zone size penalty see the same numbers.
+    Each module's ``gates`` becomes a row view of its bank, so reading a
+    module's gates (argmax, export) sees the trained values."""
+
+    def __init__(self, modules) -> None:
+        groups: dict[tuple, list] = {}
+        for m in modules:
+            groups.setdefault((m.num_candidates, m.gates.device), []).append(m)
+        self.groups = []
+        for (_, dev), mods in groups.items():
+            bank = torch.nn.Parameter(torch.stack([m.gates.detach() for m in mods]).contiguous())
+            for i, m in enumerate(mods):
+                m.gates = torch.nn.Parameter(bank.data[i], requires_grad=False)
+            coef = torch.tensor([m._bytes_per_candidate() for m in mods], dtype=torch.float32).to(dev)
+            self.groups.append((bank, mods, coef))
+
+    def parameters(self) -> list:
+        return [bank for bank, _, _ in self.groups]
+
+    def begin(self, temperature: float) -> torch.Tensor:
+        """Softmax every bank at `temperature`, hand each module its row, and
+        return the differentiable effective bytes (sum of p_k * bytes_k)."""
+        total = None
+        for bank, mods, coef in self.groups:
+            probs = torch.nn.functional.softmax(bank / max(temperature, 1e-6), dim=1)
+            for m, row in zip(mods, probs.unbind(0)):
+                m._probs_override = row
+            b = (probs * coef).sum()
+            total = b if total is None else total + b
+        return total if total is not None else torch.tensor(0.0)
+
+    def end(self) -> None:
+        for _, mods, _ in self.groups:
+            for m in mods:
+                m._probs_override = None
+
+    def release(self) -> None:
+        """Give every module back an independent gates parameter (the bank's
+        current values)."""
+        self.end()
+        for bank, mods, _ in self.groups:
+            for i, m in enumerate(mods):
+                m.gates = torch.nn.Parameter(bank.detach()[i].clone())
+        self.groups = []
+
+
 def gate_optimizer_step(trainable, opt, sched, max_norm: float = 1.0) -> None:
     torch.nn.utils.clip_grad_norm_(trainable, max_norm=max_norm)
     opt.step()
