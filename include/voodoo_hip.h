@@ -190,6 +190,18 @@ int vq_rope_qkv_bwd(const uint16_t *dq, const uint16_t *dk, const uint16_t *dv, 
 int vq_swiglu_fwd(const uint16_t *gu, int64_t tokens, int64_t F, uint16_t *out, void *stream);
 int vq_swiglu_bwd(const uint16_t *gu, const uint16_t *dy, int64_t tokens, int64_t F, uint16_t *dgu, void *stream);
 
+/* Residual add + RMSNorm in one pass over rows of dim bf16 (dim % 8 == 0):
+ * s = h + a (bf16, torch's add; a may be NULL: a plain RMSNorm of h, s_out
+ * unused), n = s * rstd * w with rstd = 1 / sqrt(mean(s^2) + eps) in fp32
+ * and one bf16 rounding (F.rms_norm).  rstd_out (fp32 [rows]) and s_out may
+ * be NULL when no backward follows.  vq_rmsnorm_bwd: dh = ds + rstd (dn w -
+ * s rstd mean(dn w s rstd)), the gradient of both h and a (ds may be NULL);
+ * the norm weight's gradient is not formed (the trainer freezes it). */
+int vq_add_rmsnorm_fwd(const uint16_t *h, const uint16_t *a, const uint16_t *w, int64_t rows, int64_t dim, float eps,
+                       uint16_t *s_out, uint16_t *n_out, float *rstd_out, void *stream);
+int vq_rmsnorm_bwd(const uint16_t *dn, const uint16_t *ds, const uint16_t *s, const uint16_t *w, const float *rstd,
+                   int64_t rows, int64_t dim, uint16_t *dh, void *stream);
+
 /* Workspace bytes of the distillation loss (per-row log-sum-exps and losses;
  * written by vq_distill_loss_fwd, read by vq_distill_loss_bwd). */
 int64_t vq_distill_loss_workspace(int64_t rows);

@@ -1,6 +1,7 @@
 """The decoder glue kernels of the step harness (rotary embedding with
-grouped-query K/V expansion, SwiGLU) against fp32 torch, forward and
-backward.  Bar: 1e-2 relative L2 (bf16 inputs and outputs, fp32 inside)."""
+grouped-query K/V expansion, SwiGLU, residual add + RMSNorm) against fp32
+torch, forward and backward.  Bar: 1e-2 relative L2 (bf16 inputs and
+outputs, fp32 inside); the residual add is torch's bf16 add bit for bit."""
 
 import pytest
 import torch
@@ -65,3 +66,57 @@ def test_swiglu_matches_torch(t, f):
     yr.backward(dy.float())
     assert _rel(y.cpu(), yr.detach()) < 1e-2
     assert _rel(x.grad.cpu(), xr.grad) < 1e-2
+
+
+@pytest.mark.parametrize("rows,dim,with_add", [(300, 1024, True), (7, 4096, True), (65, 1032, False), (1, 8, True)])
+def test_add_rmsnorm_matches_torch(rows, dim, with_add):
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    print(f"[add_rmsnorm] rows={rows} dim={dim} add={with_add}", flush=True)
+    g = torch.Generator().manual_seed(rows + dim)
+    eps = 1e-6
+    h = torch.randn(rows, dim, generator=g).to(torch.bfloat16).cuda()
+    a = torch.randn(rows, dim, generator=g).to(torch.bfloat16).cuda() if with_add else None
+    w = (1.0 + 0.1 * torch.randn(dim, generator=g)).to(torch.bfloat16).cuda()
+    hh = h.clone().requires_grad_(True)
+    aa = a.clone().requires_grad_(True) if with_add else None
+    s, n = st._AddRMSNorm.apply(hh, aa, w, eps)
+    s_ref = h + a if with_add else h
+    assert torch.equal(s.detach(), s_ref)  # torch's bf16 add, bit for bit
+    x = s_ref.float().requires_grad_(True)
+    n_ref = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+    assert _rel(n.detach().float(), n_ref.detach()) < 1e-2
+    # backward: ds from the residual path, dn from the normed output
+    ds = torch.randn(rows, dim, generator=g).to(torch.bfloat16).cuda()
+    dn = torch.randn(rows, dim, generator=g).to(torch.bfloat16).cuda()
+    (s.float() * ds.float()).sum().add((n.float() * dn.float()).sum()).backward()
+    (n_ref * dn.float()).sum().backward()
+    dh_ref = x.grad + ds.float()  # s is h itself without the add
+    assert _rel(hh.grad.float(), dh_ref) < 1e-2
+    if with_add:
+        assert torch.equal(aa.grad, hh.grad)
+
+
+def test_fused_norm_body_matches_unfused(monkeypatch):
+    """The decoder body with every residual add fused into the following
+    RMSNorm gives the unfused body's output and gate gradients."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    import copy
+    cfg = st.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, mlp=512, vocab=1000)
+    torch.manual_seed(0)
+    student, _, replaced = st.build_models(cfg, ["Q2_K", "Q4_K", "Q8_0"], torch.device("cuda", 0), seed=4, packed=False)
+    other = copy.deepcopy(student)
+    ids = torch.randint(0, cfg.vocab, (2, 64), device="cuda", generator=torch.Generator(device="cuda").manual_seed(1))
+    out_f = student(ids)
+    out_f.float().pow(2).mean().backward()
+    with monkeypatch.context() as mp:
+        mp.setattr(st, "_fused_norms", lambda h, w: False)
+        out_u = other(ids)
+        out_u.float().pow(2).mean().backward()
+    assert _rel(out_f.detach().float(), out_u.detach().float()) < 1e-2
+    names = list(replaced)
+    mods_o = dict(other.named_modules())
+    gf = torch.cat([replaced[nm].gates.grad for nm in names])
+    gu = torch.cat([mods_o[nm].gates.grad for nm in names])
+    assert _rel(gf, gu) < 3e-2

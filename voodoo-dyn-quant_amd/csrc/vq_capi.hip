@@ -379,6 +379,48 @@ int vq_swiglu_bwd(const uint16_t* gu, const uint16_t* dy, int64_t tokens, int64_
     return rc == VQ_OK ? ok() : rc;
 }
 
+static int check_norm(int64_t rows, int64_t dim) {
+    if (rows < 0 || dim <= 0 || dim > INT32_MAX)
+        return fail(VQ_ERR_SHAPE, "rows=%lld dim=%lld", (long long)rows, (long long)dim);
+    if (dim % 8) return fail(VQ_ERR_ALIGN, "dim=%lld must be a multiple of 8", (long long)dim);
+    return VQ_OK;
+}
+
+int vq_add_rmsnorm_fwd(const uint16_t* h, const uint16_t* a, const uint16_t* w, int64_t rows, int64_t dim, float eps,
+                       uint16_t* s_out, uint16_t* n_out, float* rstd_out, void* stream) {
+    int rc = check_norm(rows, dim);
+    if (rc != VQ_OK) return rc;
+    if (!(eps >= 0.0f)) return fail(VQ_ERR_SHAPE, "eps must be >= 0");
+    if (rows == 0) return ok();
+    if (!h || !w || !n_out) return fail(VQ_ERR_NULL, "h/w/n_out is NULL");
+    if (!aligned16(h) || !aligned16(w) || !aligned16(n_out) || (a && !aligned16(a)) || (s_out && !aligned16(s_out)))
+        return fail(VQ_ERR_ALIGN, "h/a/w/s_out/n_out not 16-byte aligned");
+    rc = hip_check(vq::launch_add_rmsnorm_fwd(reinterpret_cast<const vq::bf16_t*>(h),
+                                              reinterpret_cast<const vq::bf16_t*>(a),
+                                              reinterpret_cast<const vq::bf16_t*>(w), rows, (int)dim, eps,
+                                              reinterpret_cast<vq::bf16_t*>(s_out), reinterpret_cast<vq::bf16_t*>(n_out),
+                                              rstd_out, static_cast<hipStream_t>(stream)),
+                   "add_rmsnorm launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
+int vq_rmsnorm_bwd(const uint16_t* dn, const uint16_t* ds, const uint16_t* s, const uint16_t* w, const float* rstd,
+                   int64_t rows, int64_t dim, uint16_t* dh, void* stream) {
+    int rc = check_norm(rows, dim);
+    if (rc != VQ_OK) return rc;
+    if (rows == 0) return ok();
+    if (!dn || !s || !w || !rstd || !dh) return fail(VQ_ERR_NULL, "dn/s/w/rstd/dh is NULL");
+    if (!aligned16(dn) || !aligned16(s) || !aligned16(w) || !aligned16(dh) || (ds && !aligned16(ds)))
+        return fail(VQ_ERR_ALIGN, "dn/ds/s/w/dh not 16-byte aligned");
+    rc = hip_check(vq::launch_rmsnorm_bwd(reinterpret_cast<const vq::bf16_t*>(dn),
+                                          reinterpret_cast<const vq::bf16_t*>(ds),
+                                          reinterpret_cast<const vq::bf16_t*>(s),
+                                          reinterpret_cast<const vq::bf16_t*>(w), rstd, rows, (int)dim,
+                                          reinterpret_cast<vq::bf16_t*>(dh), static_cast<hipStream_t>(stream)),
+                   "rmsnorm backward launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int64_t vq_distill_loss_workspace(int64_t rows) {
     if (rows < 0) return -1;
     return align256((5 * rows + 2) * (int64_t)sizeof(float));

@@ -9,6 +9,11 @@
 //              stacked layout the grouped backward reads).
 //   swiglu:    the stacked gate/up output [tokens][2F] -> silu(g) * u [tokens][F],
 //              and its gradient back into [tokens][2F].
+//   add_rmsnorm: the residual add and the RMSNorm that follows it, one pass:
+//              s = h + a (bf16, as torch's add), n = s * rstd * w with
+//              rstd = 1 / sqrt(mean(s^2) + eps); its backward
+//              dh = ds + rstd (dn w - s rstd mean(dn w s rstd)) is also the
+//              gradient of a (the add passes it to both).
 // Arithmetic in fp32, one bf16 rounding per output (torch's separate bf16
 // ops round after each op).
 #include "vq_internal.h"
@@ -166,6 +171,97 @@ __global__ __launch_bounds__(256) void rope_qkv_bwd_kernel(const bf16_t* __restr
     st8(dst + half + d0, o2);
 }
 
+// One wave per row, 8 consecutive elements per lane and step.
+constexpr int kNormWaves = 4;
+
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float((uint32_t)f2bf(x) << 16); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(64 * kNormWaves) void add_rmsnorm_fwd_kernel(
+    const bf16_t* __restrict__ h, const bf16_t* __restrict__ a, const bf16_t* __restrict__ w, int64_t rows, int dim,
+    float eps, bf16_t* __restrict__ s_out, bf16_t* __restrict__ n_out, float* __restrict__ rstd_out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * kNormWaves + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int64_t base = r * dim;
+    float ss = 0.0f;
+    for (int c = 8 * lane; c < dim; c += 512) {
+        float x[8];
+        ld8(h + base + c, x);
+        if (a) {
+            float y[8];
+            ld8(a + base + c, y);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = bf16_round(x[j] + y[j]);
+            if (s_out) st8(s_out + base + c, x);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+    }
+    const float rstd = rsqrtf(wave_sum(ss) / (float)dim + eps);
+    if (rstd_out && lane == 0) rstd_out[r] = rstd;
+    for (int c = 8 * lane; c < dim; c += 512) {
+        float x[8], wv[8];
+        if (a && s_out) {
+            ld8(s_out + base + c, x);  // this lane's own stores
+        } else {
+            ld8(h + base + c, x);
+            if (a) {
+                float y[8];
+                ld8(a + base + c, y);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = bf16_round(x[j] + y[j]);
+            }
+        }
+        ld8(w + c, wv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = x[j] * rstd * wv[j];
+        st8(n_out + base + c, x);
+    }
+}
+
+__global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_kernel(
+    const bf16_t* __restrict__ dn, const bf16_t* __restrict__ ds, const bf16_t* __restrict__ s,
+    const bf16_t* __restrict__ w, const float* __restrict__ rstd_in, int64_t rows, int dim, bf16_t* __restrict__ dh) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * kNormWaves + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int64_t base = r * dim;
+    const float rstd = rstd_in[r];
+    float dot = 0.0f;  // sum dn w s
+    for (int c = 8 * lane; c < dim; c += 512) {
+        float g[8], x[8], wv[8];
+        ld8(dn + base + c, g);
+        ld8(s + base + c, x);
+        ld8(w + c, wv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dot += g[j] * wv[j] * x[j];
+    }
+    // mean(g xhat) with xhat = s rstd, times rstd once more for the xhat term
+    const float k = wave_sum(dot) * rstd * rstd / (float)dim;
+    for (int c = 8 * lane; c < dim; c += 512) {
+        float g[8], x[8], wv[8];
+        ld8(dn + base + c, g);
+        ld8(s + base + c, x);
+        ld8(w + c, wv);
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = rstd * (g[j] * wv[j] - x[j] * k);
+        if (ds) {
+            float d[8];
+            ld8(ds + base + c, d);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] += d[j];
+        }
+        st8(dh + base + c, o);
+    }
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // out[m][j] = silu(gu[m][j]) * gu[m][F + j]; one thread per 8 outputs.
@@ -224,6 +320,22 @@ hipError_t launch_rope_qkv_bwd(const bf16_t* dq, const bf16_t* dk, const bf16_t*
     if (items == 0) return hipSuccess;
     rope_qkv_bwd_kernel<<<blocks_for(items), 256, 0, s>>>(dq, dk, dv, sb, sh, ss, tokens, S, Hq, Hkv, D, cosb, sinb,
                                                           dqkv);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm_fwd(const bf16_t* h, const bf16_t* a, const bf16_t* w, int64_t rows, int dim, float eps,
+                                 bf16_t* s_out, bf16_t* n_out, float* rstd_out, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const dim3 grid((unsigned)((rows + kNormWaves - 1) / kNormWaves));
+    add_rmsnorm_fwd_kernel<<<grid, 64 * kNormWaves, 0, s>>>(h, a, w, rows, dim, eps, s_out, n_out, rstd_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_bwd(const bf16_t* dn, const bf16_t* ds, const bf16_t* x, const bf16_t* w, const float* rstd,
+                              int64_t rows, int dim, bf16_t* dh, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const dim3 grid((unsigned)((rows + kNormWaves - 1) / kNormWaves));
+    rmsnorm_bwd_kernel<<<grid, 64 * kNormWaves, 0, s>>>(dn, ds, x, w, rstd, rows, dim, dh);
     return hipGetLastError();
 }
 

@@ -72,6 +72,10 @@ hipError_t launch_rope_qkv_bwd(const bf16_t* dq, const bf16_t* dk, const bf16_t*
                                int64_t ss, int64_t tokens, int S, int Hq, int Hkv, int D, const float* cosb,
                                const float* sinb, bf16_t* dqkv, hipStream_t s);
 hipError_t launch_swiglu_fwd(const bf16_t* gu, int64_t tokens, int F, bf16_t* out, hipStream_t s);
+hipError_t launch_add_rmsnorm_fwd(const bf16_t* h, const bf16_t* a, const bf16_t* w, int64_t rows, int dim, float eps,
+                                 bf16_t* s_out, bf16_t* n_out, float* rstd_out, hipStream_t s);
+hipError_t launch_rmsnorm_bwd(const bf16_t* dn, const bf16_t* ds, const bf16_t* x, const bf16_t* w, const float* rstd,
+                              int64_t rows, int dim, bf16_t* dh, hipStream_t s);
 hipError_t launch_swiglu_bwd(const bf16_t* gu, const bf16_t* dy, int64_t tokens, int F, bf16_t* dgu, hipStream_t s);
 
 // Distillation loss over full logits (vq_loss.hip).  ws: 5 * rows + 2 floats

@@ -41,6 +41,8 @@ _SIGNATURES = [
     ("vq_rope_qkv_bwd", _i, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _p, _p, _p]),
     ("vq_swiglu_fwd", _i, [_p, _i64, _i64, _p, _p]),
     ("vq_swiglu_bwd", _i, [_p, _p, _i64, _i64, _p, _p]),
+    ("vq_add_rmsnorm_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _p]),
+    ("vq_rmsnorm_bwd", _i, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p]),
     ("vq_distill_loss_workspace", _i64, [_i64]),
     ("vq_distill_loss_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _i64, _p]),
     ("vq_distill_loss_bwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _i64, _p]),
@@ -328,6 +330,30 @@ def swiglu_bwd(gu: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
                                _stream(gu.device)),
            "vq_swiglu_bwd")
     return dgu
+
+
+def add_rmsnorm_fwd(h: torch.Tensor, a: torch.Tensor | None, w: torch.Tensor, eps: float,
+                    need_backward: bool = True):
+    """(s, n, rstd): s = h + a (None when a is None), n = rms_norm(s) * w,
+    rstd fp32 [rows] (None without a backward).  h, a: [rows, dim] bf16."""
+    rows, dim = h.shape
+    s = torch.empty_like(h) if a is not None else None
+    n = torch.empty_like(h)
+    rstd = torch.empty(rows, dtype=torch.float32, device=h.device) if need_backward else None
+    _check(lib().vq_add_rmsnorm_fwd(_dev_ptr(h, "h"), _dev_ptr(a, "a"), _dev_ptr(w, "w"), rows, dim, float(eps),
+                                    _dev_ptr(s, "s"), _dev_ptr(n, "n"), _dev_ptr(rstd, "rstd"), _stream(h.device)),
+           "vq_add_rmsnorm_fwd")
+    return s, n, rstd
+
+
+def rmsnorm_bwd(dn: torch.Tensor, ds: torch.Tensor | None, s: torch.Tensor, w: torch.Tensor,
+                rstd: torch.Tensor) -> torch.Tensor:
+    rows, dim = s.shape
+    dh = torch.empty_like(s)
+    _check(lib().vq_rmsnorm_bwd(_dev_ptr(dn, "dn"), _dev_ptr(ds, "ds"), _dev_ptr(s, "s"), _dev_ptr(w, "w"),
+                                _dev_ptr(rstd, "rstd"), rows, dim, _dev_ptr(dh, "dh"), _stream(s.device)),
+           "vq_rmsnorm_bwd")
+    return dh
 
 
 def distill_loss_fwd(logits: torch.Tensor, teacher_logits: torch.Tensor, labels: torch.Tensor,

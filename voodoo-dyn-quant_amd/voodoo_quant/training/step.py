@@ -181,6 +181,45 @@ def _rope_tables_f32(s: int, head_dim: int, theta: float, device) -> tuple[torch
     return t
 
 
+class _AddRMSNorm(torch.autograd.Function):
+    """(s, n) = (h + a, rms_norm(h + a) * w) in one HIP pass
+    (``vq_add_rmsnorm_fwd``; a may be None for a plain RMSNorm, then s is h);
+    the backward returns one gradient for both h and a.  The norm weight is
+    frozen (the trainer trains gates only)."""
+
+    @staticmethod
+    def forward(ctx, h, a, w, eps):
+        shape = h.shape
+        h2 = h.reshape(-1, shape[-1])
+        a2 = a.reshape(-1, shape[-1]) if a is not None else None
+        # (grad mode is off inside forward; needs_input_grad says whether a
+        # backward can come)
+        s, n, rstd = _hip.add_rmsnorm_fwd(h2, a2, w, eps, need_backward=any(ctx.needs_input_grad[:2]))
+        if s is None:
+            s = h2
+        ctx.save_for_backward(s, w, rstd)
+        ctx.has_a = a is not None
+        ctx.shape = shape
+        return s.view(shape), n.view(shape)
+
+    @staticmethod
+    def backward(ctx, ds, dn):
+        s, w, rstd = ctx.saved_tensors
+        dim = ctx.shape[-1]
+        ds2 = ds.reshape(-1, dim).contiguous() if ds is not None else None
+        if dn is None:
+            dh = ds2
+        else:
+            dh = _hip.rmsnorm_bwd(dn.reshape(-1, dim).contiguous(), ds2, s, w, rstd)
+        dh = dh.view(ctx.shape) if dh is not None else None
+        return dh, (dh if ctx.has_a else None), None, None
+
+
+def _fused_norms(h: torch.Tensor, w) -> bool:
+    return (FUSED_GLUE and h.is_cuda and h.dtype == torch.bfloat16 and h.shape[-1] % 8 == 0
+            and not w.requires_grad)
+
+
 class _Attention(nn.Module):
     def __init__(self, cfg: DecoderConfig, lin: dict[str, nn.Module]):
         super().__init__()
@@ -247,9 +286,25 @@ class _Body(nn.Module):
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         h = self.embed_tokens(input_ids).to(torch.bfloat16)
         cos, sin = _rope(input_ids.shape[1], self.cfg.head_dim, self.cfg.rope_theta, input_ids.device)
-        for layer in self.layers:
-            h = layer(h, cos, sin)
-        return F.rms_norm(h, (h.shape[-1],), self.norm, self.cfg.eps)
+        if not _fused_norms(h, self.norm):
+            for layer in self.layers:
+                h = layer(h, cos, sin)
+            return F.rms_norm(h, (h.shape[-1],), self.norm, self.cfg.eps)
+        # each residual add runs fused with the RMSNorm that reads its result:
+        # the attention add with the post-attention norm, the MLP add with the
+        # next layer's input norm (the final norm after the last layer)
+        eps = self.cfg.eps
+        layers_ = list(self.layers)
+        first = layers_[0].input_layernorm if layers_ else self.norm
+        h = h.contiguous()
+        _, n = _AddRMSNorm.apply(h, None, first, eps)
+        for i, layer in enumerate(layers_):
+            a = layer.self_attn(n, cos, sin)
+            h, n = _AddRMSNorm.apply(h, a, layer.post_attention_layernorm, eps)
+            m = layer.mlp(n)
+            w_next = layers_[i + 1].input_layernorm if i + 1 < len(layers_) else self.norm
+            h, n = _AddRMSNorm.apply(h, m, w_next, eps)
+        return n
 
 
 class Decoder(nn.Module):
