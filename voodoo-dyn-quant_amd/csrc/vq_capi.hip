@@ -666,13 +666,17 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
                            "gate GEMM launch");
             if (rc != VQ_OK) return rc;
         }
+        // every member in one launch; no tokens: a reduce over zero partials
+        // writes dL/dp = 0
+        vq::GateReduceOut out{};
+        out.kstride = cg.kstride;
         for (int i = 0; i < nmembers; ++i) {
-            // no tokens: a reduce over zero partials writes dL/dp = 0
-            rc = hip_check(vq::launch_gate_reduce_strided(partials + i * cg.kstride, m > 0 ? nparts : 0, nslot,
-                                                          ncand[i], dprobs[i], s),
-                           "gate reduce launch");
-            if (rc != VQ_OK) return rc;
+            out.dprobs[i] = dprobs[i];
+            out.ncand[i] = ncand[i];
         }
+        rc = hip_check(vq::launch_gate_reduce_group(partials, m > 0 ? nparts : 0, nslot, out, nmembers, s),
+                       "gate reduce launch");
+        if (rc != VQ_OK) return rc;
     }
     return ok();
 }

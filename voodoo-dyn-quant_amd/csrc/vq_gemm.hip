@@ -155,6 +155,31 @@ __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restric
     if (threadIdx.x == 0) dprobs[k] = (float)sh[0];
 }
 
+// Every member of a stacked product in one launch: block (k, i) reduces
+// member i's candidate k (slot i * kstride + k of each partial row).
+__global__ __launch_bounds__(256) void gate_reduce_group_kernel(const float* __restrict__ partials, int64_t ntiles,
+                                                                int stride, GateReduceOut out) {
+    __shared__ double sh[256];
+    const int k = blockIdx.x, i = blockIdx.y;
+    if (k >= out.ncand[i]) return;
+    const int slot = i * out.kstride + k;
+    double s = 0.0;
+    for (int64_t t = threadIdx.x; t < ntiles; t += 256) s += (double)partials[t * stride + slot];
+    sh[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out.dprobs[i][k] = (float)sh[0];
+}
+
+hipError_t launch_gate_reduce_group(const float* partials, int64_t ntiles, int stride, const GateReduceOut& out,
+                                    int nmembers, hipStream_t s) {
+    gate_reduce_group_kernel<<<dim3(out.kstride, nmembers), dim3(256), 0, s>>>(partials, ntiles, stride, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s) {
     return launch_gate_reduce_strided(partials, ntiles, ncand, ncand, dprobs, s);
 }

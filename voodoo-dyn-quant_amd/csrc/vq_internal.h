@@ -46,6 +46,13 @@ hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const*
                              int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s);
 hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
 // dprobs[k] = sum_t partials[t * stride + k], k < ncand
+struct GateReduceOut {
+    float* dprobs[kMaxSets];
+    int ncand[kMaxSets];
+    int kstride;
+};
+hipError_t launch_gate_reduce_group(const float* partials, int64_t ntiles, int stride, const GateReduceOut& out,
+                                    int nmembers, hipStream_t s);
 hipError_t launch_gate_reduce_strided(const float* partials, int64_t ntiles, int stride, int ncand, float* dprobs,
                                       hipStream_t s);
 

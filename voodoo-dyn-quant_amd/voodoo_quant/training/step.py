@@ -524,8 +524,21 @@ class SwiGLUStack(nn.Module):
         self.blocks = nn.ModuleList([_SwiGLUBlock(cfg, lin, device) for lin in block_linears])
 
     def forward(self, h):
-        for b in self.blocks:
-            h = b(h)
+        blocks = list(self.blocks)
+        if not blocks or not _fused_norms(h, blocks[0].norm):
+            for b in blocks:
+                h = b(h)
+            return h
+        # each block's residual add fused with the next block's norm
+        eps = blocks[0].eps
+        h = h.contiguous()
+        _, n = _AddRMSNorm.apply(h, None, blocks[0].norm, eps)
+        for i, b in enumerate(blocks):
+            m = b.mlp(n)
+            if i + 1 < len(blocks):
+                h, n = _AddRMSNorm.apply(h, m, blocks[i + 1].norm, eps)
+            else:
+                h = h + m
         return h
 
 
