@@ -773,7 +773,10 @@ __device__ __forceinline__ void wait_vmcnt_barrier() {
 //   SWITCH_READ_FIRST   reads first, so the copies can interleave the MFMAs
 //   SWITCH_FENCED       reads first, and the barrier fenced with
 //                       sched_barrier so no MFMA or read crosses it
-enum StageSwitch : int { SWITCH_COPY_FIRST = 0, SWITCH_READ_FIRST = 1, SWITCH_FENCED = 2 };
+//   SWITCH_LOOSE        reads first; inside a stage only "the first k-step's
+//                       reads, then its MFMAs" is pinned, the rest is left to
+//                       the scheduler
+enum StageSwitch : int { SWITCH_COPY_FIRST = 0, SWITCH_READ_FIRST = 1, SWITCH_FENCED = 2, SWITCH_LOOSE = 3 };
 
 template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int NS, int SWITCH>
 __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, int j0, int kbeg, int kend,
@@ -838,12 +841,14 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
             mfma(ks & 1);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);  // reads of k-step 1 first
+        if constexpr (SWITCH != SWITCH_LOOSE) {
 #pragma unroll
-        for (int ks = 1; ks + 1 < KS; ++ks) {
+            for (int ks = 1; ks + 1 < KS; ++ks) {
 #pragma unroll
-            for (int r = 0; r < FR; ++r) {
-                __builtin_amdgcn_sched_group_barrier(0x008, (MF + FR - 1) / FR, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                for (int r = 0; r < FR; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, (MF + FR - 1) / FR, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
             }
         }
         __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
