@@ -49,7 +49,7 @@ static bool small_product(int M, int N) {
     const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
     return 4 * tiles < 3 * (int64_t)device_cus();
 }
-using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_LOOSE, 2>;
+using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_FREE, 2>;
 using GateCfg = GemmCfg<GateL, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2, SWITCH_LOOSE, 2>;
 
 static GemmParams fwd_params(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D) {

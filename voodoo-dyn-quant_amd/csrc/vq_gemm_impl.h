@@ -776,7 +776,16 @@ __device__ __forceinline__ void wait_vmcnt_barrier() {
 //   SWITCH_LOOSE        reads first; inside a stage only "the first k-step's
 //                       reads, then its MFMAs" is pinned, the rest is left to
 //                       the scheduler
-enum StageSwitch : int { SWITCH_COPY_FIRST = 0, SWITCH_READ_FIRST = 1, SWITCH_FENCED = 2, SWITCH_LOOSE = 3 };
+//   SWITCH_LOOSE2       SWITCH_LOOSE with the stage switch unpinned too
+//   SWITCH_FREE         no scheduling hints at all (order of issue only)
+enum StageSwitch : int {
+    SWITCH_COPY_FIRST = 0,
+    SWITCH_READ_FIRST = 1,
+    SWITCH_FENCED = 2,
+    SWITCH_LOOSE = 3,
+    SWITCH_LOOSE2 = 4,
+    SWITCH_FREE = 5
+};
 
 template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int NS, int SWITCH>
 __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, int j0, int kbeg, int kend,
@@ -840,8 +849,8 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
             read(st, ks + 1, (ks + 1) & 1);
             mfma(ks & 1);
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);  // reads of k-step 1 first
-        if constexpr (SWITCH != SWITCH_LOOSE) {
+        if constexpr (SWITCH != SWITCH_FREE) __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);  // reads of k-step 1 first
+        if constexpr (SWITCH != SWITCH_LOOSE && SWITCH != SWITCH_FREE && SWITCH != SWITCH_LOOSE2) {
 #pragma unroll
             for (int ks = 1; ks + 1 < KS; ++ks) {
 #pragma unroll
@@ -851,7 +860,7 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
                 }
             }
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+        if constexpr (SWITCH != SWITCH_FREE) __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
         // all of stage kt is in registers: wait for stage kt + 1 (stages
         // kt + 2 .. kt + NS - 1 may still be in flight), then stage kt's
         // buffer is free for stage kt + NS (past the end: harmless zeros and
@@ -872,11 +881,13 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
             issue(kt + NS);
         }
         mfma((KS - 1) & 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, FR, 1);
+        if constexpr (SWITCH != SWITCH_FREE && SWITCH != SWITCH_LOOSE2) {
+            __builtin_amdgcn_sched_group_barrier(0x100, FR, 1);
 #pragma unroll
-        for (int r = 0; r < MF; ++r) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x020, (NI + MF - 1) / MF, 1);
+            for (int r = 0; r < MF; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                __builtin_amdgcn_sched_group_barrier(0x020, (NI + MF - 1) / MF, 1);
+            }
         }
     }
     wait_vmcnt_barrier<0>();  // the zero copies have landed before anyone reuses LDS
