@@ -207,6 +207,9 @@ CASES = [
     ("ragged", ["Q2_K", "Q5_K", "Q8_0"], 37, 136, 264, 512),
     ("single-token", ["Q6_K", "Q4_K"], 1, 256, 256, 256),
     ("multi-tile", SIX, 300, 520, 1000, 1024),
+    # 208 ragged 256x256 tiles (the 8-wave forward; rows, columns and k all
+    # partial at the edges)
+    ("large-ragged", ["Q3_K", "Q6_K", "Q8_0"], 4000, 3080, 520, 768),
 ]
 
 
