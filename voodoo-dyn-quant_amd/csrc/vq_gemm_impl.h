@@ -3,17 +3,17 @@
 // the tile configurations.
 //
 // One kernel template computes C[i][j] = sum_k A[i][k] * B[j][k] with both
-// operands staged in LDS as [rows][BK] tiles whose reduction index k is
-// contiguous, which is the operand layout the MFMA reads (each lane holds 8
-// consecutive k of one row).  Loaders fill those tiles from global memory:
-//   LoaderK  - the source already has k contiguous (row-major [rows][K]);
-//   LoaderT  - the source is [K][rows] (rows contiguous): a thread loads an
-//              8x8 bf16 block with eight 16-byte loads and transposes it in
-//              registers before its 16-byte LDS writes.
+// operands copied global -> LDS by direct-to-LDS buffer loads into XOR-
+// swizzled stages, then read as MFMA fragments (each lane holds 8
+// consecutive k of one row):
+//   DmaKS - the source has k contiguous (row-major [rows][K]); fragments
+//           with ds_read_b128;
+//   DmaNS - the source is [K][rows] (rows contiguous), kept in that
+//           orientation; fragments with ds_read_b64_tr_b16.
 // The three products of the path:
-//   forward  Y[m][n]  = sum_d X[m][d] W[n][d]        A=X (K), B=W (K)
-//   dX       dX[m][d] = sum_n dY[m][n] W[n][d]       A=dY (K), B=W (T)
-//   gate     dW[d][n] = sum_m X[m][d] dY[m][n]       A=X (T), B=dY (T)
+//   forward  Y[m][n]  = sum_d X[m][d] W[n][d]        A=X (KS), B=W (KS)
+//   dX       dX[m][d] = sum_n dY[m][n] W[n][d]       A=dY (KS), B=W (NS)
+//   gate     dW[d][n] = sum_m X[m][d] dY[m][n]       A=X (NS), B=dY (NS)
 // The gate product never reaches global memory: its epilogue keeps the fp32
 // tile in the accumulators, stages each candidate's bytes for the tile into
 // LDS (reusing the main-loop buffers) and dots the exactly decoded weights
@@ -34,17 +34,6 @@ namespace vq {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// ---------------------------------------------------------------- LDS layout
-// Tile [rows][BK] bf16 in 16-byte chunks; chunk index XOR-swizzled with bits
-// of the row so that both the MFMA fragment reads (32 consecutive rows, one
-// chunk) and the transposed loader's writes (rows 8 apart) spread over banks.
-template <int BK>
-__device__ __forceinline__ int lds_chunk(int row, int chunk) {
-    constexpr int CPR = BK / 8;
-    const int sw = (row ^ (row >> 3)) & (CPR - 1);
-    return row * CPR + (chunk ^ sw);
-}
-
 // ---------------------------------------------------------------- loaders
 // Global reads go through raw buffer loads: an element outside the matrix is
 // given an offset past the descriptor's range, and the hardware returns zeros
@@ -61,215 +50,16 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
-template <int ROWS, int BK, int THREADS>
-struct LoaderK {
-    static constexpr bool kDma = false;
-    static constexpr int kFragReads = 1;
-    static constexpr int CPR = BK / 8;
-    static constexpr int NL = ROWS * CPR / THREADS;
-    static_assert(NL * THREADS == ROWS * CPR, "tile must split evenly over threads");
-    u32x4 reg[NL];
-
-    // rows [r0, r0 + ROWS) x k [k0, k0 + BK) of src[row * ld + k], zero past kend
-    __device__ __forceinline__ void load(const bf16_t* __restrict__ src, int64_t ld, int r0, int rows, int k0,
-                                         int kend) {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)r0 * ld + k0);
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int id = i * THREADS + (int)threadIdx.x;
-            const int row = id / CPR, c = id % CPR;
-            const bool ok = r0 + row < rows && k0 + 8 * c < kend;
-            reg[i] = buf_load16(rs, ok ? (uint32_t)((row * ld + 8 * c) * 2) : kOOB);
-        }
-    }
-    __device__ __forceinline__ void store(u32x4* __restrict__ lds) const {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int id = i * THREADS + (int)threadIdx.x;
-            lds[lds_chunk<BK>(id / CPR, id % CPR)] = reg[i];
-        }
-    }
-    static constexpr int CHUNKS = ROWS * BK / 8;  // 16-byte LDS chunks per stage
-    // MFMA fragment: tile row `row + lane%32`, k = 16 ks + 8 (lane/32) .. +7
-    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
-        return __builtin_bit_cast(bf16x8_t, lds[lds_chunk<BK>(row + (lane & 31), 2 * ks + (lane >> 5))]);
-    }
-};
-
-// A thread moves one KB x 8 block (KB k-rows of 8 consecutive tile rows): KB
-// 16-byte global loads, a register transpose, then 8 LDS writes of KB bf16.
-// KB = 4 when the tile has enough blocks for every thread (fewer staging
-// registers), else 8.
-template <int ROWS, int BK, int THREADS>
-struct LoaderT {
-    static constexpr bool kDma = false;
-    static constexpr int kFragReads = 1;
-    static constexpr int RB = ROWS / 8;  // 8-row blocks along the tile rows
-    static constexpr int KB = (RB * (BK / 4) >= THREADS) ? 4 : 8;
-    static constexpr int NB = RB * (BK / KB);  // blocks per tile
-    static constexpr int NBT = (NB + THREADS - 1) / THREADS;
-    u32x4 reg[NBT][KB];
-
-    // rows [r0, r0 + ROWS) x k [k0, k0 + BK) of src[k * ld + row], zero past kend
-    __device__ __forceinline__ void load(const bf16_t* __restrict__ src, int64_t ld, int r0, int rows, int k0,
-                                         int kend) {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)k0 * ld + r0);
-#pragma unroll
-        for (int i = 0; i < NBT; ++i) {
-            const int b = i * THREADS + (int)threadIdx.x;
-            const int rb = b % RB, kb = b / RB;
-            const bool rok = (NB % THREADS == 0 || b < NB) && r0 + 8 * rb < rows;
-#pragma unroll
-            for (int kk = 0; kk < KB; ++kk) {
-                const int kr = KB * kb + kk;
-                const bool ok = rok && k0 + kr < kend;
-                reg[i][kk] = buf_load16(rs, ok ? (uint32_t)((kr * ld + 8 * rb) * 2) : kOOB);
-            }
-        }
-    }
-    // Element rr of k-rows a and b, packed as two consecutive k.
-    static __device__ __forceinline__ uint32_t pair(uint32_t a, uint32_t b, int odd) {
-        return odd ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
-    }
-    __device__ __forceinline__ void store(u32x4* __restrict__ lds) const {
-#pragma unroll
-        for (int i = 0; i < NBT; ++i) {
-            const int b = i * THREADS + (int)threadIdx.x;
-            if (NB % THREADS != 0 && b >= NB) continue;
-            const int rb = b % RB, kb = b / RB;
-#pragma unroll
-            for (int rr = 0; rr < 8; ++rr) {
-                const int w = rr >> 1, odd = rr & 1;
-                if constexpr (KB == 8) {
-                    u32x4 o;
-                    o.x = pair(reg[i][0][w], reg[i][1][w], odd);
-                    o.y = pair(reg[i][2][w], reg[i][3][w], odd);
-                    o.z = pair(reg[i][4][w], reg[i][5][w], odd);
-                    o.w = pair(reg[i][6][w], reg[i][7][w], odd);
-                    lds[lds_chunk<BK>(8 * rb + rr, kb)] = o;
-                } else {
-                    uint2 o;
-                    o.x = pair(reg[i][0][w], reg[i][1][w], odd);
-                    o.y = pair(reg[i][2][w], reg[i][3][w], odd);
-                    uint2* dst = reinterpret_cast<uint2*>(lds + lds_chunk<BK>(8 * rb + rr, kb >> 1)) + (kb & 1);
-                    *dst = o;
-                }
-            }
-        }
-    }
-    static constexpr int CHUNKS = ROWS * BK / 8;
-    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
-        return __builtin_bit_cast(bf16x8_t, lds[lds_chunk<BK>(row + (lane & 31), 2 * ks + (lane >> 5))]);
-    }
-};
-
-// Source [K][rows] (rows contiguous) kept in that orientation in LDS: k-row
-// kr of the tile is PITCH bf16 wide (ROWS + 32 of padding).  Fragments come
-// from two ds_read_b64_tr_b16 per 8 k.  That instruction, per 16-lane group,
-// gives output lane l element j = element l%4 of the 8 bytes addressed by lane
-// 16 (l/16) + 4 j + (l%16)/4 (measured on gfx950), so when lane s addresses
-//     k = kk + 8 (s/32) + (s%16)/4,   row = r + 16 ((s/16)%2) + 4 (s%4)
-// lane l receives rows r + l%32 at k = kk + 8 (l/32) + 0..3: the MFMA layout.
-// The padding puts the 4 k-rows x 2 row-halves of each 32-lane pass on
-// distinct bank groups.
-template <int ROWS, int BK, int THREADS>
-struct LoaderN {
-    static constexpr bool kDma = false;
-    static constexpr int kFragReads = 2;  // two ds_read_b64_tr_b16
-    static constexpr int PITCH = ROWS + 32;       // bf16 per k-row in LDS
-    static constexpr int RCH = ROWS / 8;          // 16-byte chunks per k-row
-    static constexpr int NL = BK * RCH / THREADS;
-    static_assert(NL * THREADS == BK * RCH, "tile must split evenly over threads");
-    static constexpr int CHUNKS = BK * PITCH / 8;
-    u32x4 reg[NL];
-
-    // rows [r0, r0 + ROWS) x k [k0, k0 + BK) of src[k * ld + row], zero past kend
-    __device__ __forceinline__ void load(const bf16_t* __restrict__ src, int64_t ld, int r0, int rows, int k0,
-                                         int kend) {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)k0 * ld + r0);
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int id = i * THREADS + (int)threadIdx.x;
-            const int kr = id / RCH, c = id % RCH;
-            const bool ok = r0 + 8 * c < rows && k0 + kr < kend;
-            reg[i] = buf_load16(rs, ok ? (uint32_t)((kr * ld + 8 * c) * 2) : kOOB);
-        }
-    }
-    __device__ __forceinline__ void store(u32x4* __restrict__ lds) const {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int id = i * THREADS + (int)threadIdx.x;
-            lds[(id / RCH) * (PITCH / 8) + id % RCH] = reg[i];
-        }
-    }
-    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
-        typedef short v4i16 __attribute__((ext_vector_type(4)));
-        const int k = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
-        const int r = row + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-        const bf16_t* base = reinterpret_cast<const bf16_t*>(lds) + k * PITCH + r;
-        typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base));
-        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + 4 * PITCH));
-        typedef short v8i16 __attribute__((ext_vector_type(8)));
-        const v8i16 v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        return __builtin_bit_cast(bf16x8_t, v);
-    }
-};
-
 // ---------------------------------------------------------------- direct-to-LDS loaders
 // buffer_load_dwordx4 ... lds: lane l of one wave instruction writes its 16
 // bytes at M0 + 16 l, so one instruction fills 64 consecutive LDS chunks and
-// no register ever holds the tile.  The stage layouts keep padding for
-// conflict-free fragment reads (one chunk per tile row in DmaK, 32 bf16 per
-// k-row in DmaN, the LoaderN layout); lanes that land on padding, or on
-// rows / k past the matrix, use an out-of-range offset and write zeros
-// without touching memory.  A lane's offset depends only on (instruction,
+// no register ever holds the tile.  Lanes on rows or k past the matrix use
+// an out-of-range offset and write zeros without touching memory.  A lane's offset depends only on (instruction,
 // wave, lane) and the tile origin, so offsets are computed once per work
 // item and the k origin moves the descriptor base.
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int ROWS, int BK, int THREADS>
-struct DmaK {
-    static constexpr bool kDma = true;
-    static constexpr int kFragReads = 1;
-    static constexpr int CPR = BK / 8;   // data chunks per tile row
-    static constexpr int PCH = CPR + 1;  // chunks per padded row
-    static constexpr int NW = THREADS / 64;
-    static constexpr int NI = (ROWS * PCH + 64 * NW - 1) / (64 * NW);  // instructions per wave per stage
-    static constexpr int CHUNKS = NI * 64 * NW;                        // LDS chunks per stage
-    uint32_t voff[NI];
-    int kpos[NI];
-
-    // tile rows [r0, r0 + ROWS) of src[row * ld + k]
-    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* = nullptr, int = 0) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int L = (i * NW + wave) * 64 + lane;
-            const int row = L / PCH, c = L % PCH;
-            const bool ok = c < CPR && row < ROWS && r0 + row < rows;
-            voff[i] = ok ? (uint32_t)((row * ld + 8 * c) * 2) : kOOB;
-            kpos[i] = 8 * c + 8;  // k extent this lane's chunk needs
-        }
-    }
-    // k range [k0, k0 + kvalid) into the stage at lds (kvalid < BK on a ragged
-    // last tile; 0 writes zeros and reads nothing)
-    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t ld, int r0, int k0,
-                                          int kvalid) const {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)r0 * ld + k0);
-        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-        for (int i = 0; i < NI; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
-                                                     kpos[i] <= kvalid ? voff[i] : kOOB, 0, 0, 0);
-    }
-    // MFMA fragment: tile row `row + lane%32`, k = 16 ks + 8 (lane/32) .. +7
-    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
-        return __builtin_bit_cast(bf16x8_t, lds[(row + (lane & 31)) * PCH + 2 * ks + (lane >> 5)]);
-    }
-};
-
-// DmaK without padding: a K-major tile row keeps its CPR = BK/8 data chunks,
+// K-major tiles: a tile row keeps its CPR = BK/8 data chunks, no padding,
 // and chunk c of row r sits in slot c ^ sw(r) of that row.  The copy fills
 // LDS slots in order (lane l of an instruction writes slot M0/16 + l), so a
 // lane fetches the global chunk its slot holds; a fragment read addresses the
@@ -277,8 +67,8 @@ struct DmaK {
 // over distinct 16-byte bank groups with 32 (64) banks of 4 bytes: for CPR = 8,
 // rows r and r + 8 differ through r >> 3; for CPR = 4 (64-byte rows, two rows
 // per 128 bytes), the rows of one parity within 8, and the rows of one residue
-// mod 4 within 16, take distinct slots.  Against DmaK the stage is 1/9 (BK 64)
-// smaller, and no copy lane writes padding.
+// mod 4 within 16, take distinct slots.  Against a layout padded by one chunk
+// per row the stage is 1/9 (BK 64) smaller, and no copy lane writes padding.
 template <int ROWS, int BK, int THREADS>
 struct DmaKS {
     static constexpr bool kDma = true;
@@ -326,50 +116,12 @@ struct DmaKS {
     }
 };
 
-template <int ROWS, int BK, int THREADS>
-struct DmaN {
-    static constexpr bool kDma = true;
-    static constexpr int kFragReads = 2;
-    static constexpr int RCH = ROWS / 8;                 // data chunks per k-row
-    static constexpr int PCH = (ROWS + 32) / 8;          // chunks per padded k-row (LoaderN pitch)
-    static constexpr int NW = THREADS / 64;
-    static constexpr int NI = (BK * PCH + 64 * NW - 1) / (64 * NW);
-    static constexpr int CHUNKS = NI * 64 * NW;
-    uint32_t voff[NI];
-    int kpos[NI];
-
-    // tile rows [r0, r0 + ROWS) of src[k * ld + row]
-    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* = nullptr, int = 0) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int L = (i * NW + wave) * 64 + lane;
-            const int kr = L / PCH, c = L % PCH;
-            const bool ok = c < RCH && kr < BK && r0 + 8 * c < rows;
-            voff[i] = ok ? (uint32_t)((kr * ld + 8 * c) * 2) : kOOB;
-            kpos[i] = kr + 1;
-        }
-    }
-    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t ld, int r0, int k0,
-                                          int kvalid) const {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + (int64_t)k0 * ld + r0);
-        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-        for (int i = 0; i < NI; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
-                                                     kpos[i] <= kvalid ? voff[i] : kOOB, 0, 0, 0);
-    }
-    static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
-        return LoaderN<ROWS, BK, THREADS>::read_frag(lds, row, ks, lane);
-    }
-};
-
-// DmaN without padding: k-row kr keeps its RCH = ROWS/8 chunks, chunk c in
+// [K][rows] tiles: k-row kr keeps its RCH = ROWS/8 chunks, no padding, chunk c in
 // slot c ^ 4 (kr % 4).  One ds_read_b64_tr_b16 pass reads 4 consecutive
 // k-rows x 32 tile rows (4 chunks, 64 bytes, aligned: fragment rows start at
 // multiples of 32); the XOR moves the 4 k-rows' 64-byte blocks onto distinct
-// quarters of 256 bytes, which the padded layout achieves with its 64-byte
-// pitch.  The read at k + 4 keeps the same XOR.
+// quarters of 256 bytes (as a 64-byte pad per k-row would).  The read at
+// k + 4 keeps the same XOR.
 template <int ROWS, int BK, int THREADS>
 struct DmaNS {
     static constexpr bool kDma = true;
@@ -404,7 +156,11 @@ struct DmaNS {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
                                                      kpos[i] <= kvalid ? voff[i] : kOOB, 0, 0, 0);
     }
-    // the LoaderN fragment (same lane -> (k, row) map), at swizzled addresses
+    // ds_read_b64_tr_b16, per 16-lane group, gives output lane l element j =
+    // element l%4 of the 8 bytes addressed by lane 16 (l/16) + 4 j + (l%16)/4
+    // (measured on gfx950), so when lane s addresses
+    //     k = kk + 8 (s/32) + (s%16)/4,   row = r + 16 ((s/16)%2) + 4 (s%4)
+    // lane l receives rows r + l%32 at k = kk + 8 (l/32) + 0..3: the MFMA layout
     static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
         typedef short v4i16 __attribute__((ext_vector_type(4)));
         typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
@@ -420,42 +176,9 @@ struct DmaNS {
     }
 };
 
-// DmaK with gathered rows: tile row r is source row map[r0 + r] (rows
+// DmaKS with gathered rows: tile row r is source row map[r0 + r] (rows
 // r0 + r >= rows are zeros).  The per-lane offsets carry the whole row offset,
 // so the descriptor base moves with k only; the host bounds m * ld * 2 < 2^31.
-template <int ROWS, int BK, int THREADS>
-struct DmaKG : DmaK<ROWS, BK, THREADS> {
-    using Base = DmaK<ROWS, BK, THREADS>;
-    using Base::CPR;
-    using Base::NI;
-    using Base::NW;
-    using Base::PCH;
-    // map_rows: valid source rows; an entry outside [0, map_rows) reads zeros
-    __device__ __forceinline__ void init(int64_t ld, int r0, int rows, const int* map, int map_rows) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int L = (i * NW + wave) * 64 + lane;
-            const int row = L / PCH, c = L % PCH;
-            const bool in_tile = c < CPR && row < ROWS && r0 + row < rows;
-            const int src = in_tile ? map[r0 + row] : -1;
-            const bool ok = in_tile && (unsigned)src < (unsigned)map_rows;
-            this->voff[i] = ok ? (uint32_t)(((int64_t)src * ld + 8 * c) * 2) : kOOB;
-            this->kpos[i] = 8 * c + 8;
-        }
-    }
-    __device__ __forceinline__ void issue(u32x4* lds, const bf16_t* __restrict__ src, int64_t, int, int k0,
-                                          int kvalid) const {
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src + k0);
-        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-        for (int i = 0; i < NI; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(lds + (i * NW + wave) * 64), 16,
-                                                     this->kpos[i] <= kvalid ? this->voff[i] : kOOB, 0, 0, 0);
-    }
-};
-
-// DmaKS with gathered rows, as DmaKG over the swizzled layout.
 template <int ROWS, int BK, int THREADS>
 struct DmaKSG : DmaKS<ROWS, BK, THREADS> {
     using Base = DmaKS<ROWS, BK, THREADS>;
@@ -611,139 +334,8 @@ struct GemmShape {
 template <class LA, class LB, int DEPTH = 1>
 struct StageLds {
     static constexpr int A_CH = LA::CHUNKS, B_CH = LB::CHUNKS;  // 16-byte chunks per stage
-    // register loaders double buffer; direct-to-LDS loaders keep DEPTH stages
-    static constexpr int NSTAGE = LA::kDma ? DEPTH : 2;
-    static constexpr size_t BYTES = (size_t)NSTAGE * (A_CH + B_CH) * 16;
+    static constexpr size_t BYTES = (size_t)DEPTH * (A_CH + B_CH) * 16;  // DEPTH stages
 };
-
-// MFMAs of one LDS stage.
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, bool SCHED = false>
-__device__ __forceinline__ void gemm_stage_mfma(const u32x4* __restrict__ sa, const u32x4* __restrict__ sb, int wi,
-                                                int wj, int lane,
-                                                f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
-                                                             [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
-    using S = GemmShape<BI, BJ, BK, WI, WJ>;
-    constexpr int KS = BK / 16;
-    // fragments of k-step ks + 1 are read while the MFMAs of ks run
-    bf16x8_t fa[2][S::MI], fb[2][S::NJ];
-    auto read = [&](int ks, int buf) {
-#pragma unroll
-        for (int a = 0; a < S::MI; ++a) fa[buf][a] = LA::read_frag(sa, wi * S::WTI + 32 * a, ks, lane);
-#pragma unroll
-        for (int b = 0; b < S::NJ; ++b) fb[buf][b] = LB::read_frag(sb, wj * S::WTJ + 32 * b, ks, lane);
-    };
-    read(0, 0);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        if (ks + 1 < KS) read(ks + 1, (ks + 1) & 1);
-#pragma unroll
-        for (int a = 0; a < S::MI; ++a)
-#pragma unroll
-            for (int b = 0; b < S::NJ; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1][a], fb[ks & 1][b], acc[a][b], 0, 0, 0);
-    }
-    if constexpr (SCHED) {
-        // Instruction order for the scheduler: the first k-step's fragment
-        // reads, then each k-step's MFMAs with the next k-step's reads spread
-        // among them (LDS latency hides behind the matrix pipe).
-        constexpr int FR = S::MI * S::NJ > 0 ? LA::kFragReads * S::MI + LB::kFragReads * S::NJ : 0;
-        constexpr int MF = S::MI * S::NJ;
-        constexpr int PER = (MF + FR - 1) / FR;  // MFMAs per read
-        __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            if (ks + 1 < KS) {
-#pragma unroll
-                for (int r = 0; r < FR; ++r) {
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);
-                }
-            } else {
-                __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
-            }
-        }
-    }
-}
-
-// Main loop over k in [kbeg, kend) with an LDS double buffer and one barrier
-// per stage.  DEPTH = 1: the global loads of stage s+1 are issued before the
-// MFMAs of stage s and written to the free LDS buffer after them.  DEPTH = 2:
-// two register stages, so the loads of stage s+2 have two stages of compute
-// to arrive (more registers).
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int DEPTH>
-__device__ __forceinline__ void gemm_mainloop(const GemmParams& p, int i0, int j0, int kbeg, int kend,
-                                              u32x4* __restrict__ smem,
-                                              f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
-                                                           [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
-    using S = GemmShape<BI, BJ, BK, WI, WJ>;
-    using L = StageLds<LA, LB>;
-    u32x4* const sA[2] = {smem, smem + L::A_CH};
-    u32x4* const sB[2] = {smem + 2 * L::A_CH, smem + 2 * L::A_CH + L::B_CH};
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wi = wave / WJ, wj = wave % WJ;
-
-#pragma unroll
-    for (int a = 0; a < S::MI; ++a)
-#pragma unroll
-        for (int b = 0; b < S::NJ; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-
-    const int nk = (kend - kbeg + BK - 1) / BK;
-    if constexpr (DEPTH == 1) {
-        LA la;
-        LB lb;
-        la.load(p.A, p.lda, i0, p.I, kbeg, kend);
-        lb.load(p.B, p.ldb, j0, p.J, kbeg, kend);
-        la.store(sA[0]);
-        lb.store(sB[0]);
-        __syncthreads();
-        for (int kt = 0; kt < nk; ++kt) {
-            const bool more = kt + 1 < nk;
-            if (more) {
-                la.load(p.A, p.lda, i0, p.I, kbeg + (kt + 1) * BK, kend);
-                lb.load(p.B, p.ldb, j0, p.J, kbeg + (kt + 1) * BK, kend);
-            }
-            gemm_stage_mfma<LA, LB, BI, BJ, BK, WI, WJ>(sA[kt & 1], sB[kt & 1], wi, wj, lane, acc);
-            if (more) {
-                la.store(sA[(kt + 1) & 1]);
-                lb.store(sB[(kt + 1) & 1]);
-            }
-            __syncthreads();
-        }
-        return;
-    }
-    LA la0, la1;
-    LB lb0, lb1;
-    la0.load(p.A, p.lda, i0, p.I, kbeg, kend);
-    lb0.load(p.B, p.ldb, j0, p.J, kbeg, kend);
-    if (nk > 1) {
-        la1.load(p.A, p.lda, i0, p.I, kbeg + BK, kend);
-        lb1.load(p.B, p.ldb, j0, p.J, kbeg + BK, kend);
-    }
-    la0.store(sA[0]);
-    lb0.store(sB[0]);
-    __syncthreads();
-
-    // stage kt: refill (holding stage kt, already in LDS) <- stage kt + 2;
-    // next (holding stage kt + 1) -> the other LDS buffer after the MFMAs
-    auto stage = [&](int kt, LA& la_refill, LB& lb_refill, const LA& la_next, const LB& lb_next) {
-        if (kt + 2 < nk) {
-            la_refill.load(p.A, p.lda, i0, p.I, kbeg + (kt + 2) * BK, kend);
-            lb_refill.load(p.B, p.ldb, j0, p.J, kbeg + (kt + 2) * BK, kend);
-        }
-        gemm_stage_mfma<LA, LB, BI, BJ, BK, WI, WJ>(sA[kt & 1], sB[kt & 1], wi, wj, lane, acc);
-        if (kt + 1 < nk) {
-            la_next.store(sA[(kt + 1) & 1]);
-            lb_next.store(sB[(kt + 1) & 1]);
-        }
-        __syncthreads();
-    };
-    for (int kt = 0; kt < nk; kt += 2) {
-        stage(kt, la0, lb0, la1, lb1);
-        if (kt + 1 < nk) stage(kt + 1, la1, lb1, la0, lb0);
-    }
-}
 
 // Main loop with direct-to-LDS loaders and NS LDS stages: the loads of stage
 // kt + NS - 1 are issued right after the barrier that retires stage kt - 1,
@@ -1174,10 +766,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
         kend = min(p.K, kbeg + chunk);
     }
     f32x16 acc[S::MI][S::NJ];
-    if constexpr (LA::kDma)
-        gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, DEPTH, C::SWITCH>(p, i0, j0, kbeg, kend, smem, acc);
-    else
-        gemm_mainloop<LA, LB, BI, BJ, BK, WI, WJ, DEPTH>(p, i0, j0, kbeg, kend, smem, acc);
+    static_assert(LA::kDma && LB::kDma, "direct-to-LDS loaders");
+    gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, DEPTH, C::SWITCH>(p, i0, j0, kbeg, kend, smem, acc);
 
     if constexpr (EPI == EPI_STORE) {
         if (w.ns > 1) {
@@ -1300,11 +890,6 @@ static hipError_t launch_gemm_cfg(GemmParams p, int cus, float* tail_ws, hipStre
     constexpr int FIX_BLOCKS = GemmShape<C::BI, C::BJ, C::BK, C::WI, C::WJ>::MI * GemmShape<C::BI, C::BJ, C::BK, C::WI, C::WJ>::NJ;
     gemm_tail_fixup_kernel<C><<<dim3(8 * p.tail_max * FIX_BLOCKS), dim3(C::THREADS), 0, s>>>(p);
     return hipGetLastError();
-}
-
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int EPI, int DEPTH = 1>
-static hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
-    return launch_gemm_cfg<GemmCfg<LA, LB, BI, BJ, BK, WI, WJ, EPI, DEPTH>>(p, 256, nullptr, s);
 }
 
 // Two products in one launch (see gemm_dual_kernel); problem 1 may be a store
