@@ -702,7 +702,10 @@ struct GemmCfg {
 // Store epilogue: the tile goes through LDS as bf16 ([BI][BJ + 8], the pad
 // puts the two row halves of an MFMA write on different banks), then out with
 // 16-byte stores, 32 consecutive threads per 512-byte row segment, so C is
-// written in whole cache lines.  C's row length J is a multiple of 8.
+// written in whole cache lines.  C's row length J is a multiple of 8.  The
+// stores are non-temporal: every CU writes its tile at about the same moment,
+// and streaming the burst past L2 measured 4-6% faster on the forward at
+// 8192 x 5120 -> 17408 and 8192 x 1024 -> 1536 / 6144 (within 1% elsewhere).
 template <int BI, int BJ, int BK, int WI, int WJ>
 __device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int j0, u32x4* __restrict__ smem,
                                                const f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
@@ -735,7 +738,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int 
             const u32x4 v = *reinterpret_cast<const u32x4*>(t + il * PITCH + 8 * jc);
             const int64_t gi = p.rowmap ? p.rowmap[i0 + il] : i0 + il;  // routed: scatter rows
             if (!p.rowmap || (uint64_t)gi < (uint64_t)p.map_rows)
-                *reinterpret_cast<u32x4*>(p.C + gi * p.ldc + j0 + 8 * jc) = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p.C + gi * p.ldc + j0 + 8 * jc));
         }
     }
 }
