@@ -379,12 +379,19 @@ enum StageSwitch : int {
     SWITCH_FREE = 5
 };
 
-template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int NS, int SWITCH>
+// COPY_SPLIT: the refill of the buffer a stage switch frees is issued in two
+// halves, the A tile at the switch and the B tile after the next stage's first
+// k-step, so the two bursts of LDS writes land apart (two stages only: every
+// switch then waits for all copies).
+enum CopyIssue : int { COPY_BURST = 0, COPY_SPLIT = 1 };
+
+template <class LA, class LB, int BI, int BJ, int BK, int WI, int WJ, int NS, int SWITCH, int COPY = COPY_BURST>
 __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, int j0, int kbeg, int kend,
                                                  u32x4* __restrict__ smem,
                                                  f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
                                                               [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
     static_assert(NS >= 2 && NS <= 4, "2 to 4 LDS stages");
+    static_assert(COPY == COPY_BURST || NS == 2, "split refills need the wait-for-all of two stages");
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     constexpr int STAGE = LA::CHUNKS + LB::CHUNKS;
     constexpr int KS = BK / 16;
@@ -414,6 +421,16 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
         la.issue(st, p.A, p.lda, i0, k0, kvalid);
         lb.issue(st + LA::CHUNKS, p.B, p.ldb, j0, k0, kvalid);
     };
+    auto issue_a = [&](int kt) {
+        u32x4* st = smem + (kt % NS) * STAGE;
+        const int k0 = min(kbeg + kt * BK, kend);
+        la.issue(st, p.A, p.lda, i0, k0, min(BK, kend - k0));
+    };
+    auto issue_b = [&](int kt) {
+        u32x4* st = smem + (kt % NS) * STAGE;
+        const int k0 = min(kbeg + kt * BK, kend);
+        lb.issue(st + LA::CHUNKS, p.B, p.ldb, j0, k0, min(BK, kend - k0));
+    };
     bf16x8_t fa[2][S::MI], fb[2][S::NJ];
     auto read = [&](const u32x4* st, int ks, int buf) {
 #pragma unroll
@@ -440,6 +457,9 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
         for (int ks = 0; ks + 1 < KS; ++ks) {
             read(st, ks + 1, (ks + 1) & 1);
             mfma(ks & 1);
+            // the B half of the refill issued at the last switch
+            if constexpr (COPY == COPY_SPLIT)
+                if (ks == 0 && kt >= 1) issue_b(kt - 1 + NS);
         }
         if constexpr (SWITCH != SWITCH_FREE) __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);  // reads of k-step 1 first
         if constexpr (SWITCH != SWITCH_LOOSE && SWITCH != SWITCH_FREE && SWITCH != SWITCH_LOOSE2) {
@@ -465,7 +485,10 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
         if constexpr (SWITCH == SWITCH_FENCED) __builtin_amdgcn_sched_barrier(0);
         // reads first: the compiler cannot tell stage buffers apart, so copies
         // issued first stay ahead of every later read (and MFMA)
-        if constexpr (SWITCH == SWITCH_COPY_FIRST) {
+        if constexpr (COPY == COPY_SPLIT) {
+            read(smem + ((kt + 1) % NS) * STAGE, 0, 0);
+            issue_a(kt + NS);
+        } else if constexpr (SWITCH == SWITCH_COPY_FIRST) {
             issue(kt + NS);
             read(smem + ((kt + 1) % NS) * STAGE, 0, 0);
         } else {
@@ -652,13 +675,14 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
 constexpr int kMinSavedSplitSteps = 10;  // see GemmCfg::plan
 
 template <class LA_, class LB_, int BI_, int BJ_, int BK_, int WI_, int WJ_, int EPI_, int DEPTH_,
-          int SWITCH_ = SWITCH_FENCED, int OCC_ = 1>
+          int SWITCH_ = SWITCH_FENCED, int OCC_ = 1, int COPY_ = COPY_BURST>
 struct GemmCfg {
     using LA = LA_;
     using LB = LB_;
     static constexpr int BI = BI_, BJ = BJ_, BK = BK_, WI = WI_, WJ = WJ_, EPI = EPI_, DEPTH = DEPTH_;
     static constexpr int SWITCH = SWITCH_;
     static constexpr int OCC = OCC_;  // waves per SIMD the registers are budgeted for
+    static constexpr int COPY = COPY_;
     static constexpr int THREADS = WI * WJ * 64;
     static constexpr size_t main_lds() { return StageLds<LA, LB, DEPTH>::BYTES; }
     static constexpr size_t lds() {
@@ -770,7 +794,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
     }
     f32x16 acc[S::MI][S::NJ];
     static_assert(LA::kDma && LB::kDma, "direct-to-LDS loaders");
-    gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, DEPTH, C::SWITCH>(p, i0, j0, kbeg, kend, smem, acc);
+    gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, DEPTH, C::SWITCH, C::COPY>(p, i0, j0, kbeg, kend, smem, acc);
 
     if constexpr (EPI == EPI_STORE) {
         if (w.ns > 1) {
@@ -960,7 +984,7 @@ void routed_gemm_kernel(GemmParams p, int tile_rows) {
     q.I = hi;  // end of the group's rows in rowmap
     const int i0 = lo + tm * BI, j0 = w.tn * BJ;
     f32x16 acc[S::MI][S::NJ];
-    gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, C::DEPTH, C::SWITCH>(q, i0, j0, 0, q.K, smem, acc);
+    gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, C::DEPTH, C::SWITCH, C::COPY>(q, i0, j0, 0, q.K, smem, acc);
     store_tile_lds<BI, BJ, BK, WI, WJ>(q, i0, j0, smem, acc);
 }
 
