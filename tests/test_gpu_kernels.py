@@ -210,6 +210,9 @@ CASES = [
     # 208 ragged 256x256 tiles (the 8-wave forward; rows, columns and k all
     # partial at the edges)
     ("large-ragged", ["Q3_K", "Q6_K", "Q8_0"], 4000, 3080, 520, 768),
+    # 336 forward tiles: one full round and a K-split tail (the split refill
+    # path with partial k ranges and the fixup); dX and the gate split too
+    ("split-tails", ["Q4_K", "Q6_K"], 4096, 5376, 2048, 2048),
 ]
 
 
