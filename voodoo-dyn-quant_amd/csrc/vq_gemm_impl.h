@@ -211,8 +211,10 @@ struct DmaKSG : DmaKS<ROWS, BK, THREADS> {
 };
 
 // ---------------------------------------------------------------- work order
-// tile-rows per group of the grouped tile order (8 measured best or within
-// 1% of best against 4 and 16 for all three products at 8192 tokens)
+// tile-rows per group of the grouped tile order. Against 4 and 16 at 8192
+// tokens (forward, dX and gate over four Linear shapes), 8 was best or within
+// 1% of best in 11 of 12 cases; 4 was 2.6% faster for the forward at
+// 4096 -> 28672, and 16 was never best.
 constexpr int kGroupM = 8;
 
 // Workgroups are dispatched round-robin over the 8 XCDs (workgroup w runs on
