@@ -233,110 +233,99 @@ __device__ __forceinline__ float dot_run(const uint8_t* __restrict__ g, int p, c
     return dl * s1;
 }
 
-// <v, W> over the 16 weights p0 + 4h + 8u + t (u, t in 0..3) of the 32-weight
-// sub-block starting at p0 (a multiple of 32), with v[4u + t] their values:
-// the per-lane footprint of a 32x32 MFMA accumulator block.  sv[hf] is the sum
-// of v over half hf (v[0..7] and v[8..15], weights 0..15 and 16..31 of the
-// sub-block); it is the same for every candidate, so the caller computes it
-// once.  Codes are unpacked four at a time (one shift and mask per 32-bit
-// word, then v_cvt_f32_ubyteN per weight) as unsigned values u; a format's
-// constant offset (Q8_0's sign via u = q ^ 0x80, Q6_K's -32, Q3_K's -4) and
-// K-quant mins are applied once per half through sv:
+// <v, W> over the 16 consecutive weights p .. p + 15 (p a multiple of 16) of
+// the group at g, with v[r] the value of weight p + r: the per-lane footprint
+// of a 32x32 MFMA accumulator block whose rows are permuted so that each lane
+// holds 16 consecutive rows.  sv is the sum of v; it is the same for every
+// candidate, so the caller computes it once.  The 16 weights share one scale
+// (K-quant scales cover 16 or 32 weights, a Q8_0 block 32).  Codes are
+// unpacked four at a time (one shift and mask per 32-bit word, then
+// v_cvt_f32_ubyteN per weight) as unsigned values u; a format's constant
+// offset o (Q8_0's sign via u = q ^ 0x80, Q6_K's -32, Q3_K's -4) and the
+// K-quant min are applied once through sv:
 //   sum v (dl (u - o) - ml) = dl (sum v u - o sv) - ml sv.
+// Field offsets follow the layouts decode_codes reads (reference
+// layers.py:62-213 for Q8_0, Q4_K, Q5_K, Q6_K; the GGUF block layouts for
+// Q2_K and Q3_K).
 template <int QT>
-__device__ __forceinline__ float dot_sub32(const uint8_t* __restrict__ g, int p0, int h, const float* __restrict__ v,
-                                           const float (&sv)[2]) {
-    uint32_t uw[4];  // four unsigned code bytes per word, weights 4u .. 4u + 3 of the lane
-    float dl[2], ml[2] = {0.0f, 0.0f}, off = 0.0f;
+__device__ __forceinline__ float dot_sub16(const uint8_t* __restrict__ g, int p, const float* __restrict__ v, float sv) {
+    uint32_t uw[4];  // four unsigned code bytes per word: weights p + 4 u .. p + 4 u + 3
+    float dl, ml = 0.0f, off = 0.0f;
+    const int l = p & 16;  // first weight within the 32-weight run
     if constexpr (QT == Q8_0) {
-        const uint8_t* b = g + 34 * (p0 >> 5);
-        dl[0] = dl[1] = h2f(*reinterpret_cast<const uint16_t*>(b));
+        const uint8_t* b = g + 34 * (p >> 5);
+        dl = h2f(*reinterpret_cast<const uint16_t*>(b));
+        const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + l);  // 2-byte aligned
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint16_t* q = reinterpret_cast<const uint16_t*>(b + 2 + 4 * h + 8 * u);
-            uw[u] = ((uint32_t)q[0] | ((uint32_t)q[1] << 16)) ^ 0x80808080u;
-        }
+        for (int u = 0; u < 4; ++u) uw[u] = ((uint32_t)q[2 * u] | ((uint32_t)q[2 * u + 1] << 16)) ^ 0x80808080u;
         off = 128.0f;
     } else if constexpr (QT == Q4_K || QT == Q5_K) {
         const uint32_t dd = *reinterpret_cast<const uint32_t*>(g);
-        const int c = p0 >> 6, nib = (p0 >> 5) & 1;
+        const int c = p >> 6, nib = (p >> 5) & 1;
         uint32_t sc, m;
         scale_min_k4(g + 4, 2 * c + nib, sc, m);
-        dl[0] = dl[1] = h2f(dd & 0xffffu) * (float)sc;
-        ml[0] = ml[1] = h2f(dd >> 16) * (float)m;
-        const uint8_t* qs = g + (QT == Q5_K ? 48 : 16) + 32 * c + 4 * h;
+        dl = h2f(dd & 0xffffu) * (float)sc;
+        ml = h2f(dd >> 16) * (float)m;
+        // 144- and 176-byte groups keep 16-byte alignment
+        const u32x4 w = *reinterpret_cast<const u32x4*>(g + (QT == Q5_K ? 48 : 16) + 32 * c + l);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) uw[u] = (*reinterpret_cast<const uint32_t*>(qs + 8 * u) >> (4 * nib)) & 0x0F0F0F0Fu;
+        for (int u = 0; u < 4; ++u) uw[u] = (w[u] >> (4 * nib)) & 0x0F0F0F0Fu;
         if constexpr (QT == Q5_K) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(g + 16 + l);
             const int xs = 2 * c + nib;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t x = *reinterpret_cast<const uint32_t*>(g + 16 + 4 * h + 8 * u);
-                uw[u] |= ((x >> xs) & 0x01010101u) << 4;
-            }
+            for (int u = 0; u < 4; ++u) uw[u] |= ((x[u] >> xs) & 0x01010101u) << 4;
         }
     } else if constexpr (QT == Q6_K) {
         const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 208));
-        const int n = p0 >> 7, t4 = (p0 >> 5) & 3;
-        dl[0] = d * (float)(int8_t)g[192 + 8 * n + 2 * t4];
-        dl[1] = d * (float)(int8_t)g[192 + 8 * n + 1 + 2 * t4];
-        const uint8_t* ql = g + 64 * n + 32 * (t4 & 1) + 4 * h;
-        const uint8_t* qh = g + 128 + 32 * n + 4 * h;
+        const int n = p >> 7, t4 = (p >> 5) & 3;
+        dl = d * (float)(int8_t)g[192 + 8 * n + 2 * t4 + (l >> 4)];
+        const uint16_t* a = reinterpret_cast<const uint16_t*>(g + 64 * n + 32 * (t4 & 1) + l);  // 2-byte aligned
+        const uint16_t* b = reinterpret_cast<const uint16_t*>(g + 128 + 32 * n + l);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const uint16_t* a = reinterpret_cast<const uint16_t*>(ql + 8 * u);
-            const uint16_t* b = reinterpret_cast<const uint16_t*>(qh + 8 * u);
-            const uint32_t lw = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
-            const uint32_t hw = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+            const uint32_t lw = (uint32_t)a[2 * u] | ((uint32_t)a[2 * u + 1] << 16);
+            const uint32_t hw = (uint32_t)b[2 * u] | ((uint32_t)b[2 * u + 1] << 16);
             uw[u] = ((lw >> (4 * (t4 >> 1))) & 0x0F0F0F0Fu) | (((hw >> (2 * t4)) & 0x03030303u) << 4);
         }
         off = 32.0f;
     } else if constexpr (QT == Q3_K) {
         const float d = h2f(*reinterpret_cast<const uint16_t*>(g + 108));
-        const int n = p0 >> 7, j = (p0 >> 5) & 3;
+        const int n = p >> 7, j = (p >> 5) & 3;
         const uint8_t* sb = g + 96;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int is = 8 * n + 2 * j + hf;
-            const uint32_t lo4 = is < 8 ? (sb[is] & 0xFu) : (uint32_t)(sb[is - 8] >> 4);
-            const uint32_t hi2 = (sb[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
-            dl[hf] = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
-        }
+        const int is = 8 * n + 2 * j + (l >> 4);
+        const uint32_t lo4 = is < 8 ? (sb[is] & 0xFu) : (uint32_t)(sb[is - 8] >> 4);
+        const uint32_t hi2 = (sb[8 + (is & 3)] >> (2 * (is >> 2))) & 3u;
+        dl = d * (float)((int)(lo4 | (hi2 << 4)) - 32);
+        const uint16_t* a = reinterpret_cast<const uint16_t*>(g + 32 + 32 * n + l);  // 2-byte aligned
+        const uint16_t* b = reinterpret_cast<const uint16_t*>(g + l);
         const int xs = 4 * n + j;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int o = 16 * (u >> 1) + 4 * h + 8 * (u & 1);  // 16 * half + l within the 32-run
-            const uint16_t* a = reinterpret_cast<const uint16_t*>(g + 32 + 32 * n + o);
-            const uint16_t* b = reinterpret_cast<const uint16_t*>(g + o);
-            const uint32_t lw = (uint32_t)a[0] | ((uint32_t)a[1] << 16);
-            const uint32_t hw = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+            const uint32_t lw = (uint32_t)a[2 * u] | ((uint32_t)a[2 * u + 1] << 16);
+            const uint32_t hw = (uint32_t)b[2 * u] | ((uint32_t)b[2 * u + 1] << 16);
             // q = low2 - (hmask bit ? 0 : 4) = (low2 | bit << 2) - 4
             uw[u] = ((lw >> (2 * j)) & 0x03030303u) | (((hw >> xs) & 0x01010101u) << 2);
         }
         off = 4.0f;
-    } else {  // Q2_K
+    } else {  // Q2_K: 84-byte groups keep 4-byte alignment
         const uint32_t dd = *reinterpret_cast<const uint32_t*>(g + 80);
-        const float d = h2f(dd & 0xffffu), dmin = h2f(dd >> 16);
-        const int n = p0 >> 7, j = (p0 >> 5) & 3;
+        const int n = p >> 7, j = (p >> 5) & 3;
+        const uint32_t sc = g[8 * n + 2 * j + (l >> 4)];
+        dl = h2f(dd & 0xffffu) * (float)(sc & 0xFu);
+        ml = h2f(dd >> 16) * (float)(sc >> 4);
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(g + 16 + 32 * n + l);
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const uint32_t sc = g[8 * n + 2 * j + hf];
-            dl[hf] = d * (float)(sc & 0xFu);
-            ml[hf] = dmin * (float)(sc >> 4);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int o = 16 * (u >> 1) + 4 * h + 8 * (u & 1);
-            uw[u] = (*reinterpret_cast<const uint32_t*>(g + 16 + 32 * n + o) >> (2 * j)) & 0x03030303u;
-        }
+        for (int u = 0; u < 4; ++u) uw[u] = (q[u] >> (2 * j)) & 0x03030303u;
     }
+    // two partial sums shorten the dependent fma chain
     float s1[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) s1[u >> 1] = fmaf(v[4 * u + t], (float)((uw[u] >> (8 * t)) & 0xffu), s1[u >> 1]);
-    float r = dl[0] * (s1[0] - off * sv[0]) + dl[1] * (s1[1] - off * sv[1]);
-    if constexpr (HasMin<QT>::value) r -= ml[0] * sv[0] + ml[1] * sv[1];
+        for (int t = 0; t < 4; ++t) s1[u & 1] = fmaf(v[4 * u + t], (float)((uw[u] >> (8 * t)) & 0xffu), s1[u & 1]);
+    float r = dl * ((s1[0] + s1[1]) - off * sv);
+    if constexpr (HasMin<QT>::value) r -= ml * sv;
     return r;
 }
 

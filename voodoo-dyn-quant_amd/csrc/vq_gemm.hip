@@ -21,6 +21,7 @@ using FwdLB = DmaKS<256, 64, 64 * kWaves>;
 using DxLA = DmaKS<256, 64, 64 * kWaves>;
 using DxLB = DmaNS<256, 64, 64 * kWaves>;
 using GateL = DmaNS<256, 64, 64 * kWaves>;
+using GateLA = DmaNS<256, 64, 64 * kWaves, 1>;  // weight rows permuted for the gate epilogue
 constexpr int kGateBI = 256, kGateBJ = 256;
 
 int device_cus() {
@@ -52,7 +53,7 @@ static bool small_product(int M, int N) {
     return 4 * tiles < 3 * (int64_t)device_cus();
 }
 using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_FREE, 2>;
-using GateCfg = GemmCfg<GateL, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2, SWITCH_LOOSE, 2>;
+using GateCfg = GemmCfg<GateLA, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2, SWITCH_LOOSE, 2>;
 
 static GemmParams fwd_params(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D) {
     GemmParams p{};

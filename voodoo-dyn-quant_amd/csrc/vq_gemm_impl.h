@@ -72,6 +72,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 template <int ROWS, int BK, int THREADS>
 struct DmaKS {
     static constexpr bool kDma = true;
+    static constexpr int kPerm = 0;
     static constexpr int kFragReads = 1;
     static constexpr int CPR = BK / 8;
     static_assert(CPR == 4 || CPR == 8, "BK 32 or 64");
@@ -122,9 +123,16 @@ struct DmaKS {
 // multiples of 32); the XOR moves the 4 k-rows' 64-byte blocks onto distinct
 // quarters of 256 bytes (as a 64-byte pad per k-row would).  The read at
 // k + 4 keeps the same XOR.
-template <int ROWS, int BK, int THREADS>
+// PERM = 1 reorders each 32-row fragment by 4-row granules: MFMA row 4 q + t
+// reads tile row 4 rot(q) + t, rot(q) = 4 (q % 2) + q / 2.  Accumulator
+// element 4 u + t of lane l (MFMA row 8 u + 4 (l / 32) + t) then holds tile
+// row 16 (l / 32) + 4 u + t: each lane's 16 values of a 32x32 block are 16
+// consecutive tile rows.  Each 32-lane half still reads whole 64-byte blocks
+// of the same 4 k-rows, so the reads stay conflict-free.
+template <int ROWS, int BK, int THREADS, int PERM = 0>
 struct DmaNS {
     static constexpr bool kDma = true;
+    static constexpr int kPerm = PERM;
     static constexpr int kFragReads = 2;
     static constexpr int RCH = ROWS / 8;  // chunks per k-row
     static_assert(RCH % 16 == 0, "the XOR of up to 12 stays inside the k-row");
@@ -161,11 +169,13 @@ struct DmaNS {
     // (measured on gfx950), so when lane s addresses
     //     k = kk + 8 (s/32) + (s%16)/4,   row = r + 16 ((s/16)%2) + 4 (s%4)
     // lane l receives rows r + l%32 at k = kk + 8 (l/32) + 0..3: the MFMA layout
+    // (PERM = 1 moves each addressed 4-row granule as described above)
     static __device__ __forceinline__ bf16x8_t read_frag(const u32x4* __restrict__ lds, int row, int ks, int lane) {
         typedef short v4i16 __attribute__((ext_vector_type(4)));
         typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
         const int k = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
-        const int r = row + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        const int q = 4 * ((lane >> 4) & 1) + (lane & 3);  // 4-row granule of the MFMA rows
+        const int r = row + 4 * (PERM ? (((q & 1) << 2) | (q >> 1)) : q);
         const bf16_t* base =
             reinterpret_cast<const bf16_t*>(lds) + 8 * (k * RCH + ((r >> 3) ^ (4 * (k & 3)))) + (r & 7);
         const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base));
@@ -573,11 +583,12 @@ __device__ __forceinline__ void gate_stage_lds(u32x4* __restrict__ buf, const ui
     }
 }
 
-// <acc, W_k> over the lane's accumulators: block (a, b) holds, for row
-// n = 32 b + lane%32, the 16 weights 32 a + 4 (lane/32) + 8 u + t of one
-// 32-weight sub-block (relative to the wave's tile origin).
+// <acc, W_k> over the lane's accumulators: with the A operand's rows
+// permuted (DmaNS PERM = 1), block (a, b) holds, for row n = 32 b + lane%32,
+// the 16 consecutive weights 32 a + 16 (lane/32) + r, r = 0..15 (relative to
+// the wave's tile origin).
 template <int QT, int MI, int NJ, int WTI, int WTJ>
-__device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const float (&sv)[MI][NJ][2],
+__device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const float (&sv)[MI][NJ],
                                               const uint8_t* __restrict__ buf, int64_t row_groups, int j0, int group,
                                               int wi, int wj, int lane, int J) {
     constexpr int GB = group_bytes(QT);
@@ -595,7 +606,7 @@ __device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const
             float v[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) v[r] = acc[a][b][r];
-            s += dot_sub32<QT>(g, wi * WTI + 32 * a, lane >> 5, v, sv[a][b]);
+            s += dot_sub16<QT>(g, wi * WTI + 32 * a + 16 * (lane >> 5), v, sv[a][b]);
         }
     }
     return s;
@@ -627,19 +638,17 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
     const int jl0 = j0 - p.cg.set_j0[g];                 // first row within the tensor
     const int jn = p.cg.set_j0[g + 1] - p.cg.set_j0[g];  // the tensor's rows
     const int64_t rg = cs.row_groups;
-    // candidate-independent half sums of each accumulator block
-    float sv[S::MI][S::NJ][2];
+    // candidate-independent sums of each accumulator block
+    float sv[S::MI][S::NJ];
 #pragma unroll
     for (int a = 0; a < S::MI; ++a)
 #pragma unroll
-        for (int b = 0; b < S::NJ; ++b)
+        for (int b = 0; b < S::NJ; ++b) {
+            float t = 0.0f;
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                float t = 0.0f;
-#pragma unroll
-                for (int r = 0; r < 8; ++r) t += acc[a][b][8 * hf + r];
-                sv[a][b][hf] = t;
-            }
+            for (int r = 0; r < 16; ++r) t += acc[a][b][r];
+            sv[a][b] = t;
+        }
     __syncthreads();  // every wave is past its last main-loop LDS read
     gate_stage_regs<BJ, S::THREADS>(smem, cs.qbytes[0], cs.qtype[0], rg, jl0, group, jn);
     for (int k = 0; k < cs.ncand; ++k) {
@@ -817,6 +826,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
         }
         store_tile_lds<BI, BJ, BK, WI, WJ>(p, i0, j0, smem, acc);
     } else {
+        static_assert(LA::kPerm == 1, "the gate epilogue reads 16 consecutive weights per accumulator block");
         gate_epilogue<BI, BJ, BK, WI, WJ>(p, block, i0, j0, smem, acc);
     }
 }
