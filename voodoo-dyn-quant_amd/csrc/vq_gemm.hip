@@ -37,8 +37,11 @@ int device_cus() {
     return cus;
 }
 
-// the forward issues each refill in two halves (measured 0.3-4% faster at
-// every swept shape; dX and the gate product are not faster that way)
+// Every 8-wave product issues each refill in two halves (COPY_SPLIT).  The
+// forward: 0.3-4% faster at every swept shape.  The backward, with dX and the
+// gate product both scheduled SWITCH_LOOSE: 3.0-3.1% faster than dX
+// SWITCH_FREE + gate SWITCH_LOOSE with single-burst refills at 8192 tokens
+// and 5120 -> 17408, 17408 -> 5120, 4096 -> 28672 (0.6-1.3% at 1024-wide).
 using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_READ_FIRST, 2, COPY_SPLIT>;
 // Products with fewer 256x256 tiles than three quarters of the CUs (the 0.8B
 // decoder's 1024-wide projections at 8192 tokens) fill the chip better with
@@ -52,8 +55,8 @@ static bool small_product(int M, int N) {
     const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
     return 4 * tiles < 3 * (int64_t)device_cus();
 }
-using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_FREE, 2>;
-using GateCfg = GemmCfg<GateLA, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2, SWITCH_LOOSE, 2>;
+using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_LOOSE, 2, COPY_SPLIT>;
+using GateCfg = GemmCfg<GateLA, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2, SWITCH_LOOSE, 2, COPY_SPLIT>;
 
 static GemmParams fwd_params(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D) {
     GemmParams p{};
