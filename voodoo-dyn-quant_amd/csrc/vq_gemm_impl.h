@@ -543,24 +543,6 @@ constexpr int kGateMaxChunks = gate_span_chunks(272);  // worst type (Q8_0)
 
 __device__ __forceinline__ int gate_row_chunks(int qt) { return gate_span_chunks(group_bytes(qt)); }
 
-// Same copy through registers (ordinary loads, then ds_write), for the first
-// candidate, which is consumed right after it is staged.
-template <int BJ, int THREADS>
-__device__ __forceinline__ void gate_stage_regs(u32x4* __restrict__ buf, const uint8_t* __restrict__ qbytes, int qt,
-                                                int64_t row_groups, int j0, int group, int J) {
-    const int gb = group_bytes(qt), nch = gate_row_chunks(qt);
-    const int64_t bytes = (int64_t)J * row_groups * gb;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(qbytes), (short)0, (int)(bytes < (int64_t)kRange ? bytes : (int64_t)kRange), 0x00020000);
-    const int total = BJ * nch;
-    for (int id = threadIdx.x; id < total; id += THREADS) {
-        const int row = id / nch, c = id % nch;
-        const int n = j0 + row < J ? j0 + row : 0;
-        const int64_t span = ((int64_t)n * row_groups + group) * gb;
-        buf[id] = buf_load16(rs, (uint32_t)((span & ~int64_t(15)) + 16 * c));
-    }
-}
-
 template <int BJ, int THREADS>
 __device__ __forceinline__ void gate_stage_lds(u32x4* __restrict__ buf, const uint8_t* __restrict__ qbytes, int qt,
                                                int64_t row_groups, int j0, int group, int J) {
@@ -650,7 +632,7 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
             sv[a][b] = t;
         }
     __syncthreads();  // every wave is past its last main-loop LDS read
-    gate_stage_regs<BJ, S::THREADS>(smem, cs.qbytes[0], cs.qtype[0], rg, jl0, group, jn);
+    gate_stage_lds<BJ, S::THREADS>(smem, cs.qbytes[0], cs.qtype[0], rg, jl0, group, jn);
     for (int k = 0; k < cs.ncand; ++k) {
         // this wave's direct-to-LDS copies of candidate k have landed, then
         // everyone's have; buffer (k+1) % 2 is no longer read
