@@ -8,22 +8,41 @@
 // row's groups contiguously and rows back to back, so the flattened group index
 // g covers weights [256 g, 256 g + 256) of the row-major [N][D_pad] matrix.
 // A workgroup streams kGroupsPerBlock consecutive groups of every candidate
-// into LDS with 16-byte loads (the byte range of 16 groups is a multiple of 16
+// into LDS with 16-byte direct-to-LDS loads (the byte range of 16 groups is a multiple of 16
 // for every format), then each thread decodes runs of 8 weights from LDS and
 // writes them with 16-byte (bf16 x8) or 2x16-byte (fp32 x8) stores.
 #include "vq_internal.h"
 
 namespace vq {
 
-// Copy `len` bytes at `src` (16-byte aligned) to LDS `dst`.
+// Copy `len` bytes at `src` (16-byte aligned) to LDS `dst` (16-byte aligned)
+// with direct-to-LDS loads (buffer_load_dwordx4 ... lds: lane l of a wave's
+// instruction lands at M0 + 16 l), so a thread's loads of every candidate are
+// in flight together and no register holds them; stage_wait() then waits for
+// them before the workgroup synchronises.  Whole 16-byte chunks only: lanes
+// past them are masked off, and the last `len % 16` bytes are copied by
+// ordinary byte loads.
 __device__ __forceinline__ void stage_bytes(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, int len) {
+    typedef __attribute__((address_space(3))) void lds_void;
     const int nvec = len >> 4;
-    const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
-    u32x4* d4 = reinterpret_cast<u32x4*>(dst);
-    for (int i = threadIdx.x; i < nvec; i += blockDim.x) d4[i] = __builtin_nontemporal_load(s4 + i);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src), (short)0, len, 0x00020000);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int stride = (int)blockDim.x;  // a multiple of 64
+    for (int base = 64 * wave; base < nvec; base += stride) {
+        // cache policy 2: streamed once (non-temporal)
+        if (base + lane < nvec)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 16 * base), 16, 16 * (base + lane), 0, 0,
+                                                     2);
+    }
     const int tail = len & 15;
     if ((int)threadIdx.x < tail) dst[(nvec << 4) + threadIdx.x] = src[(nvec << 4) + threadIdx.x];
 }
+
+// This thread's stage_bytes copies have landed in LDS (a __syncthreads()
+// after it makes everyone's visible).
+__device__ __forceinline__ void stage_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // OUT = float: ggml's fp32 values bit for bit; OUT = bf16_t: those values
 // rounded to bf16 (torch's rounding), the source-dtype candidate the
@@ -36,6 +55,7 @@ __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* 
     const int64_t g0 = (int64_t)blockIdx.x * kGroupsPerBlock;
     const int ng = (int)min<int64_t>(kGroupsPerBlock, ngroups - g0);
     stage_bytes(lds, q + g0 * GB, ng * GB);
+    stage_wait();
     __syncthreads();
     const int t = threadIdx.x;
 #pragma unroll
@@ -121,6 +141,7 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
         stage_bytes(lds + acc, cs.qbytes[k] + g0 * gb, ng * gb);
         acc += (GPB * gb + 15) & ~15;
     }
+    stage_wait();
     __syncthreads();
     const int t = threadIdx.x;
     const float* probs = mp.probs[si];
