@@ -27,22 +27,32 @@ namespace {
 // memory) plus the segment itself.
 __host__ __device__ constexpr int span_cap(int gb) { return (kGroupsPerBlock * gb + 15 + 15) & ~15; }
 
-// Copy [src, src + len) to dst + (src mod 16).  Whole 16-byte chunks move as
-// vector loads from the 16-byte boundary at or below src (never below the
-// 16-byte aligned buffer that holds src); the last partial chunk moves byte by
-// byte, so nothing past src + len is read.  Returns src mod 16.
+// Copy [src, src + len) to dst + (src mod 16), dst 16-byte aligned in LDS.
+// Whole 16-byte chunks move as direct-to-LDS loads (buffer_load_dwordx4 ...
+// lds: lane l of a wave's instruction lands at M0 + 16 l) from the 16-byte
+// boundary at or below src (never below the 16-byte aligned buffer that holds
+// src), so every candidate's copies are in flight together; the last partial
+// chunk moves byte by byte, so nothing past src + len is read.  span_wait()
+// waits for this thread's copies.  Returns src mod 16.
 __device__ __forceinline__ int stage_span(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, int len) {
+    typedef __attribute__((address_space(3))) void lds_void;
     const int head = (int)(reinterpret_cast<uintptr_t>(src) & 15u);
     const uint8_t* base = src - head;
     const int total = head + len;
     const int nvec = total >> 4;
-    const u32x4* s4 = reinterpret_cast<const u32x4*>(base);
-    u32x4* d4 = reinterpret_cast<u32x4*>(dst);
-    for (int i = threadIdx.x; i < nvec; i += blockDim.x) d4[i] = s4[i];
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, total, 0x00020000);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    for (int b = 64 * wave; b < nvec; b += (int)blockDim.x)
+        if (b + lane < nvec)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 16 * b), 16, 16 * (b + lane), 0, 0, 0);
     const int tail = total & 15;
     if ((int)threadIdx.x < tail) dst[(nvec << 4) + threadIdx.x] = base[(nvec << 4) + threadIdx.x];
     return head;
 }
+
+__device__ __forceinline__ void span_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 struct RowSeg {
     int64_t r;   // requested row (output row)
@@ -143,6 +153,7 @@ __global__ __launch_bounds__(kStreamThreads) void embed_rows_kernel(CandSet cs, 
             off += span_cap(gb);
         }
     }
+    span_wait();
     __syncthreads();
     const int t = threadIdx.x;
     const int p = 8 * (t & 31);
@@ -214,6 +225,7 @@ __global__ __launch_bounds__(kStreamThreads) void embed_rows_bwd_kernel(CandSet 
         for (int r = 0; r < 8; ++r) v[u][r] = 0.0f;
         if (live[u]) load8(grad + rs.r * dim + col, v[u]);
     }
+    span_wait();
     __syncthreads();
     const int wave = t >> 6;
     for (int k = 0; k < cs.ncand; ++k) {
