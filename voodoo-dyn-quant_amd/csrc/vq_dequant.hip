@@ -108,9 +108,9 @@ hipError_t launch_dequant_bf16(int qtype, const uint8_t* q, bf16_t* out, int64_t
 // Mixture: W_eff = bf16( (((0 + p0 W0) + p1 W1) + ...) ) with every product and
 // sum rounded separately, exactly as the fp32 torch ops of the reference.
 // One launch mixes up to kMaxSets tensors (the members of a stacked
-// product); a workgroup covers RUNS * 16 groups of one tensor, so small
-// tensors get more, shorter workgroups.  A thread takes 16 consecutive
-// weights of a group per run (one scale decode per candidate and run).
+// product); a workgroup covers RUNS * 16 groups of one tensor (launched with
+// RUNS = 1).  A thread takes 16 consecutive weights of a group per run (one
+// scale decode per candidate and run).
 // ---------------------------------------------------------------------------
 struct MixPlan {
     int nsets;
@@ -195,19 +195,10 @@ hipError_t launch_mix_sets(int nsets, const CandSet* sets, const float* const* p
                            const int64_t* ngroups, hipStream_t s) {
     MixPlan mp{};
     mp.nsets = nsets;
-    int64_t total = 0;
-    for (int i = 0; i < nsets; ++i) total += ngroups[i];
-    // 16-group workgroups when 32-group ones would not give every CU two, or
-    // would stage more than 64 KiB (wide menus of large formats)
-    size_t lds32 = 0;
-    for (int i = 0; i < nsets; ++i) {
-        size_t l = 0;
-        for (int k = 0; k < sets[i].ncand; ++k) l += (2 * kMixGroupsPerPass * group_bytes(sets[i].qtype[k]) + 15) & ~15;
-        lds32 = l > lds32 ? l : lds32;
-    }
-    const bool small = (total + 2 * kMixGroupsPerPass - 1) / (2 * kMixGroupsPerPass) < 2 * (int64_t)device_cus() ||
-                       lds32 > 64 * 1024;
-    const int gpb = small ? kMixGroupsPerPass : 2 * kMixGroupsPerPass;
+    // 16 groups per workgroup: with the staging copies all in flight at once,
+    // 32- and 64-group workgroups were 13% and 40% slower at 17408 x 5120
+    // (K = 6), and slower at 1536 x 1024 and 6144 x 1024 too
+    const int gpb = kMixGroupsPerPass;
     size_t lds = 0;
     int64_t blocks = 0;
     for (int i = 0; i < nsets; ++i) {
@@ -223,10 +214,7 @@ hipError_t launch_mix_sets(int nsets, const CandSet* sets, const float* const* p
     }
     mp.block0[nsets] = blocks;
     if (blocks <= 0) return hipSuccess;
-    if (small)
-        mix_kernel<1><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
-    else
-        mix_kernel<2><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
+    mix_kernel<1><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
     return hipGetLastError();
 }
 
