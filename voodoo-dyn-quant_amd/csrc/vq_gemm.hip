@@ -37,12 +37,15 @@ int device_cus() {
     return cus;
 }
 
-// Every 8-wave product issues each refill in two halves (COPY_SPLIT).  The
-// forward: 0.3-4% faster at every swept shape.  The backward, with dX and the
-// gate product both scheduled SWITCH_LOOSE: 3.0-3.1% faster than dX
-// SWITCH_FREE + gate SWITCH_LOOSE with single-burst refills at 8192 tokens
-// and 5120 -> 17408, 17408 -> 5120, 4096 -> 28672 (0.6-1.3% at 1024-wide).
-using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_READ_FIRST, 2, COPY_SPLIT>;
+// Every 8-wave product issues each refill in two halves (COPY_SPLIT) and
+// pins its schedule only at each stage's first k-step (SWITCH_LOOSE).  The
+// forward: split refills 0.3-4% faster at every swept shape, then SWITCH_LOOSE
+// 0.1-1.0% faster than SWITCH_READ_FIRST at 8192 tokens and 5120 -> 17408,
+// 4096 -> 28672, 14336 -> 4096, 1024 -> 6144, 1024 -> 1536.  The backward:
+// 3.0-3.1% faster than dX SWITCH_FREE + gate SWITCH_LOOSE with single-burst
+// refills at 5120 -> 17408, 17408 -> 5120, 4096 -> 28672 (0.6-1.3% at
+// 1024-wide).
+using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_LOOSE, 2, COPY_SPLIT>;
 // Products with fewer 256x256 tiles than three quarters of the CUs (the 0.8B
 // decoder's 1024-wide projections at 8192 tokens) fill the chip better with
 // 128x128 tiles, four waves of 64x64 and two workgroups per CU (measured on
