@@ -51,8 +51,11 @@ using FwdCfg = GemmCfg<FwdLA, FwdLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_LO
 // 128x128 tiles, four waves of 64x64 and two workgroups per CU (measured on
 // MI355X at 8192 tokens: 1024 -> 1024 25 vs 33 us, 3072 -> 1024 55 vs 67 us);
 // from 192 tiles on the 8-wave 256x256 tiles win (1024 -> 1536 33 vs 39 us,
-// 1024 -> 3072 65 vs 68 us).
-using FwdSmallCfg = GemmCfg<DmaKS<128, 64, 256>, DmaKS<128, 64, 256>, 128, 128, 64, 2, 2, EPI_STORE, 2, SWITCH_FENCED, 2>;
+// 1024 -> 3072 65 vs 68 us).  Reads first with split refills: 3-12% faster
+// than a fenced stage switch with one burst per refill (8192 tokens at
+// 1024 -> 1024, 2048 -> 1024, 3072 -> 1024; 4096 tokens at 1024 -> 1024).
+using FwdSmallCfg =
+    GemmCfg<DmaKS<128, 64, 256>, DmaKS<128, 64, 256>, 128, 128, 64, 2, 2, EPI_STORE, 2, SWITCH_READ_FIRST, 2, COPY_SPLIT>;
 
 static bool small_product(int M, int N) {
     const int64_t tiles = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
