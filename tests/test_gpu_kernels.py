@@ -145,12 +145,26 @@ def test_mix_weight_bit_exact(hip, types):
 
 
 def test_mix_weight_bit_exact_large(hip):
-    """A tensor large enough for the mix kernel's 32-group workgroups, with a
-    ragged last workgroup (4104 x 1280 = 20520 groups)."""
+    """A large tensor (4104 x 1280 = 20520 groups, 1283 workgroups of 16
+    groups) with a ragged last workgroup of 8 groups."""
     rng = np.random.default_rng(12)
     n, d_pad = 4104, 1280
     qbs, ws = _candidates(SIX, n, d_pad, rng)
     probs = torch.softmax(torch.randn(len(SIX), generator=torch.Generator().manual_seed(2)), 0)
+    ref = mixture.mix_weight(ws, probs).to(torch.bfloat16)
+    got = hip.mix_weight([GGML[t] for t in SIX], [_dev(q.reshape(-1)) for q in qbs], probs.cuda(), n, d_pad)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+def test_mix_weight_bit_exact_odd_tail(hip):
+    """263 groups: the last 16-group workgroup stages 7 groups, so the Q3_K
+    and Q6_K byte ranges end inside a 16-byte chunk (770 and 1470 bytes) and
+    their last bytes take the byte-copy path after the direct-to-LDS chunks."""
+    rng = np.random.default_rng(13)
+    n, d_pad = 263, 256
+    qbs, ws = _candidates(SIX, n, d_pad, rng)
+    probs = torch.softmax(torch.randn(len(SIX), generator=torch.Generator().manual_seed(3)), 0)
     ref = mixture.mix_weight(ws, probs).to(torch.bfloat16)
     got = hip.mix_weight([GGML[t] for t in SIX], [_dev(q.reshape(-1)) for q in qbs], probs.cuda(), n, d_pad)
     torch.cuda.synchronize()
