@@ -669,7 +669,11 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
 
 // ---------------------------------------------------------------- kernels
 // One GEMM configuration: loaders, tile, wave layout, epilogue, pipeline depth.
-constexpr int kMinSavedSplitSteps = 10;  // see GemmCfg::plan
+// K steps a split part of a store tile must save (see GemmCfg::plan).  14
+// against 10: the dual backward at 8192 tokens, 1024 -> 1536 (24 K steps of
+// dX, no longer split in two) 94 -> 82 us; within 0.5% at 5120 -> 17408,
+// 4096 -> 28672 and the other 1024-wide products.
+constexpr int kMinSavedSplitSteps = 14;
 
 template <class LA_, class LB_, int BI_, int BJ_, int BK_, int WI_, int WJ_, int EPI_, int DEPTH_,
           int SWITCH_ = SWITCH_FENCED, int OCC_ = 1, int COPY_ = COPY_BURST>
@@ -694,8 +698,8 @@ struct GemmCfg {
     // Fill in the work decomposition; returns the grid size (8 * blocks per XCD).
     static int plan(GemmParams& p, int cus, bool split_ok) {
         if (p.I <= 0 || p.J <= 0) return 0;
-        // a split store tile pays a fixup launch (about 6-8 K steps of one
-        // tile on MI355X): split only when a part saves more than that
+        // a split store tile pays for its partial writes and a fixup launch:
+        // split only when a part saves at least kMinSavedSplitSteps K steps
         p.split_min_saved = EPI == EPI_STORE ? kMinSavedSplitSteps : 0;
         // more than 8 parts (tried for the gate at 1024 x 1024) loses: the
         // parts of a dual launch then overflow one round of the CUs
