@@ -132,10 +132,34 @@ def test_module_construction_and_cache_reuse(isolated_cache):
     assert lin.candidate_source in ("rtn", "ggml")
     assert list(isolated_cache.rglob("combined_lazy_*.pt"))
     lin2 = _lin()
-    assert lin2.candidate_source == "cache"
+    assert lin2.candidate_source == ("cache" if lin.candidate_source == "ggml" else "cache_rtn")
     for k in range(3):
         assert torch.equal(getattr(lin, f"_qweight_{k}"), getattr(lin2, f"_qweight_{k}"))
     assert "_qweight_0" not in lin.state_dict()  # packed bytes are not checkpointed
+
+
+def test_rtn_candidates_never_land_under_the_ggml_key(isolated_cache, monkeypatch):
+    """Candidates from the RTN fallback are cached under their own mode: a run
+    (here or the reference's) that looks up llama.cpp bytes finds nothing."""
+    monkeypatch.setattr(layers, "find_libggml", lambda: None)
+    lin = _lin(name="rtn.proj", seed=3)
+    assert lin.candidate_source == "rtn"
+    padded, _, _ = layers.pad_weight_and_imatrix(
+        torch.randn(64, 512, generator=torch.Generator().manual_seed(3)) * 0.02, None)
+    wh = cache.tensor_hash(padded)
+    assert cache.load_candidates("rtn.proj", lin.candidate_types, "lazy", wh, "none", isolated_cache) == {}
+    rtn_hit = cache.load_candidates("rtn.proj", lin.candidate_types, cache.RTN_MODE, wh, "none", isolated_cache)
+    assert set(rtn_hit) == set(lin.candidate_types)
+    # without libggml the RTN entry is reused ...
+    assert _lin(name="rtn.proj", seed=3).candidate_source == "cache_rtn"
+    # ... and with libggml it is ignored: the candidates are quantized afresh
+    made = {}
+    monkeypatch.setattr(layers, "find_libggml", lambda: "libggml-base.so")
+    monkeypatch.setattr(layers, "quantize_tensor",
+                        lambda w, qt, im=None: made.setdefault(qt, rtn.rtn_quantize_tensor(w, qt)))
+    assert _lin(name="rtn.proj", seed=3).candidate_source == "ggml"
+    assert set(made) == set(lin.candidate_types)
+    assert set(cache.load_candidates("rtn.proj", lin.candidate_types, "lazy", wh, "none", isolated_cache)) == set(made)
 
 
 def test_padding_to_256(isolated_cache):

@@ -532,9 +532,12 @@ __device__ __forceinline__ void gemm_mainloop_pp(const GemmParams& p, int i0, in
 // (buffer_load_dwordx4 ... lds: lane l of an instruction lands at M0 + 16 l),
 // each span rounded out to whole 16-byte chunks so the LDS copy keeps the
 // global alignment of every field.  Candidate k+1 streams in while candidate k
-// is decoded in the accumulator layout.  The descriptor covers exactly the
-// candidate's bytes, so the rounded-out tail of the last span reads zeros;
-// rows past J load row 0 (their dW is zero).
+// is decoded in the accumulator layout.  The descriptor starts at the 16-byte
+// boundary at or below the tile's first row and ends with the candidate's
+// bytes, so the rounded-out tail of the last span reads zeros and every offset
+// stays within the tile's 256 row spans (below 2^30 for any row length the
+// C ABI accepts), however large the candidate; rows past J load the tile's
+// first row (their dW is zero).
 // A staged span takes an odd number of 16-byte chunks: the 32 rows one wave
 // reads at the same offset then fall on 16 distinct 16-byte bank groups
 // instead of 4 or 8 (even pitches repeat after 4 or 8 rows).
@@ -548,20 +551,22 @@ __device__ __forceinline__ void gate_stage_lds(u32x4* __restrict__ buf, const ui
                                                int64_t row_groups, int j0, int group, int J) {
     typedef __attribute__((address_space(3))) void lds_void;
     const int gb = group_bytes(qt), nch = gate_row_chunks(qt);
-    const int64_t bytes = (int64_t)J * row_groups * gb;
+    const int64_t origin = ((int64_t)j0 * row_groups * gb) & ~int64_t(15);
+    const int64_t bytes = (int64_t)J * row_groups * gb - origin;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(qbytes), (short)0, (int)(bytes < (int64_t)kRange ? bytes : (int64_t)kRange), 0x00020000);
+        const_cast<uint8_t*>(qbytes + origin), (short)0, (int)(bytes < (int64_t)kRange ? bytes : (int64_t)kRange),
+        0x00020000);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int NW = THREADS / 64;
     const int total = BJ * nch;
     for (int base = wave * 64; base < total; base += NW * 64) {
         const int id = base + lane;
         const int row = id / nch, c = id % nch;
-        const int n = (j0 + row < J && id < total) ? j0 + row : 0;
+        const int n = (j0 + row < J && id < total) ? j0 + row : j0;
         const int64_t span = ((int64_t)n * row_groups + group) * gb;
         // one instruction per wave: lanes land at buf + 16 (base + lane)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(buf + base), 16,
-                                                 (uint32_t)((span & ~int64_t(15)) + 16 * c), 0, 0, 0);
+                                                 (uint32_t)((span & ~int64_t(15)) - origin + 16 * c), 0, 0, 0);
     }
 }
 
@@ -579,8 +584,8 @@ __device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const
 #pragma unroll
     for (int b = 0; b < NJ; ++b) {
         const int nl = wj * WTJ + 32 * b + (lane & 31);
-        // rows past J were staged from row 0: locate their bytes the same way
-        const int n = j0 + nl < J ? j0 + nl : 0;
+        // rows past J were staged from the tile's first row: locate their bytes the same way
+        const int n = j0 + nl < J ? j0 + nl : j0;
         const int64_t span = ((int64_t)n * row_groups + group) * GB;
         const uint8_t* g = buf + nl * PITCH + (int)(span & 15);
 #pragma unroll

@@ -13,7 +13,10 @@ so caches built by either side are interchangeable:
 * writes are atomic (temporary file + ``os.replace``)
 
 The gated layers here keep candidates as packed bytes, i.e. the ``lazy``
-entries (``uint8 [nblocks, block_bytes]``).  One root governs every path: the
+entries (``uint8 [nblocks, block_bytes]``).  ``lazy`` entries hold llama.cpp
+bytes only.  Candidates made by the non-ggml RTN encoder (no libggml on the
+host) are stored under :data:`RTN_MODE` instead: same layout, a file name no
+ggml-backed run (here or in the reference) ever looks up.  One root governs every path: the
 module attribute :data:`CANDIDATE_CACHE_DIR` (or ``$VOODOO_CANDIDATE_CACHE_DIR``),
 read at call time, so tests can point it at a temporary directory.
 """
@@ -29,6 +32,10 @@ import torch
 CANDIDATE_CACHE_DIR = Path(
     os.environ.get("VOODOO_CANDIDATE_CACHE_DIR", Path(__file__).resolve().parent.parent / ".cache" / "mixed_quant_candidates")
 )
+
+
+# mode of the entries written from the RTN fallback encoder
+RTN_MODE = "lazy_rtn"
 
 
 def cache_root(root: Path | str | None = None) -> Path:

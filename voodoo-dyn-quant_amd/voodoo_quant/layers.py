@@ -434,15 +434,26 @@ class _MixedQuantBase(nn.Module):
         weight_hash = cache.tensor_hash(padded)
         imatrix_hash = cache.tensor_hash(padded_imatrix) if imatrix is not None else "none"
         root = CANDIDATE_CACHE_DIR if CANDIDATE_CACHE_DIR != cache.CANDIDATE_CACHE_DIR else None
+        # "lazy" entries hold llama.cpp bytes only (whoever wrote them); the
+        # RTN fallback's bytes live under their own mode, read only while
+        # libggml is absent, so a later libggml run never trains on them
         found = cache.load_candidates(tensor_name, self.candidate_types, "lazy", weight_hash, imatrix_hash, root)
+        self.candidate_source = "cache"
+        have_ggml = find_libggml() is not None
+        if not have_ggml and len(found) < len(self.candidate_types):
+            rest = [qt for qt in self.candidate_types if qt not in found]
+            rtn_found = cache.load_candidates(tensor_name, rest, cache.RTN_MODE, weight_hash, imatrix_hash, root)
+            if rtn_found:
+                self.candidate_source = "cache_rtn"
+                found.update(rtn_found)
         missing = [qt for qt in self.candidate_types if qt not in found]
-        self.candidate_source = "cache" if not missing else None
         if missing:
             made, source = _quantize_candidates(padded, padded_imatrix, missing)
             self.candidate_source = source
             found.update(made)
             try:
-                cache.save_candidates(tensor_name, made, "lazy", weight_hash, imatrix_hash, root)
+                mode = "lazy" if source == "ggml" else cache.RTN_MODE
+                cache.save_candidates(tensor_name, made, mode, weight_hash, imatrix_hash, root)
             except OSError as e:  # a read-only cache is not fatal
                 print(f"  [cache] {tensor_name}: not saved ({e})", file=sys.stderr)
         full_out = shard_spec.full_out if shard_spec is not None else out_features
