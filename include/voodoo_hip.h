@@ -239,6 +239,25 @@ int vq_gated_linear_bwd(const uint16_t *dy, const uint16_t *x, int64_t m, int64_
                         const uint16_t *w_eff, uint16_t *dx, float *dprobs, void *workspace, int64_t ws_bytes,
                         void *stream);
 
+/* Bytes of the library's static scratch (per device, held until the process
+ * ends) behind vq_gated_linear_bwd_static. */
+#define VQ_STATIC_SCRATCH_BYTES (4 << 20)
+
+/* vq_gated_linear_bwd with no workspace and no allocation of any kind: the
+ * gate partials (and dX's split-tail tiles, when they fit behind them) live
+ * in a static device array of VQ_STATIC_SCRATCH_BYTES, and dx needs the
+ * forward's w_eff (no re-mix).  Sizes whose gate partials exceed the scratch
+ * return VQ_ERR_WORKSPACE.  Every call on a device shares that device's
+ * scratch: calls that overlap on one device (concurrent streams, threads)
+ * race and must be serialised by the caller.  dprobs is bit-identical to
+ * vq_gated_linear_bwd's; dx too when both split dX the same way.
+ * No counterpart in the reference: this entry point is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+int vq_gated_linear_bwd_static(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
+                               int ncand, const int *qtypes, const void *const *qbytes, const uint16_t *w_eff,
+                               uint16_t *dx, float *dprobs, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,6 +2,7 @@
 // validation, error strings and kernel sequencing.  No entry point allocates.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/voodoo_hip.h"
@@ -152,6 +153,101 @@ int check_embed(int ncand, const int* qtypes, const void* const* qbytes, const i
     return VQ_OK;
 }
 
+
+// Checks shared by the two gated-Linear backward entry points.
+int check_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+              const int* qtypes, const void* const* qbytes, const uint16_t* w_eff, const uint16_t* dx) {
+    int rc = check_candidates(ncand, qtypes, qbytes, n, d, d_pad, true);
+    if (rc != VQ_OK) return rc;
+    if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
+    if (!dy || !x) return fail(VQ_ERR_NULL, "dy/x is NULL");
+    if (!aligned16(dy) || !aligned16(x)) return fail(VQ_ERR_ALIGN, "dy/x not 16-byte aligned");
+    if (dx && !aligned16(dx)) return fail(VQ_ERR_ALIGN, "dx not 16-byte aligned");
+    if (w_eff && !aligned16(w_eff)) return fail(VQ_ERR_ALIGN, "w_eff not 16-byte aligned");
+    return VQ_OK;
+}
+
+// The backward's launches: an optional re-mix of W_eff into remix_buf, the
+// dX and gate products (one launch when both run), the fixed-order reduce.
+// partials: gate_partial_count * ncand floats; tail_ws: dX's split-tail
+// partial tiles, or NULL to run dX's tiles whole.
+int run_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
+            const vq::CandSet& cs, const float* probs, const uint16_t* w_eff, uint16_t* remix_buf, uint16_t* dx,
+            float* dprobs, float* partials, float* tail_ws, hipStream_t s) {
+    int rc = VQ_OK;
+    const int ncand = cs.ncand;
+    if (dx) {
+        const uint16_t* w = w_eff;
+        if (remix_buf) {
+            rc = hip_check(vq::launch_mix(cs, probs, remix_buf, n * d_pad / 256, s), "mix launch");
+            if (rc != VQ_OK) return rc;
+            w = remix_buf;
+        }
+        if (m > 0 && dprobs) {
+            // both products in one launch: each fills the other's last round
+            rc = hip_check(vq::launch_gemm_dx_gate(dy, w, d_pad, dx, x, group_of(cs, n), partials, (int)m, (int)n,
+                                                   (int)d, tail_ws, s),
+                           "dX + gate GEMM launch");
+            if (rc != VQ_OK) return rc;
+        } else if (m > 0) {
+            rc = hip_check(vq::launch_gemm_dx(dy, w, d_pad, dx, (int)m, (int)n, (int)d, tail_ws, s),
+                           "dX GEMM launch");
+            if (rc != VQ_OK) return rc;
+        }
+    }
+    if (dprobs) {
+        if (m == 0) {
+            // no tokens: dL/dp = 0 (written by the reduce over zero partials)
+            rc = hip_check(vq::launch_gate_reduce(partials, 0, ncand, dprobs, s), "gate reduce launch");
+            return rc == VQ_OK ? ok() : rc;
+        }
+        if (!dx) {
+            rc = hip_check(vq::launch_gemm_gate(dy, x, group_of(cs, n), partials, (int)m, (int)n, (int)d, s),
+                           "gate GEMM launch");
+            if (rc != VQ_OK) return rc;
+        }
+        const int64_t nparts = vq::gate_partial_count((int)m, (int)n, (int)d);
+        rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, s), "gate reduce launch");
+        if (rc != VQ_OK) return rc;
+    }
+    return ok();
+}
+
+// Scratch memory of vq_gated_linear_bwd_static, for callers that cannot
+// allocate: gate partials, then dX's split-tail tiles when they fit.  One copy
+// per device (the code object's own global), held until the process ends;
+// its device address is looked up once per device with that device current.
+constexpr int64_t kStaticScratchBytes = VQ_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+constexpr int kMaxDevices = 64;
+char* g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the device `s` runs on (the current
+// device for the NULL stream).
+int static_scratch(hipStream_t s, char** out) {
+    int cur = 0;
+    int rc = hip_check(hipGetDevice(&cur), "hipGetDevice");
+    if (rc != VQ_OK) return rc;
+    int dev = cur;
+    if (s) {
+        rc = hip_check(hipStreamGetDevice(s, &dev), "hipStreamGetDevice");
+        if (rc != VQ_OK) return rc;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fail(VQ_ERR_HIP, "device %d: beyond the %d devices tracked", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        if (dev != cur && (rc = hip_check(hipSetDevice(dev), "hipSetDevice")) != VQ_OK) return rc;
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        rc = hip_check(e, "hipGetSymbolAddress(scratch)");
+        if (rc != VQ_OK) return rc;
+        g_scratch_ptr[dev] = static_cast<char*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return VQ_OK;
+}
 
 }  // namespace
 
@@ -510,19 +606,11 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
                         int ncand, const int* qtypes, const void* const* qbytes, const float* probs,
                         const uint16_t* w_eff, uint16_t* dx, float* dprobs, void* workspace, int64_t ws_bytes,
                         void* stream) {
-    int rc = check_candidates(ncand, qtypes, qbytes, n, d, d_pad, true);
+    int rc = check_bwd(dy, x, m, n, d, d_pad, ncand, qtypes, qbytes, w_eff, dx);
     if (rc != VQ_OK) return rc;
-    if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
-    if (!dy || !x) return fail(VQ_ERR_NULL, "dy/x is NULL");
-    if (!aligned16(dy) || !aligned16(x)) return fail(VQ_ERR_ALIGN, "dy/x not 16-byte aligned");
-    if (dx && !aligned16(dx)) return fail(VQ_ERR_ALIGN, "dx not 16-byte aligned");
-    if (w_eff && !aligned16(w_eff)) return fail(VQ_ERR_ALIGN, "w_eff not 16-byte aligned");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const vq::CandSet cs = make_set(ncand, qtypes, qbytes, d_pad);
     const bool remix = dx != nullptr && w_eff == nullptr;
     const int64_t need = vq_gated_linear_bwd_workspace(m, n, d, d_pad, ncand, remix ? 1 : 0);
-    const int64_t nparts = vq::gate_partial_count((int)m, (int)n, (int)d);
-    const int64_t part_bytes = align256(nparts * ncand * (int64_t)sizeof(float));
+    const int64_t part_bytes = align256(vq::gate_partial_count((int)m, (int)n, (int)d) * ncand * (int64_t)sizeof(float));
     if ((dprobs || remix) && (!workspace || ws_bytes < need))
         return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
                     (long long)(workspace ? ws_bytes : 0));
@@ -533,43 +621,37 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
     float* tail_ws = nullptr;
     if (workspace && tail_bytes > 0 && ws_bytes >= part_bytes + tail_bytes)
         tail_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
-    if (dx) {
-        const uint16_t* w = w_eff;
-        if (remix) {
-            if (!probs) return fail(VQ_ERR_NULL, "probs is NULL");
-            uint16_t* wbuf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes + tail_bytes);
-            rc = hip_check(vq::launch_mix(cs, probs, wbuf, n * d_pad / 256, s), "mix launch");
-            if (rc != VQ_OK) return rc;
-            w = wbuf;
-        }
-        if (m > 0 && dprobs) {
-            // both products in one launch: each fills the other's last round
-            rc = hip_check(vq::launch_gemm_dx_gate(dy, w, d_pad, dx, x, group_of(cs, n), partials, (int)m, (int)n,
-                                                   (int)d, tail_ws, s),
-                           "dX + gate GEMM launch");
-            if (rc != VQ_OK) return rc;
-        } else if (m > 0) {
-            rc = hip_check(vq::launch_gemm_dx(dy, w, d_pad, dx, (int)m, (int)n, (int)d, tail_ws, s),
-                           "dX GEMM launch");
-            if (rc != VQ_OK) return rc;
-        }
+    uint16_t* remix_buf = nullptr;
+    if (remix) {
+        if (!probs) return fail(VQ_ERR_NULL, "probs is NULL");
+        remix_buf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes + tail_bytes);
     }
-    if (dprobs) {
-        if (m == 0) {
-            // no tokens: dL/dp = 0 (written by the reduce over zero partials)
-            rc = hip_check(vq::launch_gate_reduce(partials, 0, ncand, dprobs, s), "gate reduce launch");
-            return rc == VQ_OK ? ok() : rc;
-        }
-        if (!dx) {
-            rc = hip_check(vq::launch_gemm_gate(dy, x, group_of(cs, n), partials, (int)m, (int)n, (int)d, s),
-                           "gate GEMM launch");
-            if (rc != VQ_OK) return rc;
-        }
-        rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, s),
-                       "gate reduce launch");
-        if (rc != VQ_OK) return rc;
-    }
-    return ok();
+    return run_bwd(dy, x, m, n, d, d_pad, make_set(ncand, qtypes, qbytes, d_pad), probs, w_eff, remix_buf, dx, dprobs,
+                   partials, tail_ws, static_cast<hipStream_t>(stream));
+}
+
+int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
+                               int ncand, const int* qtypes, const void* const* qbytes, const uint16_t* w_eff,
+                               uint16_t* dx, float* dprobs, void* stream) {
+    int rc = check_bwd(dy, x, m, n, d, d_pad, ncand, qtypes, qbytes, w_eff, dx);
+    if (rc != VQ_OK) return rc;
+    if (dx && !w_eff) return fail(VQ_ERR_NULL, "dx needs the forward's w_eff (this entry point does not re-mix)");
+    const int64_t part_bytes = align256(vq::gate_partial_count((int)m, (int)n, (int)d) * ncand * (int64_t)sizeof(float));
+    if (dprobs && part_bytes > kStaticScratchBytes)
+        return fail(VQ_ERR_WORKSPACE, "m=%lld n=%lld d=%lld ncand=%d needs %lld bytes of gate partials; the static "
+                    "scratch holds %lld (use vq_gated_linear_bwd with a workspace)", (long long)m, (long long)n,
+                    (long long)d, ncand, (long long)part_bytes, (long long)kStaticScratchBytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* scratch_ptr = nullptr;
+    rc = static_scratch(s, &scratch_ptr);
+    if (rc != VQ_OK) return rc;
+    // dX splits its tail tiles along K only when their partials fit behind the gate partials
+    const int64_t tail_bytes = align256(vq::dx_tail_bytes((int)m, (int)n, (int)d));
+    float* tail_ws = nullptr;
+    if (tail_bytes > 0 && part_bytes + tail_bytes <= kStaticScratchBytes)
+        tail_ws = reinterpret_cast<float*>(scratch_ptr + part_bytes);
+    return run_bwd(dy, x, m, n, d, d_pad, make_set(ncand, qtypes, qbytes, d_pad), nullptr, w_eff, nullptr, dx, dprobs,
+                   reinterpret_cast<float*>(scratch_ptr), tail_ws, s);
 }
 
 int vq_gated_linear_group_fwd(const uint16_t* x, int64_t m, int64_t d, int64_t d_pad, int nmembers, const int64_t* n,

@@ -50,6 +50,7 @@ _SIGNATURES = [
     ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
     ("vq_gated_linear_bwd", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    ("vq_gated_linear_bwd_static", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p]),
 ]
 EXPORTED = [s[0] for s in _SIGNATURES]
 
@@ -418,3 +419,20 @@ def gated_linear_bwd(dy: torch.Tensor, x: torch.Tensor, ggml_types, qbytes, prob
                                      _dev_ptr(dprobs, "dprobs"), _dev_ptr(workspace, "workspace"), ws_bytes,
                                      _stream(dy.device)),
            "vq_gated_linear_bwd")
+
+
+STATIC_SCRATCH_BYTES = 4 << 20  # VQ_STATIC_SCRATCH_BYTES of include/voodoo_hip.h
+
+
+def gated_linear_bwd_static(dy: torch.Tensor, x: torch.Tensor, ggml_types, qbytes, n: int, d_pad: int,
+                            w_eff: torch.Tensor | None, dx: torch.Tensor | None,
+                            dprobs: torch.Tensor | None) -> None:
+    """The backward without a workspace: the library's static per-device
+    scratch holds the gate partials (no allocation; overlapping calls on one
+    device race)."""
+    m, d = x.shape
+    _check(lib().vq_gated_linear_bwd_static(_dev_ptr(dy, "dy"), _dev_ptr(x, "x"), m, n, d, d_pad, len(ggml_types),
+                                            _int_array(ggml_types), _ptr_array(qbytes, "qbytes"),
+                                            _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"), _dev_ptr(dprobs, "dprobs"),
+                                            _stream(dy.device)),
+           "vq_gated_linear_bwd_static")
