@@ -31,6 +31,9 @@ LR = 0.05
 TARGET_FRAC = 0.55  # of one byte per weight
 TOL = 0.02
 LAMBDA = 4.0
+# largest gate difference accepted (gate logits are O(1)); measured on MI355X:
+# 1.3e-6 after 40 steps, 2.7e-5 after 200
+GATE_TOL = 1e-3
 
 
 def _problem():
@@ -107,11 +110,15 @@ def test_gate_argmax_matches_reference_after_short_run(steps, t0, t1):
     mods, cands, xs, targets, target_bytes = _problem()
     ref = _reference_run(cands, xs, targets, target_bytes, steps=steps, t0=t0, t1=t1)
     got = _hip_run(mods, xs, targets, target_bytes, steps=steps, t0=t0, t1=t1)
+    worst = 0.0
     for (name, types, *_), r, g in zip(SPECS, ref, got):
+        d = float((r - g).abs().max())
+        worst = max(worst, d)
         print(f"{name}: reference {types[int(r.argmax())]} {r.numpy().round(3)}  hip {types[int(g.argmax())]} "
-              f"{g.numpy().round(3)}")
+              f"{g.numpy().round(3)}  max|diff| {d:.2e}", flush=True)
         assert int(r.argmax()) == int(g.argmax()), name
-        assert float((r - g).abs().max()) < 0.1, (name, r, g)
+    print(f"[training] {steps} steps: gates agree to {worst:.2e}", flush=True)
+    assert worst < GATE_TOL
     # the run is not degenerate: the budget forces different winners, and the
     # GEMM gradients shape the result (a size-only run ends elsewhere)
     winners = {SPECS[i][1][int(r.argmax())] for i, r in enumerate(ref)}
