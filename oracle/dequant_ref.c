@@ -159,6 +159,33 @@ void oracle_dequant_q6_K(const uint8_t *x, float *y, int64_t k) {
     }
 }
 
+/*
+ * The Q3_K and Q2_K routines below follow llama.cpp's dequantize_row_q3_K and
+ * dequantize_row_q2_K (ggml/src/ggml-quants.c) step for step, so that the
+ * oracle reproduces ggml's arithmetic; that code is under the MIT License:
+ *
+ *   Copyright (c) 2023-2024 The ggml authors
+ *
+ *   Permission is hereby granted, free of charge, to any person obtaining a
+ *   copy of this software and associated documentation files (the
+ *   "Software"), to deal in the Software without restriction, including
+ *   without limitation the rights to use, copy, modify, merge, publish,
+ *   distribute, sublicense, and/or sell copies of the Software, and to permit
+ *   persons to whom the Software is furnished to do so, subject to the
+ *   following conditions:
+ *
+ *   The above copyright notice and this permission notice shall be included
+ *   in all copies or substantial portions of the Software.
+ *
+ *   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS
+ *   OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF
+ *   MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN
+ *   NO EVENT SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM,
+ *   DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR
+ *   OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE
+ *   USE OR OTHER DEALINGS IN THE SOFTWARE.
+ */
+
 /* Q3_K: 110-byte blocks {hmask[32]; qs[64]; scales[12]; fp16 d} */
 void oracle_dequant_q3_K(const uint8_t *x, float *y, int64_t k) {
     const int64_t nb = k / 256;

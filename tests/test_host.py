@@ -367,12 +367,29 @@ def test_wrap_q8_teacher():
     assert torch.equal(up.qweight, sd["layers.0.up.weight"])
     assert up.out_features == 32 and up.in_features == 64
     assert torch.equal(up.bias.detach(), sd["layers.0.up.bias"])  # carried over the constructor's copy
-    assert torch.equal(up._voodoo_qb_src[0], sd["layers.0.up.weight"])
     # non-Q8 tensors are carried over under the model's names
     assert torch.equal(model.model.layers[1].norm.weight, torch.full((64,), 3.0))
     assert model.model.embed_tokens.num_embeddings == 40
     with pytest.raises(RuntimeError, match="ROCm"):
         model.lm_head(torch.randn(2, 64))
+
+
+def test_wrap_q8_teacher_metadata_naming_and_strays():
+    """quant_meta may name the module instead of its weight, and with the
+    `model.` prefix; bytes without metadata stay put; checkpoint tensors the
+    model lacks are reported, not loaded."""
+    from voodoo_quant.training.q8_teacher import Q8Embedding, Q8Linear, wrap_q8_teacher
+
+    model, sd, meta = _q8_teacher_checkpoint()
+    meta = {("model." + k[: -len(".weight")]) if k.startswith("layers") else k: v for k, v in meta.items()}
+    del meta["model.layers.1.up"]
+    sd["layers.9.extra.weight"] = torch.zeros(3)
+    with pytest.warns(UserWarning) as rec:
+        wrap_q8_teacher(model, sd, meta)
+    msgs = " ".join(str(w.message) for w in rec)
+    assert "layers.1.up" in msgs and "layers.9.extra.weight" in msgs
+    assert isinstance(model.model.layers[0].up, Q8Linear) and isinstance(model.model.embed_tokens, Q8Embedding)
+    assert isinstance(model.model.layers[1].up, torch.nn.Linear)
 
 
 def test_q8_padding_repacks_rows():

@@ -239,93 +239,91 @@ def q8_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
     return [o.reshape(*lead, m.out_features).to(x.dtype) for m, o in zip(modules, outs)]
 
 
-def _layer_index(name: str) -> int | None:
+def _canonical(key: str) -> str:
+    """A tensor or module name as the teacher checkpoint stores it: the text
+    stack's leading ``model.`` removed (``lm_head`` and other top-level names
+    are unchanged)."""
+    return key[len("model."):] if key.startswith("model.") else key
+
+
+def _layer_of(name: str) -> int | None:
+    """N of the first ``layers.N`` in a dotted name (None outside the layers)."""
     parts = name.split(".")
-    if len(parts) >= 2 and parts[-2] == "layers":
-        try:
-            return int(parts[-1])
-        except ValueError:
-            return None
+    for a, b in zip(parts, parts[1:]):
+        if a == "layers" and b.isdigit():
+            return int(b)
     return None
 
 
 def wrap_q8_teacher(model: nn.Module, teacher_state_dict: dict, quant_meta: dict,
                     layer_devices: dict[int, torch.device] | None = None) -> nn.Module:
-    """Replace the model's Linears/Embeddings whose ``<name>.weight`` is a 2-D
-    uint8 (Q8_0) tensor of the checkpoint with :class:`Q8Linear` /
-    :class:`Q8Embedding`, and load every other checkpoint tensor as-is
-    (reference ``q8_teacher.py:176-294``).
+    """Turn a freshly built model into the Q8_0 teacher, in place
+    (the interface of the reference's ``q8_teacher.py:176-294``).
 
-    Lookups try the module's own name and the name without a leading
-    ``model.`` (the checkpoint stores the stripped names); shapes come from
-    ``quant_meta[...]["out_features"/"in_features"]``.  ``layer_devices``
-    ({layer index: device}) places each decoder layer's modules and tensors on
-    its device."""
+    The checkpoint contract: a Linear's or Embedding's weight stored as Q8_0
+    is a 2-D ``uint8`` tensor under ``<module>.weight``, named the checkpoint
+    way (:func:`_canonical`), with its ``out_features``/``in_features`` in
+    ``quant_meta`` under the weight's or the module's name (either naming).
+    Such a module becomes a :class:`Q8Linear` / :class:`Q8Embedding` over
+    those bytes.  Every other checkpoint tensor (norms, biases, ...) is
+    assigned to the model tensor with the same checkpoint name.  With
+    ``layer_devices`` ({N: device}) everything under ``layers.N`` -- wrapped
+    modules and carried tensors -- lives on that device.  A Q8_0 tensor with
+    no metadata is left in place, with a warning."""
+    import logging
+    import warnings
+
+    ckpt = {_canonical(k): v for k, v in teacher_state_dict.items()}
+    shapes = {}
+    for k, v in quant_meta.items():
+        c = _canonical(k)
+        shapes[c[: -len(".weight")] if c.endswith(".weight") else c] = v
+
+    def device_of(name: str):
+        n = _layer_of(name)
+        return layer_devices.get(n) if layer_devices and n is not None else None
+
+    # every Linear / Embedding with its parent, found before any is replaced
+    sites = [(parent, attr, f"{pname}.{attr}" if pname else attr, child)
+             for pname, parent in model.named_modules() for attr, child in parent.named_children()
+             if isinstance(child, (nn.Linear, nn.Embedding))]
+    consumed, wrapped = set(), 0
+    for parent, attr, name, child in sites:
+        key = _canonical(name)
+        qb = ckpt.get(key + ".weight")
+        if not (isinstance(qb, torch.Tensor) and qb.dtype == torch.uint8 and qb.dim() == 2):
+            continue
+        consumed.add(key + ".weight")  # Q8_0 bytes never load into a dense weight
+        shape = shapes.get(key)
+        if shape is None:
+            warnings.warn(f"Q8_0 teacher: {name} has Q8_0 bytes but no quant_meta entry; kept as is")
+            continue
+        dev = device_of(name)
+        if isinstance(child, nn.Linear):
+            bias = child.bias.detach() if child.bias is not None else None
+            q8 = Q8Linear(qb, shape["out_features"], shape["in_features"], bias, device=dev)
+        else:
+            q8 = Q8Embedding(qb, child.num_embeddings, child.embedding_dim, device=dev)
+        setattr(parent, attr, q8)
+        wrapped += 1
+
+    # the remaining checkpoint tensors, under the model's own names
+    by_canonical = {_canonical(k): k for k in model.state_dict()}
+    carry, stray = {}, []
+    for k, v in ckpt.items():
+        if k in consumed:
+            continue
+        if k in by_canonical:
+            carry[by_canonical[k]] = v
+        else:
+            stray.append(k)
+    model.load_state_dict(carry, strict=False, assign=True)
+    if stray:
+        warnings.warn(f"Q8_0 teacher: {len(stray)} checkpoint tensors match no model tensor (e.g. {stray[:3]})")
     if layer_devices:
-        for name, module in model.named_modules():
-            idx = _layer_index(name)
-            dev = layer_devices.get(idx) if idx is not None else None
-            if dev is not None and name.count(".") <= 2:
-                module._q8_target_device = dev
-
-    def lookup(key: str):
-        for k in (key, key.removeprefix("model.")):
-            if k in teacher_state_dict:
-                return teacher_state_dict[k]
-        return None
-
-    def meta_for(full: str, weight_key: str):
-        for k in (weight_key, weight_key.removeprefix("model."), full, full.removeprefix("model.")):
-            if k in quant_meta:
-                return quant_meta[k]
-        return None
-
-    replaced = 0
-    wrapped: set[str] = set()
-    for name, module in list(model.named_modules()):
-        for child_name, child in list(module.named_children()):
-            full = f"{name}.{child_name}" if name else child_name
-            weight_key = full + ".weight"
-            qb = lookup(weight_key)
-            if qb is None or qb.dim() != 2 or qb.dtype != torch.uint8:
-                continue
-            meta = meta_for(full, weight_key)
-            if meta is None:
-                print(f"  q8 teacher WARNING: no quant_meta for {full}; skipping", flush=True)
-                continue
-            dev = getattr(module, "_q8_target_device", None)
-            if isinstance(child, nn.Linear):
-                new = Q8Linear(qb, meta["out_features"], meta["in_features"],
-                               child.bias.detach() if child.bias is not None else None, device=dev)
-            elif isinstance(child, nn.Embedding):
-                new = Q8Embedding(qb, child.num_embeddings, child.embedding_dim, device=dev)
-            else:
-                continue
-            # the host source of the bytes and the full-tensor shard descriptor,
-            # for a trainer that drops and re-creates teacher buffers per step
-            new._voodoo_qb_src = (qb,)
-            new._voodoo_qb_shard = (qb, meta["out_features"], meta["in_features"], {})
-            setattr(module, child_name, new)
-            replaced += 1
-            wrapped.add(weight_key)
-            wrapped.add(weight_key.removeprefix("model."))
-
-    def carry_key(k: str) -> str:
-        # the teacher nests its text stack as `model.`; the checkpoint strips it
-        return k if (k.startswith("model.") or k == "lm_head.weight") else "model." + k
-
-    carry = {carry_key(k): v for k, v in teacher_state_dict.items()
-             if carry_key(k) not in wrapped and k not in wrapped}
-    missing, unexpected = model.load_state_dict(carry, strict=False, assign=True)
-    print(f"  q8 teacher: wrapped {replaced} Q8_0 tensors; carried {len(carry)} as-is "
-          f"({len(missing)} missing, {len(unexpected)} unexpected)", flush=True)
-    if unexpected:
-        print(f"  q8 teacher WARNING: {len(unexpected)} unexpected keys (e.g. {unexpected[:3]})", flush=True)
-    if layer_devices:
-        # the reference's rule, applied to the tensor's own name
         for name, t in list(model.named_parameters()) + list(model.named_buffers()):
-            idx = _layer_index(name)
-            dev = layer_devices.get(idx) if idx is not None else None
-            if dev is not None and t.device.type == "cpu":
+            dev = device_of(name)
+            if dev is not None and t.device != torch.device(dev):
                 t.data = t.data.to(dev)
+    logging.getLogger(__name__).info("Q8_0 teacher: %d modules wrapped, %d tensors carried", wrapped, len(carry))
     return model
