@@ -18,6 +18,13 @@ Also reported in the same JSON line:
                 bytes (packed read + fp32 write) / time, against 8 TB/s
   cpu_baseline  the oracle's fp32 torch restatement of the reference step on
                 the host cores, on a row sample of the same layer
+  peaks         the chip's sustained bf16 MFMA rate and HBM read / copy
+                bandwidth, measured by probe kernels (libvq_probe.so) in the
+                same run; the roofline is also stated against them
+  cpu_extra     the single-Linear configuration (512 tokens x 1024 -> 1024,
+                K = 4) on the host (median of 5) and on the GPU, and the C
+                dequant restatement per format, single- and multi-threaded
+  host          nproc, the CPU model and sockets of the box
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 """
@@ -74,6 +81,142 @@ def time_events(torch, fn, reps: int) -> float:
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / reps
+
+
+def host_info() -> dict:
+    """Core count, CPU model and sockets of the host running the bench."""
+    import platform
+    import subprocess
+
+    info = {"nproc": os.cpu_count(), "cpu_share_threads": int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or None}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Socket(s)", "Thread(s) per core", "Core(s) per socket"):
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        info["Model name"] = platform.processor()
+    return info
+
+
+def measured_peaks(torch, dev) -> dict:
+    """Sustained bf16 MFMA rate (a long register-only stream of
+    v_mfma_f32_32x32x16_bf16 on every SIMD, about 0.3 s, so the clock settles
+    where the power limit puts it) and HBM bandwidth (a 4 GiB read, a
+    2 GiB -> 2 GiB copy), timed with HIP events on the launch stream."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(ROOT / "voodoo-dyn-quant_amd" / "voodoo_quant" / "libvq_probe.so"))
+    lib.vq_probe_mfma.argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    lib.vq_probe_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    lib.vq_probe_hbm_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    blocks = lib.vq_probe_mfma_blocks()
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+
+    def mfma(iters):
+        rc = lib.vq_probe_mfma(iters, sink.data_ptr(), stream)
+        if rc:
+            raise RuntimeError(f"vq_probe_mfma: hip error {rc}")
+
+    t = time_events(torch, lambda: mfma(20000), 1)
+    iters = max(20000, int(20000 * 300.0 / max(t, 1e-3)))
+    t = time_events(torch, lambda: mfma(iters), 2)
+    flop = blocks * 4.0 * iters * 8 * 32768
+    rec = {"mfma_bf16_TFLOPs": round(flop / (t * 1e-3) / 1e12, 1), "mfma_probe_ms": round(t, 2)}
+    hb = lib.vq_probe_hbm_blocks()
+    hsink = torch.empty(hb * 256, dtype=torch.int32, device=dev)
+    nbytes = 4 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    t = time_events(torch, lambda: lib.vq_probe_hbm_read(buf.data_ptr(), nbytes, hsink.data_ptr(), stream), 5)
+    rec["hbm_read_GBps"] = round(nbytes / (t * 1e-3) / 1e9, 1)
+    half = nbytes // 2
+    t = time_events(torch, lambda: lib.vq_probe_hbm_copy(buf.data_ptr(), buf.data_ptr() + half, half, stream), 5)
+    rec["hbm_copy_GBps"] = round(2 * half / (t * 1e-3) / 1e9, 1)
+    del buf
+    torch.cuda.empty_cache()
+    log(f"measured peaks: {rec}")
+    return rec
+
+
+def _random_blocks_np(np, qt: str, nrows: int, ncols: int, rng):
+    """Random valid blocks: random payload, fp16 scales with exponent 7..14."""
+    bs, bb = BLOCK[qt]
+    qb = rng.integers(0, 256, size=(nrows * ncols // bs, bb), dtype=np.uint8)
+    for off in F16_OFFSETS[qt]:
+        qb[:, off + 1] = (qb[:, off + 1] & 0x83) | (0x1C + (rng.integers(0, 8, size=qb.shape[0], dtype=np.uint8) << 2))
+    return qb
+
+
+def cpu_extra(torch, dev) -> dict:
+    """The single-Linear configuration (1024 -> 1024, 512 tokens, K = 4:
+    Q8_0, Q6_K, Q4_K, Q3_K; T = 1) as the oracle's fp32 torch step on the host
+    (median of 5 after one warm-up) and as the HIP step on the GPU; and the C
+    dequant restatement on the host per format, one thread and all threads
+    (a 512 x 14336 row sample of the 4096 x 14336 microbench tensor)."""
+    import numpy as np
+
+    from oracle import cdequant, mixture
+    from voodoo_quant import _hip
+
+    types = ["Q8_0", "Q6_K", "Q4_K", "Q3_K"]
+    m, n, d = 512, 1024, 1024
+    rng = np.random.default_rng(1)
+    g = torch.Generator().manual_seed(1)
+    qbs = [_random_blocks_np(np, qt, n, d, rng) for qt in types]
+    cands = [torch.from_numpy(cdequant.oracle_dequant(qt, qb, n * d).reshape(n, d)) for qt, qb in zip(types, qbs)]
+    x = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    dy = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    gates = torch.randn(len(types), generator=g)
+    mixture.reference_step_fp32(x, dy, cands, gates, 1.0)
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        mixture.reference_step_fp32(x, dy, cands, gates, 1.0)
+        times.append(time.perf_counter() - t0)
+    cpu_ms = sorted(times)[2] * 1e3
+    flops = mixture.gated_linear_flops(m, n, d)
+    # the same step on the GPU (forward with W_eff, backward with dX and dL/dp)
+    ids = [GGML[t] for t in types]
+    qd = [torch.from_numpy(q.reshape(-1)).to(dev) for q in qbs]
+    xd, dyd = x.to(dev), dy.to(dev)
+    probs = torch.softmax(gates, 0).to(dev)
+    w_eff = torch.empty(n, d, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    dx = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    dp = torch.empty(len(types), dtype=torch.float32, device=dev)
+    ws = torch.empty(_hip.bwd_workspace_bytes(m, n, d, d, len(types), False), dtype=torch.uint8, device=dev)
+
+    def step():
+        _hip.gated_linear_fwd(xd, ids, qd, probs, n, d, w_eff, y)
+        _hip.gated_linear_bwd(dyd, xd, ids, qd, probs, n, d, w_eff, dx, dp, ws)
+
+    gpu_ms = time_events(torch, step, 50)
+    rec = {"config1_1024x1024_m512_k4": {
+        "cpu_ms": round(cpu_ms, 3), "cpu_TFLOPs": round(flops / (cpu_ms * 1e-3) / 1e12, 4),
+        "gpu_ms": round(gpu_ms, 4), "gpu_TFLOPs": round(flops / (gpu_ms * 1e-3) / 1e12, 2),
+        "cpu_threads": torch.get_num_threads(),
+        "sample": "oracle fp32 torch step (mix + F.linear + autograd + <dW, W_k>), median of 5"}}
+    dq = {}
+    rows, cols = 512, 14336
+    nthreads = torch.get_num_threads()
+    for qt in TYPES:
+        qb = _random_blocks_np(np, qt, rows, cols, rng)
+        nbytes = qb.size + 4 * rows * cols
+        r = {}
+        for label, fn in (("1_thread", lambda: cdequant.oracle_dequant(qt, qb, rows * cols)),
+                          (f"{nthreads}_threads",
+                           lambda: cdequant.oracle_dequant_parallel(qt, qb, rows * cols, nthreads))):
+            fn()
+            t0 = time.perf_counter()
+            fn()
+            r[label + "_GBps"] = round(nbytes / (time.perf_counter() - t0) / 1e9, 2)
+        dq[qt] = r
+    rec["dequant_c_restatement"] = dq
+    rec["dequant_sample"] = f"{rows} x {cols} rows of random valid blocks per format; bytes = packed read + fp32 write"
+    log(f"cpu extra: config 1 cpu {cpu_ms:.1f} ms, gpu {gpu_ms:.3f} ms; dequant C {dq}")
+    return rec
 
 
 def cpu_baseline(torch, m: int, n_total: int, d: int, budget_s: float = 12.0) -> dict:
@@ -213,6 +356,7 @@ def main() -> int:
     ap.add_argument("--only-train", action="store_true",
                     help="measure only the decoder gate-training step and print its record")
     ap.add_argument("--no-stack", action="store_true", help="skip the 8-block SwiGLU stress measurement")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the MFMA / HBM probe kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -349,10 +493,13 @@ def main() -> int:
         log("copy calibration: 3 x 1 GiB elementwise copy kernels")
         del src, dst
 
-    cpu = None
+    peaks = None if args.no_peaks else measured_peaks(torch, dev)
+
+    cpu = extra = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
         cpu = cpu_baseline(torch, m, n, d)
+        extra = cpu_extra(torch, dev)
 
     rec = {
         "metric": METRIC,
@@ -375,7 +522,10 @@ def main() -> int:
         "roofline": {
             "kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+            "peak_measured": peaks["mfma_bf16_TFLOPs"] if peaks else None,
+            "frac_of_measured": round(achieved / peaks["mfma_bf16_TFLOPs"], 4) if peaks else None,
         },
+        "peaks": peaks,
         "kernels_ms": {k: round(v, 4) for k, v in kernels.items()},
         "hipblaslt_ms": {k: round(v, 4) for k, v in lib.items()},
         "dequant_gbps": dq,
@@ -383,6 +533,8 @@ def main() -> int:
         "train": train,
         "stress": stack,
         "cpu_baseline": cpu,
+        "cpu_extra": extra,
+        "host": host_info(),
     }
     print(json.dumps(rec), flush=True)
     return 0

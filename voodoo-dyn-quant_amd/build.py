@@ -4,7 +4,9 @@
 
 Each ``csrc/*.hip`` file is compiled to an object with hipcc in parallel, then
 linked into ``voodoo_quant/libvoodoo_hip.so`` next to the Python package that
-loads it.  Objects go to ``_build/`` (git-ignored).
+loads it.  ``csrc/probe/*.hip`` (measurement probes for bench.py, outside the
+product's C ABI) becomes ``voodoo_quant/libvq_probe.so``.  Objects go to
+``_build/`` (git-ignored).
 """
 
 from __future__ import annotations
@@ -21,6 +23,7 @@ ROOT = Path(__file__).resolve().parent
 CSRC = ROOT / "csrc"
 OUT_DIR = ROOT / "_build"
 LIB = ROOT / "voodoo_quant" / "libvoodoo_hip.so"
+PROBE_LIB = ROOT / "voodoo_quant" / "libvq_probe.so"
 ARCH = os.environ.get("VQ_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -51,20 +54,28 @@ def _run(cmd: list[str]) -> None:
         print(err, file=sys.stderr)
 
 
+def _link(hipcc: str, objs: list[Path], lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, lib)
+
+
 def build(jobs: int | None = None, verbose: bool = True) -> Path:
     t0 = time.time()
     OUT_DIR.mkdir(exist_ok=True)
     hipcc = _hipcc()
     sources = sorted(CSRC.glob("*.hip"))
+    probes = sorted((CSRC / "probe").glob("*.hip"))
     objs = [OUT_DIR / (s.stem + ".o") for s in sources]
-    with ThreadPoolExecutor(max_workers=jobs or min(8, len(sources))) as ex:
+    probe_objs = [OUT_DIR / ("probe_" + s.stem + ".o") for s in probes]
+    with ThreadPoolExecutor(max_workers=jobs or min(8, len(sources) + len(probes))) as ex:
         list(ex.map(lambda so: _run([hipcc, *HIPCC_FLAGS, "-c", str(so[0]), "-o", str(so[1])]),
-                    zip(sources, objs)))
-    tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
-    os.replace(tmp, LIB)
+                    zip(sources + probes, objs + probe_objs)))
+    _link(hipcc, objs, LIB)
+    if probe_objs:
+        _link(hipcc, probe_objs, PROBE_LIB)
     if verbose:
-        print(f"built {LIB} in {time.time() - t0:.1f}s")
+        print(f"built {LIB} (and {PROBE_LIB.name}) in {time.time() - t0:.1f}s")
     return LIB
 
 
