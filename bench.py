@@ -25,6 +25,14 @@ Also reported in the same JSON line:
                 K = 4) on the host (median of 5) and on the GPU, and the C
                 dequant restatement per format, single- and multi-threaded
   host          nproc, the CPU model and sockets of the box
+  fused         the few-token products with W_eff built in LDS (never in
+                memory) against mix + GEMM, forward + dX, at 1-64 tokens on
+                three tensor sizes: the measured crossover behind the module's
+                choice of path
+
+  python bench.py --fused-workload runs only that comparison's kernels at 16
+  tokens (three passes each), the workload the rocprof HBM-traffic summary of
+  the fused kernels is taken on.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 """
@@ -219,6 +227,67 @@ def cpu_extra(torch, dev) -> dict:
     return rec
 
 
+FUSED_SHAPES = [(1024, 3072), (4096, 4096), (5120, 17408)]  # (in_features, out_features)
+
+
+def fused_compare(torch, dev, gen, tokens=(1, 16, 32, 64), reps: int = 20, passes: int = 0) -> dict:
+    """Forward + dX of one gated Linear (K = 6) at a few tokens: the fused
+    kernels (W_eff built tile by tile in LDS) against mix + GEMM (W_eff written
+    to HBM, read by both GEMMs), in microseconds.  passes > 0 only runs each
+    path that many times at 16 tokens (the profiling workload)."""
+    from voodoo_quant import _hip
+
+    ids = [GGML[t] for t in TYPES]
+    out = {}
+    for d, n in FUSED_SHAPES:
+        qb = [synthetic_qbytes(torch, t, n, d, dev, gen) for t in TYPES]
+        probs = torch.softmax(torch.randn(len(TYPES), device=dev, generator=gen), 0)
+        w = torch.empty(n, d, dtype=torch.bfloat16, device=dev)
+        rows = {}
+        for m in ((16,) if passes else tokens):
+            x = torch.randn(m, d, device=dev, generator=gen).to(torch.bfloat16)
+            dy = torch.randn(m, n, device=dev, generator=gen).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            dx = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+            wsf = torch.empty(max(_hip.fused_workspace_bytes(m, n, d, False), 16), dtype=torch.uint8, device=dev)
+            wsd = torch.empty(max(_hip.fused_workspace_bytes(m, n, d, True), 16), dtype=torch.uint8, device=dev)
+
+            def fused():
+                _hip.gated_linear_fwd_fused(x, ids, qb, probs, n, d, y, wsf)
+                _hip.gated_linear_dx_fused(dy, ids, qb, probs, d, d, dx, wsd)
+
+            def materialised():
+                _hip.gated_linear_fwd(x, ids, qb, probs, n, d, w, y)
+                _hip.gated_linear_bwd(dy, x, ids, qb, probs, n, d, w, dx, None, None)
+
+            if passes:
+                for fn in (fused, materialised):
+                    for _ in range(passes):
+                        fn()
+                    torch.cuda.synchronize()
+                continue
+            rows[m] = {"fused_us": round(time_events(torch, fused, reps) * 1e3, 1),
+                       "materialised_us": round(time_events(torch, materialised, reps) * 1e3, 1)}
+        out[f"{n}x{d}"] = rows
+        del qb, w
+        torch.cuda.empty_cache()
+    if not passes:
+        log(f"fused vs materialised (fwd + dX, us): {out}")
+    return out
+
+
+def copy_calibration(torch, dev) -> None:
+    """Three elementwise copies of 1 GiB (known bytes: 1 GiB read, 1 GiB
+    written each), to scale rocprof's FETCH_SIZE / WRITE_SIZE."""
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    log("copy calibration: 3 x 1 GiB elementwise copy kernels")
+    del src, dst
+
+
 def cpu_baseline(torch, m: int, n_total: int, d: int, budget_s: float = 12.0) -> dict:
     """The reference step on the host: oracle fp32 torch restatement of
     _MixedWeightFunction + F.linear + autograd backward (voodoo_quant/
@@ -357,6 +426,8 @@ def main() -> int:
                     help="measure only the decoder gate-training step and print its record")
     ap.add_argument("--no-stack", action="store_true", help="skip the 8-block SwiGLU stress measurement")
     ap.add_argument("--no-peaks", action="store_true", help="skip the MFMA / HBM probe kernels")
+    ap.add_argument("--fused-workload", action="store_true",
+                    help="only run the fused and materialising few-token products (16 tokens, 3 passes each)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -371,6 +442,11 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.fused_workload:
+        fused_compare(torch, dev, torch.Generator(device=dev).manual_seed(0), passes=3)
+        if args.copy_calibration:
+            copy_calibration(torch, dev)
+        return 0
     if args.only_train:
         print(json.dumps({"train": train_step_bench(torch, dev, args.train_steps, 2)}), flush=True)
         return 0
@@ -485,15 +561,10 @@ def main() -> int:
         stack = stack_step_bench(torch, dev, 3, 2)
 
     if args.copy_calibration:
-        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.mul(src, 1.0, out=dst)  # an elementwise kernel: reads 1 GiB, writes 1 GiB
-        torch.cuda.synchronize()
-        log("copy calibration: 3 x 1 GiB elementwise copy kernels")
-        del src, dst
+        copy_calibration(torch, dev)
 
     peaks = None if args.no_peaks else measured_peaks(torch, dev)
+    fused = fused_compare(torch, dev, gen)
 
     cpu = extra = None
     if not args.no_cpu_baseline:
@@ -526,6 +597,7 @@ def main() -> int:
             "frac_of_measured": round(achieved / peaks["mfma_bf16_TFLOPs"], 4) if peaks else None,
         },
         "peaks": peaks,
+        "fused": fused,
         "kernels_ms": {k: round(v, 4) for k, v in kernels.items()},
         "hipblaslt_ms": {k: round(v, 4) for k, v in lib.items()},
         "dequant_gbps": dq,

@@ -94,6 +94,32 @@ int vq_gated_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int6
                         const int *qtypes, const void *const *qbytes, const float *probs, uint16_t *w_eff,
                         uint16_t *y, void *workspace, int64_t ws_bytes, void *stream);
 
+/* Workspace bytes of vq_gated_linear_fwd_fused (dx == 0) or
+ * vq_gated_linear_dx_fused (dx != 0): fp32 parts of the reduction, split
+ * across workgroups when the output alone gives too few (0: no split). */
+int64_t vq_gated_linear_fused_workspace(int64_t m, int64_t n, int64_t d, int dx);
+
+/* The gated Linear's products for few tokens with W_eff never in memory: each
+ * workgroup decodes the K candidates' packed bytes for its 32-row x 256-weight
+ * tiles into LDS, mixes them with probs in fp32 (fma(p_k dl, u, acc): within
+ * a bf16 ulp of vq_mix_weight's W_eff, not bit-identical) and multiplies them
+ * there.  The tiles are decoded again for every 32 tokens, so the caller
+ * picks these below a measured token count and the materialising entry
+ * points above it.
+ *   vq_gated_linear_fwd_fused: y[m][n] = x[m][d] . W_eff^T
+ *     (replaces get_mixed_weight + F.linear, voodoo_quant/layers.py:1729-1731);
+ *   vq_gated_linear_dx_fused: dx[m][d] = dy[m][n] . W_eff
+ *     (the dX half of the backward, voodoo_quant/layers.py:354-363 via
+ *     F.linear's autograd; dL/dp comes from vq_gated_linear_bwd with dx NULL,
+ *     whose gate product never needs W_eff).
+ * workspace: vq_gated_linear_fused_workspace bytes. */
+int vq_gated_linear_fwd_fused(const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                              const int *qtypes, const void *const *qbytes, const float *probs, uint16_t *y,
+                              void *workspace, int64_t ws_bytes, void *stream);
+int vq_gated_linear_dx_fused(const uint16_t *dy, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                             const int *qtypes, const void *const *qbytes, const float *probs, uint16_t *dx,
+                             void *workspace, int64_t ws_bytes, void *stream);
+
 /* Per-token quant routing (PTQR) forward: y[t] = x[t] . W_{k(t)}^T, every
  * token through ONE candidate.  perm (device int32 [m]) lists the tokens
  * grouped by candidate, group_off (device int32 [ncand + 1]) the group bounds

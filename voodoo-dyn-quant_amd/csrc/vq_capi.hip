@@ -654,6 +654,47 @@ int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m,
                    reinterpret_cast<float*>(scratch_ptr), tail_ws, s);
 }
 
+int64_t vq_gated_linear_fused_workspace(int64_t m, int64_t n, int64_t d, int dx) {
+    if (m < 0 || n <= 0 || d <= 0 || m > INT32_MAX || n > (1 << 21) || d > (1 << 21)) return -1;
+    if (m == 0) return 0;
+    return align256(vq::fused_plan(dx != 0, (int)m, (int)n, (int)d).ws_bytes);
+}
+
+namespace {
+int run_fused(bool dx, const uint16_t* act, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+              const int* qtypes, const void* const* qbytes, const float* probs, uint16_t* out, void* workspace,
+              int64_t ws_bytes, void* stream) {
+    int rc = check_candidates(ncand, qtypes, qbytes, n, d, d_pad, true);
+    if (rc != VQ_OK) return rc;
+    if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
+    if (!act || !probs || !out) return fail(VQ_ERR_NULL, "%s/probs/%s is NULL", dx ? "dy" : "x", dx ? "dx" : "y");
+    if (!aligned16(act) || !aligned16(out)) return fail(VQ_ERR_ALIGN, "activations/output not 16-byte aligned");
+    if (m == 0) return ok();
+    const int64_t need = vq::fused_plan(dx, (int)m, (int)n, (int)d).ws_bytes;
+    if (need > 0 && (!workspace || ws_bytes < need))
+        return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
+                    (long long)(workspace ? ws_bytes : 0));
+    if (workspace && !aligned16(workspace)) return fail(VQ_ERR_ALIGN, "workspace not 16-byte aligned");
+    rc = hip_check(vq::launch_fused(dx, act, make_set(ncand, qtypes, qbytes, d_pad), probs, (int)m, (int)n, (int)d,
+                                    out, need > 0 ? static_cast<float*>(workspace) : nullptr,
+                                    static_cast<hipStream_t>(stream)),
+                   dx ? "fused dX launch" : "fused forward launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+}  // namespace
+
+int vq_gated_linear_fwd_fused(const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                              const int* qtypes, const void* const* qbytes, const float* probs, uint16_t* y,
+                              void* workspace, int64_t ws_bytes, void* stream) {
+    return run_fused(false, x, m, n, d, d_pad, ncand, qtypes, qbytes, probs, y, workspace, ws_bytes, stream);
+}
+
+int vq_gated_linear_dx_fused(const uint16_t* dy, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
+                             const int* qtypes, const void* const* qbytes, const float* probs, uint16_t* dx,
+                             void* workspace, int64_t ws_bytes, void* stream) {
+    return run_fused(true, dy, m, n, d, d_pad, ncand, qtypes, qbytes, probs, dx, workspace, ws_bytes, stream);
+}
+
 int vq_gated_linear_group_fwd(const uint16_t* x, int64_t m, int64_t d, int64_t d_pad, int nmembers, const int64_t* n,
                               const int* ncand, const int* qtypes, const void* const* qbytes,
                               const float* const* probs, uint16_t* w_eff, uint16_t* y, void* workspace,

@@ -337,12 +337,15 @@ __device__ __forceinline__ float dot_sub16(const uint8_t* __restrict__ g, int p,
 // once, like ggml's; only the sign of a zero may differ, which the mixture
 // cannot see (+0 + (+-0) = +0).  A run of 16 never crosses a 16-weight scale
 // block, so each run decodes one scale.
-template <int QT, int R = 8>
-__device__ __forceinline__ void decode_mix(const uint8_t* __restrict__ g, int p, float (&y)[R]) {
+//
+// decode_affine gives the run's unsigned codes (four per word: weight
+// p + 4 i + t is byte t of uw[i]) and its affine map, weight = dl * u + c;
+// decode_mix applies it.
+template <int QT, int R>
+__device__ __forceinline__ void decode_affine(const uint8_t* __restrict__ g, int p, uint32_t (&uw)[R / 4], float& dl,
+                                              float& c) {
     static_assert(R == 8 || R == 16, "runs of 8 or 16 weights");
     constexpr int W = R / 4;
-    uint32_t uw[W];
-    float dl, c;
     if constexpr (QT == Q8_0) {
         const uint8_t* b = g + 34 * (p >> 5);
         const float d = h2f_hw(*reinterpret_cast<const uint16_t*>(b));
@@ -405,6 +408,13 @@ __device__ __forceinline__ void decode_mix(const uint8_t* __restrict__ g, int p,
 #pragma unroll
         for (int i = 0; i < W; ++i) uw[i] = (uw[i] >> (2 * j)) & 0x03030303u;
     }
+}
+
+template <int QT, int R = 8>
+__device__ __forceinline__ void decode_mix(const uint8_t* __restrict__ g, int p, float (&y)[R]) {
+    uint32_t uw[R / 4];
+    float dl, c;
+    decode_affine<QT, R>(g, p, uw, dl, c);
 #pragma unroll
     for (int r = 0; r < R; ++r) y[r] = fmaf(dl, (float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu), c);
 }

@@ -56,6 +56,19 @@ hipError_t launch_gate_reduce_group(const float* partials, int64_t ntiles, int s
 hipError_t launch_gate_reduce_strided(const float* partials, int64_t ntiles, int stride, int ncand, float* dprobs,
                                       hipStream_t s);
 
+// Fused decode + mix GEMMs for few tokens (vq_fused.hip): W_eff is built in
+// LDS tile by tile from the packed candidates and never written.
+//   forward (dx = false): out = Y[M][N] = act . W_eff^T, act = X [M][D]
+//   dx      (dx = true):  out = dX[M][D] = act . W_eff,  act = dY [M][N]
+// ws: fused_plan(...).ws_bytes of fp32 parts (NULL when 0).
+struct FusedPlan {
+    int splits, per_split, grid_x, grid_z;
+    int64_t ws_bytes;
+};
+FusedPlan fused_plan(bool dx, int M, int N, int D);
+hipError_t launch_fused(bool dx, const bf16_t* act, const CandSet& cs, const float* probs, int M, int N, int D,
+                        bf16_t* out, float* ws, hipStream_t s);
+
 // Embedding rows (vq_embed.hip): one workgroup per (requested row, segment of
 // at most kGroupsPerBlock groups); gused = groups covering dim.
 struct EmbedPlan {

@@ -51,6 +51,9 @@ _SIGNATURES = [
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
     ("vq_gated_linear_bwd", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_static", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p]),
+    ("vq_gated_linear_fused_workspace", _i64, [_i64, _i64, _i64, _i]),
+    ("vq_gated_linear_fwd_fused", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _i64, _p]),
+    ("vq_gated_linear_dx_fused", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _i64, _p]),
 ]
 EXPORTED = [s[0] for s in _SIGNATURES]
 
@@ -419,6 +422,36 @@ def gated_linear_bwd(dy: torch.Tensor, x: torch.Tensor, ggml_types, qbytes, prob
                                      _dev_ptr(dprobs, "dprobs"), _dev_ptr(workspace, "workspace"), ws_bytes,
                                      _stream(dy.device)),
            "vq_gated_linear_bwd")
+
+
+def fused_workspace_bytes(m: int, n: int, d: int, dx: bool) -> int:
+    v = int(lib().vq_gated_linear_fused_workspace(m, n, d, int(dx)))
+    if v < 0:
+        raise ValueError(f"invalid fused sizes m={m} n={n} d={d}")
+    return v
+
+
+def _fused(entry: str, act: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, n: int, d: int, d_pad: int,
+           out: torch.Tensor, workspace: torch.Tensor | None) -> None:
+    m = act.shape[0]
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(getattr(lib(), entry)(_dev_ptr(act, "activations"), m, n, d, d_pad, len(ggml_types),
+                                 _int_array(ggml_types), _ptr_array(qbytes, "qbytes"), _dev_ptr(probs, "probs"),
+                                 _dev_ptr(out, "out"), _dev_ptr(workspace, "workspace"), ws_bytes,
+                                 _stream(act.device)),
+           entry)
+
+
+def gated_linear_fwd_fused(x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, n: int, d_pad: int,
+                           y: torch.Tensor, workspace: torch.Tensor | None = None) -> None:
+    """y [m, n] = x @ W_eff^T with W_eff built in LDS (never in memory)."""
+    _fused("vq_gated_linear_fwd_fused", x, ggml_types, qbytes, probs, n, x.shape[1], d_pad, y, workspace)
+
+
+def gated_linear_dx_fused(dy: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor, d: int, d_pad: int,
+                          dx: torch.Tensor, workspace: torch.Tensor | None = None) -> None:
+    """dx [m, d] = dy @ W_eff with W_eff built in LDS (never in memory)."""
+    _fused("vq_gated_linear_dx_fused", dy, ggml_types, qbytes, probs, dy.shape[1], d, d_pad, dx, workspace)
 
 
 STATIC_SCRATCH_BYTES = 4 << 20  # VQ_STATIC_SCRATCH_BYTES of include/voodoo_hip.h

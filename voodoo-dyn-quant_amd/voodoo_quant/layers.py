@@ -161,6 +161,25 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+# The fused few-token products (vq_gated_linear_fwd_fused / _dx_fused: W_eff
+# built tile by tile in LDS, never written) replace mix + GEMM when a call
+# has at most FUSED_MAX_TOKENS tokens and the tensor at most
+# FUSED_MAX_WEIGHTS weights.  Measured on MI355X, K = 6 (Q2_K..Q8_0),
+# forward + dX at 1-32 tokens: fused against materialised 34 vs 47 us
+# (1024 x 1024), 53 vs 101 (4096 x 1024), 45 vs 57 (1024 x 4096), 105 vs 181
+# (8192 x 2048), 100 vs 121 (4096 x 4096); the 27B projections (31-89M
+# weights) are 5-10% slower fused, and at 64 tokens the two paths trade
+# places, so both limits sit at the last point where fused won everywhere.
+FUSED_MAX_TOKENS = 32
+FUSED_MAX_WEIGHTS = 1 << 24
+
+
+def use_fused(m: int, n: int, d_pad: int) -> bool:
+    """Whether a gated product of m tokens over an [n, d_pad] tensor takes the
+    fused path."""
+    return 0 < m <= FUSED_MAX_TOKENS and n * d_pad <= FUSED_MAX_WEIGHTS
+
+
 class GatedLinearFunction(Function):
     """y = x W_eff^T with W_eff = sum_k probs_k W_k, on libvoodoo_hip.
 
@@ -173,13 +192,22 @@ class GatedLinearFunction(Function):
     def forward(ctx, x, probs, meta, *qbytes):
         types, n, d_pad = meta
         x2 = _aligned(x)
+        m, d = x2.shape
         p = probs.detach().to(device=x.device, dtype=torch.float32).contiguous()
-        w_eff = torch.empty(n, d_pad, dtype=torch.bfloat16, device=x.device)
-        y = torch.empty(x2.shape[0], n, dtype=torch.bfloat16, device=x.device)
-        nbytes = _hip.fwd_workspace_bytes(x2.shape[0], n, x2.shape[1])
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
-        _hip.gated_linear_fwd(x2, types, qbytes, p, n, d_pad, w_eff, y, ws)
-        ctx.save_for_backward(x2, p, w_eff)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
+        ctx.fused = use_fused(m, n, d_pad)
+        if ctx.fused:
+            # W_eff only ever exists tile by tile in LDS
+            nbytes = _hip.fused_workspace_bytes(m, n, d, False)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+            _hip.gated_linear_fwd_fused(x2, types, qbytes, p, n, d_pad, y, ws)
+            ctx.save_for_backward(x2, p)
+        else:
+            w_eff = torch.empty(n, d_pad, dtype=torch.bfloat16, device=x.device)
+            nbytes = _hip.fwd_workspace_bytes(m, n, d)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+            _hip.gated_linear_fwd(x2, types, qbytes, p, n, d_pad, w_eff, y, ws)
+            ctx.save_for_backward(x2, p, w_eff)
         ctx.meta = meta
         ctx.qbytes = qbytes
         ctx.probs_device = probs.device
@@ -187,10 +215,26 @@ class GatedLinearFunction(Function):
 
     @staticmethod
     def backward(ctx, dy):
-        x2, p, w_eff = ctx.saved_tensors
         types, n, d_pad = ctx.meta
         need_dx, need_dp = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dy2 = _aligned(dy.to(torch.bfloat16))
+        if ctx.fused:
+            x2, p = ctx.saved_tensors
+            m, d = x2.shape
+            dx = dprobs = None
+            if need_dx:  # dX through the fused kernel: W_eff never materialised
+                dx = torch.empty_like(x2)
+                nbytes = _hip.fused_workspace_bytes(m, n, d, True)
+                ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device) if nbytes > 0 else None
+                _hip.gated_linear_dx_fused(dy2, types, ctx.qbytes, p, d, d_pad, dx, ws)
+            if need_dp:  # the gate product reads the packed candidates, never W_eff
+                dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device)
+                nbytes = _hip.bwd_workspace_bytes(m, n, d, d_pad, len(types), False)
+                ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
+                _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, None, None, dprobs, ws)
+                dprobs = dprobs.to(ctx.probs_device)
+            return (dx, dprobs, None) + (None,) * len(ctx.qbytes)
+        x2, p, w_eff = ctx.saved_tensors
         dx = torch.empty_like(x2) if need_dx else None
         dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device) if need_dp else None
         ws = None
