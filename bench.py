@@ -332,7 +332,7 @@ def cpu_baseline(torch, m: int, n_total: int, d: int, budget_s: float = 12.0) ->
     }
 
 
-def train_step_bench(torch, dev, steps: int, warmup: int) -> dict:
+def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False) -> dict:
     """Gate-training steps of the 0.8B-class decoder (24 layers, hidden 1024,
     16x64 query heads, 4 KV heads, SwiGLU 3072, vocabulary 151936 tied; every
     Linear and the embedding gated over 6 candidates; Q8_0 teacher), batch
@@ -349,7 +349,8 @@ def train_step_bench(torch, dev, steps: int, warmup: int) -> dict:
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randint(0, cfg.vocab, (b, s), device=dev, generator=g)
     y = torch.randint(0, cfg.vocab, (b, s), device=dev, generator=g)
-    tr = st.GateTrainer(student, teacher, replaced, st.StepConfig(max_steps=max(steps + warmup, 2)),
+    tr = st.GateTrainer(student, teacher, replaced,
+                        st.StepConfig(max_steps=max(steps + warmup, 2), prefetch_mix=prefetch),
                         total_8bit_bytes=float(cfg.gated_weights()))
     for _ in range(warmup):
         tr.step(x, y)
@@ -374,7 +375,7 @@ def train_step_bench(torch, dev, steps: int, warmup: int) -> dict:
     return rec
 
 
-def stack_step_bench(torch, dev, steps: int, warmup: int) -> dict:
+def stack_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False) -> dict:
     """The long-context, wide-menu stress configuration: 8 SwiGLU blocks at
     hidden 4096, MLP 14336 (MLP-only blocks), K = 8 candidates per tensor
     (the six formats, Q4_K and Q6_K twice with their own bytes), 2 x 8192
@@ -390,7 +391,7 @@ def stack_step_bench(torch, dev, steps: int, warmup: int) -> dict:
     g = torch.Generator(device=dev).manual_seed(6)
     x = torch.randn(tokens, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
     tr = st.StackTrainer(student, teacher, replaced,
-                         st.StepConfig(max_steps=200, temp_start=2.0, temp_end=0.1),
+                         st.StepConfig(max_steps=200, temp_start=2.0, temp_end=0.1, prefetch_mix=prefetch),
                          total_8bit_bytes=float(cfg.gated_weights()))
     for _ in range(warmup):
         tr.step(x)
@@ -425,6 +426,10 @@ def main() -> int:
     ap.add_argument("--only-train", action="store_true",
                     help="measure only the decoder gate-training step and print its record")
     ap.add_argument("--no-stack", action="store_true", help="skip the 8-block SwiGLU stress measurement")
+    ap.add_argument("--only-stack", action="store_true",
+                    help="measure only the 8-block SwiGLU stress step and print its record")
+    ap.add_argument("--prefetch-mix", action="store_true",
+                    help="train/stress steps mix each W_eff ahead on a second stream (layers.MixPrefetch)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the MFMA / HBM probe kernels")
     ap.add_argument("--fused-workload", action="store_true",
                     help="only run the fused and materialising few-token products (16 tokens, 3 passes each)")
@@ -448,7 +453,10 @@ def main() -> int:
             copy_calibration(torch, dev)
         return 0
     if args.only_train:
-        print(json.dumps({"train": train_step_bench(torch, dev, args.train_steps, 2)}), flush=True)
+        print(json.dumps({"train": train_step_bench(torch, dev, args.train_steps, 2, args.prefetch_mix)}), flush=True)
+        return 0
+    if args.only_stack:
+        print(json.dumps({"stress": stack_step_bench(torch, dev, 3, 2, args.prefetch_mix)}), flush=True)
         return 0
     m, n, d = 8192, 17408, 5120
     d_pad = d
@@ -555,10 +563,10 @@ def main() -> int:
     if not args.no_train:
         del qbytes, w_eff, y, dx, ws, fws, out
         torch.cuda.empty_cache()
-        train = train_step_bench(torch, dev, args.train_steps, 2)
+        train = train_step_bench(torch, dev, args.train_steps, 2, args.prefetch_mix)
     stack = None
     if not args.no_stack:
-        stack = stack_step_bench(torch, dev, 3, 2)
+        stack = stack_step_bench(torch, dev, 3, 2, args.prefetch_mix)
 
     if args.copy_calibration:
         copy_calibration(torch, dev)

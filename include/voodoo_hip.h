@@ -87,7 +87,8 @@ int vq_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, const uint
 /* Forward of the gated Linear: mixes W_eff into `w_eff` ([n][d_pad] bf16,
  * caller-owned, kept for the backward) and writes y[m][n] = x[m][d] . W_eff^T.
  * `workspace` (optional, ws_bytes >= vq_gated_linear_fwd_workspace) lets the
- * GEMM split its last round of tiles along K; NULL runs them whole.
+ * GEMM split its last round of tiles along K; NULL runs them whole.  With
+ * m == 0 it only mixes (x and y may then be NULL).
  * Replaces get_mixed_weight + F.linear in MixedQuantLinear.forward
  * (voodoo_quant/layers.py:1729-1731). */
 int vq_gated_linear_fwd(const uint16_t *x, int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand,
@@ -171,7 +172,8 @@ int vq_embedding_rows_bwd(int ncand, const int *qtypes, const void *const *qbyte
  * qtypes/qbytes, and probs[i] (device fp32 [ncand[i]]).  Mixes every member
  * into its rows of w_eff ([sum n][d_pad] bf16) and runs ONE GEMM:
  * y[m][sum n] = x . w_eff^T (member i's outputs are columns
- * [n[0] + ... + n[i-1], ... + n[i]) of y).  1 <= nmembers <= 4.  Replaces the
+ * [n[0] + ... + n[i-1], ... + n[i]) of y).  1 <= nmembers <= 4; with m == 0
+ * only the mixes run (x and y may be NULL).  Replaces the
  * separate forwards of MixedQuantLinear (voodoo_quant/layers.py:1729-1731)
  * for projections of one input; no counterpart entry in the reference. */
 int vq_gated_linear_group_fwd(const uint16_t *x, int64_t m, int64_t d, int64_t d_pad, int nmembers, const int64_t *n,

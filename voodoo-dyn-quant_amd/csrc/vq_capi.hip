@@ -577,7 +577,8 @@ int vq_gated_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int6
     int rc = check_candidates(ncand, qtypes, qbytes, n, d, d_pad, true);
     if (rc != VQ_OK) return rc;
     if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
-    if (!x || !probs || !w_eff || !y) return fail(VQ_ERR_NULL, "x/probs/w_eff/y is NULL");
+    if (!probs || !w_eff) return fail(VQ_ERR_NULL, "probs/w_eff is NULL");
+    if (m > 0 && (!x || !y)) return fail(VQ_ERR_NULL, "x/y is NULL");  // m == 0: the mix alone
     if (!aligned16(x) || !aligned16(w_eff) || !aligned16(y))
         return fail(VQ_ERR_ALIGN, "x/w_eff/y not 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -704,7 +705,8 @@ int vq_gated_linear_group_fwd(const uint16_t* x, int64_t m, int64_t d, int64_t d
     int rc = check_group(nmembers, n, ncand, qtypes, qbytes, d, d_pad, cg, n_total);
     if (rc != VQ_OK) return rc;
     if (m < 0 || m > INT32_MAX) return fail(VQ_ERR_SHAPE, "m=%lld out of range", (long long)m);
-    if (!x || !probs || !w_eff || !y) return fail(VQ_ERR_NULL, "x/probs/w_eff/y is NULL");
+    if (!probs || !w_eff) return fail(VQ_ERR_NULL, "probs/w_eff is NULL");
+    if (m > 0 && (!x || !y)) return fail(VQ_ERR_NULL, "x/y is NULL");  // m == 0: the mixes alone
     if (!aligned16(x) || !aligned16(w_eff) || !aligned16(y))
         return fail(VQ_ERR_ALIGN, "x/w_eff/y not 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);

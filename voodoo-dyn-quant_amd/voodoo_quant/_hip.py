@@ -293,6 +293,31 @@ def gated_linear_group_bwd(dy: torch.Tensor, x: torch.Tensor, members, d_pad: in
            "vq_gated_linear_group_bwd")
 
 
+def mix_only_call(members, probs, d_pad: int, w_eff: torch.Tensor, stream: int):
+    """A zero-argument callable that mixes `members` ([(ggml_types, qbytes, n)],
+    stacked in order) with `probs` (one fp32 [K_i] tensor per member) into
+    w_eff [sum n, d_pad] on `stream`: the tensors' addresses are marshalled
+    once, so every call is one C call.  The tensors must outlive the callable
+    and keep their storage."""
+    if len(members) == 1:
+        types, qbytes, n = members[0]
+        args = (None, 0, n, d_pad, d_pad, len(types), _int_array(types), _ptr_array(qbytes, "qbytes"),
+                _dev_ptr(probs[0], "probs"), _dev_ptr(w_eff, "w_eff"), None, None, 0, stream)
+        fn, what = lib().vq_gated_linear_fwd, "vq_gated_linear_fwd"
+    else:
+        ns, nc, types, qbs = _group_arrays(members)
+        pp = (ctypes.c_void_p * len(members))(*[_dev_ptr(p, f"probs[{i}]") for i, p in enumerate(probs)])
+        args = (None, 0, d_pad, d_pad, len(members), ns, nc, types, qbs, pp, _dev_ptr(w_eff, "w_eff"), None, None, 0,
+                stream)
+        fn, what = lib().vq_gated_linear_group_fwd, "vq_gated_linear_group_fwd"
+
+    def call() -> None:
+        _check(fn(*args), what)
+
+    call.keepalive = (args,)
+    return call
+
+
 def rope_qkv_fwd(qkv: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, D: int, cos: torch.Tensor, sin: torch.Tensor):
     """(q, k, v), each bf16 [B*S, Hq, D], from the stacked projection output."""
     dev = qkv.device

@@ -183,20 +183,28 @@ def use_fused(m: int, n: int, d_pad: int) -> bool:
 class GatedLinearFunction(Function):
     """y = x W_eff^T with W_eff = sum_k probs_k W_k, on libvoodoo_hip.
 
-    forward(ctx, x [M, D] bf16, probs [K] fp32, meta, *qbytes) -> y [M, N] bf16
-    where meta = (ggml type ids, N, D_pad).  The backward returns dX and
-    dL/dprobs; qbytes receive no gradient (they are constants, as the
-    candidates are for the reference's ``_MixedWeightFunction``)."""
+    forward(ctx, x [M, D] bf16, probs [K] fp32, meta, premixed, *qbytes) -> y [M, N] bf16
+    where meta = (ggml type ids, N, D_pad) and premixed is None or this
+    step's W_eff [N, D_pad] already mixed from probs (see
+    :class:`MixPrefetch`).  The backward returns dX and dL/dprobs; qbytes
+    receive no gradient (they are constants, as the candidates are for the
+    reference's ``_MixedWeightFunction``)."""
 
     @staticmethod
-    def forward(ctx, x, probs, meta, *qbytes):
+    def forward(ctx, x, probs, meta, premixed, *qbytes):
         types, n, d_pad = meta
         x2 = _aligned(x)
         m, d = x2.shape
         p = probs.detach().to(device=x.device, dtype=torch.float32).contiguous()
         y = torch.empty(m, n, dtype=torch.bfloat16, device=x.device)
-        ctx.fused = use_fused(m, n, d_pad)
-        if ctx.fused:
+        ctx.fused = premixed is None and use_fused(m, n, d_pad)
+        if premixed is not None:  # W_eff mixed ahead on the prefetch stream: the GEMM only
+            nbytes = _hip.fwd_workspace_bytes(m, n, d)
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
+            if m > 0:
+                _hip.linear_fwd(x2, premixed, n, y, ws)
+            ctx.save_for_backward(x2, p, premixed)
+        elif ctx.fused:
             # W_eff only ever exists tile by tile in LDS
             nbytes = _hip.fused_workspace_bytes(m, n, d, False)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes > 0 else None
@@ -233,7 +241,7 @@ class GatedLinearFunction(Function):
                 ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
                 _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, None, None, dprobs, ws)
                 dprobs = dprobs.to(ctx.probs_device)
-            return (dx, dprobs, None) + (None,) * len(ctx.qbytes)
+            return (dx, dprobs, None, None) + (None,) * len(ctx.qbytes)
         x2, p, w_eff = ctx.saved_tensors
         dx = torch.empty_like(x2) if need_dx else None
         dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device) if need_dp else None
@@ -245,7 +253,7 @@ class GatedLinearFunction(Function):
             _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, w_eff, dx, dprobs, ws)
         if dprobs is not None:
             dprobs = dprobs.to(ctx.probs_device)
-        return (dx, dprobs, None) + (None,) * len(ctx.qbytes)
+        return (dx, dprobs, None, None) + (None,) * len(ctx.qbytes)
 
 
 class GatedLinearGroupFunction(Function):
@@ -255,12 +263,13 @@ class GatedLinearGroupFunction(Function):
     backward is one launch for dX (which also sums the members' input
     gradients) and every member's gate gradients.
 
-    forward(ctx, x [M, D] bf16, meta, *probs_then_qbytes) -> y [M, sum N] bf16
-    with meta = (((ggml types, N) per member), D_pad), then each member's probs
-    [K_i] and finally every member's qbytes in order."""
+    forward(ctx, x [M, D] bf16, meta, premixed, *probs_then_qbytes) -> y [M, sum N] bf16
+    with meta = (((ggml types, N) per member), D_pad), premixed None or the
+    step's stacked W_eff [sum N, D_pad] mixed ahead (see :class:`MixPrefetch`),
+    then each member's probs [K_i] and finally every member's qbytes in order."""
 
     @staticmethod
-    def forward(ctx, x, meta, *tensors):
+    def forward(ctx, x, meta, premixed, *tensors):
         members, d_pad = meta
         nm = len(members)
         probs, qbytes = tensors[:nm], tensors[nm:]
@@ -272,11 +281,16 @@ class GatedLinearGroupFunction(Function):
             spec.append((types, qbytes[off:off + len(types)], n))
             off += len(types)
         n_total = sum(n for _, n in members)
-        w_eff = torch.empty(n_total, d_pad, dtype=torch.bfloat16, device=dev)
         y = torch.empty(x2.shape[0], n_total, dtype=torch.bfloat16, device=dev)
         nbytes = _hip.fwd_workspace_bytes(x2.shape[0], n_total, x2.shape[1])
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
-        _hip.gated_linear_group_fwd(x2, spec, ps, d_pad, w_eff, y, ws)
+        if premixed is not None:  # mixed ahead on the prefetch stream: the GEMM only
+            w_eff = premixed
+            if x2.shape[0] > 0:
+                _hip.linear_fwd(x2, w_eff, n_total, y, ws)
+        else:
+            w_eff = torch.empty(n_total, d_pad, dtype=torch.bfloat16, device=dev)
+            _hip.gated_linear_group_fwd(x2, spec, ps, d_pad, w_eff, y, ws)
         ctx.save_for_backward(x2, w_eff)
         ctx.spec = spec
         ctx.meta = meta
@@ -289,7 +303,7 @@ class GatedLinearGroupFunction(Function):
         members, d_pad = ctx.meta
         nm = len(members)
         need_dx = ctx.needs_input_grad[0]
-        need_dp = any(ctx.needs_input_grad[2:2 + nm])
+        need_dp = any(ctx.needs_input_grad[3:3 + nm])
         dx = torch.empty_like(x2) if need_dx else None
         dprobs = None
         if need_dp:
@@ -301,7 +315,123 @@ class GatedLinearGroupFunction(Function):
             _hip.gated_linear_group_bwd(dy2, x2, ctx.spec, d_pad, w_eff if need_dx else None, dx, dprobs, ws)
         grads_p = [None] * nm if dprobs is None else [g.to(d) for g, d in zip(dprobs, ctx.probs_devices)]
         n_q = sum(len(t) for t, _ in members)
-        return (dx, None, *grads_p) + (None,) * n_q
+        return (dx, None, None, *grads_p) + (None,) * n_q
+
+
+class MixPrefetch:
+    """Mixes the step's W_eff of the listed gated products on a second stream,
+    a few products ahead of the forward that uses them.
+
+    The mix is HBM- and VALU-bound, the GEMMs MFMA-bound, and a training step
+    fixes every gate probability before its forward starts.  So while the
+    forward runs product i, the mix of product i + ``ahead`` runs on a side
+    stream (default priority), fenced by one event per product.  A gated
+    forward that finds its product prefetched waits for that event only, runs
+    the GEMM on the buffer (its backward reuses it), and issues the next mix.
+
+    ``groups`` lists the products in forward order as the forward runs them: a
+    list of :class:`MixedQuantLinear` that one stacked product reads, or a
+    single module.  W_eff buffers live as long as the prefetcher (0.58 GB for
+    the 0.8B-class decoder).  Launch arguments are marshalled once; each step
+    copies the probabilities into persistent buffers with one multi-tensor
+    copy, so issuing a mix is one C call and one event record.  Call
+    :meth:`launch` after the step's probabilities are final (after
+    ``GateBank.begin``).  The forward differentiates through the same
+    probabilities, so W_eff, every output and every gradient are
+    bit-identical to the unprefetched step's."""
+
+    def __init__(self, groups: list, device=None, ahead: int = 8):
+        self.groups = [list(g) if isinstance(g, (list, tuple)) else [g] for g in groups]
+        dev = torch.device(device) if device is not None else self.groups[0][0].gates.device
+        self.device = dev
+        self.ahead = max(int(ahead), 1)
+        self.stream = torch.cuda.Stream(device=dev)  # default priority
+        self.buffers, self.events, self.probs, self._pbuf, self._calls = [], [], [], [], []
+        self.pending = [False] * len(self.groups)
+        self._next = 0  # the next product to mix in the current step
+        sptr = self.stream.cuda_stream
+        for gi, mods in enumerate(self.groups):
+            d_pad = mods[0].padded_in_features
+            if any(m.padded_in_features != d_pad for m in mods):
+                raise ValueError("a prefetched product's members must share their input width")
+            for m in mods:
+                m._move_qbytes(dev)
+            n_total = sum(m.out_features for m in mods)
+            buf = torch.empty(n_total, d_pad, dtype=torch.bfloat16, device=dev)
+            pbuf = [torch.zeros(m.num_candidates, dtype=torch.float32, device=dev) for m in mods]
+            # the side stream writes both: when they are freed, the caching
+            # allocator waits for the side stream's queued work too
+            buf.record_stream(self.stream)
+            for b in pbuf:
+                b.record_stream(self.stream)
+            self.buffers.append(buf)
+            self._pbuf.append(pbuf)
+            self.events.append(torch.cuda.Event())
+            self.probs.append(None)
+            self._calls.append(_hip.mix_only_call(
+                [(m._ggml_types(), m._qbytes(), m.out_features) for m in mods], pbuf, d_pad, buf, sptr))
+            for m in mods:
+                m.__dict__["_prefetch"] = (self, gi)
+
+    def _issue(self) -> None:
+        gi = self._next
+        if gi >= len(self.groups):
+            return
+        self._next += 1
+        with torch.cuda.stream(self.stream):
+            self._calls[gi]()
+            self.events[gi].record(self.stream)
+        self.pending[gi] = True
+
+    def launch(self) -> None:
+        main = torch.cuda.current_stream(self.device)
+        probs = [[m.get_probs() for m in mods] for mods in self.groups]
+        torch._foreach_copy_([b for pb in self._pbuf for b in pb],
+                             [p.detach().to(torch.float32) for ps in probs for p in ps])
+        ready = torch.cuda.Event()
+        ready.record(main)  # the probabilities, and the previous step's use of the buffers
+        self.stream.wait_event(ready)
+        self.probs = probs
+        self.pending = [False] * len(self.groups)
+        self._next = 0
+        for _ in range(min(self.ahead, len(self.groups))):
+            self._issue()
+
+    @staticmethod
+    def take(modules: list):
+        """(W_eff, probabilities) when `modules` are one prefetched product whose
+        mix is pending: the current stream then waits for that mix, and the mix
+        `ahead` products later is issued."""
+        ref = modules[0].__dict__.get("_prefetch")
+        if ref is None:
+            return None
+        pf, gi = ref
+        mods = pf.groups[gi]
+        if not pf.pending[gi] or len(mods) != len(modules) or any(a is not b for a, b in zip(mods, modules)):
+            return None
+        pf.pending[gi] = False
+        pf._issue()
+        torch.cuda.current_stream(pf.device).wait_event(pf.events[gi])
+        return pf.buffers[gi], pf.probs[gi][:]
+
+    def release(self) -> None:
+        """Detach the prefetcher from its modules; the current stream waits
+        for mixes still queued on the side stream."""
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)
+        for mods in self.groups:
+            for m in mods:
+                m.__dict__.pop("_prefetch", None)
+        self.pending = [False] * len(self.groups)
+
+
+def groupable(modules: list) -> bool:
+    """Whether gated Linears that read one input run as one stacked product:
+    2 to 4 :class:`MixedQuantLinear` modules with the same input width,
+    out_features multiples of 256, no sharding, PTQR off."""
+    return (2 <= len(modules) <= 4 and not _PTQR_STATE.enabled
+            and all(isinstance(m, MixedQuantLinear) for m in modules)
+            and len({(m.in_features, m.padded_in_features) for m in modules}) == 1
+            and all(m.out_features % 256 == 0 and m.shard_spec is None for m in modules))
 
 
 def gated_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
@@ -313,25 +443,22 @@ def gated_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
 
     stacked=True returns the stacked output [tokens, sum out_features] itself
     (None when the modules cannot be stacked)."""
-    groupable = (2 <= len(modules) <= 4 and not _PTQR_STATE.enabled and x.device.type == "cuda"
-                 and all(isinstance(m, MixedQuantLinear) for m in modules)
-                 and len({(m.in_features, m.padded_in_features) for m in modules}) == 1
-                 and all(m.out_features % 256 == 0 and m.shard_spec is None for m in modules))
-    if not groupable:
+    if not (x.device.type == "cuda" and groupable(modules)):
         return None if stacked else [m(x) for m in modules]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype != torch.bfloat16:
         x2 = x2.to(torch.bfloat16)
+    pre = MixPrefetch.take(modules)
     probs, qbytes, members = [], [], []
-    for m in modules:
+    for i, m in enumerate(modules):
         m._move_qbytes(x.device)
-        p = m.get_probs()
+        p = pre[1][i] if pre is not None else m.get_probs()
         probs.append(p if p.device == x.device else p.to(x.device))
         qbytes.extend(m._qbytes())
         members.append((m._ggml_types(), m.out_features))
     meta = (tuple(members), modules[0].padded_in_features)
-    y = GatedLinearGroupFunction.apply(x2, meta, *probs, *qbytes)
+    y = GatedLinearGroupFunction.apply(x2, meta, pre[0] if pre is not None else None, *probs, *qbytes)
     if stacked:
         return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     outs = torch.split(y, [m.out_features for m in modules], dim=1)
@@ -748,7 +875,8 @@ class MixedQuantLinear(_MixedQuantBase):
         if x.device.type != "cuda":
             raise RuntimeError(f"{self._tensor_name}: MixedQuantLinear runs on a ROCm device only (got {x.device})")
         self._move_qbytes(x.device)
-        probs = self.get_probs()
+        pre = None if _PTQR_STATE.enabled else MixPrefetch.take([self])
+        probs = pre[1][0] if pre is not None else self.get_probs()
         if probs.device != x.device:
             probs = probs.to(x.device)
         lead = x.shape[:-1]
@@ -761,7 +889,7 @@ class MixedQuantLinear(_MixedQuantBase):
             y = RoutedLinearFunction.apply(x2, probs, routing, meta, self._bf16_candidates(x.device),
                                            *self._qbytes())
         else:
-            y = GatedLinearFunction.apply(x2, probs, meta, *self._qbytes())
+            y = GatedLinearFunction.apply(x2, probs, meta, pre[0] if pre is not None else None, *self._qbytes())
         if x.dtype != torch.bfloat16:
             y = y.to(x.dtype)
         out = y.reshape(*lead, self.out_features)

@@ -426,6 +426,11 @@ class StepConfig:
     logits_chunk: int = 0
     fused_loss: bool = True         # CE + KL on the HIP kernels (full-logits path)
     gate_bank: bool = True          # one softmax launch for all gates (trainer.GateBank)
+    # mix each W_eff a few products ahead on a second stream (layers.MixPrefetch).
+    # Off by default: measured on MI355X the mixes then overlap the GEMMs
+    # (1.4 ms of 2.1 ms per 0.8B step) but share their CUs, and the step time
+    # does not move (60.8 ms both ways; stress step 157 ms both ways)
+    prefetch_mix: bool = False
 
 
 class GateTrainer:
@@ -442,6 +447,8 @@ class GateTrainer:
         self.target_bytes = cfg.target_fraction * total_8bit_bytes
         self.non_targeted_bytes = non_targeted_bytes
         self.step_index = 0
+        # after the bank: the prefetch reads each module's probabilities row
+        self.prefetch = _make_prefetch(cfg, student)
 
     def step(self, x: torch.Tensor, y: torch.Tensor) -> dict[str, torch.Tensor]:
         """One optimizer step on batch (x, y); returns the detached losses (no host sync)."""
@@ -451,6 +458,8 @@ class GateTrainer:
         dev = x.device
         t = c.distill_temperature
         bank_bytes = self.bank.begin(tau) if self.bank else None
+        if self.prefetch:
+            self.prefetch.launch()
         try:
             if c.logits_chunk > 0:
                 lm, kl = trainer.chunked_forward_loss(self.student, self.teacher, x, y, t, c.logits_chunk)
@@ -477,6 +486,35 @@ class GateTrainer:
         trainer.gate_optimizer_step(self.trainable, self.opt, self.sched, max_norm=1.0)
         self.step_index += 1
         return {"lm": lm_loss.detach(), "kl": distill.detach(), "size": size.detach(), "tau": tau}
+
+
+def prefetch_groups(model: nn.Module) -> list[list[nn.Module]]:
+    """The gated products of `model` in forward order, as its forward runs
+    them: q/k/v stacked, o, gate/up stacked, down per layer or block (products
+    whose members are not all gated are left out)."""
+    groups = []
+    for mod in model.modules():
+        if isinstance(mod, _Attention):
+            cand = [[mod.q_proj, mod.k_proj, mod.v_proj], [mod.o_proj]]
+        elif isinstance(mod, _MLP):
+            cand = [[mod.gate_proj, mod.up_proj], [mod.down_proj]]
+        else:
+            continue
+        for g in cand:
+            if not all(isinstance(m, layers.MixedQuantLinear) for m in g):
+                continue
+            # the forward stacks a product only when it can; otherwise its members run singly
+            groups += [g] if len(g) == 1 or (GROUP_PROJECTIONS and layers.groupable(g)) else [[m] for m in g]
+    return groups
+
+
+def _make_prefetch(cfg: StepConfig, student: nn.Module):
+    if not cfg.prefetch_mix or cfg.logits_chunk > 0:
+        return None
+    groups = prefetch_groups(student)
+    if not groups or groups[0][0].gates.device.type != "cuda":
+        return None
+    return layers.MixPrefetch(groups)
 
 
 def step_flops(cfg: DecoderConfig, tokens: int, seq: int) -> float:
@@ -581,12 +619,15 @@ class StackTrainer:
         self.opt, self.sched = trainer.build_gate_optimizer(self.trainable, cfg.lr, cfg.max_steps)
         self.target_bytes = cfg.target_fraction * total_8bit_bytes
         self.step_index = 0
+        self.prefetch = _make_prefetch(cfg, student)
 
     def step(self, x: torch.Tensor) -> dict[str, torch.Tensor]:
         c = self.cfg
         tau = trainer.anneal_temperature(self.step_index, c.max_steps, c.temp_start, c.temp_end)
         trainer.set_temperature_all(self.replaced, tau)
         bank_bytes = self.bank.begin(tau) if self.bank else None
+        if self.prefetch:
+            self.prefetch.launch()
         try:
             y = self.student(x)
             with torch.no_grad():
