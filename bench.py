@@ -14,8 +14,11 @@ Also reported in the same JSON line:
   kernels_ms    per-kernel average durations
   hipblaslt_ms  torch's bf16 matmul (hipBLASLt) on the same plain products
                 (Y = X W_eff^T, dX = dY W_eff), for scale
-  dequant_gbps  dequant microbench (4096 x 14336, each format): algorithmic
-                bytes (packed read + fp32 write) / time, against 8 TB/s
+  recipe_menu   the same step with the reference's 27B recipe menu (Q8_0,
+                Q5_K, IQ3_S, IQ2_S, IQ2_XXS, IQ1_S): the IQ decode paths
+  dequant_gbps  dequant microbench (4096 x 14336, each of the 14 formats):
+                algorithmic bytes (packed read + fp32 write) / time, against
+                8 TB/s
   cpu_baseline  the oracle's fp32 torch restatement of the reference step on
                 the host cores, on a row sample of the same layer
   peaks         the chip's sustained bf16 MFMA rate and HBM read / copy
@@ -52,10 +55,18 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "gated-Linear fwd+bwd TFLOP/s + dequant HBM GB/s (% roofline); train tokens/sec"
 TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
-GGML = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+IQ_TYPES = ["IQ1_S", "IQ1_M", "IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S", "IQ4_XS"]
+# the reference's 27B recipe menu (configs/qwen38_27b_voodoo30_tp4.sh:90)
+RECIPE_TYPES = ["Q8_0", "Q5_K", "IQ3_S", "IQ2_S", "IQ2_XXS", "IQ1_S"]
+GGML = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ2_XXS": 16, "IQ2_XS": 17,
+        "IQ3_XXS": 18, "IQ1_S": 19, "IQ3_S": 21, "IQ2_S": 22, "IQ4_XS": 23, "IQ1_M": 29}
 BLOCK = {"Q8_0": (32, 34), "Q2_K": (256, 84), "Q3_K": (256, 110), "Q4_K": (256, 144), "Q5_K": (256, 176),
-         "Q6_K": (256, 210)}
-F16_OFFSETS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,)}
+         "Q6_K": (256, 210), "IQ1_S": (256, 50), "IQ1_M": (256, 56), "IQ2_XXS": (256, 66), "IQ2_XS": (256, 74),
+         "IQ2_S": (256, 82), "IQ3_XXS": (256, 98), "IQ3_S": (256, 110), "IQ4_XS": (256, 136)}
+# fp16 scale fields (IQ1_M: none, its scale is spread over the top nibbles of bytes 49, 51, 53, 55)
+F16_OFFSETS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,),
+               "IQ1_S": (0,), "IQ1_M": (), "IQ2_XXS": (0,), "IQ2_XS": (0,), "IQ2_S": (0,), "IQ3_XXS": (0,),
+               "IQ3_S": (0,), "IQ4_XS": (0,)}
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
 
@@ -70,9 +81,13 @@ def synthetic_qbytes(torch, qt: str, nrows: int, ncols: int, dev, gen):
     bs, bb = BLOCK[qt]
     nblocks = nrows * ncols // bs
     q = torch.randint(0, 256, (nblocks, bb), dtype=torch.uint8, device=dev, generator=gen)
-    for off in F16_OFFSETS[qt]:
+    for off in F16_OFFSETS[qt] or (None,):
         h = torch.randint(0, 1 << 16, (nblocks,), dtype=torch.int32, device=dev, generator=gen)
         h = (h & 0x83FF) | (0x1C00 + ((h >> 10) & 0x7) * 0x0400)  # exponent 7..14
+        if off is None:  # IQ1_M: nibble t of the scale tops byte 49 + 2 t
+            for t in range(4):
+                q[:, 49 + 2 * t] = ((q[:, 49 + 2 * t].to(torch.int32) & 0x0F) | (((h >> (4 * t)) & 0xF) << 4)).to(torch.uint8)
+            continue
         q[:, off] = (h & 0xFF).to(torch.uint8)
         q[:, off + 1] = ((h >> 8) & 0xFF).to(torch.uint8)
     return q.reshape(-1)
@@ -521,6 +536,28 @@ def main() -> int:
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get(dom)
     log("kernels ms: " + ", ".join(f"{k} {v:.3f}" for k, v in kernels.items()))
+
+    # the same step with the reference's 27B recipe menu (four IQ formats): the
+    # IQ instantiations of the mix, gate epilogue and dual backward
+    iq_ids = [GGML[t] for t in RECIPE_TYPES]
+    iq_q = [synthetic_qbytes(torch, qt, n, d_pad, dev, gen) for qt in RECIPE_TYPES]
+    iq_probs = torch.softmax(torch.randn(len(RECIPE_TYPES), device=dev, generator=gen), 0)
+
+    def iq_fwd():
+        _hip.gated_linear_fwd(x, iq_ids, iq_q, iq_probs, n, d_pad, w_eff, y, fws)
+
+    def iq_bwd():
+        _hip.gated_linear_bwd(dy, x, iq_ids, iq_q, iq_probs, n, d_pad, w_eff, dx, dp, ws)
+
+    t_iq_step = time_events(torch, lambda: (iq_fwd(), iq_bwd()), reps)
+    t_iq_mix = time_events(torch, lambda: _hip.mix_weight(iq_ids, iq_q, iq_probs, n, d_pad, w_eff), reps)
+    t_iq_bwd = time_events(torch, iq_bwd, reps)
+    iq_menu = {"candidates": RECIPE_TYPES, "step_ms": round(t_iq_step, 4),
+               "TFLOPs": round(flops / (t_iq_step * 1e-3) / 1e12, 1), "mix_w_eff_ms": round(t_iq_mix, 4),
+               "bwd_dx_gate_ms": round(t_iq_bwd, 4),
+               "candidate_bytes": sum(int(q.numel()) for q in iq_q)}
+    del iq_q
+    log(f"recipe menu {RECIPE_TYPES}: step {t_iq_step:.3f} ms, mix {t_iq_mix:.3f} ms, bwd {t_iq_bwd:.3f} ms")
     # the vendor library on the same plain products, for scale: torch's bf16
     # matmul (hipBLASLt) for Y = X W_eff^T and dX = dY W_eff
     w_c = w_eff[:, :d].contiguous()
@@ -550,7 +587,7 @@ def main() -> int:
     dq = {}
     nr, nc = 4096, 14336
     out = torch.empty(nr, nc, dtype=torch.float32, device=dev)
-    for qt in TYPES:
+    for qt in TYPES + IQ_TYPES:
         qb = synthetic_qbytes(torch, qt, nr, nc, dev, gen)
         t = time_events(torch, lambda: _hip.dequant(GGML[qt], qb, nr, nc, out), 10)
         nbytes = qb.numel() + 4 * nr * nc
@@ -607,6 +644,7 @@ def main() -> int:
         "peaks": peaks,
         "fused": fused,
         "kernels_ms": {k: round(v, 4) for k, v in kernels.items()},
+        "recipe_menu": iq_menu,
         "hipblaslt_ms": {k: round(v, 4) for k, v in lib.items()},
         "dequant_gbps": dq,
         "ptqr": ptqr,

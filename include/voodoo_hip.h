@@ -9,7 +9,9 @@
  * Conventions
  *   - Matrices are row-major.  bf16 values travel as uint16_t bit patterns.
  *   - qtype is the ggml type id: 8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K,
- *     14 Q6_K.  A candidate is the ggml byte stream of an [N][D_pad] weight
+ *     14 Q6_K, 16 IQ2_XXS, 17 IQ2_XS, 18 IQ3_XXS, 19 IQ1_S, 21 IQ3_S, 22 IQ2_S,
+ *     23 IQ4_XS, 29 IQ1_M (the reference's quant registry, voodoo_quant/
+ *     ggml.py:51-66, less the ternary TQ1_0/TQ2_0).  A candidate is the ggml byte stream of an [N][D_pad] weight
  *     (rows back to back, D_pad a multiple of 256 as in the reference's
  *     256-padding of in_features, voodoo_quant/layers.py:973-997).
  *   - Every pointer except `stream` and the host arrays `qtypes`/`qbytes` is a
@@ -53,7 +55,7 @@ int64_t vq_group_bytes(int qtype);
 int64_t vq_qbytes_size(int qtype, int64_t nrows, int64_t ncols);
 
 /* Host-side checks of a candidate set (no GPU work): supported types, D_pad a
- * multiple of 256, D <= D_pad, N and D multiples of 8, 1 <= ncand <= 12. */
+ * multiple of 256, D <= D_pad, N and D multiples of 8, 1 <= ncand <= 16. */
 int vq_validate_candidates(int ncand, const int *qtypes, int64_t n, int64_t d, int64_t d_pad);
 
 /* out[nrows*ncols] fp32 = ggml dequantize_row_<qtype>(qbytes) bit for bit.

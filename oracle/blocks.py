@@ -24,8 +24,13 @@ import numpy as np
 
 F32 = np.float32
 
-BLOCK_BYTES = {"Q8_0": 34, "Q2_K": 84, "Q3_K": 110, "Q4_K": 144, "Q5_K": 176, "Q6_K": 210}
-BLOCK_SIZE = {"Q8_0": 32, "Q2_K": 256, "Q3_K": 256, "Q4_K": 256, "Q5_K": 256, "Q6_K": 256}
+BLOCK_BYTES = {"Q8_0": 34, "Q2_K": 84, "Q3_K": 110, "Q4_K": 144, "Q5_K": 176, "Q6_K": 210,
+               "IQ1_S": 50, "IQ1_M": 56, "IQ2_XXS": 66, "IQ2_XS": 74, "IQ2_S": 82, "IQ3_XXS": 98, "IQ3_S": 110,
+               "IQ4_XS": 136}
+BLOCK_SIZE = {qt: 32 if qt == "Q8_0" else 256 for qt in BLOCK_BYTES}
+# The IQ formats: sub-block scales times grid (code book) values; no closed-form
+# packer here, their decoders are pinned by the reference's own outputs.
+IQ_TYPES = ("IQ1_S", "IQ1_M", "IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ3_XXS", "IQ3_S", "IQ4_XS")
 
 
 def h2f(h: np.ndarray) -> np.ndarray:
@@ -250,7 +255,30 @@ def packed_and_values(qtype: str, nb: int, rng: np.random.Generator, **f16kw):
 
 
 # Byte offsets of the fp16 fields inside each block (d first, then dmin).
-F16_OFFSETS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,)}
+# IQ1_M has none: its fp16 scale is spread over the top nibbles of the four
+# little-endian 16-bit scale words at bytes 48..55 (see set_iq1m_scale).
+F16_OFFSETS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,),
+               "IQ1_S": (0,), "IQ1_M": (), "IQ2_XXS": (0,), "IQ2_XS": (0,), "IQ2_S": (0,), "IQ3_XXS": (0,),
+               "IQ3_S": (0,), "IQ4_XS": (0,)}
+
+
+def set_iq1m_scale(blk: np.ndarray, h: np.ndarray) -> None:
+    """Write fp16 bit patterns ``h`` as IQ1_M super-block scales: nibble t of
+    the scale is the top nibble of scale word t (bits 12..15 of the byte pair
+    48 + 2t, 49 + 2t)."""
+    h = np.asarray(h, dtype=np.uint16)
+    for t in range(4):
+        nib = ((h >> (4 * t)) & 0xF).astype(np.uint8)
+        blk[:, 49 + 2 * t] = (blk[:, 49 + 2 * t] & 0x0F) | (nib << 4)
+
+
+def set_scale(qtype: str, blk: np.ndarray, h, which: int = 0) -> None:
+    """Write fp16 field ``which`` (0 = d, 1 = dmin) of every block."""
+    if qtype == "IQ1_M":
+        assert which == 0
+        set_iq1m_scale(blk, np.broadcast_to(np.asarray(h, dtype=np.uint16), (blk.shape[0],)))
+    else:
+        _put16(blk, F16_OFFSETS[qtype][which], np.broadcast_to(np.asarray(h, dtype=np.uint16), (blk.shape[0],)))
 
 
 def random_blocks(qtype: str, nb: int, rng: np.random.Generator, **f16kw) -> np.ndarray:
@@ -258,6 +286,6 @@ def random_blocks(qtype: str, nb: int, rng: np.random.Generator, **f16kw) -> np.
     block is a valid block of the format."""
     bb = BLOCK_BYTES[qtype]
     out = rng.integers(0, 256, size=(nb, bb), dtype=np.uint16).astype(np.uint8)
-    for off in F16_OFFSETS[qtype]:
-        _put16(out, off, random_finite_f16(rng, nb, **f16kw))
+    for which in range(len(F16_OFFSETS[qtype]) or 1):
+        set_scale(qtype, out, random_finite_f16(rng, nb, **f16kw), which)
     return out

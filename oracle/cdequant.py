@@ -14,8 +14,10 @@ _LIB_PATH = _HERE / "liboracle_dequant.so"
 _LIB = None
 
 # ggml type ids and bytes per 256 weights (Q8_0: eight 34-byte blocks)
-GGML_TYPE = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
-BYTES_PER_256 = {"Q8_0": 272, "Q2_K": 84, "Q3_K": 110, "Q4_K": 144, "Q5_K": 176, "Q6_K": 210}
+GGML_TYPE = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ2_XXS": 16, "IQ2_XS": 17,
+             "IQ3_XXS": 18, "IQ1_S": 19, "IQ3_S": 21, "IQ2_S": 22, "IQ4_XS": 23, "IQ1_M": 29}
+BYTES_PER_256 = {"Q8_0": 272, "Q2_K": 84, "Q3_K": 110, "Q4_K": 144, "Q5_K": 176, "Q6_K": 210, "IQ2_XXS": 66,
+                 "IQ2_XS": 74, "IQ3_XXS": 98, "IQ1_S": 50, "IQ3_S": 110, "IQ2_S": 82, "IQ4_XS": 136, "IQ1_M": 56}
 
 
 def build_oracle_lib(force: bool = False) -> Path:

@@ -252,7 +252,198 @@ void oracle_dequant_q2_K(const uint8_t *x, float *y, int64_t k) {
     }
 }
 
-/* Dispatch by ggml type id (8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K).
+/* ---------------------------------------------------------------------------
+ * IQ formats: restatement of the reference's decoders in
+ * voodoo_quant/quants/gpu_dequant.py (line numbers below), which follow
+ * ggml's dequantize_row_iq*.  Every weight is a product of an fp16-derived
+ * sub-block scale and a grid value (sign applied last), in the reference's
+ * order of float operations.  The grids are the GGUF code books, carried as
+ * data in voodoo-dyn-quant_amd/csrc/vq_iq_grids.inc; the sign byte of a 7-bit
+ * index is its even-parity completion.
+ * ------------------------------------------------------------------------- */
+#define VQ_IQ_TABLE(type, name, n) static const type name[n]
+#include "../voodoo-dyn-quant_amd/csrc/vq_iq_grids.inc"
+#undef VQ_IQ_TABLE
+
+static uint32_t rd32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+static uint8_t parity_signs(uint32_t i7) { /* ksigns_iq2xs[i7] */
+    return (uint8_t)(i7 | ((uint32_t)__builtin_parity(i7) << 7));
+}
+
+static float sgn(uint32_t signs, int j) { return (signs >> j) & 1u ? -1.f : 1.f; }
+
+/* IQ2_XXS, 66-byte blocks {fp16 d; u16 qs[32]}: gpu_dequant.py:53-114 */
+void oracle_dequant_iq2_xxs(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 66;
+        const float d = oracle_fp16_to_fp32(rd16(b));
+        for (int ib32 = 0; ib32 < 8; ++ib32) {
+            const uint8_t *q = b + 2 + 8 * ib32;
+            const uint32_t aux1 = rd32(q + 4);
+            const float db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+            for (int l = 0; l < 4; ++l) {
+                const uint8_t *grid = (const uint8_t *)&iq2xxs_grid[q[l]];
+                const uint32_t signs = parity_signs((aux1 >> (7 * l)) & 127u);
+                for (int j = 0; j < 8; ++j) *y++ = db * (float)grid[j] * sgn(signs, j);
+            }
+        }
+    }
+}
+
+/* IQ2_XS, 74-byte blocks {fp16 d; u16 qs[32]; scales[8]}: gpu_dequant.py:121-166 */
+void oracle_dequant_iq2_xs(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 74;
+        const float d = oracle_fp16_to_fp32(rd16(b));
+        for (int ib32 = 0; ib32 < 8; ++ib32) {
+            const uint8_t sc = b[66 + ib32];
+            const float db0 = d * (0.5f + (float)(sc & 0xf)) * 0.25f;
+            const float db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t q = rd16(b + 2 + 2 * (4 * ib32 + l));
+                const uint8_t *grid = (const uint8_t *)&iq2xs_grid[q & 511u];
+                const uint32_t signs = parity_signs(q >> 9);
+                const float db = l < 2 ? db0 : db1;
+                for (int j = 0; j < 8; ++j) *y++ = db * (float)grid[j] * sgn(signs, j);
+            }
+        }
+    }
+}
+
+/* IQ2_S, 82-byte blocks {fp16 d; qs[32] + signs[32]; qh[8]; scales[8]}: gpu_dequant.py:173-217 */
+void oracle_dequant_iq2_s(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 82;
+        const float d = oracle_fp16_to_fp32(rd16(b));
+        const uint8_t *qs = b + 2, *qh = b + 66, *scales = b + 74;
+        for (int ib32 = 0; ib32 < 8; ++ib32) {
+            const float db0 = d * (0.5f + (float)(scales[ib32] & 0xf)) * 0.25f;
+            const float db1 = d * (0.5f + (float)(scales[ib32] >> 4)) * 0.25f;
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t idx = qs[4 * ib32 + l] | (((uint32_t)qh[ib32] << (8 - 2 * l)) & 0x300u);
+                const uint8_t *grid = (const uint8_t *)&iq2s_grid[idx];
+                const uint32_t signs = qs[32 + 4 * ib32 + l];
+                const float db = l < 2 ? db0 : db1;
+                for (int j = 0; j < 8; ++j) *y++ = db * (float)grid[j] * sgn(signs, j);
+            }
+        }
+    }
+}
+
+/* IQ3_XXS, 98-byte blocks {fp16 d; qs[64]; u32 scales_and_signs[8]}: gpu_dequant.py:224-265 */
+void oracle_dequant_iq3_xxs(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 98;
+        const float d = oracle_fp16_to_fp32(rd16(b));
+        const uint8_t *qs = b + 2;
+        for (int ib32 = 0; ib32 < 8; ++ib32) {
+            const uint32_t aux = rd32(qs + 64 + 4 * ib32);
+            const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+            for (int l = 0; l < 4; ++l) {
+                const uint32_t signs = parity_signs((aux >> (7 * l)) & 127u);
+                const uint8_t *g1 = (const uint8_t *)&iq3xxs_grid[qs[8 * ib32 + 2 * l]];
+                const uint8_t *g2 = (const uint8_t *)&iq3xxs_grid[qs[8 * ib32 + 2 * l + 1]];
+                for (int j = 0; j < 4; ++j) y[j] = db * (float)g1[j] * sgn(signs, j);
+                for (int j = 0; j < 4; ++j) y[j + 4] = db * (float)g2[j] * sgn(signs, j + 4);
+                y += 8;
+            }
+        }
+    }
+}
+
+/* IQ3_S, 110-byte blocks {fp16 d; qs[64]; qh[8]; signs[32]; scales[4]}: gpu_dequant.py:272-349 */
+void oracle_dequant_iq3_s(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 110;
+        const float d = oracle_fp16_to_fp32(rd16(b));
+        const uint8_t *qs = b + 2, *qh = b + 66, *sg = b + 74, *scales = b + 106;
+        for (int ib32 = 0; ib32 < 8; ++ib32) {
+            const uint32_t s4 = ib32 & 1 ? (uint32_t)scales[ib32 / 2] >> 4 : scales[ib32 / 2] & 0xfu;
+            const float db = d * (float)(1 + 2 * (int)s4);
+            const uint32_t h = qh[ib32];
+            for (int l = 0; l < 4; ++l) {
+                const uint8_t *g1 = (const uint8_t *)&iq3s_grid[qs[8 * ib32 + 2 * l] | ((h << (8 - 2 * l)) & 256u)];
+                const uint8_t *g2 = (const uint8_t *)&iq3s_grid[qs[8 * ib32 + 2 * l + 1] | ((h << (7 - 2 * l)) & 256u)];
+                const uint32_t signs = sg[4 * ib32 + l];
+                for (int j = 0; j < 4; ++j) y[j] = db * (float)g1[j] * sgn(signs, j);
+                for (int j = 0; j < 4; ++j) y[j + 4] = db * (float)g2[j] * sgn(signs, j + 4);
+                y += 8;
+            }
+        }
+    }
+}
+
+#define IQ1S_DELTA 0.125f
+
+/* IQ1_S, 50-byte blocks {fp16 d; qs[32]; u16 qh[8]}: gpu_dequant.py:356-383 */
+void oracle_dequant_iq1_s(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 50;
+        const float d = oracle_fp16_to_fp32(rd16(b));
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t qh = rd16(b + 34 + 2 * ib);
+            const float dl = d * (float)(2 * ((qh >> 12) & 7) + 1);
+            const float delta = qh & 0x8000 ? -IQ1S_DELTA : IQ1S_DELTA;
+            for (int l = 0; l < 4; ++l) {
+                const int8_t *grid = (const int8_t *)&iq1s_grid[b[2 + 4 * ib + l] | (((qh >> (3 * l)) & 7) << 8)];
+                for (int j = 0; j < 8; ++j) *y++ = dl * ((float)grid[j] + delta);
+            }
+        }
+    }
+}
+
+/* IQ1_M, 56-byte blocks {qs[32]; qh[16]; u16 scales[4]} with the fp16 super-block
+ * scale spread over the top nibbles of the four scale words: gpu_dequant.py:390-450 */
+void oracle_dequant_iq1_m(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 56;
+        const uint8_t *qs = b, *qh = b + 32;
+        uint32_t sc[4];
+        for (int t = 0; t < 4; ++t) sc[t] = rd16(b + 48 + 2 * t);
+        const uint16_t dh = (uint16_t)((sc[0] >> 12) | ((sc[1] >> 8) & 0x00f0u) | ((sc[2] >> 4) & 0x0f00u) | (sc[3] & 0xf000u));
+        const float d = oracle_fp16_to_fp32(dh);
+        for (int ib = 0; ib < 8; ++ib) {
+            const uint32_t s = sc[ib / 2];
+            const float dl1 = d * (float)(2 * ((s >> (6 * (ib % 2) + 0)) & 7) + 1);
+            const float dl2 = d * (float)(2 * ((s >> (6 * (ib % 2) + 3)) & 7) + 1);
+            const uint32_t h0 = qh[2 * ib], h1 = qh[2 * ib + 1];
+            const uint32_t idx[4] = {qs[4 * ib + 0] | ((h0 << 8) & 0x700u), qs[4 * ib + 1] | ((h0 << 4) & 0x700u),
+                                     qs[4 * ib + 2] | ((h1 << 8) & 0x700u), qs[4 * ib + 3] | ((h1 << 4) & 0x700u)};
+            const float delta[4] = {h0 & 0x08 ? -IQ1S_DELTA : IQ1S_DELTA, h0 & 0x80 ? -IQ1S_DELTA : IQ1S_DELTA,
+                                    h1 & 0x08 ? -IQ1S_DELTA : IQ1S_DELTA, h1 & 0x80 ? -IQ1S_DELTA : IQ1S_DELTA};
+            for (int l = 0; l < 4; ++l) {
+                const int8_t *grid = (const int8_t *)&iq1s_grid[idx[l]];
+                const float dl = l < 2 ? dl1 : dl2;
+                for (int j = 0; j < 8; ++j) *y++ = dl * ((float)grid[j] + delta[l]);
+            }
+        }
+    }
+}
+
+/* IQ4_XS, 136-byte blocks {fp16 d; u16 scales_h; scales_l[4]; qs[128]}: gpu_dequant.py:457-519 */
+void oracle_dequant_iq4_xs(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; i++) {
+        const uint8_t *b = x + i * 136;
+        const float d = oracle_fp16_to_fp32(rd16(b));
+        const uint32_t sh = rd16(b + 2);
+        const uint8_t *sl = b + 4, *qs = b + 8;
+        for (int ib = 0; ib < 8; ++ib) {
+            const int ls = (int)(((sl[ib / 2] >> (4 * (ib % 2))) & 0xf) | (((sh >> (2 * ib)) & 3) << 4));
+            const float dl = d * ((float)ls - 32.0f);
+            for (int j = 0; j < 16; ++j) {
+                y[j] = dl * (float)iq4nl_values[qs[16 * ib + j] & 0xf];
+                y[j + 16] = dl * (float)iq4nl_values[qs[16 * ib + j] >> 4];
+            }
+            y += 32;
+        }
+    }
+}
+
+/* Dispatch by ggml type id (8 Q8_0, 10 Q2_K, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K,
+ * 16 IQ2_XXS, 17 IQ2_XS, 18 IQ3_XXS, 19 IQ1_S, 21 IQ3_S, 22 IQ2_S, 23 IQ4_XS, 29 IQ1_M).
  * Returns 0 on success, -1 for an unknown type. */
 int oracle_dequant(int ggml_type, const uint8_t *x, float *y, int64_t k) {
     switch (ggml_type) {
@@ -262,6 +453,14 @@ int oracle_dequant(int ggml_type, const uint8_t *x, float *y, int64_t k) {
     case 12: oracle_dequant_q4_K(x, y, k); return 0;
     case 13: oracle_dequant_q5_K(x, y, k); return 0;
     case 14: oracle_dequant_q6_K(x, y, k); return 0;
+    case 16: oracle_dequant_iq2_xxs(x, y, k); return 0;
+    case 17: oracle_dequant_iq2_xs(x, y, k); return 0;
+    case 18: oracle_dequant_iq3_xxs(x, y, k); return 0;
+    case 19: oracle_dequant_iq1_s(x, y, k); return 0;
+    case 21: oracle_dequant_iq3_s(x, y, k); return 0;
+    case 22: oracle_dequant_iq2_s(x, y, k); return 0;
+    case 23: oracle_dequant_iq4_xs(x, y, k); return 0;
+    case 29: oracle_dequant_iq1_m(x, y, k); return 0;
     default: return -1;
     }
 }
@@ -280,6 +479,14 @@ int oracle_dequant_parallel(int ggml_type, const uint8_t *x, float *y, int64_t k
     case 12: bb = 144; break;
     case 13: bb = 176; break;
     case 14: bb = 210; break;
+    case 16: bb = 66; break;
+    case 17: bb = 74; break;
+    case 18: bb = 98; break;
+    case 19: bb = 50; break;
+    case 21: bb = 110; break;
+    case 22: bb = 82; break;
+    case 23: bb = 136; break;
+    case 29: bb = 56; break;
     default: return -1;
     }
     const int64_t ngroups = k / 256;

@@ -13,7 +13,13 @@ decoder against a packer written from the format description, but only an
 independent implementation pins the byte layout itself.  Q2_K and Q3_K have no
 decoder in the reference, so they have no golden vectors here.
 
-Usage:  python tests/golden/make_golden.py
+The IQ formats (``ref_iq_decoders.npz``) come from the reference's
+``voodoo_quant/quants/gpu_dequant.py:53-519`` decoders, which it marks as
+bit-identical to ggml's (``layers.py:217-225``).  Nothing else pins them: their
+code books admit no closed form and the reference's own tests of them need a
+libggml that is not present.
+
+Usage:  python tests/golden/make_golden.py [k|iq|all]
 """
 
 from __future__ import annotations
@@ -40,7 +46,35 @@ EDGE_CASES = [
 ]
 
 
+def _edge_blocks(blocks, qt: str, per_edge: int) -> list[np.ndarray]:
+    out = []
+    for fill, d, dmin in EDGE_CASES:
+        blk = np.full((per_edge, blocks.BLOCK_BYTES[qt]), fill, np.uint8)
+        for which, h in enumerate((d, dmin)[:max(len(blocks.F16_OFFSETS[qt]), 1)]):
+            blocks.set_scale(qt, blk, h, which)
+        out.append(blk)
+    return out
+
+
+def _vectors(torch, blocks, fns: dict, seed0: int, nb_rand: dict, dst: Path) -> None:
+    out: dict[str, np.ndarray] = {}
+    for seed, (qt, fn) in enumerate(fns.items()):
+        rng = np.random.default_rng(seed0 + seed)
+        rand = blocks.random_blocks(qt, nb_rand.get(qt, nb_rand["default"]), rng)
+        edge = _edge_blocks(blocks, qt, 1 if qt != "Q8_0" else 8)
+        qbytes = np.concatenate([rand] + edge, axis=0)
+        n_weights = qbytes.shape[0] * blocks.BLOCK_SIZE[qt]
+        rows = n_weights // 256
+        y = fn(torch.from_numpy(qbytes.reshape(-1).copy()), rows, 256)
+        out[f"{qt}_qbytes"] = qbytes
+        out[f"{qt}_out"] = y.reshape(-1).numpy().astype(np.float32)
+        print(f"{qt}: {qbytes.shape[0]} blocks -> {n_weights} weights")
+    np.savez_compressed(dst, **out)
+    print(f"wrote {dst} ({dst.stat().st_size} bytes)")
+
+
 def main() -> None:
+    which = sys.argv[1] if len(sys.argv) > 1 else "all"
     sys.dont_write_bytecode = True
     cache = tempfile.mkdtemp(prefix="vq_golden_")
     # the reference package sets these with setdefault at import time
@@ -51,41 +85,23 @@ def main() -> None:
     import torch
 
     from voodoo_quant import layers as ref_layers  # the REFERENCE package
+    from voodoo_quant.quants import gpu_dequant as ref_iq
 
-    assert Path(ref_layers.__file__).resolve().is_relative_to(REF.resolve()), ref_layers.__file__
+    for mod in (ref_layers, ref_iq):
+        assert Path(mod.__file__).resolve().is_relative_to(REF.resolve()), mod.__file__
     from oracle import blocks
 
-    fns = {
-        "Q8_0": ref_layers._dequantize_q8_0_gpu,
-        "Q4_K": ref_layers._dequantize_q4_K_gpu,
-        "Q5_K": ref_layers._dequantize_q5_K_gpu,
-        "Q6_K": ref_layers._dequantize_q6_K_gpu,
-    }
-    out: dict[str, np.ndarray] = {}
-    for seed, (qt, fn) in enumerate(fns.items()):
-        rng = np.random.default_rng(1000 + seed)
-        bb = blocks.BLOCK_BYTES[qt]
-        nb_rand = 48 if qt != "Q8_0" else 384
-        rand = blocks.random_blocks(qt, nb_rand, rng)
-        per_edge = 1 if qt != "Q8_0" else 8
-        edge = []
-        for fill, d, dmin in EDGE_CASES:
-            blk = np.full((per_edge, bb), fill, np.uint8)
-            offs = blocks.F16_OFFSETS[qt]
-            for off, h in zip(offs, (d, dmin)):
-                blk[:, off] = h & 0xFF
-                blk[:, off + 1] = h >> 8
-            edge.append(blk)
-        qbytes = np.concatenate([rand] + edge, axis=0)
-        n_weights = qbytes.shape[0] * blocks.BLOCK_SIZE[qt]
-        rows = n_weights // 256
-        y = fn(torch.from_numpy(qbytes.reshape(-1).copy()), rows, 256)
-        out[f"{qt}_qbytes"] = qbytes
-        out[f"{qt}_out"] = y.reshape(-1).numpy().astype(np.float32)
-        print(f"{qt}: {qbytes.shape[0]} blocks -> {n_weights} weights")
-    dst = HERE / "ref_decoders.npz"
-    np.savez_compressed(dst, **out)
-    print(f"wrote {dst} ({dst.stat().st_size} bytes)")
+    if which in ("k", "all"):
+        fns = {
+            "Q8_0": ref_layers._dequantize_q8_0_gpu,
+            "Q4_K": ref_layers._dequantize_q4_K_gpu,
+            "Q5_K": ref_layers._dequantize_q5_K_gpu,
+            "Q6_K": ref_layers._dequantize_q6_K_gpu,
+        }
+        _vectors(torch, blocks, fns, 1000, {"default": 48, "Q8_0": 384}, HERE / "ref_decoders.npz")
+    if which in ("iq", "all"):
+        fns = {qt: getattr(ref_iq, f"_dequantize_{qt.lower()}_gpu") for qt in blocks.IQ_TYPES}
+        _vectors(torch, blocks, fns, 2000, {"default": 128}, HERE / "ref_iq_decoders.npz")
 
 
 if __name__ == "__main__":

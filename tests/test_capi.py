@@ -30,16 +30,19 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_group_bytes():
     lib = _hip.lib()
     assert lib.vq_version() >= 100
-    expect = {8: 272, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210}
+    expect = {8: 272, 10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 16: 66, 17: 74, 18: 98, 19: 50, 21: 110, 22: 82,
+              23: 136, 29: 56}
     for t, gb in expect.items():
         assert _hip.group_bytes(t) == gb
-    assert _hip.group_bytes(16) == 0  # IQ2_XXS: no HIP decoder
+    assert _hip.group_bytes(34) == 0  # TQ1_0: no HIP decoder
+    assert _hip.group_bytes(35) == 0  # TQ2_0
 
 
 def test_qbytes_size_matches_reference_arithmetic():
     from voodoo_quant.ggml import get_quant_info
 
-    for qt in ("Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"):
+    for qt in ("Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "IQ1_S", "IQ1_M", "IQ2_XXS", "IQ2_XS", "IQ2_S",
+               "IQ3_XXS", "IQ3_S", "IQ4_XS"):
         info = get_quant_info(qt)
         assert _hip.qbytes_size(info.ggml_type, 17, 1024) == 17 * 1024 // info.block_size * info.block_bytes
     with pytest.raises(ValueError, match="in_features"):
@@ -52,7 +55,7 @@ def test_validate_candidates_errors():
     assert lib.vq_validate_candidates(2, ok, 64, 512, 512) == _hip.VQ_OK
     assert lib.vq_validate_candidates(2, ok, 64, 512, 500) == _hip.VQ_ERR_ALIGN
     assert b"256" in lib.vq_last_error_string()
-    bad = (ctypes.c_int * 2)(8, 16)
+    bad = (ctypes.c_int * 2)(8, 34)  # TQ1_0: no HIP decoder
     assert lib.vq_validate_candidates(2, bad, 64, 512, 512) == _hip.VQ_ERR_QTYPE
     assert lib.vq_validate_candidates(0, ok, 64, 512, 512) == _hip.VQ_ERR_SHAPE
     assert lib.vq_validate_candidates(2, ok, 64, 768, 512) == _hip.VQ_ERR_SHAPE
@@ -94,7 +97,7 @@ def test_embedding_rows_argument_checks():
     # workspace: one fp32 partial per (row, segment of <= 16 groups) and candidate
     assert lib.vq_embedding_rows_bwd_workspace(100, 5120, 6) == 100 * 2 * 6 * 4 + 64
     assert lib.vq_embedding_rows_bwd_workspace(0, 256, 1) == 0
-    assert lib.vq_embedding_rows_bwd_workspace(4, 256, 13) == -1
+    assert lib.vq_embedding_rows_bwd_workspace(4, 256, 17) == -1  # more than 16 candidates
 
 
 def test_linear_fwd_argument_checks():

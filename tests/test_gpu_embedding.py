@@ -13,8 +13,8 @@ Bars:
 
 Ports the reference's tests/test_ptqr.py:93-119 (routed embedding rows),
 :121-186 (module toggle, embedding part) and :187-219 (routed lazy embedding
-on the GPU).  The reference's menus there include IQ2_XXS/IQ3_XXS, which have
-no HIP decoder here; the ports use K-quant menus of the same sizes.
+on the GPU), with the reference's own menus (IQ2_XXS/Q4_K and
+IQ2_XXS/IQ3_XXS/Q8_0).
 """
 
 import numpy as np
@@ -27,7 +27,7 @@ from voodoo_quant import layers
 pytestmark = pytest.mark.gpu
 
 SIX = ["Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"]
-GGML = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+GGML = dict(cdequant.GGML_TYPE)
 
 
 @pytest.fixture(scope="module")
@@ -178,10 +178,10 @@ def _rtn_cands(types, vocab, dim, weight):
 
 
 def test_routed_embedding_rows(hip):
-    """Port of tests/test_ptqr.py:93-119 (menu IQ2_XXS/Q4_K -> Q2_K/Q4_K)."""
+    """Port of tests/test_ptqr.py:93-119 (menu IQ2_XXS/Q4_K)."""
     torch.manual_seed(11)
     vocab, dim = 64, 256
-    qts = ["Q2_K", "Q4_K"]
+    qts = ["IQ2_XXS", "Q4_K"]
     weight = torch.randn(vocab, dim, dtype=torch.float32)
     qbs, cands = _rtn_cands(qts, vocab, dim, weight)
     base = torch.softmax(torch.randn(len(qts)), dim=0)
@@ -199,11 +199,11 @@ def test_routed_embedding_rows(hip):
 
 
 def test_module_toggle_embedding(hip):
-    """Port of tests/test_ptqr.py:121-186, embedding part (menu IQ2_XXS/IQ3_XXS/Q8_0 -> Q2_K/Q3_K/Q8_0),
+    """Port of tests/test_ptqr.py:121-186, embedding part (menu IQ2_XXS/IQ3_XXS/Q8_0),
     plus the gate gradient through the softmax and the toggled-off mixture."""
     torch.manual_seed(23)
     in_f = 256
-    qts = ["Q2_K", "Q3_K", "Q8_0"]
+    qts = ["IQ2_XXS", "IQ3_XXS", "Q8_0"]
     emb = layers.MixedQuantEmbedding(num_embeddings=64, embedding_dim=in_f, candidate_types=qts,
                                      source_weight=torch.randn(64, in_f, dtype=torch.float32),
                                      tensor_name="tests.ptqr.embedding").cuda()

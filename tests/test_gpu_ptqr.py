@@ -17,7 +17,7 @@ from voodoo_quant import layers
 
 pytestmark = pytest.mark.gpu
 
-GGML = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+GGML = dict(cdequant.GGML_TYPE)
 SIX = ["Q8_0", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K"]
 TOL = 1e-2
 
@@ -68,7 +68,8 @@ def _routed(hip, types, qbs, x, routing, n, d_pad):
 
 
 @pytest.mark.parametrize("m,n,d,d_pad,types,mode", [
-    (10, 8 * 4, 256, 256, ["Q2_K", "Q3_K", "Q4_K", "Q8_0"], "random"),      # test_ptqr.py:46-91 shape class
+    (10, 8 * 4, 256, 256, ["IQ2_XXS", "IQ3_XXS", "Q4_K", "Q8_0"], "random"),  # test_ptqr.py:46-91, its menu
+    (10, 8 * 4, 256, 256, ["Q2_K", "Q3_K", "Q4_K", "Q8_0"], "random"),
     (1000, 520, 1000, 1024, SIX, "random"),                                # multi-tile, ragged groups
     (777, 264, 512, 512, ["Q2_K", "Q6_K", "Q8_0"], "one-empty"),            # a candidate with no tokens
     (300, 256, 256, 256, ["Q4_K", "Q8_0"], "all-one"),                      # every token to one candidate
@@ -119,8 +120,8 @@ def test_routed_linear_forward_and_backward(hip, m, n, d, d_pad, types, mode):
 
 
 def test_module_toggle(hip):
-    """Port of tests/test_ptqr.py:121-186 (linear part) on the HIP module."""
-    types = ["Q2_K", "Q3_K", "Q8_0"]
+    """Port of tests/test_ptqr.py:121-186 (linear part) on the HIP module, with its menu."""
+    types = ["IQ2_XXS", "IQ3_XXS", "Q8_0"]
     in_f, out_f = 256, 64
     g = torch.Generator().manual_seed(23)
     lin = layers.MixedQuantLinear(in_f, out_f, types, torch.randn(out_f, in_f, generator=g) * 0.02,

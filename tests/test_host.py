@@ -54,6 +54,54 @@ def test_rtn_blocks_are_valid_and_accurate(qt):
     assert err < ceil, f"{qt} roundtrip error {err:.3f}"
 
 
+IQ_CEIL = {"IQ1_S": 0.55, "IQ1_M": 0.5, "IQ2_XXS": 0.45, "IQ2_XS": 0.4, "IQ2_S": 0.35, "IQ3_XXS": 0.25,
+           "IQ3_S": 0.2, "IQ4_XS": 0.12}
+
+
+@pytest.mark.parametrize("qt", list(IQ_CEIL))
+def test_iq_encoder_blocks_are_valid_and_accurate(qt):
+    """Relative L2 round trip on 8 x 512 N(0, 1) weights (the reference's
+    tests/test_ggml.py:38-49 bars: IQ4_XS < 0.12, IQ2_XXS < 0.45, measured with
+    llama.cpp's quantizer at 0.080 and 0.352), decoded by the oracle."""
+    from voodoo_quant import iq_encode
+
+    torch.manual_seed(0)
+    w = torch.randn(8, 512)
+    qb = rtn.rtn_quantize_tensor(w, qt)
+    assert qb.dtype == torch.uint8 and qb.shape == (8 * 2, iq_encode.IQ_BLOCK_BYTES[qt])
+    y = torch.from_numpy(cdequant.oracle_dequant(qt, qb.numpy(), w.numel()).reshape(w.shape))
+    assert torch.isfinite(y).all()
+    rel = float((y - w).norm() / w.norm())
+    assert rel < IQ_CEIL[qt], f"{qt} roundtrip error {rel:.3f}"
+
+
+def test_iq_encoder_zero_rows_and_scale_invariance():
+    """All-zero rows decode to zeros; scaling the weights by 2 scales every
+    decoded weight by 2 (the encoder's choices depend only on ratios)."""
+    torch.manual_seed(2)
+    w = torch.randn(4, 256)
+    w[1] = 0
+    for qt in IQ_CEIL:
+        y1 = cdequant.oracle_dequant(qt, rtn.rtn_quantize_tensor(w, qt).numpy(), w.numel()).reshape(4, 256)
+        y2 = cdequant.oracle_dequant(qt, rtn.rtn_quantize_tensor(2 * w, qt).numpy(), w.numel()).reshape(4, 256)
+        assert np.all(np.abs(y1[1]) < 1e-20), qt
+        assert np.array_equal(y2, 2 * y1), qt
+
+
+def test_iq_code_books_parse():
+    from voodoo_quant import iq_encode
+
+    t = iq_encode.tables()
+    assert t["iq2xxs_grid"].shape == (256, 8) and set(np.unique(t["iq2xxs_grid"])) == {8, 25, 43}
+    assert t["iq2xs_grid"].shape == (512, 8) and t["iq2s_grid"].shape == (1024, 8)
+    assert t["iq3xxs_grid"].shape == (256, 4) and t["iq3s_grid"].shape == (512, 4)
+    assert t["iq1s_grid"].shape == (2048, 8) and set(np.unique(t["iq1s_grid"])) == {-1, 0, 1}
+    assert t["iq4nl_values"].tolist()[:2] == [-127, -104] and len(t["iq4nl_values"]) == 16
+    # every grid row is distinct (a decoder indexing a wrong table would repeat rows)
+    for name in ("iq2xxs_grid", "iq2xs_grid", "iq2s_grid", "iq3xxs_grid", "iq3s_grid", "iq1s_grid"):
+        assert len({r.tobytes() for r in t[name]}) == t[name].shape[0], name
+
+
 def test_rtn_error_ladder_is_monotone():
     torch.manual_seed(1)
     w = torch.randn(16, 1024) * 0.02
@@ -172,7 +220,7 @@ def test_padding_to_256(isolated_cache):
 
 def test_rejects_types_without_hip_decoder(isolated_cache):
     with pytest.raises(ValueError, match="HIP decoder"):
-        _lin(types=("IQ2_XXS", "Q8_0"), name="bad.proj")
+        _lin(types=("TQ2_0", "Q8_0"), name="bad.proj")
 
 
 def test_effective_bytes_and_assignment(isolated_cache):

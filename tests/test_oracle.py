@@ -30,6 +30,48 @@ def test_oracle_matches_reference_decoders(qt):
     assert np.array_equal(bits(y), bits(ref)), f"{qt}: {np.sum(bits(y) != bits(ref))} mismatching weights"
 
 
+GOLDEN_IQ = Path(__file__).resolve().parent / "golden" / "ref_iq_decoders.npz"
+
+
+@pytest.mark.parametrize("qt", blocks.IQ_TYPES)
+def test_oracle_matches_reference_iq_decoders(qt):
+    """Bit-exact against the reference's IQ decoders (quants/gpu_dequant.py:53-519)
+    on 128 random blocks and six edge blocks (zero/all-ones payload, subnormal,
+    largest finite and signed-zero scales)."""
+    g = np.load(GOLDEN_IQ)
+    qb, ref = g[f"{qt}_qbytes"], g[f"{qt}_out"]
+    y = cdequant.oracle_dequant(qt, qb, ref.size)
+    assert np.array_equal(bits(y), bits(ref)), f"{qt}: {np.sum(bits(y) != bits(ref))} mismatching weights"
+
+
+@pytest.mark.parametrize("qt", blocks.IQ_TYPES)
+def test_iq_scale_linearity(qt):
+    """Every IQ weight is the super-block scale d times a factor fixed by the
+    other bytes: raising d's exponent by one doubles every weight exactly."""
+    rng = np.random.default_rng(11)
+    blk = blocks.random_blocks(qt, 16, rng)
+    h = (0x3000 + rng.integers(0, 0x400, size=16)).astype(np.uint16)  # 2^-3 <= d < 2^-2
+    blocks.set_scale(qt, blk, h)
+    y1 = cdequant.oracle_dequant(qt, blk, 16 * 256)
+    blocks.set_scale(qt, blk, h + np.uint16(0x400))
+    y2 = cdequant.oracle_dequant(qt, blk, 16 * 256)
+    assert np.array_equal(bits(y2), bits(2 * y1))
+    if qt not in ("IQ4_XS",):  # IQ4_XS sub-block scales (ls - 32) can be 0
+        assert np.all(y1 != 0)
+
+
+@pytest.mark.parametrize("qt", ["IQ2_XXS", "IQ2_XS", "IQ3_XXS"])
+def test_iq_stored_signs_have_even_parity(qt):
+    """Formats that store 7 of 8 signs make the eighth even the count of
+    negative weights in every group of 8 (positive d, nonzero grid values)."""
+    rng = np.random.default_rng(12)
+    blk = blocks.random_blocks(qt, 32, rng)
+    blocks.set_scale(qt, blk, 0x3C00)
+    y = cdequant.oracle_dequant(qt, blk, 32 * 256).reshape(-1, 8)
+    assert np.all(y != 0)
+    assert np.all((y < 0).sum(axis=1) % 2 == 0)
+
+
 @pytest.mark.parametrize("qt", SIX)
 @pytest.mark.parametrize("seed", [0, 1])
 def test_oracle_matches_closed_form(qt, seed):

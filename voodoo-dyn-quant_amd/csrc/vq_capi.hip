@@ -42,6 +42,14 @@ const char* qtype_name(int qt) {
     case vq::Q4_K: return "Q4_K";
     case vq::Q5_K: return "Q5_K";
     case vq::Q6_K: return "Q6_K";
+    case vq::IQ2_XXS: return "IQ2_XXS";
+    case vq::IQ2_XS: return "IQ2_XS";
+    case vq::IQ3_XXS: return "IQ3_XXS";
+    case vq::IQ1_S: return "IQ1_S";
+    case vq::IQ3_S: return "IQ3_S";
+    case vq::IQ2_S: return "IQ2_S";
+    case vq::IQ4_XS: return "IQ4_XS";
+    case vq::IQ1_M: return "IQ1_M";
     default: return "?";
     }
 }

@@ -15,13 +15,18 @@
 namespace vq {
 
 // ggml type ids (ggml.h), the only ones this library decodes
-enum QType : int { Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14 };
+enum QType : int {
+    Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14,
+    IQ2_XXS = 16, IQ2_XS = 17, IQ3_XXS = 18, IQ1_S = 19, IQ3_S = 21, IQ2_S = 22, IQ4_XS = 23, IQ1_M = 29
+};
 
 // Bytes per 256 weights.  Q8_0 is handled as groups of eight 34-byte blocks, so
-// every format advances in 256-weight "groups" along a row.
+// every format advances in 256-weight "groups" along a row.  Every size is
+// even, so a group starts on a 2-byte boundary whatever its index.
 __host__ __device__ constexpr int group_bytes(int qt) {
     return qt == Q8_0 ? 272 : qt == Q2_K ? 84 : qt == Q3_K ? 110 : qt == Q4_K ? 144 : qt == Q5_K ? 176
-         : qt == Q6_K ? 210 : 0;
+         : qt == Q6_K ? 210 : qt == IQ2_XXS ? 66 : qt == IQ2_XS ? 74 : qt == IQ3_XXS ? 98 : qt == IQ1_S ? 50
+         : qt == IQ3_S ? 110 : qt == IQ2_S ? 82 : qt == IQ4_XS ? 136 : qt == IQ1_M ? 56 : 0;
 }
 
 __host__ __device__ constexpr bool qtype_supported(int qt) { return group_bytes(qt) != 0; }
@@ -71,6 +76,12 @@ __device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32
 
 __device__ __forceinline__ uint32_t rd_u8(const uint8_t* p) { return p[0]; }
 __device__ __forceinline__ uint32_t rd_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+}  // namespace vq
+
+#include "vq_iq.h"
+
+namespace vq {
 
 // ---------------------------------------------------------------------------
 // Block decoders.  decode_codes<QT, R>(g, p, q, dl, ml) reads weights
@@ -424,6 +435,64 @@ __device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p
     decode_mix<QT, 8>(g, p, y);
 }
 
+// ---------------------------------------------------------------------------
+// The IQ formats, one runtime-dispatched path (their decode is table lookups,
+// not shifts, so one instantiation per consumer serves all eight): the same
+// four operations as the K-quant templates above, on iq_affine's codes.
+// ---------------------------------------------------------------------------
+template <int R>
+__device__ __forceinline__ void decode_run_iq(int qt, const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
+    uint32_t uw[R / 4];
+    float dl;
+    iq_affine<R>(qt, g, p, uw, dl);
+#pragma unroll
+    for (int r = 0; r < R; ++r) y[r] = dl * ((float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu) - 128.0f);
+}
+
+template <int R>
+__device__ __forceinline__ void decode_affine_iq(int qt, const uint8_t* __restrict__ g, int p, uint32_t (&uw)[R / 4],
+                                                 float& dl, float& c) {
+    iq_affine<R>(qt, g, p, uw, dl);
+    c = -128.0f * dl;
+}
+
+template <int R>
+__device__ __forceinline__ void decode_mix_iq(int qt, const uint8_t* __restrict__ g, int p, float (&y)[R]) {
+    uint32_t uw[R / 4];
+    float dl, c;
+    decode_affine_iq<R>(qt, g, p, uw, dl, c);
+#pragma unroll
+    for (int r = 0; r < R; ++r) y[r] = fmaf(dl, (float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu), c);
+}
+
+template <int R>
+__device__ __forceinline__ float dot_run_iq(int qt, const uint8_t* __restrict__ g, int p, const float* __restrict__ v) {
+    uint32_t uw[R / 4];
+    float dl;
+    iq_affine<R>(qt, g, p, uw, dl);
+    float s1 = 0.0f, s0 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        s1 = fmaf(v[r], (float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu), s1);
+        s0 += v[r];
+    }
+    return dl * (s1 - 128.0f * s0);
+}
+
+// dot_sub16 for the IQ formats: sum v (dl (u - 128)) = dl (sum v u - 128 sv)
+__device__ __forceinline__ float dot_sub16_iq(int qt, const uint8_t* __restrict__ g, int p, const float* __restrict__ v,
+                                              float sv) {
+    uint32_t uw[4];
+    float dl;
+    iq_affine<16>(qt, g, p, uw, dl);
+    float s1[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) s1[u & 1] = fmaf(v[4 * u + t], (float)((uw[u] >> (8 * t)) & 0xffu), s1[u & 1]);
+    return dl * ((s1[0] + s1[1]) - 128.0f * sv);
+}
+
 // Runtime-type dispatch (the type is uniform across a wave).
 template <int R>
 __device__ __forceinline__ void decode_run_rt(int qt, const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
@@ -433,13 +502,15 @@ __device__ __forceinline__ void decode_run_rt(int qt, const uint8_t* __restrict_
     case Q3_K: decode_run<Q3_K, R>(g, p, y); break;
     case Q4_K: decode_run<Q4_K, R>(g, p, y); break;
     case Q5_K: decode_run<Q5_K, R>(g, p, y); break;
-    default: decode_run<Q6_K, R>(g, p, y); break;
+    case Q6_K: decode_run<Q6_K, R>(g, p, y); break;
+    default: decode_run_iq<R>(qt, g, p, y); break;
     }
 }
 
-// Up to this many candidates per gated tensor (the reference's widest menus
-// are 12 types, its training recipes use 4-8).
-constexpr int kMaxCand = 12;
+// Up to this many candidates per gated tensor: every format this library
+// decodes (the reference's default menu, list_quant_types(), has 14 types
+// of which 12 decode here; its training recipes use 4-8).
+constexpr int kMaxCand = 16;
 
 struct CandSet {
     const uint8_t* qbytes[kMaxCand];  // packed rows [N][D_pad/256 groups]
@@ -447,6 +518,13 @@ struct CandSet {
     int ncand;
     int64_t row_groups;  // D_pad / 256
 };
+
+// Whether a launch must take the instantiation that decodes IQ formats.
+inline bool any_iq(const CandSet& cs) {
+    for (int k = 0; k < cs.ncand; ++k)
+        if (is_iq(cs.qtype[k])) return true;
+    return false;
+}
 
 // Gated tensors that share one input, stacked along N: set g owns rows
 // [set_j0[g], set_j0[g + 1]) of the stacked weight (boundaries on 256-row
@@ -459,5 +537,11 @@ struct CandGroup {
     int set_j0[kMaxSets + 1];
     CandSet sets[kMaxSets];
 };
+
+inline bool any_iq(const CandGroup& cg) {
+    for (int i = 0; i < cg.nsets; ++i)
+        if (any_iq(cg.sets[i])) return true;
+    return false;
+}
 
 }  // namespace vq

@@ -11,9 +11,27 @@
 // into LDS with 16-byte direct-to-LDS loads (the byte range of 16 groups is a multiple of 16
 // for every format), then each thread decodes runs of 8 weights from LDS and
 // writes them with 16-byte (bf16 x8) or 2x16-byte (fp32 x8) stores.
+#include <mutex>
+#include <unordered_set>
+
 #include "vq_internal.h"
 
 namespace vq {
+
+hipError_t allow_dynamic_lds(const void* kern, size_t lds) {
+    if (lds <= 64 * 1024) return hipSuccess;
+    static std::mutex mu;
+    static std::unordered_set<const void*> done;
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count(kern)) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return e;
+    }
+    done.insert(kern);
+    return hipSuccess;
+}
 
 // Copy `len` bytes at `src` (16-byte aligned) to LDS `dst` (16-byte aligned)
 // with direct-to-LDS loads (buffer_load_dwordx4 ... lds: lane l of a wave's
@@ -63,7 +81,10 @@ __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* 
         const int j = (t >> 5) + 8 * u;
         if (j < ng) {
             float y[8];
-            decode_run<QT, 8>(lds + j * GB, 8 * (t & 31), y);
+            if constexpr (is_iq(QT))
+                decode_run_iq<8>(QT, lds + j * GB, 8 * (t & 31), y);  // the type is a constant: the switch folds
+            else
+                decode_run<QT, 8>(lds + j * GB, 8 * (t & 31), y);
             if constexpr (sizeof(OUT) == 4) {
                 float4* o = reinterpret_cast<float4*>(out + (g0 + j) * 256 + 8 * (t & 31));
                 o[0] = make_float4(y[0], y[1], y[2], y[3]);
@@ -91,6 +112,14 @@ static hipError_t launch_dequant_t(int qtype, const uint8_t* q, OUT* out, int64_
     case Q4_K: dequant_kernel<Q4_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
     case Q5_K: dequant_kernel<Q5_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
     case Q6_K: dequant_kernel<Q6_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ2_XXS: dequant_kernel<IQ2_XXS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ2_XS: dequant_kernel<IQ2_XS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ2_S: dequant_kernel<IQ2_S, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ3_XXS: dequant_kernel<IQ3_XXS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ3_S: dequant_kernel<IQ3_S, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ1_S: dequant_kernel<IQ1_S, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ1_M: dequant_kernel<IQ1_M, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case IQ4_XS: dequant_kernel<IQ4_XS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -124,7 +153,9 @@ struct MixPlan {
 constexpr int kMixRun = 16;                                     // weights per thread and run
 constexpr int kMixGroupsPerPass = kStreamThreads * kMixRun / 256;  // 16
 
-template <int RUNS>
+// IQ: the sets may hold IQ formats (the K-quant-only instantiation keeps its
+// lower register count and occupancy).
+template <int RUNS, bool IQ>
 __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int GPB = kMixGroupsPerPass * RUNS;  // groups per workgroup
@@ -166,7 +197,13 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
             case Q3_K: decode_mix<Q3_K, kMixRun>(g, p, w); break;
             case Q4_K: decode_mix<Q4_K, kMixRun>(g, p, w); break;
             case Q5_K: decode_mix<Q5_K, kMixRun>(g, p, w); break;
-            default: decode_mix<Q6_K, kMixRun>(g, p, w); break;
+            case Q6_K: decode_mix<Q6_K, kMixRun>(g, p, w); break;
+            default:
+                if constexpr (IQ)
+                    decode_mix_iq<kMixRun>(qt, g, p, w);
+                else
+                    decode_mix<Q6_K, kMixRun>(g, p, w);
+                break;
             }
             off += (GPB * gb + 15) & ~15;
             const float pk = probs[k];
@@ -214,7 +251,15 @@ hipError_t launch_mix_sets(int nsets, const CandSet* sets, const float* const* p
     }
     mp.block0[nsets] = blocks;
     if (blocks <= 0) return hipSuccess;
-    mix_kernel<1><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
+    bool iq = false;
+    for (int i = 0; i < nsets; ++i) iq = iq || any_iq(sets[i]);
+    // 16 Q8_0 candidates stage 68 KiB
+    const hipError_t e = allow_dynamic_lds(iq ? (const void*)mix_kernel<1, true> : (const void*)mix_kernel<1, false>, lds);
+    if (e != hipSuccess) return e;
+    if (iq)
+        mix_kernel<1, true><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
+    else
+        mix_kernel<1, false><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(mp);
     return hipGetLastError();
 }
 

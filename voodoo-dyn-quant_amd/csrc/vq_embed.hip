@@ -76,7 +76,8 @@ __device__ __forceinline__ void decode8_mix_rt(int qt, const uint8_t* g, int p, 
     case Q3_K: decode8_mix<Q3_K>(g, p, w); break;
     case Q4_K: decode8_mix<Q4_K>(g, p, w); break;
     case Q5_K: decode8_mix<Q5_K>(g, p, w); break;
-    default: decode8_mix<Q6_K>(g, p, w); break;
+    case Q6_K: decode8_mix<Q6_K>(g, p, w); break;
+    default: decode_mix_iq<8>(qt, g, p, w); break;
     }
 }
 
@@ -87,7 +88,8 @@ __device__ __forceinline__ float dot8_rt(int qt, const uint8_t* g, int p, const 
     case Q3_K: return dot_run<Q3_K, 8>(g, p, v);
     case Q4_K: return dot_run<Q4_K, 8>(g, p, v);
     case Q5_K: return dot_run<Q5_K, 8>(g, p, v);
-    default: return dot_run<Q6_K, 8>(g, p, v);
+    case Q6_K: return dot_run<Q6_K, 8>(g, p, v);
+    default: return dot_run_iq<8>(qt, g, p, v);
     }
 }
 
@@ -268,25 +270,29 @@ static size_t embed_lds(const CandSet& cs, bool routed) {
 }
 
 template <class OUT>
-static void embed_rows_t(const CandSet& cs, const float* probs, const int64_t* routing, const int64_t* ids,
-                         int64_t vocab, int64_t dim, const EmbedPlan& pl, OUT* out, hipStream_t s) {
+static hipError_t embed_rows_t(const CandSet& cs, const float* probs, const int64_t* routing, const int64_t* ids,
+                               int64_t vocab, int64_t dim, const EmbedPlan& pl, OUT* out, hipStream_t s) {
     const dim3 grid((unsigned)pl.blocks);
+    const size_t lds = embed_lds(cs, routing != nullptr);
+    const hipError_t e = allow_dynamic_lds(
+        routing ? (const void*)embed_rows_kernel<true, OUT> : (const void*)embed_rows_kernel<false, OUT>, lds);
+    if (e != hipSuccess) return e;
     if (routing)
-        embed_rows_kernel<true, OUT><<<grid, kStreamThreads, embed_lds(cs, true), s>>>(
-            cs, probs, routing, ids, vocab, pl.nseg, pl.seg, pl.gused, dim, out);
+        embed_rows_kernel<true, OUT><<<grid, kStreamThreads, lds, s>>>(cs, probs, routing, ids, vocab, pl.nseg, pl.seg,
+                                                                       pl.gused, dim, out);
     else
-        embed_rows_kernel<false, OUT><<<grid, kStreamThreads, embed_lds(cs, false), s>>>(
-            cs, probs, nullptr, ids, vocab, pl.nseg, pl.seg, pl.gused, dim, out);
+        embed_rows_kernel<false, OUT><<<grid, kStreamThreads, lds, s>>>(cs, probs, nullptr, ids, vocab, pl.nseg,
+                                                                        pl.seg, pl.gused, dim, out);
+    return hipSuccess;
 }
 
 hipError_t launch_embed_rows(const CandSet& cs, const float* probs, const int64_t* routing, const int64_t* ids,
                              int64_t nids, int64_t vocab, int64_t dim, void* out, bool out_f32, hipStream_t s) {
     const EmbedPlan pl = embed_plan(nids, dim);
     if (pl.blocks <= 0) return hipSuccess;
-    if (out_f32)
-        embed_rows_t(cs, probs, routing, ids, vocab, dim, pl, static_cast<float*>(out), s);
-    else
-        embed_rows_t(cs, probs, routing, ids, vocab, dim, pl, static_cast<bf16_t*>(out), s);
+    const hipError_t e = out_f32 ? embed_rows_t(cs, probs, routing, ids, vocab, dim, pl, static_cast<float*>(out), s)
+                                 : embed_rows_t(cs, probs, routing, ids, vocab, dim, pl, static_cast<bf16_t*>(out), s);
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 
@@ -299,6 +305,9 @@ hipError_t launch_embed_rows_bwd(const CandSet& cs, const int64_t* ids, int64_t 
     }
     const dim3 grid((unsigned)pl.blocks);
     const size_t lds = embed_lds(cs, false);
+    const hipError_t ea = allow_dynamic_lds(
+        grad_f32 ? (const void*)embed_rows_bwd_kernel<float> : (const void*)embed_rows_bwd_kernel<bf16_t>, lds);
+    if (ea != hipSuccess) return ea;
     if (grad_f32)
         embed_rows_bwd_kernel<float><<<grid, kStreamThreads, lds, s>>>(cs, ids, vocab, pl.nseg, pl.seg, pl.gused,
                                                                        dim, static_cast<const float*>(grad), partials);

@@ -168,6 +168,7 @@ __device__ __forceinline__ void fz_stage_dy(u32x4* slot, const bf16_t* __restric
 // weights 16 (t % 16) .. + 15 of the group) of the staged candidate.  Only
 // the decode is specialised per format; the accumulation is shared, so the
 // accumulators stay in the same registers whichever format a step holds.
+template <bool IQ>
 __device__ __forceinline__ void fz_decode_rt(int qt, const u32x4* slot, int64_t rg, int r0, int g, int N, float pk,
                                              float (&acc)[16], float& cacc) {
     const FzRows rw(qt, rg, r0);
@@ -184,7 +185,13 @@ __device__ __forceinline__ void fz_decode_rt(int qt, const u32x4* slot, int64_t 
     case Q3_K: decode_affine<Q3_K, 16>(gp, p, uw, dl, c); break;
     case Q4_K: decode_affine<Q4_K, 16>(gp, p, uw, dl, c); break;
     case Q5_K: decode_affine<Q5_K, 16>(gp, p, uw, dl, c); break;
-    default: decode_affine<Q6_K, 16>(gp, p, uw, dl, c); break;
+    case Q6_K: decode_affine<Q6_K, 16>(gp, p, uw, dl, c); break;
+    default:
+        if constexpr (IQ)
+            decode_affine_iq<16>(qt, gp, p, uw, dl, c);
+        else
+            decode_affine<Q6_K, 16>(gp, p, uw, dl, c);
+        break;
     }
     const float pdl = pk * dl;
     cacc = fmaf(pk, c, cacc);
@@ -215,7 +222,7 @@ __device__ __forceinline__ void fz_put_w(u32x4* wt, float (&acc)[16], float cacc
 // stages its operand tile; consume(slot, W tile, u) runs after the operand
 // step's wait with the W tile complete.  The issue position (unit, step) is
 // carried along with the consume position, so no step needs a division.
-template <class UnitOf, class StageOp, class Consume, class PutW>
+template <bool IQ, class UnitOf, class StageOp, class Consume, class PutW>
 __device__ __forceinline__ void fz_steps(const FusedParams& p, u32x4* smem, int nunits, UnitOf unit_of,
                                          StageOp stage_op, PutW put_w, Consume consume) {
     const CandSet& cs = p.cs;
@@ -271,7 +278,7 @@ __device__ __forceinline__ void fz_steps(const FusedParams& p, u32x4* smem, int 
 #pragma unroll
                 for (int q = 1; q < kMaxCand; ++q)
                     if (j == q) pk = pr[q];
-                fz_decode_rt(cs.qtype[j], slot, cs.row_groups, r0, g, p.N, pk, acc, cacc);
+                fz_decode_rt<IQ>(cs.qtype[j], slot, cs.row_groups, r0, g, p.N, pk, acc, cacc);
             } else {
                 put_w(wt, acc, cacc);
                 cacc = 0.0f;
@@ -288,7 +295,11 @@ __device__ __forceinline__ void fz_steps(const FusedParams& p, u32x4* smem, int 
 // Forward: work item (32-row block blockIdx.x, group split blockIdx.y, token
 // block blockIdx.z).  Wave w multiplies k slice [32 w, 32 w + 32) of every
 // group; the eight partial tiles are summed in wave order at the end.
-__global__ __launch_bounds__(kFzThreads) void fused_fwd_kernel(FusedParams p) {
+// IQ: the candidate set may hold IQ formats.  Their table-lookup decode needs
+// more registers; held to 4 waves per SIMD (two workgroups per CU) it spills
+// a few bytes, which the K-quant-only instantiation does not.
+template <bool IQ>
+__global__ __launch_bounds__(kFzThreads) __attribute__((amdgpu_waves_per_eu(4))) void fused_fwd_kernel(FusedParams p) {
     extern __shared__ u32x4 smem[];
     const int r0 = blockIdx.x * kFzRows;
     const int G = (p.D + 255) / 256;  // groups past D only hold zero-padding columns
@@ -319,7 +330,7 @@ __global__ __launch_bounds__(kFzThreads) void fused_fwd_kernel(FusedParams p) {
             yacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, yacc, 0, 0, 0);
         }
     };
-    fz_steps(p, smem, ng, unit_of, stage_op, put_w, consume);
+    fz_steps<IQ>(p, smem, ng, unit_of, stage_op, put_w, consume);
     // sum the waves' partial tiles in wave order: [wave][register][lane]
     float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
@@ -347,7 +358,8 @@ __global__ __launch_bounds__(kFzThreads) void fused_fwd_kernel(FusedParams p) {
 // share one XCD's L2.  The W tile is [32 rows (the reduction)][256 columns]
 // in the [K][rows] layout the transposed fragment reads want; wave w owns
 // output columns [32 w, 32 w + 32) of the group.
-__global__ __launch_bounds__(kFzThreads) void fused_dx_kernel(FusedParams p) {
+template <bool IQ>
+__global__ __launch_bounds__(kFzThreads) __attribute__((amdgpu_waves_per_eu(4))) void fused_dx_kernel(FusedParams p) {
     extern __shared__ u32x4 smem[];
     using WL = DmaNS<256, 32, kFzThreads>;  // W tile as [32 k-rows][256 columns]
     const int G = (p.D + 255) / 256;
@@ -383,7 +395,7 @@ __global__ __launch_bounds__(kFzThreads) void fused_dx_kernel(FusedParams p) {
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
         }
     };
-    fz_steps(p, smem, nblk, unit_of, stage_op, put_w, consume);
+    fz_steps<IQ>(p, smem, nblk, unit_of, stage_op, put_w, consume);
     const int d = 256 * g + 32 * wave + (lane & 31);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -468,9 +480,11 @@ hipError_t launch_fused(bool dx, const bf16_t* act, const CandSet& cs, const flo
     p.ws = ws;
     p.splits = pl.splits;
     p.per_split = pl.per_split;
-    static bool attr_fwd = false, attr_dx = false;
-    const void* kern = dx ? (const void*)fused_dx_kernel : (const void*)fused_fwd_kernel;
-    bool& done = dx ? attr_dx : attr_fwd;
+    static bool attr_done[2][2] = {};  // [dx][iq]
+    const bool iq = any_iq(cs);
+    const void* kern = dx ? (iq ? (const void*)fused_dx_kernel<true> : (const void*)fused_dx_kernel<false>)
+                          : (iq ? (const void*)fused_fwd_kernel<true> : (const void*)fused_fwd_kernel<false>);
+    bool& done = attr_done[dx][iq];
     if (!done) {
         hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kFzLds);
         if (e != hipSuccess) {
@@ -480,10 +494,14 @@ hipError_t launch_fused(bool dx, const bf16_t* act, const CandSet& cs, const flo
         done = true;
     }
     const dim3 grid(pl.grid_x, dx ? 1 : pl.splits, pl.grid_z);
-    if (dx)
-        fused_dx_kernel<<<grid, dim3(kFzThreads), kFzLds, s>>>(p);
+    if (dx && iq)
+        fused_dx_kernel<true><<<grid, dim3(kFzThreads), kFzLds, s>>>(p);
+    else if (dx)
+        fused_dx_kernel<false><<<grid, dim3(kFzThreads), kFzLds, s>>>(p);
+    else if (iq)
+        fused_fwd_kernel<true><<<grid, dim3(kFzThreads), kFzLds, s>>>(p);
     else
-        fused_fwd_kernel<<<grid, dim3(kFzThreads), kFzLds, s>>>(p);
+        fused_fwd_kernel<false><<<grid, dim3(kFzThreads), kFzLds, s>>>(p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || pl.splits == 1) return e;
     const int64_t count = (int64_t)M * (dx ? D : N);

@@ -123,6 +123,8 @@ hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t
 
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
                             int D, hipStream_t s) {
+    if (any_iq(cg))
+        return launch_gemm_cfg<GateCfg, true>(gate_params(dY, X, cg, partials, M, N, D), device_cus(), nullptr, s);
     return launch_gemm_cfg<GateCfg>(gate_params(dY, X, cg, partials, M, N, D), device_cus(), nullptr, s);
 }
 
@@ -131,6 +133,10 @@ hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& 
 hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
                                const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
                                hipStream_t s) {
+    if (any_iq(cg))
+        return launch_gemm_dual<DxCfg, GateCfg, true>(dx_params(dY, W, ldw, dX, M, N, D),
+                                                        gate_params(dY, X, cg, partials, M, N, D), device_cus(),
+                                                        tail_ws, s);
     return launch_gemm_dual<DxCfg, GateCfg>(dx_params(dY, W, ldw, dX, M, N, D),
                                             gate_params(dY, X, cg, partials, M, N, D), device_cus(), tail_ws, s);
 }

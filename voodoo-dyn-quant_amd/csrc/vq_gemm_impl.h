@@ -599,7 +599,34 @@ __device__ __forceinline__ float gate_dot_lds(const f32x16 (&acc)[MI][NJ], const
     return s;
 }
 
-template <int BI, int BJ, int BK, int WI, int WJ>
+// gate_dot_lds for the IQ formats (type known at run time, uniform)
+template <int MI, int NJ, int WTI, int WTJ>
+__device__ __forceinline__ float gate_dot_lds_iq(int qt, const f32x16 (&acc)[MI][NJ], const float (&sv)[MI][NJ],
+                                                 const uint8_t* __restrict__ buf, int64_t row_groups, int j0,
+                                                 int group, int wi, int wj, int lane, int J) {
+    const int gb = group_bytes(qt);
+    const int pitch = 16 * gate_span_chunks(gb);
+    float s = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NJ; ++b) {
+        const int nl = wj * WTJ + 32 * b + (lane & 31);
+        const int n = j0 + nl < J ? j0 + nl : j0;
+        const int64_t span = ((int64_t)n * row_groups + group) * gb;
+        const uint8_t* g = buf + nl * pitch + (int)(span & 15);
+#pragma unroll
+        for (int a = 0; a < MI; ++a) {
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = acc[a][b][r];
+            s += dot_sub16_iq(qt, g, wi * WTI + 32 * a + 16 * (lane >> 5), v, sv[a][b]);
+        }
+    }
+    return s;
+}
+
+// IQ: the candidate set may hold IQ formats (their table-lookup decode needs
+// registers the K-quant-only instantiation keeps for itself).
+template <int BI, int BJ, int BK, int WI, int WJ, bool IQ>
 __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, int i0, int j0,
                                               u32x4* __restrict__ smem,
                                               const f32x16 (&acc)[GemmShape<BI, BJ, BK, WI, WJ>::MI]
@@ -654,7 +681,16 @@ __device__ __forceinline__ void gate_epilogue(const GemmParams& p, int block, in
         case Q3_K: sum = gate_dot_lds<Q3_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
         case Q4_K: sum = gate_dot_lds<Q4_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
         case Q5_K: sum = gate_dot_lds<Q5_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
-        default: sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn); break;
+        default:
+            if constexpr (IQ) {
+                if (is_iq(cs.qtype[k])) {
+                    sum = gate_dot_lds_iq<S::MI, S::NJ, S::WTI, S::WTJ>(cs.qtype[k], acc, sv, buf, rg, jl0, group, wi,
+                                                                        wj, lane, jn);
+                    break;
+                }
+            }
+            sum = gate_dot_lds<Q6_K, S::MI, S::NJ, S::WTI, S::WTJ>(acc, sv, buf, rg, jl0, group, wi, wj, lane, jn);
+            break;
         }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
@@ -773,8 +809,10 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int 
     }
 }
 
-// Work item `block` of problem p.
-template <class C>
+// Work item `block` of problem p.  IQ: a gate product whose candidate sets
+// may hold IQ formats (their table-lookup decode needs registers the
+// K-quant-only instantiation keeps for itself).
+template <class C, bool IQ = false>
 __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4* __restrict__ smem) {
     using LA = typename C::LA;
     using LB = typename C::LB;
@@ -818,7 +856,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
         store_tile_lds<BI, BJ, BK, WI, WJ>(p, i0, j0, smem, acc);
     } else {
         static_assert(LA::kPerm == 1, "the gate epilogue reads 16 consecutive weights per accumulator block");
-        gate_epilogue<BI, BJ, BK, WI, WJ>(p, block, i0, j0, smem, acc);
+        gate_epilogue<BI, BJ, BK, WI, WJ, IQ>(p, block, i0, j0, smem, acc);
     }
 }
 
@@ -868,11 +906,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_tail_fixup_kernel(GemmParams 
 // for eight-wave ones or two 128x128 workgroups per CU): telling the compiler
 // so lets it keep fragments in flight instead of minimising registers for an
 // occupancy the LDS use rules out anyway.
-template <class C>
+template <class C, bool IQ = false>
 __global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::OCC, C::OCC)))
 void gemm_kernel(GemmParams p) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass needs only the launch stub (see gemm_dual_kernel)
     extern __shared__ u32x4 smem[];
-    gemm_body<C>(p, blockIdx.x, smem);
+    gemm_body<C, IQ>(p, blockIdx.x, smem);
+#endif
 }
 
 // Two independent products in one launch: blocks [0, n1) run problem 1,
@@ -880,17 +920,24 @@ void gemm_kernel(GemmParams p) {
 // mapping of map_work; blocks past problem 1's items exit).  One grid lets
 // the second product's work items fill the last, partial round of the first
 // instead of each launch idling CUs in its own tail.
-template <class C1, class C2>
+template <class C1, class C2, bool IQ1 = false, bool IQ2 = false>
 __global__ __launch_bounds__(C1::THREADS) __attribute__((amdgpu_waves_per_eu(C1::OCC, C1::OCC)))
 void gemm_dual_kernel(GemmParams p1, int items1, int n1, GemmParams p2) {
     static_assert(C1::THREADS == C2::THREADS && C1::OCC == C2::OCC, "both problems use the same workgroup shape");
+    // Kernel bodies are compiled for the device only: the host pass needs just
+    // the launch stub, and with a configuration instantiated for both IQ
+    // values it rejects the second instantiation of gemm_mainloop_pp
+    // (a substitution failure on the accumulator array parameter that the
+    // device pass does not report).
+#if defined(__HIP_DEVICE_COMPILE__)
     extern __shared__ u32x4 smem[];
     const int b = blockIdx.x;
     if (b < n1) {
-        if (b < items1) gemm_body<C1>(p1, b, smem);
+        if (b < items1) gemm_body<C1, IQ1>(p1, b, smem);
     } else {
-        gemm_body<C2>(p2, b - n1, smem);
+        gemm_body<C2, IQ2>(p2, b - n1, smem);
     }
+#endif
 }
 
 template <class C>
@@ -906,7 +953,7 @@ static hipError_t set_lds_attr(const void* kern, size_t lds, bool& done) {
 
 // Launch of one product.  `cus` is the device's CU count; a store epilogue
 // splits tail tiles only when `tail_ws` (tail_bytes of the plan) is given.
-template <class C>
+template <class C, bool IQ = false>
 static hipError_t launch_gemm_cfg(GemmParams p, int cus, float* tail_ws, hipStream_t s) {
     const bool split_ok = C::EPI == EPI_GATE || tail_ws != nullptr;
     const int grid = C::plan(p, cus, split_ok);
@@ -915,7 +962,7 @@ static hipError_t launch_gemm_cfg(GemmParams p, int cus, float* tail_ws, hipStre
     constexpr size_t lds = C::lds();
     static_assert(lds <= 160 * 1024, "exceeds the 160 KiB of LDS per workgroup");
     static bool attr_set = false;  // per instantiation
-    auto kern = gemm_kernel<C>;
+    auto kern = gemm_kernel<C, IQ>;
     hipError_t e = set_lds_attr<C>((const void*)kern, lds, attr_set);
     if (e != hipSuccess) return e;
     kern<<<dim3(grid), dim3(C::THREADS), lds, s>>>(p);
@@ -932,18 +979,18 @@ static hipError_t launch_gemm_cfg(GemmParams p, int cus, float* tail_ws, hipStre
 // tail (its split parts are fixed up after the launch): 0.8-1.5% faster than
 // the other order at 8192 tokens and 5120 -> 17408, 0.9-1.2% at
 // 4096 -> 28672, neutral at 17408 -> 5120 and the 1024-wide products.
-template <class C1, class C2>
+template <class C1, class C2, bool IQ2 = false>
 static hipError_t launch_gemm_dual(GemmParams p1, GemmParams p2, int cus, float* tail_ws1, hipStream_t s) {
     static_assert(C1::EPI == EPI_STORE && C2::EPI == EPI_GATE, "a store product and a gate product");
     const int grid1 = C1::plan(p1, cus, tail_ws1 != nullptr);
     const int grid2 = C2::plan(p2, cus, true);
     p1.partials = tail_ws1;
-    if (grid1 == 0) return launch_gemm_cfg<C2>(p2, cus, nullptr, s);
+    if (grid1 == 0) return launch_gemm_cfg<C2, IQ2>(p2, cus, nullptr, s);
     if (grid2 == 0) return launch_gemm_cfg<C1>(p1, cus, tail_ws1, s);
     constexpr size_t lds = C1::lds() > C2::lds() ? C1::lds() : C2::lds();
     static_assert(lds <= 160 * 1024, "exceeds the 160 KiB of LDS per workgroup");
     static bool attr_set = false;
-    auto kern = gemm_dual_kernel<C2, C1>;
+    auto kern = gemm_dual_kernel<C2, C1, IQ2, false>;
     hipError_t e = set_lds_attr<C2>((const void*)kern, lds, attr_set);
     if (e != hipSuccess) return e;
     kern<<<dim3(grid2 + grid1), dim3(C2::THREADS), lds, s>>>(p2, grid2, grid2, p1);

@@ -15,6 +15,10 @@ constexpr int kStreamThreads = 256;
 constexpr int kRunsPerThread = 2;
 constexpr int kGroupsPerBlock = kStreamThreads * 8 * kRunsPerThread / 256;  // 16
 
+// Lets `kern` take `lds` bytes of dynamic LDS: above 64 KiB a kernel needs
+// the opt-in attribute (set once per kernel, process-wide).
+hipError_t allow_dynamic_lds(const void* kern, size_t lds);
+
 hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s);
 hipError_t launch_dequant_bf16(int qtype, const uint8_t* q, bf16_t* out, int64_t ngroups, hipStream_t s);
 hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int64_t ngroups, hipStream_t s);

@@ -70,8 +70,11 @@ _QUANT_REGISTRY: dict[str, QuantTypeInfo] = {
     "TQ2_0": _info("TQ2_0", 35, 256, 66),
 }
 
-# The formats the HIP kernels decode (the gated-Linear candidate menu).
-HIP_TYPES: tuple[str, ...] = ("Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0")
+# The formats the HIP kernels decode (the gated-Linear candidate menu): every
+# registry type but the ternary TQ1_0/TQ2_0, which the reference's default
+# menu leaves out too (``ggml.py:156-158``).
+HIP_TYPES: tuple[str, ...] = ("IQ1_S", "IQ1_M", "IQ2_XXS", "IQ2_XS", "IQ2_S", "Q2_K", "IQ3_XXS", "Q3_K", "IQ3_S",
+                              "IQ4_XS", "Q4_K", "Q5_K", "Q6_K", "Q8_0")
 
 # Quality ladder, coarsest to finest (reference ladder plus Q2_K/Q3_K at their
 # bytes-per-weight positions).

@@ -218,7 +218,12 @@ _ENCODERS = {
 
 
 def rtn_quantize_tensor(weight: torch.Tensor, quant_type: str, chunk_rows: int | None = None) -> torch.Tensor:
-    """[out, in] float weights -> uint8 [nblocks, block_bytes] (non-ggml RTN)."""
+    """[out, in] float weights -> uint8 [nblocks, block_bytes] (non-ggml RTN;
+    the IQ formats go to :func:`voodoo_quant.iq_encode.iq_quantize_tensor`)."""
+    if quant_type.startswith("IQ"):
+        from voodoo_quant.iq_encode import iq_quantize_tensor
+
+        return iq_quantize_tensor(weight, quant_type, chunk_rows)
     if quant_type not in _ENCODERS:
         raise ValueError(f"the RTN encoder covers {sorted(_ENCODERS)}, not {quant_type}")
     bs, bb = BLOCK[quant_type]
