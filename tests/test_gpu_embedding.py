@@ -198,6 +198,14 @@ def test_routed_embedding_rows(hip):
     assert torch.allclose(probs.grad.cpu(), gp_ref, rtol=1e-5, atol=1e-5)
 
 
+def _oracle_candidates(mod, ncols):
+    """The module's candidates decoded by the oracle from its packed bytes
+    (fp32 [out, ncols]), not by the kernels under test."""
+    rows, dp = mod.out_features if hasattr(mod, "out_features") else mod.num_embeddings, mod.padded_in_features
+    return [torch.from_numpy(cdequant.oracle_dequant(qt, getattr(mod, f"_qweight_{k}").cpu().numpy(), rows * dp))
+            .reshape(rows, dp)[:, :ncols] for k, qt in enumerate(mod.candidate_types)]
+
+
 def test_module_toggle_embedding(hip):
     """Port of tests/test_ptqr.py:121-186, embedding part (menu IQ2_XXS/IQ3_XXS/Q8_0),
     plus the gate gradient through the softmax and the toggled-off mixture."""
@@ -208,7 +216,7 @@ def test_module_toggle_embedding(hip):
                                      source_weight=torch.randn(64, in_f, dtype=torch.float32),
                                      tensor_name="tests.ptqr.embedding").cuda()
     ids = torch.randint(0, 64, (6,)).cuda()
-    cands = [getattr(emb, f"_w_{k}")[:, :in_f] for k in range(len(qts))]
+    cands = [c.cuda() for c in _oracle_candidates(emb, in_f)]
     layers.set_ptqr(True)
     try:
         ey = emb(ids)

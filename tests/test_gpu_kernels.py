@@ -270,6 +270,14 @@ def test_gate_gradient_deterministic(hip):
                            if v.dtype != torch.float32 else v)
 
 
+def _oracle_candidates(mod, ncols):
+    """The module's candidates decoded by the oracle from its packed bytes
+    (fp32 [out, ncols]), not by the kernels under test."""
+    rows, dp = mod.out_features if hasattr(mod, "out_features") else mod.num_embeddings, mod.padded_in_features
+    return [torch.from_numpy(cdequant.oracle_dequant(qt, getattr(mod, f"_qweight_{k}").cpu().numpy(), rows * dp))
+            .reshape(rows, dp)[:, :ncols] for k, qt in enumerate(mod.candidate_types)]
+
+
 def test_module_gates_grad_matches_softmax_jacobian(hip):
     """Port of tests/test_ptqr.py:161-186 (soft mixture) onto the HIP module."""
     from voodoo_quant.layers import MixedQuantLinear
@@ -287,7 +295,7 @@ def test_module_gates_grad_matches_softmax_jacobian(hip):
     y = lin(x)
     G = torch.randn_like(y)
     y.backward(G)
-    cands = [getattr(lin, f"_w_{k}").double().cpu() for k in range(3)]
+    cands = [c.double() for c in _oracle_candidates(lin, in_f)]
     xf, Gf = x.double().cpu(), G.double().cpu()
     gp = torch.stack([(Gf * (xf @ c.t())).sum() for c in cands])
     p = lin.soft_probs().detach().double().cpu()

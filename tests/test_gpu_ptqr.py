@@ -119,6 +119,14 @@ def test_routed_linear_forward_and_backward(hip, m, n, d, d_pad, types, mode):
     assert _rel(xd.grad.cpu(), dx_ref) < TOL
 
 
+def _oracle_candidates(mod, ncols):
+    """The module's candidates decoded by the oracle from its packed bytes
+    (fp32 [out, ncols]), not by the kernels under test."""
+    rows, dp = mod.out_features if hasattr(mod, "out_features") else mod.num_embeddings, mod.padded_in_features
+    return [torch.from_numpy(cdequant.oracle_dequant(qt, getattr(mod, f"_qweight_{k}").cpu().numpy(), rows * dp))
+            .reshape(rows, dp)[:, :ncols] for k, qt in enumerate(mod.candidate_types)]
+
+
 def test_module_toggle(hip):
     """Port of tests/test_ptqr.py:121-186 (linear part) on the HIP module, with its menu."""
     types = ["IQ2_XXS", "IQ3_XXS", "Q8_0"]
@@ -127,7 +135,7 @@ def test_module_toggle(hip):
     lin = layers.MixedQuantLinear(in_f, out_f, types, torch.randn(out_f, in_f, generator=g) * 0.02,
                                   tensor_name="tests.ptqr.linear").cuda()
     x = torch.randn(16, in_f, generator=g).to(torch.bfloat16).cuda()
-    cands = [getattr(lin, f"_w_{k}")[:, :in_f].float() for k in range(len(types))]
+    cands = [c.cuda() for c in _oracle_candidates(lin, in_f)]
     outs = [x.float() @ c.t() for c in cands]
     layers.set_ptqr(True)
     try:

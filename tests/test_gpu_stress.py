@@ -1,7 +1,9 @@
 """The wide-menu stress configuration at a size the oracle's CPU run covers:
 a stack of 2 SwiGLU blocks (hidden 512, MLP 1024), every gate/up/down gated
-over K = 8 candidates with repeated formats (Q2_K, Q3_K, Q4_K, Q4_K, Q5_K,
-Q6_K, Q6_K, Q8_0), temperature annealed 2.0 -> 0.1 over 200 steps.
+over K = 8 candidates, temperature annealed 2.0 -> 0.1 over 200 steps.  Two
+menus: repeated K-quants (Q2_K, Q3_K, Q4_K, Q4_K, Q5_K, Q6_K, Q6_K, Q8_0) and
+eight distinct formats, four of them IQ (IQ1_S, IQ2_XXS, Q2_K, IQ3_S, IQ4_XS,
+Q5_K, Q6_K, Q8_0).
 
 The HIP side is the product's stress harness (``training.step.StackTrainer``:
 stacked gate/up projections, the fused add + RMSNorm and SwiGLU kernels, the
@@ -30,6 +32,8 @@ from oracle import cdequant, mixture
 from voodoo_quant import ggml, rtn
 
 TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q4_K", "Q5_K", "Q6_K", "Q6_K", "Q8_0"]
+# eight distinct formats from 1.56 to 8.5 bits per weight, four of them IQ
+IQ_TYPES = ["IQ1_S", "IQ2_XXS", "Q2_K", "IQ3_S", "IQ4_XS", "Q5_K", "Q6_K", "Q8_0"]
 BLOCKS, HIDDEN, MLP = 2, 512, 1024
 TOKENS = 256
 STEPS, T0, T1 = 200, 2.0, 0.1
@@ -41,7 +45,7 @@ STDS = (0.01, 0.05)
 SHAPES = {"mlp.gate_proj": (MLP, HIDDEN), "mlp.up_proj": (MLP, HIDDEN), "mlp.down_proj": (HIDDEN, MLP)}
 
 
-def _problem(seed=0, stds=STDS):
+def _problem(seed=0, stds=STDS, types=TYPES):
     """{tensor name: (candidate bytes [K] (uint8, CPU), teacher Q8_0 bytes, (o, i))} and the input."""
     g = torch.Generator().manual_seed(seed)
     tensors = {}
@@ -50,7 +54,7 @@ def _problem(seed=0, stds=STDS):
             w = torch.randn(o, i, generator=g) * stds[b]
             seen = set()
             qbs = []
-            for qt in TYPES:
+            for qt in types:
                 src = w if qt not in seen else w + torch.randn(o, i, generator=g) * (0.3 * stds[b])
                 seen.add(qt)
                 qbs.append(rtn.rtn_quantize_tensor(src, qt).reshape(-1))
@@ -63,13 +67,13 @@ def _decode(qt, qb, o, i):
     return torch.from_numpy(cdequant.oracle_dequant(qt, qb.numpy(), o * i).reshape(o, i))
 
 
-def _reference_run(tensors, x, steps=STEPS, with_mse=True):
+def _reference_run(tensors, x, steps=STEPS, with_mse=True, types=TYPES):
     """The reference's step on the CPU in bf16; returns {name: final gates}."""
-    cands = {nm: [_decode(qt, qb, *shape) for qt, qb in zip(TYPES, qbs)] for nm, (qbs, _, shape) in tensors.items()}
+    cands = {nm: [_decode(qt, qb, *shape) for qt, qb in zip(types, qbs)] for nm, (qbs, _, shape) in tensors.items()}
     teach = {nm: _decode("Q8_0", tq, *shape).to(torch.bfloat16) for nm, (_, tq, shape) in tensors.items()}
     norm = torch.ones(HIDDEN, dtype=torch.bfloat16)
-    gates = {nm: torch.zeros(len(TYPES), requires_grad=True) for nm in tensors}
-    bpw = [ggml.bytes_per_weight(qt) for qt in TYPES]
+    gates = {nm: torch.zeros(len(types), requires_grad=True) for nm in tensors}
+    bpw = [ggml.bytes_per_weight(qt) for qt in types]
     n_weights = sum(o * i for _, _, (o, i) in tensors.values())
     target = TARGET_FRAC * n_weights  # of one byte per weight
     opt, sched = mixture.make_gate_optimizer(list(gates.values()), LR, steps)
@@ -105,7 +109,7 @@ def _reference_run(tensors, x, steps=STEPS, with_mse=True):
     return {nm: g.detach() for nm, g in gates.items()}
 
 
-def _hip_run(tensors, x, steps=STEPS):
+def _hip_run(tensors, x, steps=STEPS, types=TYPES):
     from voodoo_quant import layers
     from voodoo_quant.training import step as st
     from voodoo_quant.training.q8_teacher import Q8Linear
@@ -118,7 +122,7 @@ def _hip_run(tensors, x, steps=STEPS):
         for n, (o, i) in SHAPES.items():
             nm = f"blocks.{b}.{n}"
             qbs, tq, _ = tensors[nm]
-            lin[n] = layers.MixedQuantLinear.from_packed(i, o, TYPES, [q.to(dev) for q in qbs], tensor_name=nm,
+            lin[n] = layers.MixedQuantLinear.from_packed(i, o, types, [q.to(dev) for q in qbs], tensor_name=nm,
                                                          device=dev)
             replaced[nm] = lin[n]
             tlin[n] = Q8Linear(tq.to(dev), o, i)
@@ -139,42 +143,43 @@ def _hip_run(tensors, x, steps=STEPS):
 
 
 @pytest.mark.gpu
-def test_stress_stack_k8_argmax_matches_reference():
+@pytest.mark.parametrize("types", [TYPES, IQ_TYPES], ids=["repeated-k-quants", "iq-menu"])
+def test_stress_stack_k8_argmax_matches_reference(types):
     if not torch.cuda.is_available():
         pytest.skip("no ROCm device")
-    tensors, x = _problem()
-    print("[stress] reference run on the CPU", flush=True)
-    ref = _reference_run(tensors, x)
+    tensors, x = _problem(types=types)
+    print(f"[stress] {types}: reference run on the CPU", flush=True)
+    ref = _reference_run(tensors, x, types=types)
     print("[stress] HIP run", flush=True)
-    got = _hip_run(tensors, x)
+    got = _hip_run(tensors, x, types=types)
     worst = 0.0
     for nm in tensors:
         r, g = ref[nm], got[nm]
         d = float((r - g).abs().max())
         worst = max(worst, d)
-        print(f"{nm}: reference {TYPES[int(r.argmax())]}#{int(r.argmax())} {r.numpy().round(3)}  "
-              f"hip {TYPES[int(g.argmax())]}#{int(g.argmax())} {g.numpy().round(3)}  max|diff| {d:.2e}", flush=True)
+        print(f"{nm}: reference {types[int(r.argmax())]}#{int(r.argmax())} {r.numpy().round(3)}  "
+              f"hip {types[int(g.argmax())]}#{int(g.argmax())} {g.numpy().round(3)}  max|diff| {d:.2e}", flush=True)
     for nm in tensors:
         assert int(ref[nm].argmax()) == int(got[nm].argmax()), nm
     print(f"[stress] gates agree to {worst:.2e}", flush=True)
     assert worst < GATE_TOL
     # not degenerate: more than one winner, and the loss's GEMM gradients decide
     assert len({int(r.argmax()) for r in ref.values()}) >= 2
-    ctrl = _reference_run(tensors, x, with_mse=False)
+    ctrl = _reference_run(tensors, x, with_mse=False, types=types)
     assert any(int(ref[nm].argmax()) != int(ctrl[nm].argmax()) for nm in tensors)
 
 
 # largest gate difference accepted (gate logits are O(1)); measured on MI355X:
-# 4.1e-4 after the 200 steps
+# 4.1e-4 (repeated K-quants) and 8.8e-4 (IQ menu) after the 200 steps
 GATE_TOL = 2e-3
 
 
-def reference_margins():
+def reference_margins(types=TYPES, with_mse=True):
     """CPU-only helper: the reference run's winners and their logit margins."""
-    tensors, x = _problem()
-    ref = _reference_run(tensors, x)
+    tensors, x = _problem(types=types)
+    ref = _reference_run(tensors, x, with_mse=with_mse, types=types)
     out = []
     for nm, r in ref.items():
         s = r.sort(descending=True).values
-        out.append((nm, TYPES[int(r.argmax())], int(r.argmax()), float(s[0] - s[1]), r.numpy().round(3)))
+        out.append((nm, types[int(r.argmax())], int(r.argmax()), float(s[0] - s[1]), r.numpy().round(3)))
     return out
