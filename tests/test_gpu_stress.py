@@ -111,9 +111,21 @@ def _reference_run(tensors, x, steps=STEPS, with_mse=True, types=TYPES):
 
 def _hip_run(tensors, x, steps=STEPS, types=TYPES):
     from voodoo_quant import layers
+    from voodoo_quant.training import q8_teacher
     from voodoo_quant.training import step as st
     from voodoo_quant.training.q8_teacher import Q8Linear
 
+    # the teacher as the product's stack builder runs it (decodes kept, gate/up
+    # as one stacked GEMM), whatever an earlier caller left the switch at
+    keep = q8_teacher._KEEP_DECODED
+    q8_teacher.set_keep_decoded(True)
+    try:
+        return _hip_run_body(tensors, x, steps, types, layers, st, Q8Linear)
+    finally:
+        q8_teacher.set_keep_decoded(keep)
+
+
+def _hip_run_body(tensors, x, steps, types, layers, st, Q8Linear):
     dev = torch.device("cuda", 0)
     cfg = st.StackConfig(blocks=BLOCKS, hidden=HIDDEN, mlp=MLP, eps=EPS)
     replaced, s_blocks, t_blocks = {}, [], []
@@ -169,9 +181,12 @@ def test_stress_stack_k8_argmax_matches_reference(types):
     assert any(int(ref[nm].argmax()) != int(ctrl[nm].argmax()) for nm in tensors)
 
 
-# largest gate difference accepted (gate logits are O(1)); measured on MI355X:
-# 4.1e-4 (repeated K-quants) and 8.8e-4 (IQ menu) after the 200 steps
-GATE_TOL = 2e-3
+# largest gate difference accepted (gate logits are O(1), the winners' margins
+# 0.07-0.3); measured on MI355X after the 200 steps: 6.5e-4 (repeated
+# K-quants) and 2.1e-3 (IQ menu, whose winners sit closer together).  The
+# teacher's GEMM order alone moves the IQ menu's figure between 8.8e-4 (one
+# GEMM per projection) and 2.1e-3 (gate/up stacked).
+GATE_TOL = 3e-3
 
 
 def reference_margins(types=TYPES, with_mse=True):

@@ -12,7 +12,7 @@
 // for every format), then each thread decodes runs of 8 weights from LDS and
 // writes them with 16-byte (bf16 x8) or 2x16-byte (fp32 x8) stores.
 #include <mutex>
-#include <unordered_set>
+#include <unordered_map>
 
 #include "vq_internal.h"
 
@@ -21,15 +21,17 @@ namespace vq {
 hipError_t allow_dynamic_lds(const void* kern, size_t lds) {
     if (lds <= 64 * 1024) return hipSuccess;
     static std::mutex mu;
-    static std::unordered_set<const void*> done;
+    static std::unordered_map<const void*, size_t> granted;  // largest size set per kernel
     std::lock_guard<std::mutex> lock(mu);
-    if (done.count(kern)) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    auto it = granted.find(kern);
+    if (it != granted.end() && it->second >= lds) return hipSuccess;
+    // exactly the size asked for: the kernel's static LDS counts against the same 160 KiB
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return e;
     }
-    done.insert(kern);
+    granted[kern] = lds;
     return hipSuccess;
 }
 
@@ -148,6 +150,10 @@ struct MixPlan {
     bf16_t* out[kMaxSets];
     int64_t ngroups[kMaxSets];
     int64_t block0[kMaxSets + 1];  // first workgroup of each set
+    // per set and candidate: bytes per group, and where the candidate's
+    // staged groups start in LDS (filled on the host)
+    int gbytes[kMaxSets][kMaxCand];
+    int lds_off[kMaxSets][kMaxCand];
 };
 
 constexpr int kMixRun = 16;                                     // weights per thread and run
@@ -166,16 +172,17 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
     const CandSet& cs = mp.sets[si];
     const int64_t g0 = ((int64_t)blockIdx.x - mp.block0[si]) * GPB;
     const int ng = (int)min<int64_t>(GPB, mp.ngroups[si] - g0);
-    int acc = 0;
     for (int k = 0; k < cs.ncand; ++k) {
-        const int gb = group_bytes(cs.qtype[k]);
-        stage_bytes(lds + acc, cs.qbytes[k] + g0 * gb, ng * gb);
-        acc += (GPB * gb + 15) & ~15;
+        const int gb = mp.gbytes[si][k];
+        stage_bytes(lds + mp.lds_off[si][k], cs.qbytes[k] + g0 * gb, ng * gb);
     }
+    // the probabilities, read once per workgroup (one short LDS read per
+    // candidate and run instead of a global load in the loop)
+    __shared__ float sp[kMaxCand];
+    if ((int)threadIdx.x < cs.ncand) sp[threadIdx.x] = mp.probs[si][threadIdx.x];
     stage_wait();
     __syncthreads();
     const int t = threadIdx.x;
-    const float* probs = mp.probs[si];
     bf16_t* w_eff = mp.out[si];
     const int p = kMixRun * (t & 15);
 #pragma unroll
@@ -185,12 +192,10 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
         float mixed[kMixRun];
 #pragma unroll
         for (int r = 0; r < kMixRun; ++r) mixed[r] = 0.0f;
-        int off = 0;
         for (int k = 0; k < cs.ncand; ++k) {
             const int qt = cs.qtype[k];
-            const int gb = group_bytes(qt);
             float w[kMixRun];
-            const uint8_t* g = lds + off + j * gb;
+            const uint8_t* g = lds + mp.lds_off[si][k] + j * mp.gbytes[si][k];
             switch (qt) {
             case Q8_0: decode_mix<Q8_0, kMixRun>(g, p, w); break;
             case Q2_K: decode_mix<Q2_K, kMixRun>(g, p, w); break;
@@ -205,8 +210,7 @@ __global__ __launch_bounds__(kStreamThreads) void mix_kernel(MixPlan mp) {
                     decode_mix<Q6_K, kMixRun>(g, p, w);
                 break;
             }
-            off += (GPB * gb + 15) & ~15;
-            const float pk = probs[k];
+            const float pk = sp[k];
             {
                 // product and sum rounded separately, like the two torch ops
 #pragma clang fp contract(off)
@@ -246,7 +250,11 @@ hipError_t launch_mix_sets(int nsets, const CandSet* sets, const float* const* p
         mp.block0[i] = blocks;
         blocks += (ngroups[i] + gpb - 1) / gpb;
         size_t l = 0;
-        for (int k = 0; k < sets[i].ncand; ++k) l += (gpb * group_bytes(sets[i].qtype[k]) + 15) & ~15;
+        for (int k = 0; k < sets[i].ncand; ++k) {
+            mp.gbytes[i][k] = group_bytes(sets[i].qtype[k]);
+            mp.lds_off[i][k] = (int)l;
+            l += (gpb * mp.gbytes[i][k] + 15) & ~15;
+        }
         lds = l > lds ? l : lds;
     }
     mp.block0[nsets] = blocks;

@@ -135,10 +135,12 @@ __global__ __launch_bounds__(kStreamThreads) void embed_rows_kernel(CandSet cs, 
                                                                     OUT* __restrict__ out) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ int sbase[kMaxCand];
+    __shared__ float sp[kMaxCand];  // the probabilities, read once per workgroup
     const RowSeg rs = row_segment(nseg, seg, gused);
     const int64_t id = ids[rs.r];
     bool valid = id >= 0 && id < vocab;
     int k0 = 0, k1 = cs.ncand;
+    if (!ROUTED && (int)threadIdx.x < cs.ncand) sp[threadIdx.x] = probs[threadIdx.x];
     if constexpr (ROUTED) {
         const int64_t kr = routing[rs.r];
         valid = valid && kr >= 0 && kr < cs.ncand;
@@ -177,7 +179,7 @@ __global__ __launch_bounds__(kStreamThreads) void embed_rows_kernel(CandSet cs, 
                     const int qt = cs.qtype[k];
                     float w[8];
                     decode8_mix_rt(qt, lds + sbase[k] + j * group_bytes(qt), p, w);
-                    const float pk = probs[k];
+                    const float pk = sp[k];
                     {
                         // product and sum rounded separately, as in the mix kernel
 #pragma clang fp contract(off)

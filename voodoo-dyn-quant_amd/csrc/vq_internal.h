@@ -16,7 +16,7 @@ constexpr int kRunsPerThread = 2;
 constexpr int kGroupsPerBlock = kStreamThreads * 8 * kRunsPerThread / 256;  // 16
 
 // Lets `kern` take `lds` bytes of dynamic LDS: above 64 KiB a kernel needs
-// the opt-in attribute (set once per kernel, process-wide).
+// the opt-in attribute (raised per kernel as larger sizes are asked for).
 hipError_t allow_dynamic_lds(const void* kern, size_t lds);
 
 hipError_t launch_dequant(int qtype, const uint8_t* q, float* out, int64_t ngroups, hipStream_t s);
