@@ -5,10 +5,11 @@ the embedding gated, a Q8_0 teacher).
   whose gated layers are the reference's formulation in torch: W_eff = fp32
   k-ordered mixture of the oracle's decoded candidates, cast to bf16, then
   F.linear / F.embedding with autograd through softmax(gates / T)
-  (``layers.py:336-363, 1729-1731, 1842``), on the CE + KL loss.  Bar: 3e-2
-  relative L2 over all gate gradients (the Linear-level bar is 1e-2; bf16
-  activations through two layers add their rounding) and every tensor's
-  gradient within 25 degrees of the reference's.
+  (``layers.py:336-363, 1729-1731, 1842``), on the CE + KL loss.  Bar: 1.5e-2
+  relative L2 over all gate gradients (measured on MI355X: 9.7e-3; the
+  Linear-level bar is 1e-2, and bf16 activations through two layers and
+  torch's attention add their rounding) and every tensor's gradient within
+  25 degrees of the reference's.
 * The chunked loss path reproduces the full-logits path's gradients.
 * Several optimizer steps stay finite and move the gates.
 """
@@ -110,7 +111,7 @@ def test_step_gate_gradients_match_reference_formulation(models):
     exp = torch.cat([mapping[n].gates.grad for n in mapping]).double()
     rel = float((got - exp).norm() / exp.norm())
     print(f"gate-gradient relative L2 {rel:.2e} over {len(mapping)} tensors", flush=True)
-    assert rel < 3e-2
+    assert rel < 1.5e-2
     # per tensor: every gradient points the same way
     for n in mapping:
         a, b = replaced[n].gates.grad.double(), mapping[n].gates.grad.double()
