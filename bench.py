@@ -392,15 +392,15 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
 
 def stack_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False) -> dict:
     """The long-context, wide-menu stress configuration: 8 SwiGLU blocks at
-    hidden 4096, MLP 14336 (MLP-only blocks), K = 8 candidates per tensor
-    (the six formats, Q4_K and Q6_K twice with their own bytes), 2 x 8192
-    tokens, temperature annealed 2.0 -> 0.1 over 200 steps; tokens per second
-    of the whole step (student, Q8_0 teacher, MSE + size loss, backward,
-    optimizer)."""
+    hidden 4096, MLP 14336 (MLP-only blocks), K = 8 distinct formats per
+    tensor (the six K-quant and Q8_0 formats plus IQ2_XXS and IQ3_S, two of the
+    reference's 27B recipe types), 2 x 8192 tokens, temperature annealed
+    2.0 -> 0.1 over 200 steps; tokens per second of the whole step (student,
+    Q8_0 teacher, MSE + size loss, backward, optimizer)."""
     from voodoo_quant.training import step as st
 
     cfg = st.StackConfig()
-    types = ["Q2_K", "Q3_K", "Q4_K", "Q4_K", "Q5_K", "Q6_K", "Q6_K", "Q8_0"]
+    types = ["Q2_K", "IQ2_XXS", "Q3_K", "IQ3_S", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
     student, teacher, replaced = st.build_stack(cfg, types, dev, seed=1)
     tokens = 2 * 8192
     g = torch.Generator(device=dev).manual_seed(6)
@@ -421,7 +421,8 @@ def stack_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
            "warmup": warmup, "model_TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
            "loss": {k: round(float(v), 5) for k, v in out.items()},
            "workload": "8 SwiGLU blocks (MLP-only) at hidden 4096, MLP 14336: 24 gated tensors, 1.409e9 weights, "
-                       "K=8 (Q2_K, Q3_K, Q4_K x2, Q5_K, Q6_K x2, Q8_0); 2 x 8192 tokens; T 2.0 -> 0.1 over 200 steps; "
+                       "K=8 (Q2_K, IQ2_XXS, Q3_K, IQ3_S, Q4_K, Q5_K, Q6_K, Q8_0); 2 x 8192 tokens; "
+                       "T 2.0 -> 0.1 over 200 steps; "
                        "relative MSE to a Q8_0 teacher + dead-zone size loss at 45% of 8-bit",
            "candidate_bytes": "random valid GGUF blocks, scales sized for N(0, 0.02)-like weights"}
     log(f"stack: {ms:.1f} ms/step -> {rec['tokens_per_s']:.0f} tokens/s ({rec['model_TFLOPs']} model TFLOP/s)")

@@ -334,8 +334,14 @@ class _TiedHead(nn.Module):
 # from [base, 2 base)), chosen so that decoded weights stay within about
 # +-0.2 (standard deviations 0.02-0.06).
 _SYNTH_SCALE_BASE = {"Q8_0": 2.0 ** -11, "Q6_K": 2.0 ** -16, "Q5_K": 2.0 ** -15, "Q4_K": 2.0 ** -14,
-                     "Q3_K": 2.0 ** -11, "Q2_K": 2.0 ** -9}
-_F16_FIELDS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,)}
+                     "Q3_K": 2.0 ** -11, "Q2_K": 2.0 ** -9, "IQ1_S": 2.0 ** -8, "IQ1_M": 2.0 ** -8,
+                     "IQ2_XXS": 2.0 ** -11, "IQ2_XS": 2.0 ** -11, "IQ2_S": 2.0 ** -11, "IQ3_XXS": 2.0 ** -13,
+                     "IQ3_S": 2.0 ** -13, "IQ4_XS": 2.0 ** -16}
+# fp16 scale fields; IQ1_M has none (its scale is spread over the top nibbles
+# of bytes 49, 51, 53 and 55)
+_F16_FIELDS = {"Q8_0": (0,), "Q2_K": (80, 82), "Q3_K": (108,), "Q4_K": (0, 2), "Q5_K": (0, 2), "Q6_K": (208,),
+               "IQ1_S": (0,), "IQ1_M": (None,), "IQ2_XXS": (0,), "IQ2_XS": (0,), "IQ2_S": (0,), "IQ3_XXS": (0,),
+               "IQ3_S": (0,), "IQ4_XS": (0,)}
 # dmin / d of the formats with mins: the mean code, so weights centre on 0
 _SYNTH_MIN_RATIO = {"Q2_K": 1.5, "Q4_K": 7.5, "Q5_K": 15.5}
 
@@ -353,6 +359,11 @@ def synthetic_candidate_bytes(qt: str, rows: int, cols: int, device, gen: torch.
         base = _SYNTH_SCALE_BASE[qt] * (_SYNTH_MIN_RATIO[qt] if i == 1 else 1.0)
         d = base * (1.0 + torch.rand(nblocks, device=device, generator=gen))
         h = d.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+        if off is None:
+            for t in range(4):
+                b = q[:, 49 + 2 * t].to(torch.int32)
+                q[:, 49 + 2 * t] = ((b & 0x0F) | (((h >> (4 * t)) & 0xF) << 4)).to(torch.uint8)
+            continue
         q[:, off] = (h & 0xFF).to(torch.uint8)
         q[:, off + 1] = (h >> 8).to(torch.uint8)
     return q.reshape(-1)
