@@ -225,7 +225,9 @@ CASES = [
     # partial at the edges)
     ("large-ragged", ["Q3_K", "Q6_K", "Q8_0"], 4000, 3080, 520, 768),
     # 336 forward tiles: one full round and a K-split tail (the split refill
-    # path with partial k ranges and the fixup); dX and the gate split too
+    # path with partial k ranges and the fixup); dX splits too (16 tiles per
+    # XCD, 2 parts), the gate's 21 tiles per XCD run whole (its 3-way splits
+    # run in tests/test_gpu_headline.py at 8192 x 5120 -> 17408)
     ("split-tails", ["Q4_K", "Q6_K"], 4096, 5376, 2048, 2048),
 ]
 
