@@ -247,3 +247,54 @@ def test_gate_gradient_candidate_past_2gib(hip):
     # the rows past the boundary carry far more than the bar: losing them fails it
     assert float(ref_past.norm()) > 100 * 1e-4 * float(ref.norm())
     assert err < 1e-4
+
+
+def test_vocab_head_module_matches_oracle(hip):
+    """A vocabulary-scale gated head (151936 x 1024, 155.6M weights per
+    candidate, K = 6 including two IQ formats) through MixedQuantLinear and
+    autograd, 512 tokens.  The reference routes heads of 64M+ elements to
+    _BlockedCandidateLinear (layers.py:1560-1637), Y = sum_k p_k X W_k^T in
+    row blocks; here the same mixture goes through the one fused path.  Y on
+    sampled rows and dX against fp64 of the oracle's W_eff; gates.grad against
+    the softmax Jacobian of <dY^T X, W_k> evaluated on the device in fp32 over
+    the oracle's decodes (layers.py:354-363)."""
+    from voodoo_quant import layers
+
+    dev = torch.device("cuda", 0)
+    n, d, m = 151936, 1024, 512
+    types = ["Q8_0", "Q6_K", "Q4_K", "IQ4_XS", "Q2_K", "IQ2_XXS"]
+    rng = np.random.default_rng(77)
+    qbs, cands = [], []
+    for qt in types:
+        per = 8 if qt == "Q8_0" else 1
+        qb = blocks.random_blocks(qt, n * d // 256 * per, rng)
+        for which in range(len(blocks.F16_OFFSETS[qt]) or 1):  # scales in [2^-8, 2^-5)
+            blocks.set_scale(qt, qb, (0x1C00 + rng.integers(0, 0x0C00, size=qb.shape[0])).astype(np.uint16), which)
+        qbs.append(torch.from_numpy(qb.reshape(-1)))
+        cands.append(torch.from_numpy(cdequant.oracle_dequant_parallel(qt, qb, n * d)).reshape(n, d))
+    lin = layers.MixedQuantLinear.from_packed(d, n, types, [q.to(dev) for q in qbs], tensor_name="tests.vocab_head",
+                                              device=dev)
+    with torch.no_grad():
+        lin.gates.copy_(torch.tensor([0.4, -0.1, 0.3, 0.0, -0.3, 0.2]))
+    lin.set_temperature(0.8)
+    g = torch.Generator().manual_seed(78)
+    x = torch.randn(m, d, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+    y = lin(x)
+    G = torch.randn(m, n, generator=g).to(torch.bfloat16).to(dev)
+    y.backward(G)
+    torch.cuda.synchronize()
+    p = lin.soft_probs().detach().cpu()
+    w_eff = mixture.mix_weight(cands, p).to(torch.bfloat16)  # the reference's fp32 mixture, source dtype
+    rows = torch.from_numpy(np.sort(rng.choice(m, size=64, replace=False)))
+    y_ref = x.detach().cpu()[rows].double() @ w_eff.double().t()
+    e_y = mixture.relative_l2(y.detach().cpu()[rows].double(), y_ref)
+    wd = w_eff.to(dev)
+    e_dx = mixture.relative_l2(x.grad.double(), G.double() @ wd.double())
+    # <dY^T X, W_k>: dW once in fp32 on the device, then one dot per oracle decode
+    dw = G.float().t() @ x.detach().float()  # [n, d]
+    gp = torch.stack([(dw * c.to(dev)).sum(dtype=torch.float64) for c in cands]).cpu()
+    pd = p.double()
+    ref = (torch.diag(pd) - torch.outer(pd, pd)) @ gp / 0.8
+    e_g = mixture.relative_l2(lin.gates.grad.double().cpu(), ref)
+    _say(f"[vocab-head] Y {e_y:.2e} dX {e_dx:.2e} gates.grad {e_g:.2e}")
+    assert e_y < TOL and e_dx < TOL and e_g < TOL
