@@ -28,6 +28,9 @@ Also reported in the same JSON line:
                 K = 4) on the host (median of 5) and on the GPU, and the C
                 dequant restatement per format, single- and multi-threaded
   host          nproc, the CPU model and sockets of the box
+  shapes        mix, forward GEMM and backward launch times of the 27B-class
+                layer's four products (q, o, gate/up, down) and the 0.8B-class
+                decoder's four stacked products, 8192 tokens, K = 6
   fused         the few-token products with W_eff built in LDS (never in
                 memory) against mix + GEMM, forward + dX, at 1-64 tokens on
                 three tensor sizes: the measured crossover behind the module's
@@ -35,7 +38,7 @@ Also reported in the same JSON line:
 
   python bench.py --fused-workload runs only that comparison's kernels at 16
   tokens (three passes each), the workload the rocprof HBM-traffic summary of
-  the fused kernels is taken on.
+  the fused kernels is taken on; --shapes-workload runs only the shape sweep.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 """
@@ -291,6 +294,50 @@ def fused_compare(torch, dev, gen, tokens=(1, 16, 32, 64), reps: int = 20, passe
     return out
 
 
+# Gated Linears timed by shape_sweep, M = 8192 tokens, K = 6 (Q2_K..Q8_0):
+# the 27B-class layer's four products (hidden 5120, q/o 5120 x 6144, gate/up
+# 5120 -> 17408, down 17408 -> 5120) and the 0.8B-class decoder's four stacked
+# products (hidden 1024: q/k/v 1024 -> 1536, o 1024 -> 1024, gate/up
+# 1024 -> 6144, down 3072 -> 1024), as (name, in_features, out_features).
+SWEEP_SHAPES = [("27b_q", 5120, 6144), ("27b_o", 6144, 5120), ("27b_gate_up", 5120, 17408),
+                ("27b_down", 17408, 5120), ("0p8b_qkv", 1024, 1536), ("0p8b_o", 1024, 1024),
+                ("0p8b_gate_up", 1024, 6144), ("0p8b_down", 3072, 1024)]
+
+
+def shape_sweep(torch, dev, gen, m: int = 8192, reps: int = 5) -> dict:
+    """Per shape: the mix, the forward GEMM (forward minus mix) and the
+    backward launch (dX + gate products, plus the gate reduce), HIP events on
+    the stream the C ABI uses, with their TFLOP/s (2 m n d per product)."""
+    from voodoo_quant import _hip
+
+    ids = [GGML[t] for t in TYPES]
+    res = {}
+    for name, d, n in SWEEP_SHAPES:
+        qbytes = [synthetic_qbytes(torch, qt, n, d, dev, gen) for qt in TYPES]
+        x = torch.randn(m, d, device=dev, generator=gen).to(torch.bfloat16)
+        dy = torch.randn(m, n, device=dev, generator=gen).to(torch.bfloat16)
+        probs = torch.softmax(torch.randn(len(TYPES), device=dev, generator=gen), 0)
+        w_eff = torch.empty(n, d, dtype=torch.bfloat16, device=dev)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+        dx = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+        dp = torch.empty(len(TYPES), dtype=torch.float32, device=dev)
+        ws = torch.empty(_hip.bwd_workspace_bytes(m, n, d, d, len(TYPES), False), dtype=torch.uint8, device=dev)
+        fws = torch.empty(max(_hip.fwd_workspace_bytes(m, n, d), 256), dtype=torch.uint8, device=dev)
+        t_mix = time_events(torch, lambda: _hip.mix_weight(ids, qbytes, probs, n, d, w_eff), reps)
+        t_fwd = time_events(torch, lambda: _hip.gated_linear_fwd(x, ids, qbytes, probs, n, d, w_eff, y, fws), reps)
+        t_bwd = time_events(torch, lambda: _hip.gated_linear_bwd(dy, x, ids, qbytes, probs, n, d, w_eff, dx, dp, ws),
+                            reps)
+        f = 2.0 * m * n * d
+        res[name] = {"in": d, "out": n, "mix_ms": round(t_mix, 4), "fwd_gemm_ms": round(t_fwd - t_mix, 4),
+                     "bwd_dx_gate_ms": round(t_bwd, 4),
+                     "fwd_TFLOPs": round(f / ((t_fwd - t_mix) * 1e-3) / 1e12, 1),
+                     "bwd_TFLOPs": round(2 * f / (t_bwd * 1e-3) / 1e12, 1),
+                     "step_TFLOPs": round(3 * f / ((t_fwd + t_bwd) * 1e-3) / 1e12, 1)}
+        log(f"shape {name} {d}->{n}: mix {t_mix:.3f} ms, fwd gemm {t_fwd - t_mix:.3f} ms, bwd {t_bwd:.3f} ms")
+        del qbytes, x, dy, w_eff, y, dx, ws, fws
+    return res
+
+
 def copy_calibration(torch, dev) -> None:
     """Three elementwise copies of 1 GiB (known bytes: 1 GiB read, 1 GiB
     written each), to scale rocprof's FETCH_SIZE / WRITE_SIZE."""
@@ -449,6 +496,8 @@ def main() -> int:
     ap.add_argument("--no-peaks", action="store_true", help="skip the MFMA / HBM probe kernels")
     ap.add_argument("--fused-workload", action="store_true",
                     help="only run the fused and materialising few-token products (16 tokens, 3 passes each)")
+    ap.add_argument("--shapes-workload", action="store_true",
+                    help="only time the 27B-class and 0.8B-class gated Linear shapes and print their record")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -467,6 +516,10 @@ def main() -> int:
         fused_compare(torch, dev, torch.Generator(device=dev).manual_seed(0), passes=3)
         if args.copy_calibration:
             copy_calibration(torch, dev)
+        return 0
+    if args.shapes_workload:
+        print(json.dumps({"shapes": shape_sweep(torch, dev, torch.Generator(device=dev).manual_seed(0))}),
+              flush=True)
         return 0
     if args.only_train:
         print(json.dumps({"train": train_step_bench(torch, dev, args.train_steps, 2, args.prefetch_mix)}), flush=True)
@@ -597,9 +650,11 @@ def main() -> int:
         del qb
     log("dequant GB/s: " + ", ".join(f"{k} {v['GBps']}" for k, v in dq.items()))
 
+    del qbytes, w_eff, y, dx, ws, fws, out
+    torch.cuda.empty_cache()
+    shapes = shape_sweep(torch, dev, gen)
     train = None
     if not args.no_train:
-        del qbytes, w_eff, y, dx, ws, fws, out
         torch.cuda.empty_cache()
         train = train_step_bench(torch, dev, args.train_steps, 2, args.prefetch_mix)
     stack = None
@@ -649,6 +704,7 @@ def main() -> int:
         "hipblaslt_ms": {k: round(v, 4) for k, v in lib.items()},
         "dequant_gbps": dq,
         "ptqr": ptqr,
+        "shapes": shapes,
         "train": train,
         "stress": stack,
         "cpu_baseline": cpu,

@@ -175,15 +175,42 @@ int check_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64
     return VQ_OK;
 }
 
+// The gate product's share of a backward workspace: its partials (one per
+// gate block, or one per dot block where the product writes fp32 dW parts)
+// and those parts.  With allow_parts the partial area holds either count, so
+// the workspace sizes (which see d but not d_pad) bound every call; the parts
+// run when the shape asks for them and d_pad is d rounded up to 256.  Without
+// allow_parts: the fused epilogue and its partials only.
+struct GateWs {
+    bool parts;
+    int64_t part_bytes;  // 256-aligned partial area
+    int64_t dwp_bytes;   // 256-aligned parts area (0 without allow_parts or parts)
+};
+
+GateWs gate_ws(int64_t m, int64_t d, int64_t d_pad, int nsets, const int64_t* n, int64_t n_total, int nslot,
+               bool allow_parts) {
+    GateWs g{};
+    const int64_t fused = vq::gate_partial_count((int)m, (int)n_total, (int)d);
+    const bool possible = allow_parts && vq::gate_parts((int)m, (int)n_total, (int)d) > 0;
+    const int64_t dot = possible ? vq::gate_dot_blocks(nsets, n, (d + 255) / 256) : 0;
+    g.parts = possible && d_pad == (d + 255) / 256 * 256;
+    g.part_bytes = align256((fused > dot ? fused : dot) * nslot * (int64_t)sizeof(float));
+    g.dwp_bytes = possible ? align256(vq::gate_parts_bytes((int)m, (int)n_total, (int)d)) : 0;
+    return g;
+}
+
 // The backward's launches: an optional re-mix of W_eff into remix_buf, the
 // dX and gate products (one launch when both run), the fixed-order reduce.
-// partials: gate_partial_count * ncand floats; tail_ws: dX's split-tail
-// partial tiles, or NULL to run dX's tiles whole.
+// partials: gw.part_bytes of gate partials; tail_ws: dX's split-tail partial
+// tiles, or NULL to run dX's tiles whole; dwp: the gate's dW parts when
+// gw.parts.
 int run_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
             const vq::CandSet& cs, const float* probs, const uint16_t* w_eff, uint16_t* remix_buf, uint16_t* dx,
-            float* dprobs, float* partials, float* tail_ws, hipStream_t s) {
+            float* dprobs, const GateWs& gw, float* partials, float* tail_ws, float* dwp, hipStream_t s) {
     int rc = VQ_OK;
     const int ncand = cs.ncand;
+    // the parts path when the shape takes it and its buffer is there
+    float* parts = gw.parts ? dwp : nullptr;
     if (dx) {
         const uint16_t* w = w_eff;
         if (remix_buf) {
@@ -194,7 +221,7 @@ int run_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t
         if (m > 0 && dprobs) {
             // both products in one launch: each fills the other's last round
             rc = hip_check(vq::launch_gemm_dx_gate(dy, w, d_pad, dx, x, group_of(cs, n), partials, (int)m, (int)n,
-                                                   (int)d, tail_ws, s),
+                                                   (int)d, tail_ws, parts, s),
                            "dX + gate GEMM launch");
             if (rc != VQ_OK) return rc;
         } else if (m > 0) {
@@ -210,11 +237,13 @@ int run_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t
             return rc == VQ_OK ? ok() : rc;
         }
         if (!dx) {
-            rc = hip_check(vq::launch_gemm_gate(dy, x, group_of(cs, n), partials, (int)m, (int)n, (int)d, s),
+            rc = hip_check(vq::launch_gemm_gate(dy, x, group_of(cs, n), partials, (int)m, (int)n, (int)d, parts, s),
                            "gate GEMM launch");
             if (rc != VQ_OK) return rc;
         }
-        const int64_t nparts = vq::gate_partial_count((int)m, (int)n, (int)d);
+        // partials: one per dot block on the parts path, one per gate block otherwise
+        const int64_t nparts = parts ? vq::gate_dot_blocks(1, &n, d_pad / 256)
+                                     : vq::gate_partial_count((int)m, (int)n, (int)d);
         rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, s), "gate reduce launch");
         if (rc != VQ_OK) return rc;
     }
@@ -604,9 +633,9 @@ int vq_gated_linear_fwd(const uint16_t* x, int64_t m, int64_t n, int64_t d, int6
 
 int64_t vq_gated_linear_bwd_workspace(int64_t m, int64_t n, int64_t d, int64_t d_pad, int ncand, int need_w_eff) {
     if (m < 0 || n <= 0 || d <= 0 || ncand < 1 || m > INT32_MAX || n > INT32_MAX || d > INT32_MAX) return -1;
-    // [gate partials][dX split-tail partial tiles][re-mixed W_eff]
-    int64_t bytes = align256(vq::gate_partial_count((int)m, (int)n, (int)d) * ncand * (int64_t)sizeof(float));
-    bytes += align256(vq::dx_tail_bytes((int)m, (int)n, (int)d));
+    // [gate partials][dX split-tail partial tiles][gate dW parts][re-mixed W_eff]
+    const GateWs gw = gate_ws(m, d, d_pad, 1, &n, n, ncand, true);
+    int64_t bytes = gw.part_bytes + align256(vq::dx_tail_bytes((int)m, (int)n, (int)d)) + gw.dwp_bytes;
     if (need_w_eff) bytes += align256(n * d_pad * 2);
     return bytes;
 }
@@ -619,7 +648,8 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
     if (rc != VQ_OK) return rc;
     const bool remix = dx != nullptr && w_eff == nullptr;
     const int64_t need = vq_gated_linear_bwd_workspace(m, n, d, d_pad, ncand, remix ? 1 : 0);
-    const int64_t part_bytes = align256(vq::gate_partial_count((int)m, (int)n, (int)d) * ncand * (int64_t)sizeof(float));
+    const GateWs gw = gate_ws(m, d, d_pad, 1, &n, n, ncand, true);
+    const int64_t part_bytes = gw.part_bytes;
     if ((dprobs || remix) && (!workspace || ws_bytes < need))
         return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
                     (long long)(workspace ? ws_bytes : 0));
@@ -630,13 +660,16 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
     float* tail_ws = nullptr;
     if (workspace && tail_bytes > 0 && ws_bytes >= part_bytes + tail_bytes)
         tail_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
+    float* dwp = gw.parts && workspace && ws_bytes >= need
+                     ? reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes + tail_bytes)
+                     : nullptr;
     uint16_t* remix_buf = nullptr;
     if (remix) {
         if (!probs) return fail(VQ_ERR_NULL, "probs is NULL");
-        remix_buf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes + tail_bytes);
+        remix_buf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes + tail_bytes + gw.dwp_bytes);
     }
     return run_bwd(dy, x, m, n, d, d_pad, make_set(ncand, qtypes, qbytes, d_pad), probs, w_eff, remix_buf, dx, dprobs,
-                   partials, tail_ws, static_cast<hipStream_t>(stream));
+                   gw, partials, tail_ws, dwp, static_cast<hipStream_t>(stream));
 }
 
 int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
@@ -645,7 +678,9 @@ int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m,
     int rc = check_bwd(dy, x, m, n, d, d_pad, ncand, qtypes, qbytes, w_eff, dx);
     if (rc != VQ_OK) return rc;
     if (dx && !w_eff) return fail(VQ_ERR_NULL, "dx needs the forward's w_eff (this entry point does not re-mix)");
-    const int64_t part_bytes = align256(vq::gate_partial_count((int)m, (int)n, (int)d) * ncand * (int64_t)sizeof(float));
+    // the fused gate epilogue only: dW parts would not fit the scratch
+    const GateWs gw = gate_ws(m, d, d_pad, 1, &n, n, ncand, false);
+    const int64_t part_bytes = gw.part_bytes;
     if (dprobs && part_bytes > kStaticScratchBytes)
         return fail(VQ_ERR_WORKSPACE, "m=%lld n=%lld d=%lld ncand=%d needs %lld bytes of gate partials; the static "
                     "scratch holds %lld (use vq_gated_linear_bwd with a workspace)", (long long)m, (long long)n,
@@ -660,7 +695,7 @@ int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m,
     if (tail_bytes > 0 && part_bytes + tail_bytes <= kStaticScratchBytes)
         tail_ws = reinterpret_cast<float*>(scratch_ptr + part_bytes);
     return run_bwd(dy, x, m, n, d, d_pad, make_set(ncand, qtypes, qbytes, d_pad), nullptr, w_eff, nullptr, dx, dprobs,
-                   reinterpret_cast<float*>(scratch_ptr), tail_ws, s);
+                   gw, reinterpret_cast<float*>(scratch_ptr), tail_ws, nullptr, s);
 }
 
 int64_t vq_gated_linear_fused_workspace(int64_t m, int64_t n, int64_t d, int dx) {
@@ -747,10 +782,10 @@ int64_t vq_gated_linear_group_bwd_workspace(int64_t m, int64_t d, int nmembers, 
         kstride = ncand[i] > kstride ? ncand[i] : kstride;
     }
     if (n_total > INT32_MAX) return -1;
-    int64_t bytes =
-        align256(vq::gate_partial_count((int)m, (int)n_total, (int)d) * nmembers * kstride * (int64_t)sizeof(float));
-    bytes += align256(vq::dx_tail_bytes((int)m, (int)n_total, (int)d));
-    return bytes;
+    // [gate partials][dX split-tail partial tiles][gate dW parts]; d_pad = the
+    // 256-multiple the candidates are padded to
+    const GateWs gw = gate_ws(m, d, (d + 255) / 256 * 256, nmembers, n, n_total, nmembers * kstride, true);
+    return gw.part_bytes + align256(vq::dx_tail_bytes((int)m, (int)n_total, (int)d)) + gw.dwp_bytes;
 }
 
 int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t d, int64_t d_pad, int nmembers,
@@ -771,9 +806,9 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
             if (!dprobs[i]) return fail(VQ_ERR_NULL, "dprobs[%d] is NULL", i);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t need = vq_gated_linear_group_bwd_workspace(m, d, nmembers, n, ncand);
-    const int64_t nparts = vq::gate_partial_count((int)m, (int)n_total, (int)d);
     const int nslot = nmembers * cg.kstride;
-    const int64_t part_bytes = align256(nparts * nslot * (int64_t)sizeof(float));
+    const GateWs gw = gate_ws(m, d, d_pad, nmembers, n, n_total, nslot, true);
+    const int64_t part_bytes = gw.part_bytes;
     if (dprobs && (!workspace || ws_bytes < need))
         return fail(VQ_ERR_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
                     (long long)(workspace ? ws_bytes : 0));
@@ -783,10 +818,22 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
     float* tail_ws = nullptr;
     if (workspace && tail_bytes > 0 && ws_bytes >= part_bytes + tail_bytes)
         tail_ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes);
+    float* dwp = gw.parts && workspace && ws_bytes >= need
+                     ? reinterpret_cast<float*>(static_cast<char*>(workspace) + part_bytes + tail_bytes)
+                     : nullptr;
+    // every member in one reduce; no tokens: a reduce over zero partials
+    // writes dL/dp = 0; the parts path when the shape takes it and its buffer is there
+    vq::GateReduceOut out{};
+    out.kstride = cg.kstride;
+    if (dprobs)
+        for (int i = 0; i < nmembers; ++i) {
+            out.dprobs[i] = dprobs[i];
+            out.ncand[i] = ncand[i];
+        }
     if (dx && m > 0) {
         if (dprobs)
             rc = hip_check(vq::launch_gemm_dx_gate(dy, w_eff, d_pad, dx, x, cg, partials, (int)m, (int)n_total, (int)d,
-                                                   tail_ws, s),
+                                                   tail_ws, dwp, s),
                            "dX + gate GEMM launch");
         else
             rc = hip_check(vq::launch_gemm_dx(dy, w_eff, d_pad, dx, (int)m, (int)n_total, (int)d, tail_ws, s),
@@ -795,20 +842,15 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
     }
     if (dprobs) {
         if (!dx && m > 0) {
-            rc = hip_check(vq::launch_gemm_gate(dy, x, cg, partials, (int)m, (int)n_total, (int)d, s),
+            rc = hip_check(vq::launch_gemm_gate(dy, x, cg, partials, (int)m, (int)n_total, (int)d, dwp, s),
                            "gate GEMM launch");
             if (rc != VQ_OK) return rc;
         }
-        // every member in one launch; no tokens: a reduce over zero partials
-        // writes dL/dp = 0
-        vq::GateReduceOut out{};
-        out.kstride = cg.kstride;
-        for (int i = 0; i < nmembers; ++i) {
-            out.dprobs[i] = dprobs[i];
-            out.ncand[i] = ncand[i];
-        }
-        rc = hip_check(vq::launch_gate_reduce_group(partials, m > 0 ? nparts : 0, nslot, out, nmembers, s),
-                       "gate reduce launch");
+        // partials: one per dot block on the parts path, one per gate block otherwise
+        const int64_t nparts = m == 0 ? 0
+                               : dwp  ? vq::gate_dot_blocks(nmembers, n, d_pad / 256)
+                                      : vq::gate_partial_count((int)m, (int)n_total, (int)d);
+        rc = hip_check(vq::launch_gate_reduce_group(partials, nparts, nslot, out, nmembers, s), "gate reduce launch");
         if (rc != VQ_OK) return rc;
     }
     return ok();

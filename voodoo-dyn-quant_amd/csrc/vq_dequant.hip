@@ -275,4 +275,172 @@ hipError_t launch_mix(const CandSet& cs, const float* probs, bf16_t* w_eff, int6
     return launch_mix_sets(1, &cs, &probs, &w_eff, &ngroups, s);
 }
 
+// ---------------------------------------------------------------------------
+// Gate dots from dW parts (the EPI_PARTS gate product):
+//   partials[block][set * kstride + k] = sum over the block's weights of
+//   dW[n][d] * W_k[n][d],
+// dW[n][d] the fp32 sum, in part order, of the parts
+//   dwp[(tm * tiles_j + tn) * parts + part][n % 256][d % 256],
+// tm = d / 256, tn = n / 256, n counted over the stacked members.  A
+// workgroup takes 16 consecutive groups (row, 256 weights) of one member and
+// stages every candidate's bytes for them in LDS as the mix does; a thread
+// takes 16 consecutive weights of one group.  Weights past D have no
+// gradient.  The block sums are reduced in a fixed order (launch_gate_reduce*).
+// ---------------------------------------------------------------------------
+struct GateDotPlan {
+    int nsets, kstride, parts, tiles_j, dlimit;
+    int64_t row_groups;
+    const float* dwp;
+    float* partials;
+    CandSet sets[kMaxSets];
+    int set_j0[kMaxSets + 1];
+    int64_t ngroups[kMaxSets];
+    int64_t block0[kMaxSets + 1];
+    int gbytes[kMaxSets][kMaxCand];
+    int lds_off[kMaxSets][kMaxCand];
+};
+
+template <bool IQ>
+__global__ __launch_bounds__(kStreamThreads) void gate_dot_kernel(GateDotPlan gp) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[kStreamThreads / 64][kMaxCand];
+    int si = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxSets; ++q)
+        if (q < gp.nsets && (int64_t)blockIdx.x >= gp.block0[q]) si = q;
+    const CandSet& cs = gp.sets[si];
+    const int64_t g0 = ((int64_t)blockIdx.x - gp.block0[si]) * kMixGroupsPerPass;
+    const int ng = (int)min<int64_t>(kMixGroupsPerPass, gp.ngroups[si] - g0);
+    for (int k = 0; k < cs.ncand; ++k) {
+        const int gb = gp.gbytes[si][k];
+        stage_bytes(lds + gp.lds_off[si][k], cs.qbytes[k] + g0 * gb, ng * gb);
+    }
+    // this thread's 16 weights of dW, summed over the parts while the copies fly
+    const int t = threadIdx.x, j = t >> 4, p = kMixRun * (t & 15);
+    float v[kMixRun];
+#pragma unroll
+    for (int r = 0; r < kMixRun; ++r) v[r] = 0.0f;
+    if (j < ng) {
+        const int64_t gi = g0 + j;
+        const int grp = (int)(gi % gp.row_groups);
+        const int d0 = grp * 256 + p;
+        if (d0 < gp.dlimit) {
+            const int64_t n = gp.set_j0[si] + gi / gp.row_groups;
+            const float4* src = reinterpret_cast<const float4*>(
+                gp.dwp + ((int64_t)grp * gp.tiles_j + n / 256) * gp.parts * 65536 + (n % 256) * 256 + p);
+            // every part's loads in flight before the first add (one wave per
+            // SIMD: a load-add loop would wait out one memory latency per part)
+            float4 q[kMaxGateParts][kMixRun / 4];
+#pragma unroll
+            for (int part = 0; part < kMaxGateParts; ++part)
+                if (part < gp.parts)
+#pragma unroll
+                    for (int h = 0; h < kMixRun / 4; ++h) q[part][h] = src[part * 16384 + h];
+#pragma unroll
+            for (int part = 0; part < kMaxGateParts; ++part)
+                if (part < gp.parts)
+#pragma unroll
+                    for (int h = 0; h < kMixRun / 4; ++h) {
+                        v[4 * h] += q[part][h].x;
+                        v[4 * h + 1] += q[part][h].y;
+                        v[4 * h + 2] += q[part][h].z;
+                        v[4 * h + 3] += q[part][h].w;
+                    }
+#pragma unroll
+            for (int r = 0; r < kMixRun; ++r)
+                if (d0 + r >= gp.dlimit) v[r] = 0.0f;
+        }
+    }
+    stage_wait();
+    __syncthreads();
+    const int lane = t & 63, wave = t >> 6;
+    for (int k = 0; k < cs.ncand; ++k) {
+        float dot = 0.0f;
+        if (j < ng) {
+            const int qt = cs.qtype[k];
+            const uint8_t* g = lds + gp.lds_off[si][k] + j * gp.gbytes[si][k];
+            switch (qt) {
+            case Q8_0: dot = dot_run<Q8_0, kMixRun>(g, p, v); break;
+            case Q2_K: dot = dot_run<Q2_K, kMixRun>(g, p, v); break;
+            case Q3_K: dot = dot_run<Q3_K, kMixRun>(g, p, v); break;
+            case Q4_K: dot = dot_run<Q4_K, kMixRun>(g, p, v); break;
+            case Q5_K: dot = dot_run<Q5_K, kMixRun>(g, p, v); break;
+            case Q6_K: dot = dot_run<Q6_K, kMixRun>(g, p, v); break;
+            default:
+                if constexpr (IQ)
+                    dot = dot_run_iq<kMixRun>(qt, g, p, v);
+                else
+                    dot = dot_run<Q6_K, kMixRun>(g, p, v);
+                break;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) dot += __shfl_xor(dot, off);
+        if (lane == 0) red[wave][k] = dot;
+    }
+    __syncthreads();
+    // this block's slots of every member: its own sums, zeros for the others
+    const int nslot = gp.nsets * gp.kstride;
+    if (t < nslot) {
+        const int k = t - si * gp.kstride;
+        float sum = 0.0f;
+        if (k >= 0 && k < cs.ncand)
+            for (int w = 0; w < kStreamThreads / 64; ++w) sum += red[w][k];
+        gp.partials[(int64_t)blockIdx.x * nslot + t] = sum;
+    }
+}
+
+int64_t gate_dot_blocks(int nsets, const int64_t* n, int64_t row_groups) {
+    int64_t b = 0;
+    for (int i = 0; i < nsets; ++i) b += (n[i] * row_groups + kMixGroupsPerPass - 1) / kMixGroupsPerPass;
+    return b;
+}
+
+hipError_t launch_gate_dot(const CandGroup& cg, int N, int D, const float* dwp, int parts, float* partials,
+                           hipStream_t s) {
+    if (cg.nsets < 1 || cg.nsets > kMaxSets || cg.nsets * cg.kstride > kStreamThreads || parts < 1 ||
+        parts > kMaxGateParts)
+        return hipErrorInvalidValue;
+    GateDotPlan gp{};
+    gp.nsets = cg.nsets;
+    gp.kstride = cg.kstride;
+    gp.parts = parts;
+    gp.tiles_j = (N + 255) / 256;
+    gp.dlimit = D;
+    gp.row_groups = cg.sets[0].row_groups;
+    gp.dwp = dwp;
+    gp.partials = partials;
+    size_t lds = 0;
+    int64_t blocks = 0;
+    bool iq = false;
+    for (int i = 0; i < cg.nsets; ++i) {
+        if (cg.sets[i].row_groups != gp.row_groups || (int64_t)(D + 255) / 256 > gp.row_groups)
+            return hipErrorInvalidValue;
+        gp.sets[i] = cg.sets[i];
+        gp.set_j0[i] = cg.set_j0[i];
+        gp.ngroups[i] = (int64_t)(cg.set_j0[i + 1] - cg.set_j0[i]) * gp.row_groups;
+        gp.block0[i] = blocks;
+        blocks += (gp.ngroups[i] + kMixGroupsPerPass - 1) / kMixGroupsPerPass;
+        size_t l = 0;
+        for (int k = 0; k < cg.sets[i].ncand; ++k) {
+            gp.gbytes[i][k] = group_bytes(cg.sets[i].qtype[k]);
+            gp.lds_off[i][k] = (int)l;
+            l += (kMixGroupsPerPass * gp.gbytes[i][k] + 15) & ~15;
+        }
+        lds = l > lds ? l : lds;
+        iq = iq || any_iq(cg.sets[i]);
+    }
+    gp.set_j0[cg.nsets] = cg.set_j0[cg.nsets];
+    gp.block0[cg.nsets] = blocks;
+    if (blocks <= 0) return hipSuccess;
+    const void* kern = iq ? (const void*)gate_dot_kernel<true> : (const void*)gate_dot_kernel<false>;
+    const hipError_t e = allow_dynamic_lds(kern, lds);
+    if (e != hipSuccess) return e;
+    if (iq)
+        gate_dot_kernel<true><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(gp);
+    else
+        gate_dot_kernel<false><<<dim3((unsigned)blocks), kStreamThreads, lds, s>>>(gp);
+    return hipGetLastError();
+}
+
 }  // namespace vq

@@ -63,6 +63,7 @@ static bool small_product(int M, int N) {
 }
 using DxCfg = GemmCfg<DxLA, DxLB, 256, 256, 64, 4, 2, EPI_STORE, 2, SWITCH_LOOSE, 2, COPY_SPLIT>;
 using GateCfg = GemmCfg<GateLA, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_GATE, 2, SWITCH_LOOSE, 2, COPY_SPLIT>;
+using GatePartsCfg = GemmCfg<GateLA, GateL, kGateBI, kGateBJ, 64, 4, 2, EPI_PARTS, 2, SWITCH_LOOSE, 2, COPY_SPLIT>;
 
 static GemmParams fwd_params(const bf16_t* X, const bf16_t* W, int64_t ldw, bf16_t* Y, int M, int N, int D) {
     GemmParams p{};
@@ -89,6 +90,46 @@ static GemmParams gate_params(const bf16_t* dY, const bf16_t* X, const CandGroup
 int64_t gate_partial_count(int M, int N, int D) {
     GemmParams p = gate_params(nullptr, nullptr, CandGroup{}, nullptr, M, N, D);
     return GateCfg::plan(p, device_cus(), true);
+}
+
+// Gate products whose 256x256 dW tiles are few enough that the fused plan
+// splits them along M run every candidate's decode and dot once per part, and
+// the epilogue (VALU-bound, K decodes of 65536 weights) then outlasts the
+// part's main loop.  Where the fused plan splits tiles 4 ways or more, those
+// products write fp32 parts instead (EPI_PARTS) and one pass over the summed
+// parts takes the dots (launch_gate_dot).  Measured on MI355X at 8192 tokens,
+// K = 6, backward launches together: 1024 -> 1536 93 -> 76 us, 3072 -> 1024
+// 140 -> 126 us, 1024 -> 1024 65 -> 63 us; at 1024 -> 6144 (tiles split 2
+// ways) the parts lost, 217 -> 238 us: the parts' round trip through memory
+// (the dot pass reads them at about 4 TB/s) outweighs a twice-run epilogue.
+// Parts per tile: what the CUs left over by dX's work items hold, at least 2,
+// at most kMaxGateParts, each part at least 4 K steps; the buffer is capped at
+// kMaxPartsBytes.
+constexpr int64_t kMaxPartsBytes = (int64_t)64 << 20;
+
+int gate_parts(int M, int N, int D) {
+    if (M <= 0 || N <= 0 || D <= 0) return 0;
+    const int cus = device_cus();
+    GemmParams g = gate_params(nullptr, nullptr, CandGroup{}, nullptr, M, N, D);
+    GateCfg::plan(g, cus, true);
+    if (g.s_max < 4) return 0;  // each tile's epilogue runs at most 3 times
+    const int64_t tiles = (int64_t)GateCfg::tiles_i(g) * GateCfg::tiles_j(g);
+    GemmParams x = dx_params(nullptr, nullptr, 0, nullptr, M, N, D);
+    const int dx_items = DxCfg::plan(x, cus, true);
+    int64_t s = (cus - dx_items) / tiles;
+    s = s < 2 ? 2 : s > kMaxGateParts ? kMaxGateParts : s;
+    if (s > GateCfg::ksteps(g) / 4) s = GateCfg::ksteps(g) / 4;
+    if (s < 2 || tiles * s * kGateBI * kGateBJ * 4 > kMaxPartsBytes) return 0;
+    return (int)s;
+}
+
+static int64_t parts_floats(int parts, int N, int D) {
+    return (int64_t)((D + kGateBI - 1) / kGateBI) * ((N + kGateBJ - 1) / kGateBJ) * parts * kGateBI * kGateBJ;
+}
+
+int64_t gate_parts_bytes(int M, int N, int D) {
+    const int s = gate_parts(M, N, D);
+    return s == 0 ? 0 : parts_floats(s, N, D) * 4;
 }
 
 // fp32 workspace for the K parts of dX's split tail tiles.
@@ -121,8 +162,23 @@ hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t
     return launch_gemm_cfg<DxCfg>(dx_params(dY, W, ldw, dX, M, N, D), device_cus(), tail_ws, s);
 }
 
+static GemmParams parts_params(const bf16_t* dY, const bf16_t* X, float* dwp, int parts, int M, int N, int D) {
+    GemmParams p = gate_params(dY, X, CandGroup{}, nullptr, M, N, D);
+    p.dwp = dwp;
+    p.parts = parts;
+    return p;
+}
+
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
-                            int D, hipStream_t s) {
+                            int D, float* dwp, hipStream_t s) {
+    if (dwp) {
+        const int np = gate_parts(M, N, D);
+        if (np == 0) return hipErrorInvalidValue;
+        const hipError_t e =
+            launch_gemm_cfg<GatePartsCfg>(parts_params(dY, X, dwp, np, M, N, D), device_cus(), nullptr, s);
+        if (e != hipSuccess) return e;
+        return launch_gate_dot(cg, N, D, dwp, np, partials, s);
+    }
     if (any_iq(cg))
         return launch_gemm_cfg<GateCfg, true>(gate_params(dY, X, cg, partials, M, N, D), device_cus(), nullptr, s);
     return launch_gemm_cfg<GateCfg>(gate_params(dY, X, cg, partials, M, N, D), device_cus(), nullptr, s);
@@ -132,7 +188,16 @@ hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& 
 // the longer ones, first).
 hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
                                const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
-                               hipStream_t s) {
+                               float* dwp, hipStream_t s) {
+    if (dwp) {
+        const int np = gate_parts(M, N, D);
+        if (np == 0) return hipErrorInvalidValue;
+        const hipError_t e = launch_gemm_dual<DxCfg, GatePartsCfg>(dx_params(dY, W, ldw, dX, M, N, D),
+                                                                   parts_params(dY, X, dwp, np, M, N, D),
+                                                                   device_cus(), tail_ws, s);
+        if (e != hipSuccess) return e;
+        return launch_gate_dot(cg, N, D, dwp, np, partials, s);
+    }
     if (any_iq(cg))
         return launch_gemm_dual<DxCfg, GateCfg, true>(dx_params(dY, W, ldw, dX, M, N, D),
                                                         gate_params(dY, X, cg, partials, M, N, D), device_cus(),

@@ -307,7 +307,11 @@ __device__ __forceinline__ WorkItem map_work(int w, int tiles_m, int tiles_n, in
     return wi;
 }
 
-enum Epi : int { EPI_STORE = 0, EPI_GATE = 1 };
+// EPI_STORE: C rounded to bf16.  EPI_GATE: the tile's dots with every
+// candidate (partials per block).  EPI_PARTS: a gate product whose tiles are
+// split along K into p.parts parts writes each part's fp32 tile to p.dwp and
+// leaves the candidate dots to one pass over the summed parts.
+enum Epi : int { EPI_STORE = 0, EPI_GATE = 1, EPI_PARTS = 2 };
 
 struct GemmParams {
     const bf16_t* A;
@@ -330,6 +334,9 @@ struct GemmParams {
     // gate epilogue: [grid blocks][nsets * kstride] partial sums; store epilogue with
     // split tails: [8 * tail_max][s_max][BI * BJ] fp32 partial tiles
     float* partials;
+    // parts epilogue: [tile (tm * tiles_j + tn)][part][BJ][BI] fp32, n-major
+    float* dwp;
+    int parts;
     // routed product: A rows gathered and C rows scattered through rowmap;
     // group g owns rowmap[group_off[g] .. group_off[g + 1]) and multiplies
     // by bk[g]
@@ -730,7 +737,7 @@ struct GemmCfg {
     static constexpr size_t lds() {
         constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16 + (size_t)WI * WJ * kMaxCand * 4;  // two candidate buffers, wave sums
         constexpr size_t store = (size_t)BI * (BJ + 8) * 2;            // bf16 staging of the tile
-        constexpr size_t epi = EPI == EPI_GATE ? gate : store;
+        constexpr size_t epi = EPI == EPI_GATE ? gate : EPI == EPI_PARTS ? 0 : store;
         return epi > main_lds() ? epi : main_lds();
     }
     static int tiles_i(const GemmParams& p) { return (p.I + BI - 1) / BI; }
@@ -739,6 +746,20 @@ struct GemmCfg {
     // Fill in the work decomposition; returns the grid size (8 * blocks per XCD).
     static int plan(GemmParams& p, int cus, bool split_ok) {
         if (p.I <= 0 || p.J <= 0) return 0;
+        if constexpr (EPI == EPI_PARTS) {
+            // every tile in p.parts parts, the XCDs' tile ranges as for whole tiles
+            p.cus_per_xcd = cus / 8 > 0 ? cus / 8 : 1;
+            p.split_ok = 0;
+            p.tail_max = 0;
+            p.s_max = 1;
+            const int tiles = tiles_i(p) * tiles_j(p);
+            int items = 0;
+            for (int x = 0; x < 8; ++x) {
+                const XcdPlan pl = xcd_plan(x, tiles, p.cus_per_xcd, ksteps(p), false);
+                items = pl.tiles * p.parts > items ? pl.tiles * p.parts : items;
+            }
+            return 8 * items;
+        }
         // a split store tile pays for its partial writes and a fixup launch:
         // split only when a part saves at least kMinSavedSplitSteps K steps
         p.split_min_saved = EPI == EPI_STORE ? kMinSavedSplitSteps : 0;
@@ -820,6 +841,38 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     const int tiles_i = (p.I + BI - 1) / BI, tiles_j = (p.J + BJ - 1) / BJ;
     const int ksteps = (p.K + BK - 1) / BK;
+    if constexpr (EPI == EPI_PARTS) {
+        // item (tile, part): XCD x = block % 8 takes its tile range part by part
+        static_assert(LA::kPerm == 1, "each lane holds 16 consecutive rows i of an accumulator block");
+        const int x = block % 8, local = block / 8;
+        const XcdPlan pl = xcd_plan(x, tiles_i * tiles_j, p.cus_per_xcd, ksteps, false);
+        if (local >= pl.tiles * p.parts) return;
+        int tm, tn;
+        tile_coords(pl.t0 + local / p.parts, tiles_i, tiles_j, kGroupM, tm, tn);
+        const int part = local % p.parts;
+        const int chunk = (ksteps + p.parts - 1) / p.parts * BK;
+        const int kbeg = min(p.K, part * chunk), kend = min(p.K, kbeg + chunk);
+        f32x16 acc[S::MI][S::NJ];
+        gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, DEPTH, C::SWITCH, C::COPY>(p, tm * BI, tn * BJ, kbeg, kend, smem,
+                                                                                acc);
+        // acc[a][b][r] is element (i, j) = (wi WTI + 32 a + 16 (lane >> 5) + r, wj WTJ + 32 b + lane % 32):
+        // four 16-byte stores per lane and block, two lanes per 128-byte row segment
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        const int wi = wave / WJ, wj = wave % WJ;
+        float* slot = p.dwp + ((int64_t)(tm * tiles_j + tn) * p.parts + part) * (BI * BJ);
+#pragma unroll
+        for (int a = 0; a < S::MI; ++a)
+#pragma unroll
+            for (int b = 0; b < S::NJ; ++b) {
+                const int jl = wj * S::WTJ + 32 * b + (lane & 31);
+                const int il = wi * S::WTI + 32 * a + 16 * (lane >> 5);
+                float4* o = reinterpret_cast<float4*>(slot + jl * BI + il);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    o[q] = make_float4(acc[a][b][4 * q], acc[a][b][4 * q + 1], acc[a][b][4 * q + 2], acc[a][b][4 * q + 3]);
+            }
+        return;
+    }
     const WorkItem w = map_work(block, tiles_i, tiles_j, ksteps, p.cus_per_xcd, p.split_ok != 0, p.tail_max, kGroupM,
                                 p.split_min_saved, p.split_max);
     if (w.idle) {
@@ -854,7 +907,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p, int block, u32x4*
             return;
         }
         store_tile_lds<BI, BJ, BK, WI, WJ>(p, i0, j0, smem, acc);
-    } else {
+    } else if constexpr (EPI == EPI_GATE) {
         static_assert(LA::kPerm == 1, "the gate epilogue reads 16 consecutive weights per accumulator block");
         gate_epilogue<BI, BJ, BK, WI, WJ, IQ>(p, block, i0, j0, smem, acc);
     }
@@ -981,7 +1034,8 @@ static hipError_t launch_gemm_cfg(GemmParams p, int cus, float* tail_ws, hipStre
 // 4096 -> 28672, neutral at 17408 -> 5120 and the 1024-wide products.
 template <class C1, class C2, bool IQ2 = false>
 static hipError_t launch_gemm_dual(GemmParams p1, GemmParams p2, int cus, float* tail_ws1, hipStream_t s) {
-    static_assert(C1::EPI == EPI_STORE && C2::EPI == EPI_GATE, "a store product and a gate product");
+    static_assert(C1::EPI == EPI_STORE && (C2::EPI == EPI_GATE || C2::EPI == EPI_PARTS),
+                  "a store product and a gate product");
     const int grid1 = C1::plan(p1, cus, tail_ws1 != nullptr);
     const int grid2 = C2::plan(p2, cus, true);
     p1.partials = tail_ws1;

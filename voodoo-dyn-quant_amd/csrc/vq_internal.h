@@ -40,21 +40,40 @@ hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t
 int device_cus();
 int64_t gate_partial_count(int M, int N, int D);  // gate partials per candidate (one per grid block)
 int64_t dx_tail_bytes(int M, int N, int D);       // dX split-tail workspace bytes
-hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
-                            int D, hipStream_t s);
-hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
-                               const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
-                               hipStream_t s);
-// PTQR: Y[perm[r]] = X[perm[r]] . W_g^T for r in [group_off[g], group_off[g+1])
-hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const* cand_bf16, int64_t ldw, int N,
-                             int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s);
-hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
-// dprobs[k] = sum_t partials[t * stride + k], k < ncand
+// Where the gate reduce writes dL/dp: member i's candidate k from partial
+// slot i * kstride + k.
 struct GateReduceOut {
     float* dprobs[kMaxSets];
     int ncand[kMaxSets];
     int kstride;
 };
+// Most parts per tile of a gate product that writes dW parts.
+constexpr int kMaxGateParts = 8;
+// Gate products at sizes whose tiles split along M 4 ways or more: parts per
+// tile when the product writes fp32 dW parts and one pass takes the candidate
+// dots (0: the fused epilogue), and that parts buffer's bytes.
+int gate_parts(int M, int N, int D);
+int64_t gate_parts_bytes(int M, int N, int D);
+// Gate partials of the parts path: one per dot block, sum over members of
+// ceil(n_i * row_groups / 16).
+int64_t gate_dot_blocks(int nsets, const int64_t* n, int64_t row_groups);
+// dwp: NULL for the fused epilogue (partials: gate_partial_count blocks),
+// else gate_parts_bytes of workspace for the parts path (partials:
+// gate_dot_blocks blocks); either way launch_gate_reduce* sums the partials
+hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
+                            int D, float* dwp, hipStream_t s);
+hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
+                               const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
+                               float* dwp, hipStream_t s);
+// partials[block][nsets * kstride] = sum over the block's weights of
+// dW[n][d] * W_k[n][d], dW the sum of the parts dwp in part order
+hipError_t launch_gate_dot(const CandGroup& cg, int N, int D, const float* dwp, int parts, float* partials,
+                           hipStream_t s);
+// PTQR: Y[perm[r]] = X[perm[r]] . W_g^T for r in [group_off[g], group_off[g+1])
+hipError_t launch_routed_fwd(const bf16_t* X, int M, int D, const bf16_t* const* cand_bf16, int64_t ldw, int N,
+                             int ncand, const int* perm, const int* group_off, bf16_t* Y, hipStream_t s);
+hipError_t launch_gate_reduce(const float* partials, int64_t ntiles, int ncand, float* dprobs, hipStream_t s);
+// dprobs[k] = sum_t partials[t * stride + k], k < ncand
 hipError_t launch_gate_reduce_group(const float* partials, int64_t ntiles, int stride, const GateReduceOut& out,
                                     int nmembers, hipStream_t s);
 hipError_t launch_gate_reduce_strided(const float* partials, int64_t ntiles, int stride, int ncand, float* dprobs,
