@@ -259,8 +259,10 @@ int64_t vq_gated_linear_bwd_workspace(int64_t m, int64_t n, int64_t d, int64_t d
 
 /* Backward of the gated Linear.  dx (nullable) = dy . W_eff;
  * dprobs (nullable) [ncand] fp32 = <dy^T x, W_k> with the dW tiles kept on
- * chip (registers and LDS, never written to memory) and the candidates decoded
- * exactly.  `w_eff` is
+ * chip (registers and LDS) and the candidates decoded exactly; at shapes with
+ * few dW tiles (the plan splits each along m 4 ways or more) the tiles' fp32
+ * parts go through the workspace (at most 64 MiB) and one pass takes the
+ * dots.  `w_eff` is
  * the forward's buffer, or NULL to re-mix into the workspace.  Replaces the
  * F.linear autograd backward and _MixedWeightFunction.backward
  * (voodoo_quant/layers.py:354-363). */
