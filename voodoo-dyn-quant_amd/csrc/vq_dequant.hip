@@ -78,6 +78,11 @@ __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* 
     stage_wait();
     __syncthreads();
     const int t = threadIdx.x;
+    // fp32 output goes through LDS so that each store instruction writes 1 KB
+    // in one piece (a thread's own run is two 16-byte halves 32 bytes apart):
+    // 6.2-6.5 against 5.2-5.9 TB/s for the K-quants and Q8_0 at 4096 x 14336,
+    // 4.5-4.8 against 3.9-4.2 for the code-book IQ formats
+    __shared__ __attribute__((aligned(16))) float ob[sizeof(OUT) == 4 ? kGroupsPerBlock * 256 : 1];
 #pragma unroll
     for (int u = 0; u < kRunsPerThread; ++u) {
         const int j = (t >> 5) + 8 * u;
@@ -88,7 +93,7 @@ __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* 
             else
                 decode_run<QT, 8>(lds + j * GB, 8 * (t & 31), y);
             if constexpr (sizeof(OUT) == 4) {
-                float4* o = reinterpret_cast<float4*>(out + (g0 + j) * 256 + 8 * (t & 31));
+                float4* o = reinterpret_cast<float4*>(ob + j * 256 + 8 * (t & 31));
                 o[0] = make_float4(y[0], y[1], y[2], y[3]);
                 o[1] = make_float4(y[4], y[5], y[6], y[7]);
             } else {
@@ -100,6 +105,12 @@ __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* 
                 *reinterpret_cast<uint4*>(out + (g0 + j) * 256 + 8 * (t & 31)) = v;
             }
         }
+    }
+    if constexpr (sizeof(OUT) == 4) {
+        __syncthreads();
+        const float4* src = reinterpret_cast<const float4*>(ob);
+        float4* dst = reinterpret_cast<float4*>(out + g0 * 256);
+        for (int i = t; i < ng * 64; i += kStreamThreads) dst[i] = src[i];
     }
 }
 
