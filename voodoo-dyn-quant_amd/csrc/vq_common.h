@@ -131,6 +131,16 @@ __device__ __forceinline__ void load_run(const uint8_t* __restrict__ p, uint32_t
     }
 }
 
+// The code words as opaque values: without this the compiler folds a word's
+// mask and each byte's shift into one v_bfe_u32 per weight (Q4_K, Q2_K)
+// instead of letting v_cvt_f32_ubyteN read the byte: 16 extra VALU
+// instructions per run of 16.
+template <int W>
+__device__ __forceinline__ void opaque_words(uint32_t (&uw)[W]) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) asm volatile("" : "+v"(uw[i]));
+}
+
 template <int R>
 __device__ __forceinline__ uint32_t run_byte(const uint32_t (&w)[R / 4], int r) {
     return (w[r >> 2] >> (8 * (r & 3))) & 0xffu;
@@ -329,6 +339,7 @@ __device__ __forceinline__ float dot_sub16(const uint8_t* __restrict__ g, int p,
 #pragma unroll
         for (int u = 0; u < 4; ++u) uw[u] = (q[u] >> (2 * j)) & 0x03030303u;
     }
+    opaque_words(uw);
     // two partial sums shorten the dependent fma chain
     float s1[2] = {0.0f, 0.0f};
 #pragma unroll
@@ -426,6 +437,7 @@ __device__ __forceinline__ void decode_mix(const uint8_t* __restrict__ g, int p,
     uint32_t uw[R / 4];
     float dl, c;
     decode_affine<QT, R>(g, p, uw, dl, c);
+    opaque_words(uw);
 #pragma unroll
     for (int r = 0; r < R; ++r) y[r] = fmaf(dl, (float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu), c);
 }
