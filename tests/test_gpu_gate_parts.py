@@ -79,6 +79,9 @@ SINGLE = [  # (name, m, d, d_pad, n, types)
     ("o_2048_tokens", 2048, 1024, 1024, 1024, SIX),
     ("ragged_d1000", 8192, 1000, 1024, 1024, ["Q8_0", "Q4_K", "Q2_K", "Q6_K"]),
     ("recipe_iq", 8192, 1024, 1024, 1536, ["Q8_0", "Q5_K", "IQ3_S", "IQ2_S", "IQ2_XXS", "IQ1_S"]),
+    # ragged output rows (the last tile column half full) and a token count that
+    # splits into uneven K parts (8000 = 125 steps of 64)
+    ("ragged_n1000_m8000", 8000, 1024, 1024, 1000, ["Q6_K", "Q3_K", "Q8_0"]),
 ]
 
 
