@@ -122,3 +122,31 @@ def test_workspace_size():
     assert n >= tiles * 6 * 4 and n % 256 == 0
     assert _hip.bwd_workspace_bytes(8192, 17408, 5120, 5120, 6, True) >= n + 17408 * 5120 * 2
     assert _hip.bwd_workspace_bytes(0, 64, 256, 256, 2, False) > 0
+
+
+TILE = 256 * 256 * 4  # one fp32 dW tile
+
+
+@pytest.mark.parametrize("m, n, d", [(8192, 1024, 1024), (8192, 1536, 1024), (8192, 1024, 3072), (2048, 1024, 1024),
+                                     (8000, 1000, 1024)])
+def test_backward_workspace_holds_gate_parts_at_few_tile_shapes(m, n, d):
+    """Few dW tiles (the plan splits each 4 ways or more): the workspace holds
+    at least two fp32 parts per tile and at most 64 MiB of them (the CU count
+    falls back to 256, MI355X's, without a device)."""
+    tiles = ((n + 255) // 256) * ((d + 255) // 256)
+    ws = _hip.bwd_workspace_bytes(m, n, d, (d + 255) // 256 * 256, 6, False)
+    assert 2 * tiles * TILE <= ws <= (64 << 20) + (8 << 20)
+    # a group of the same total rows sizes the same parts
+    g = _hip.group_bwd_workspace_bytes(m, d, [((8,), [], n)])
+    assert 2 * tiles * TILE <= g
+
+
+@pytest.mark.parametrize("m, n, d", [(8192, 17408, 5120), (8192, 6144, 5120), (8192, 5120, 6144),
+                                     (8192, 5120, 17408), (256, 1024, 1024)])
+def test_backward_workspace_keeps_the_fused_gate_elsewhere(m, n, d):
+    """Many tiles, or too few tokens to split: no parts, only the partials and
+    dX's split-tail tiles (at these shapes less than two fp32 tiles per dW
+    tile would take)."""
+    ws = _hip.bwd_workspace_bytes(m, n, d, d, 6, False)
+    tiles = ((n + 255) // 256) * ((d + 255) // 256)
+    assert ws < 2 * tiles * TILE
