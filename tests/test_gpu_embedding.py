@@ -327,6 +327,34 @@ def test_q8_linear(hip, out_f, in_f, bias):
     assert torch.equal(_bits(y1), _bits(y)) and torch.equal(_bits(y2), _bits(y))
 
 
+def test_q8_linear_vocabulary_width_head(hip):
+    """A kept decode of vocabulary width runs its plain bf16 GEMM on the vendor
+    library (q8_teacher._LIBRARY_GEMM_ROWS): same product within bf16 rounding
+    of the library's own GEMM on the decode, and of fp64."""
+    from voodoo_quant.training import q8_teacher
+    from voodoo_quant.training.q8_teacher import Q8Linear
+
+    out_f, in_f = q8_teacher._LIBRARY_GEMM_ROWS + 264, 512
+    print(f"[q8 linear] vocabulary-width head out={out_f} in={in_f}", flush=True)
+    qb, dec = _q8_bytes(out_f, in_f, seed=3)
+    lin = Q8Linear(qb.cuda(), out_f, in_f)
+    x = torch.randn(5, 33, in_f, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    q8_teacher.set_keep_decoded(False)
+    y_lib = lin(x.cuda())
+    q8_teacher.set_keep_decoded(True)
+    try:
+        y_keep = lin(x.cuda())
+    finally:
+        q8_teacher.set_keep_decoded(False)
+    torch.cuda.synchronize()
+    assert y_keep.shape == (5, 33, out_f)
+    ref = x.double().reshape(-1, in_f) @ dec.to(torch.bfloat16).double().t()
+    for y in (y_lib, y_keep):
+        got = y.reshape(-1, out_f).cpu().double()
+        assert float((got - ref).norm() / ref.norm()) < 1e-2
+    assert float((y_keep.float() - y_lib.float()).norm() / y_lib.float().norm()) < 1e-2
+
+
 @pytest.mark.parametrize("vocab,dim", [(100, 160), (57, 512)])
 def test_q8_embedding_rows_exact(hip, vocab, dim):
     from voodoo_quant.training.q8_teacher import Q8Embedding

@@ -39,6 +39,14 @@ _Q8_BLOCK_BYTES = 34  # fp16 scale + 32 int8
 
 _KEEP_DECODED = False
 
+# A kept decode at least this many rows wide (the vocabulary-width output
+# head) is a plain bf16 GEMM with a short reduction (hidden 1024), where
+# hipBLASLt's stream-K kernel beats the library's tile-per-workgroup forward:
+# measured on MI355X at 8192 x 1024 -> 151936, 2.15 against 2.63 ms; at
+# 1024 -> 1536 the library's GEMM wins (33 against 46 us), so the decoder's
+# projections keep it.  The student's head is a plain Linear on hipBLASLt too.
+_LIBRARY_GEMM_ROWS = 32768
+
 
 def set_keep_decoded(enabled: bool) -> None:
     """Keep each Q8Linear's bf16 decode from one forward to the next.
@@ -131,8 +139,12 @@ class Q8Linear(nn.Module):
             x2 = x2.contiguous().clone()
         m = x2.shape[0]
         dev = x2.device
-        y = torch.empty(m, rows, dtype=torch.bfloat16, device=dev)
-        if m:
+        library = _KEEP_DECODED and m > 0 and rows >= _LIBRARY_GEMM_ROWS
+        if library:
+            y = torch.nn.functional.linear(x2, self._decoded()[:, : self.in_features])
+        else:
+            y = torch.empty(m, rows, dtype=torch.bfloat16, device=dev)
+        if m and not library:
             nbytes = _hip.fwd_workspace_bytes(m, rows, self.in_features)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
             if _KEEP_DECODED:
