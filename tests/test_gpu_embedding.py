@@ -316,7 +316,8 @@ def test_q8_linear(hip, out_f, in_f, bias):
     assert torch.equal(_bits(lin._weight().cpu()), _bits(dec.to(torch.bfloat16)))
     yf = lin(x.float().cuda())
     assert yf.dtype == torch.float32
-    # the decode kept between forwards (vq_linear_fwd on it) gives the same output
+    # the decode kept between forwards (a plain GEMM on it, on hipBLASLt) gives
+    # the same product within bf16 rounding, the same bits on every call
     from voodoo_quant.training import q8_teacher
 
     q8_teacher.set_keep_decoded(True)
@@ -324,17 +325,20 @@ def test_q8_linear(hip, out_f, in_f, bias):
         y1, y2 = lin(x.cuda()), lin(x.cuda())
     finally:
         q8_teacher.set_keep_decoded(False)
-    assert torch.equal(_bits(y1), _bits(y)) and torch.equal(_bits(y2), _bits(y))
+    assert torch.equal(_bits(y1), _bits(y2))
+    g1 = y1.reshape(-1, out_f).cpu().double()
+    assert float((g1 - ref).norm() / ref.norm()) < 1e-2
+    assert float((g1 - got).norm() / got.norm()) < 1e-2
 
 
 def test_q8_linear_vocabulary_width_head(hip):
-    """A kept decode of vocabulary width runs its plain bf16 GEMM on the vendor
-    library (q8_teacher._LIBRARY_GEMM_ROWS): same product within bf16 rounding
-    of the library's own GEMM on the decode, and of fp64."""
+    """A vocabulary-width Q8Linear: the decode-every-forward path (the library's
+    mixture with one candidate and its GEMM) and the kept decode (a plain GEMM
+    on hipBLASLt) give the same product within bf16 rounding, and of fp64."""
     from voodoo_quant.training import q8_teacher
     from voodoo_quant.training.q8_teacher import Q8Linear
 
-    out_f, in_f = q8_teacher._LIBRARY_GEMM_ROWS + 264, 512
+    out_f, in_f = 32768 + 264, 512
     print(f"[q8 linear] vocabulary-width head out={out_f} in={in_f}", flush=True)
     qb, dec = _q8_bytes(out_f, in_f, seed=3)
     lin = Q8Linear(qb.cuda(), out_f, in_f)

@@ -39,13 +39,13 @@ _Q8_BLOCK_BYTES = 34  # fp16 scale + 32 int8
 
 _KEEP_DECODED = False
 
-# A kept decode at least this many rows wide (the vocabulary-width output
-# head) is a plain bf16 GEMM with a short reduction (hidden 1024), where
-# hipBLASLt's stream-K kernel beats the library's tile-per-workgroup forward:
-# measured on MI355X at 8192 x 1024 -> 151936, 2.15 against 2.63 ms; at
-# 1024 -> 1536 the library's GEMM wins (33 against 46 us), so the decoder's
-# projections keep it.  The student's head is a plain Linear on hipBLASLt too.
-_LIBRARY_GEMM_ROWS = 32768
+# With the decode kept, a teacher forward is a plain bf16 GEMM, and it runs on
+# hipBLASLt (as the student's plain output head does): its stream-K kernels
+# measured as fast or faster at every teacher shape on MI355X at 8192 tokens,
+# 1024 -> 151936 2.15 against 2.63 ms, 1024 -> 6144 88 against 109 us,
+# 3072 -> 1024 48 against 53 us, 1024 -> 1536 and 1024 -> 1024 within 5%.
+# Without the kept decode every forward decodes and mixes through the library
+# (vq_gated_linear_fwd with one candidate), as the reference's teacher does.
 
 
 def set_keep_decoded(enabled: bool) -> None:
@@ -139,7 +139,7 @@ class Q8Linear(nn.Module):
             x2 = x2.contiguous().clone()
         m = x2.shape[0]
         dev = x2.device
-        library = _KEEP_DECODED and m > 0 and rows >= _LIBRARY_GEMM_ROWS
+        library = _KEEP_DECODED and m > 0
         if library:
             y = torch.nn.functional.linear(x2, self._decoded()[:, : self.in_features])
         else:
@@ -147,12 +147,9 @@ class Q8Linear(nn.Module):
         if m and not library:
             nbytes = _hip.fwd_workspace_bytes(m, rows, self.in_features)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes > 0 else None
-            if _KEEP_DECODED:
-                _hip.linear_fwd(x2, self._decoded(), rows, y, ws)
-            else:
-                w = torch.empty(rows, d_pad, dtype=torch.bfloat16, device=dev)
-                one = torch.ones(1, dtype=torch.float32, device=dev)
-                _hip.gated_linear_fwd(x2, (_Q8_0,), [qb], one, rows, d_pad, w, y, ws)
+            w = torch.empty(rows, d_pad, dtype=torch.bfloat16, device=dev)
+            one = torch.ones(1, dtype=torch.float32, device=dev)
+            _hip.gated_linear_fwd(x2, (_Q8_0,), [qb], one, rows, d_pad, w, y, ws)
         if rows != self.out_features:
             y = y[:, : self.out_features]
         if self.bias is not None:
@@ -217,8 +214,9 @@ _GROUP_DECODES: dict[tuple, torch.Tensor] = {}
 
 def q8_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
     """Outputs of Q8Linears that all read `x`.  With kept decodes and no
-    biases, their decodes are stacked once and the outputs come from ONE GEMM
-    (``vq_linear_fwd``); otherwise each module runs its own forward.
+    biases, their decodes are stacked once and the outputs come from ONE plain
+    GEMM (on hipBLASLt, as Q8Linear's kept-decode forward); otherwise each
+    module runs its own forward.
     stacked=True returns the stacked output [tokens, sum out_features] (None
     when the modules cannot be stacked)."""
     ok = (_KEEP_DECODED and len(modules) >= 2 and x.device.type == "cuda"
@@ -239,12 +237,7 @@ def q8_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
         x2 = x2.to(torch.bfloat16)
     if not x2.is_contiguous() or x2.data_ptr() % 16:
         x2 = x2.contiguous().clone()
-    m_rows, n_total = x2.shape[0], w.shape[0]
-    y = torch.empty(m_rows, n_total, dtype=torch.bfloat16, device=x2.device)
-    if m_rows:
-        nbytes = _hip.fwd_workspace_bytes(m_rows, n_total, modules[0].in_features)
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device) if nbytes > 0 else None
-        _hip.linear_fwd(x2, w, n_total, y, ws)
+    y = torch.nn.functional.linear(x2, w[:, : modules[0].in_features])
     if stacked:
         return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     outs = torch.split(y, [m.out_features for m in modules], dim=1)
