@@ -8,7 +8,9 @@ device and decodes them when it runs.
   with one candidate and probability 1: ``vq_gated_linear_fwd`` writes the
   bf16 decode of the bytes (``bf16(0 + 1 * w)``, the reference's
   ``dequantize_tensor_gpu`` value) and runs the MFMA GEMM on it, then the bias
-  is added as in ``F.linear``.  The reference's row-blocked path for
+  is added as in ``F.linear``.  With the decode kept (:func:`set_keep_decoded`)
+  a forward is a plain bf16 GEMM over that decode, run by ``F.linear``
+  (hipBLASLt).  The reference's row-blocked path for
   vocabulary-scale heads (``q8_teacher.py:39-59, 102-120``) exists to bound
   transients on 32 GB cards; here the whole bf16 weight is one transient
   buffer (2.5 GB for 248320 x 5120, against 288 GB of HBM).
