@@ -736,7 +736,7 @@ struct GemmCfg {
     static constexpr size_t main_lds() { return StageLds<LA, LB, DEPTH>::BYTES; }
     static constexpr size_t lds() {
         constexpr size_t gate = (size_t)2 * BJ * kGateMaxChunks * 16 + (size_t)WI * WJ * kMaxCand * 4;  // two candidate buffers, wave sums
-        constexpr size_t store = (size_t)BI * (BJ + 8) * 2;            // bf16 staging of the tile
+        constexpr size_t store = (size_t)BI * (BJ + 8) * 2 + BI * 4;   // bf16 staging of the tile, row map
         constexpr size_t epi = EPI == EPI_GATE ? gate : EPI == EPI_PARTS ? 0 : store;
         return epi > main_lds() ? epi : main_lds();
     }
@@ -799,11 +799,18 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int 
                                                                   [GemmShape<BI, BJ, BK, WI, WJ>::NJ]) {
     using S = GemmShape<BI, BJ, BK, WI, WJ>;
     constexpr int PITCH = BJ + 8;  // bf16 per LDS row
-    static_assert((size_t)BI * PITCH * 2 <= 160 * 1024, "tile fits in LDS");
+    static_assert((size_t)BI * PITCH * 2 + BI * 4 <= 160 * 1024, "tile and row map fit in LDS");
+    static_assert(S::THREADS >= BI, "one thread per tile row loads the row map");
     bf16_t* t = reinterpret_cast<bf16_t*>(smem);
+    int* rows_at = reinterpret_cast<int*>(t + BI * PITCH);  // routed: the tile's destination rows
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wi = wave / WJ, wj = wave % WJ;
+    // one map load per tile row, in flight while the accumulators go to LDS
+    // (the store loop below would otherwise wait on a global load per chunk)
+    int dest = -1;
+    if (p.rowmap && (int)threadIdx.x < BI && i0 + (int)threadIdx.x < p.I) dest = p.rowmap[i0 + threadIdx.x];
     __syncthreads();  // every wave is past its last main-loop LDS read
+    if (p.rowmap && (int)threadIdx.x < BI) rows_at[threadIdx.x] = dest;
 #pragma unroll
     for (int a = 0; a < S::MI; ++a)
 #pragma unroll
@@ -823,7 +830,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int 
         const int il = c / CPR, jc = c % CPR;
         if (il < rows && 8 * jc < cols) {
             const u32x4 v = *reinterpret_cast<const u32x4*>(t + il * PITCH + 8 * jc);
-            const int64_t gi = p.rowmap ? p.rowmap[i0 + il] : i0 + il;  // routed: scatter rows
+            const int64_t gi = p.rowmap ? rows_at[il] : i0 + il;  // routed: scatter rows
             if (!p.rowmap || (uint64_t)gi < (uint64_t)p.map_rows)
                 __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p.C + gi * p.ldc + j0 + 8 * jc));
         }
@@ -1059,9 +1066,13 @@ static hipError_t launch_gemm_dual(GemmParams p1, GemmParams p2, int cus, float*
 // Grouped GEMM: C[rowmap[r]] = A[rowmap[r]] . bk[g]^T for the rows r of each
 // group g (group_off on the device, so the host never waits for the counts).
 // The grid covers ceil(m / BI) + ngroups - 1 tile-rows, the most the groups can
-// need; every block counts the tile-rows the groups do need, maps itself onto
-// those as in map_work (so the XCDs share the work evenly and the spare blocks
-// spread over all of them), then finds its group by walking the group sizes.
+// need; every block counts the tile-rows the groups do need, takes its tile of
+// those (the XCDs get even contiguous ranges, the spare blocks spread over all
+// of them) and finds the tile's group by walking the group sizes.  Measured on
+// MI355X at 8192 tokens, 5120 -> 17408, six candidates: group-ordered tiles and
+// the row map staged once per tile took six Gumbel-sized groups from 1.380 to
+// 1.338 ms and six 256-aligned groups from 1.236-1.260 to 1.214 ms (one group
+// 1.145 ms, the dense forward 1.147 ms).
 template <class C>
 __global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(C::OCC, C::OCC)))
 void routed_gemm_kernel(GemmParams p, int tile_rows) {
@@ -1081,21 +1092,29 @@ void routed_gemm_kernel(GemmParams p, int tile_rows) {
         used_rows += (h - l + BI - 1) / BI;
     }
     used_rows = min(used_rows, tile_rows);
-    const WorkItem w = map_work(blockIdx.x, used_rows, tiles_j, 0, p.cus_per_xcd, false, 0, 8);
-    if (w.idle) return;
-    int tm = w.tm, g = 0, lo = 0, hi = 0;
+    // the XCDs take contiguous ranges of the tiles (as in map_work); the tiles
+    // run group by group, each group's tile-rows in blocks of kGroupM with the
+    // tile-rows fastest, so the tiles an XCD runs at once read one candidate's
+    // B panels and share them in its L2
+    const int x = blockIdx.x % 8, local = blockIdx.x / 8;
+    const XcdPlan pl = xcd_plan(x, used_rows * tiles_j, p.cus_per_xcd, 0, false);
+    if (local >= pl.items()) return;
+    int tile = pl.t0 + local, tm = 0, tn = 0, g = 0, lo = 0, hi = 0;
     for (; g < p.ngroups; ++g) {
         lo = min(max(p.group_off[g], hi), p.map_rows);
         hi = min(max(p.group_off[g + 1], lo), p.map_rows);
         const int nt = (hi - lo + BI - 1) / BI;
-        if (tm < nt) break;
-        tm -= nt;
+        if (tile < nt * tiles_j) {
+            tile_coords(tile, nt, tiles_j, kGroupM, tm, tn);
+            break;
+        }
+        tile -= nt * tiles_j;
     }
     if (g >= p.ngroups) return;
     GemmParams q = p;
     q.B = p.bk[g];
     q.I = hi;  // end of the group's rows in rowmap
-    const int i0 = lo + tm * BI, j0 = w.tn * BJ;
+    const int i0 = lo + tm * BI, j0 = tn * BJ;
     f32x16 acc[S::MI][S::NJ];
     gemm_mainloop_pp<LA, LB, BI, BJ, BK, WI, WJ, C::DEPTH, C::SWITCH, C::COPY>(q, i0, j0, 0, q.K, smem, acc);
     store_tile_lds<BI, BJ, BK, WI, WJ>(q, i0, j0, smem, acc);
