@@ -72,6 +72,15 @@ __device__ __forceinline__ uint32_t f2bf2(float a, float b) {
     return r;
 }
 
+// Two values -> packed bf16 pair by v_cvt_pk_bf16_f32 alone: f2bf2's bits for
+// every non-NaN value; a NaN comes out as some quiet NaN.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    const f2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2_t));
+}
+
 __device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 __device__ __forceinline__ uint32_t rd_u8(const uint8_t* p) { return p[0]; }

@@ -811,15 +811,20 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, int i0, int 
     if (p.rowmap && (int)threadIdx.x < BI && i0 + (int)threadIdx.x < p.I) dest = p.rowmap[i0 + threadIdx.x];
     __syncthreads();  // every wave is past its last main-loop LDS read
     if (p.rowmap && (int)threadIdx.x < BI) rows_at[threadIdx.x] = dest;
+    // rows il and il + 1 of a lane's column convert as one pair
+    // (v_cvt_pk_bf16_f32: one instruction for two values, where the software
+    // rounding takes six per value; a NaN stays a quiet NaN)
 #pragma unroll
     for (int a = 0; a < S::MI; ++a)
 #pragma unroll
         for (int b = 0; b < S::NJ; ++b) {
             const int jl = wj * S::WTJ + 32 * b + (lane & 31);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
+            for (int r = 0; r < 16; r += 2) {
                 const int il = wi * S::WTI + 32 * a + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                t[il * PITCH + jl] = f2bf(acc[a][b][r]);
+                const uint32_t h = pk_bf16(acc[a][b][r], acc[a][b][r + 1]);
+                t[il * PITCH + jl] = (bf16_t)h;
+                t[(il + 1) * PITCH + jl] = (bf16_t)(h >> 16);
             }
         }
     __syncthreads();
