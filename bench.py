@@ -399,7 +399,8 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
     16x64 query heads, 4 KV heads, SwiGLU 3072, vocabulary 151936 tied; every
     Linear and the embedding gated over 6 candidates; Q8_0 teacher), batch
     4 x 2048 uniform-random token ids: tokens per second of the whole step
-    (forwards, CE + KL + size loss, backward, clip, AdamW)."""
+    (forwards, CE + KL + size loss, backward, clip, AdamW).  The teacher's
+    forward runs on a second stream beside the student's."""
     from voodoo_quant.training import step as st
 
     cfg = st.DecoderConfig()
@@ -412,7 +413,8 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
     x = torch.randint(0, cfg.vocab, (b, s), device=dev, generator=g)
     y = torch.randint(0, cfg.vocab, (b, s), device=dev, generator=g)
     tr = st.GateTrainer(student, teacher, replaced,
-                        st.StepConfig(max_steps=max(steps + warmup, 2), prefetch_mix=prefetch),
+                        st.StepConfig(max_steps=max(steps + warmup, 2), prefetch_mix=prefetch,
+                                      teacher_stream=True),
                         total_8bit_bytes=float(cfg.gated_weights()))
     for _ in range(warmup):
         tr.step(x, y)

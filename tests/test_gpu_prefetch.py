@@ -1,10 +1,13 @@
-"""The W_eff prefetch (layers.MixPrefetch: every mix of a step on a second
-stream, event-fenced ahead of its GEMMs) leaves the training step unchanged.
+"""The step's side streams leave the training step unchanged: the W_eff
+prefetch (layers.MixPrefetch: every mix of a step on a second stream,
+event-fenced ahead of its GEMMs) and the teacher's forward on a second stream
+beside the student's (StepConfig.teacher_stream, step._forwards).
 
 The mix is deterministic and the prefetched W_eff is the same buffer contents
-the inline mix would write, so on the SwiGLU stack (no attention) the gates
-after three steps, and every loss on the way, must be bit-identical.  The
-decoder step adds torch's fused attention; its gates must agree to 1e-6.
+the inline mix would write, and the teacher's output does not depend on the
+stream it runs on, so on the SwiGLU stack (no attention) the gates after three
+steps, and every loss on the way, must be bit-identical.  The decoder step adds
+torch's fused attention; its gates must agree to 1e-6.
 """
 
 import pytest
@@ -18,7 +21,7 @@ def _need_gpu():
         pytest.skip("no ROCm device")
 
 
-def _stack_run(prefetch: bool, steps: int = 3):
+def _stack_run(prefetch: bool, steps: int = 3, teacher_stream: bool = False):
     from voodoo_quant.training import step as st
 
     dev = torch.device("cuda", 0)
@@ -26,9 +29,11 @@ def _stack_run(prefetch: bool, steps: int = 3):
     types = ["Q2_K", "Q4_K", "Q6_K", "Q8_0"]
     student, teacher, replaced = st.build_stack(cfg, types, dev, seed=3)
     tr = st.StackTrainer(student, teacher, replaced,
-                         st.StepConfig(max_steps=10, temp_start=2.0, temp_end=0.5, prefetch_mix=prefetch),
+                         st.StepConfig(max_steps=10, temp_start=2.0, temp_end=0.5, prefetch_mix=prefetch,
+                                       teacher_stream=teacher_stream),
                          total_8bit_bytes=float(cfg.gated_weights()))
     assert (tr.prefetch is not None) == prefetch
+    assert (tr.t_stream is not None) == teacher_stream
     x = torch.randn(256, cfg.hidden, device=dev, generator=torch.Generator(device=dev).manual_seed(4))
     x = x.to(torch.bfloat16)
     losses = []
@@ -79,3 +84,37 @@ def test_prefetched_decoder_step_matches():
     diff = float((res[0] - res[1]).abs().max())
     print(f"[prefetch] decoder gates max |diff| {diff:.3e}", flush=True)
     assert diff < 1e-6
+
+
+def test_teacher_stream_stack_step_is_bit_identical():
+    _need_gpu()
+    g0, l0, _ = _stack_run(False)
+    g1, l1, _ = _stack_run(False, teacher_stream=True)
+    assert torch.equal(l0.view(torch.int32), l1.view(torch.int32)), (l0, l1)
+    assert torch.equal(g0.view(torch.int32), g1.view(torch.int32)), (g0 - g1).abs().max()
+
+
+def test_teacher_stream_decoder_step_matches():
+    _need_gpu()
+    from voodoo_quant.training import step as st
+
+    dev = torch.device("cuda", 0)
+    cfg = st.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, mlp=512, vocab=1024)
+    types = ["Q3_K", "Q4_K", "Q8_0"]
+    gates, losses = [], []
+    for side in (False, True):
+        student, teacher, replaced = st.build_models(cfg, types, dev, seed=7, packed=True)
+        tr = st.GateTrainer(student, teacher, replaced, st.StepConfig(max_steps=10, teacher_stream=side),
+                            total_8bit_bytes=float(cfg.gated_weights()))
+        assert (tr.t_stream is not None) == side
+        g = torch.Generator(device=dev).manual_seed(8)
+        x = torch.randint(0, cfg.vocab, (2, 128), device=dev, generator=g)
+        y = torch.randint(0, cfg.vocab, (2, 128), device=dev, generator=g)
+        out = [tr.step(x, y) for _ in range(2)]
+        torch.cuda.synchronize()
+        gates.append(torch.stack([m.gates.detach().clone().float() for m in replaced.values()]))
+        losses.append(torch.stack([torch.stack([o["lm"], o["kl"]]).float() for o in out]))
+    diff = float((gates[0] - gates[1]).abs().max())
+    ldiff = float((losses[0] - losses[1]).abs().max())
+    print(f"[teacher stream] decoder gates max |diff| {diff:.3e}, losses {ldiff:.3e}", flush=True)
+    assert diff < 1e-6 and ldiff < 1e-5

@@ -442,6 +442,13 @@ class StepConfig:
     # (1.4 ms of 2.1 ms per 0.8B step) but share their CUs, and the step time
     # does not move (60.8 ms both ways; stress step 157 ms both ways)
     prefetch_mix: bool = False
+    # run the teacher's forward on a second stream (default priority) beside
+    # the student's forward, fenced by events (_forwards); the step's values
+    # do not change.  Measured on MI355X: the 0.8B-class decoder step 58.3 ->
+    # 57.7 ms (its small products and attention leave room on the chip), the
+    # SwiGLU stress stack 155.5 -> 156.9 ms (its teacher's 4096 x 14336
+    # products fill the chip alone), so it is left to the caller
+    teacher_stream: bool = False
 
 
 class GateTrainer:
@@ -460,6 +467,7 @@ class GateTrainer:
         self.step_index = 0
         # after the bank: the prefetch reads each module's probabilities row
         self.prefetch = _make_prefetch(cfg, student)
+        self.t_stream = _make_teacher_stream(cfg, student)
 
     def step(self, x: torch.Tensor, y: torch.Tensor) -> dict[str, torch.Tensor]:
         """One optimizer step on batch (x, y); returns the detached losses (no host sync)."""
@@ -476,9 +484,7 @@ class GateTrainer:
                 lm, kl = trainer.chunked_forward_loss(self.student, self.teacher, x, y, t, c.logits_chunk)
                 lm_loss, distill = torch.tensor(lm), torch.tensor(kl)
             else:
-                logits = self.student(x)
-                with torch.no_grad():
-                    t_logits = self.teacher(x)
+                logits, t_logits = _forwards(self.student, self.teacher, x, self.t_stream)
                 fused = (c.fused_loss and logits.is_cuda and logits.dtype == torch.bfloat16
                          and logits.size(-1) % 8 == 0)
                 losses = trainer.distill_losses_fused if fused else trainer.distill_losses
@@ -517,6 +523,36 @@ def prefetch_groups(model: nn.Module) -> list[list[nn.Module]]:
             # the forward stacks a product only when it can; otherwise its members run singly
             groups += [g] if len(g) == 1 or (GROUP_PROJECTIONS and layers.groupable(g)) else [[m] for m in g]
     return groups
+
+
+def _make_teacher_stream(cfg: StepConfig, student: nn.Module):
+    if not cfg.teacher_stream or cfg.logits_chunk > 0:
+        return None
+    dev = next(student.parameters()).device
+    return torch.cuda.Stream(device=dev) if dev.type == "cuda" else None
+
+
+def _forwards(student: nn.Module, teacher: nn.Module, x: torch.Tensor, t_stream):
+    """The student's forward (recorded for autograd) and the teacher's (no
+    grad).  With t_stream the teacher runs on that stream beside the student:
+    the side stream first waits for the work queued before the step (x and
+    anything that wrote the teacher's inputs), and the caller's stream waits
+    for the teacher before it reads the teacher's output.  Both outputs are
+    the ones the sequential order gives."""
+    if t_stream is None:
+        s_out = student(x)
+        with torch.no_grad():
+            t_out = teacher(x)
+        return s_out, t_out
+    cur = torch.cuda.current_stream(x.device)
+    t_stream.wait_stream(cur)
+    x.record_stream(t_stream)  # x may be freed by the caller before the teacher is done
+    with torch.cuda.stream(t_stream), torch.no_grad():
+        t_out = teacher(x)
+    s_out = student(x)
+    cur.wait_stream(t_stream)
+    t_out.record_stream(cur)  # allocated on the side stream, read and freed on the caller's
+    return s_out, t_out
 
 
 def _make_prefetch(cfg: StepConfig, student: nn.Module):
@@ -631,6 +667,7 @@ class StackTrainer:
         self.target_bytes = cfg.target_fraction * total_8bit_bytes
         self.step_index = 0
         self.prefetch = _make_prefetch(cfg, student)
+        self.t_stream = _make_teacher_stream(cfg, student)
 
     def step(self, x: torch.Tensor) -> dict[str, torch.Tensor]:
         c = self.cfg
@@ -640,9 +677,8 @@ class StackTrainer:
         if self.prefetch:
             self.prefetch.launch()
         try:
-            y = self.student(x)
-            with torch.no_grad():
-                t = self.teacher(x).float()
+            y, t = _forwards(self.student, self.teacher, x, self.t_stream)
+            t = t.float()
             mse = ((y.float() - t) ** 2).mean() / (t ** 2).mean()
             gated = bank_bytes if bank_bytes is not None else layers.total_effective_bytes(self.replaced)
             size = trainer.size_loss(gated.to(x.device), self.target_bytes, c.size_tolerance)
