@@ -14,6 +14,8 @@
 // the cross-entropy, as F.cross_entropy's default ignore_index).
 // Backward: one more pass writes
 //   dS = g_ce / N_ce (softmax(s) - onehot(y)) + g_kl T / N (softmax(s/T) - softmax(t/T)).
+// At T = 1 (the trainer's default) s/T is s: both passes then take one
+// exponential of s per logit instead of two (UNIT).
 #include <cfloat>
 
 #include "vq_internal.h"
@@ -76,6 +78,7 @@ __device__ __forceinline__ RowAcc shfl_acc(const RowAcc& a, int lane) {
 
 }  // namespace
 
+template <bool UNIT>
 __global__ __launch_bounds__(kLossThreads) void distill_fwd_kernel(const bf16_t* __restrict__ S,
                                                                    const bf16_t* __restrict__ Tl,
                                                                    const int64_t* __restrict__ labels, int64_t V,
@@ -98,23 +101,30 @@ __global__ __launch_bounds__(kLossThreads) void distill_fwd_kernel(const bf16_t*
             ct = fmaxf(ct, tv[j]);
         }
         // rescale the running sums once per 8 values
-        const float ns = fmaxf(a.ms, cs), nq = fmaxf(a.mq, cs * inv_tau), nt = fmaxf(a.mt, ct * inv_tau);
+        const float ns = fmaxf(a.ms, cs), nt = fmaxf(a.mt, UNIT ? ct : ct * inv_tau);
         a.zs *= fexp(a.ms - ns);
-        a.zq *= fexp(a.mq - nq);
         const float ft = fexp(a.mt - nt);
         a.zt *= ft;
         a.at *= ft;
         a.ms = ns;
-        a.mq = nq;
         a.mt = nt;
+        if constexpr (!UNIT) {
+            const float nq = fmaxf(a.mq, cs * inv_tau);
+            a.zq *= fexp(a.mq - nq);
+            a.mq = nq;
+        }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             a.zs += fexp(sv[j] - ns);
-            a.zq += fexp(sv[j] * inv_tau - nq);
-            const float e = fexp(tv[j] * inv_tau - nt);
+            if constexpr (!UNIT) a.zq += fexp(sv[j] * inv_tau - a.mq);
+            const float e = fexp((UNIT ? tv[j] : tv[j] * inv_tau) - nt);
             a.zt += e;
             a.at += e > 0.f ? e * (tv[j] - sv[j]) : 0.f;
         }
+    }
+    if constexpr (UNIT) {
+        a.mq = a.ms;
+        a.zq = a.zs;
     }
     // wave then workgroup reduction (fixed order)
 #pragma unroll
@@ -174,6 +184,7 @@ __global__ __launch_bounds__(256) void distill_reduce_kernel(const float* __rest
     }
 }
 
+template <bool UNIT>
 __global__ __launch_bounds__(kLossThreads) void distill_bwd_kernel(const bf16_t* __restrict__ S,
                                                                    const bf16_t* __restrict__ Tl,
                                                                    const int64_t* __restrict__ labels, int64_t V,
@@ -196,8 +207,10 @@ __global__ __launch_bounds__(kLossThreads) void distill_bwd_kernel(const bf16_t*
         load8_bf16(t + i, tv);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float ps = fexp(sv[j] - lse_s) - ((i + j) == y ? 1.f : 0.f);
-            const float dq = fexp(sv[j] * inv_tau - lse_q) - fexp(tv[j] * inv_tau - lse_t);
+            const float es = fexp(sv[j] - lse_s);
+            const float ps = es - ((i + j) == y ? 1.f : 0.f);
+            const float dq = UNIT ? es - fexp(tv[j] - lse_t)
+                                  : fexp(sv[j] * inv_tau - lse_q) - fexp(tv[j] * inv_tau - lse_t);
             g[j] = a * ps + b * dq;
         }
         uint4 q;
@@ -214,8 +227,12 @@ hipError_t launch_distill_fwd(const bf16_t* S, const bf16_t* T, const int64_t* l
     float* stats = ws;
     float* row_loss = ws + 3 * rows;
     float* aux = ws + 5 * rows;
-    distill_fwd_kernel<<<dim3((unsigned)rows), kLossThreads, 0, s>>>(S, T, labels, V, 1.0f / temperature,
-                                                                      temperature * temperature, stats, row_loss);
+    if (temperature == 1.0f)
+        distill_fwd_kernel<true><<<dim3((unsigned)rows), kLossThreads, 0, s>>>(S, T, labels, V, 1.0f, 1.0f, stats,
+                                                                            row_loss);
+    else
+        distill_fwd_kernel<false><<<dim3((unsigned)rows), kLossThreads, 0, s>>>(
+            S, T, labels, V, 1.0f / temperature, temperature * temperature, stats, row_loss);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     distill_reduce_kernel<<<1, 256, 0, s>>>(row_loss, labels, rows, out, aux);
@@ -224,8 +241,12 @@ hipError_t launch_distill_fwd(const bf16_t* S, const bf16_t* T, const int64_t* l
 
 hipError_t launch_distill_bwd(const bf16_t* S, const bf16_t* T, const int64_t* labels, int64_t rows, int64_t V,
                               float temperature, const float* grad_out, bf16_t* dS, const float* ws, hipStream_t s) {
-    distill_bwd_kernel<<<dim3((unsigned)rows), kLossThreads, 0, s>>>(S, T, labels, V, 1.0f / temperature, temperature,
-                                                                      ws, ws + 5 * rows, grad_out, dS);
+    if (temperature == 1.0f)
+        distill_bwd_kernel<true><<<dim3((unsigned)rows), kLossThreads, 0, s>>>(S, T, labels, V, 1.0f, 1.0f, ws,
+                                                                            ws + 5 * rows, grad_out, dS);
+    else
+        distill_bwd_kernel<false><<<dim3((unsigned)rows), kLossThreads, 0, s>>>(
+            S, T, labels, V, 1.0f / temperature, temperature, ws, ws + 5 * rows, grad_out, dS);
     return hipGetLastError();
 }
 
