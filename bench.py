@@ -496,6 +496,8 @@ def main() -> int:
     ap.add_argument("--prefetch-mix", action="store_true",
                     help="train/stress steps mix each W_eff ahead on a second stream (layers.MixPrefetch)")
     ap.add_argument("--no-peaks", action="store_true", help="skip the MFMA / HBM probe kernels")
+    ap.add_argument("--no-sweeps", action="store_true",
+                    help="skip the per-shape and few-token sweeps (profiles of the headline shape alone)")
     ap.add_argument("--fused-workload", action="store_true",
                     help="only run the fused and materialising few-token products (16 tokens, 3 passes each)")
     ap.add_argument("--shapes-workload", action="store_true",
@@ -657,7 +659,7 @@ def main() -> int:
 
     del qbytes, w_eff, y, dx, ws, fws, out
     torch.cuda.empty_cache()
-    shapes = shape_sweep(torch, dev, gen)
+    shapes = None if args.no_sweeps else shape_sweep(torch, dev, gen)
     train = None
     if not args.no_train:
         torch.cuda.empty_cache()
@@ -670,7 +672,7 @@ def main() -> int:
         copy_calibration(torch, dev)
 
     peaks = None if args.no_peaks else measured_peaks(torch, dev)
-    fused = fused_compare(torch, dev, gen)
+    fused = None if args.no_sweeps else fused_compare(torch, dev, gen)
 
     cpu = extra = None
     if not args.no_cpu_baseline:
