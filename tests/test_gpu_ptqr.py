@@ -73,6 +73,9 @@ def _routed(hip, types, qbs, x, routing, n, d_pad):
     (1000, 520, 1000, 1024, SIX, "random"),                                # multi-tile, ragged groups
     (777, 264, 512, 512, ["Q2_K", "Q6_K", "Q8_0"], "one-empty"),            # a candidate with no tokens
     (300, 256, 256, 256, ["Q4_K", "Q8_0"], "all-one"),                      # every token to one candidate
+    # groups of more than 8 tile-rows run in blocks of 8 tile-rows (the last block shorter)
+    (2600, 264, 256, 256, ["Q4_K", "Q8_0"], "all-one"),                     # one group of 11 tile-rows
+    (3000, 264, 256, 256, ["Q2_K", "Q5_K", "Q8_0"], "skewed"),              # 85% of the tokens to one candidate
 ])
 def test_routed_linear_forward_and_backward(hip, m, n, d, d_pad, types, mode):
     print(f"[ptqr] m={m} n={n} d={d} types={types} mode={mode}", flush=True)
@@ -84,6 +87,9 @@ def test_routed_linear_forward_and_backward(hip, m, n, d, d_pad, types, mode):
         routing = torch.randint(0, k, (m,), generator=g)
     elif mode == "one-empty":
         routing = torch.randint(0, k - 1, (m,), generator=g)  # candidate k-1 gets no token
+    elif mode == "skewed":
+        routing = torch.where(torch.rand(m, generator=g) < 0.85, torch.tensor(1),
+                              torch.randint(0, k, (m,), generator=g))
     else:
         routing = torch.full((m,), k - 1, dtype=torch.int64)
     probs = torch.softmax(torch.randn(k, generator=g), 0)
