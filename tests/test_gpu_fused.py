@@ -4,7 +4,7 @@ memory) against the oracle, through the C ABI.
 The fused kernels mix with fma(p_k dl, u, acc) instead of the reference's
 separately rounded fp32 ops, so their W_eff tile is within a bf16 ulp of the
 oracle's, not bit-identical: Y and dX are held to 1e-2 relative L2 of the
-fp64 product with the oracle's W_eff, and to 1e-2 of the
+fp64 product with the oracle's W_eff (the stated tolerance), and to 1e-2 of the
 materialising path's outputs.  Results must be bitwise deterministic.
 """
 

@@ -1,7 +1,7 @@
 """GPU parity of libvoodoo_hip against the oracle (needs an MI355X).
 
 Bars: dequant and the W_eff mixture bit-exact; Y, dX and dL/dp within 1e-2
-relative L2 of the fp32/fp64 oracle (bf16 products).
+relative L2 of the fp32/fp64 oracle (bf16 products; the path's stated tolerance).
 Every call goes through the C ABI (ctypes binding of include/voodoo_hip.h).
 """
 
