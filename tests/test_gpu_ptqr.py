@@ -165,3 +165,30 @@ def test_module_toggle(hip):
     p = lin.soft_probs().detach()
     w_mix = sum(p[k] * cands[k] for k in range(len(types)))
     assert _rel(y_mix.cpu(), (x.float() @ w_mix.t()).cpu()) < TOL
+
+
+def test_routed_forward_ignores_out_of_range_map_entries(hip):
+    """A routing map entry outside [0, m) reads zero rows and writes nothing,
+    and group offsets are clamped to [0, m] and made non-decreasing, so a bad
+    map or bad offsets cannot make the kernel touch memory outside x and y."""
+    m, n, d = 100, 264, 256
+    types = ["Q4_K", "Q6_K", "Q8_0"]
+    qbs, ws = _rtn(types, n, d, seed=5)
+    x = torch.randn(m, d, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    cands = [w.to(torch.bfloat16).cuda() for w in ws]
+    perm = torch.arange(m, dtype=torch.int32)
+    perm[7] = -5
+    perm[60] = m + 3
+    goff = torch.tensor([0, 50, 30, 200], dtype=torch.int32)  # clamped: [0, 50), empty, [50, 100)
+    sentinel = torch.full((m, n), 7.0, dtype=torch.bfloat16)
+    y = sentinel.cuda()
+    hip.routed_linear_fwd(x.cuda(), cands, perm.cuda(), goff.cuda(), n, d, y)
+    torch.cuda.synchronize()
+    yc = y.cpu().double()
+    for r in range(m):
+        if r in (7, 60):  # no map entry names these rows: left as they were
+            assert torch.equal(y[r].cpu(), sentinel[r]), r
+            continue
+        w = ws[0] if r < 50 else ws[2]
+        ref = x[r].double() @ w.to(torch.bfloat16).double().t()
+        assert _rel(yc[r], ref) < TOL, r
