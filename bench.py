@@ -269,14 +269,19 @@ def fused_compare(torch, dev, gen, tokens=(1, 16, 32, 64), reps: int = 20, passe
             dx = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
             wsf = torch.empty(max(_hip.fused_workspace_bytes(m, n, d, False), 16), dtype=torch.uint8, device=dev)
             wsd = torch.empty(max(_hip.fused_workspace_bytes(m, n, d, True), 16), dtype=torch.uint8, device=dev)
+            # the materialised path with the workspaces the module passes (K-split
+            # parts of the last tiles: at a few tokens the products have few tiles)
+            wmf = torch.empty(max(_hip.fwd_workspace_bytes(m, n, d), 16), dtype=torch.uint8, device=dev)
+            wmb = torch.empty(max(_hip.bwd_workspace_bytes(m, n, d, d, len(ids), False), 16), dtype=torch.uint8,
+                              device=dev)
 
             def fused():
                 _hip.gated_linear_fwd_fused(x, ids, qb, probs, n, d, y, wsf)
                 _hip.gated_linear_dx_fused(dy, ids, qb, probs, d, d, dx, wsd)
 
             def materialised():
-                _hip.gated_linear_fwd(x, ids, qb, probs, n, d, w, y)
-                _hip.gated_linear_bwd(dy, x, ids, qb, probs, n, d, w, dx, None, None)
+                _hip.gated_linear_fwd(x, ids, qb, probs, n, d, w, y, wmf)
+                _hip.gated_linear_bwd(dy, x, ids, qb, probs, n, d, w, dx, None, wmb)
 
             if passes:
                 for fn in (fused, materialised):

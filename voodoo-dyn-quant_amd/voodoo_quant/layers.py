@@ -165,13 +165,14 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
 # built tile by tile in LDS, never written) replace mix + GEMM when a call
 # has at most FUSED_MAX_TOKENS tokens and the tensor at most
 # FUSED_MAX_WEIGHTS weights.  Measured on MI355X, K = 6 (Q2_K..Q8_0),
-# forward + dX at 1-32 tokens: fused against materialised 34 vs 47 us
-# (1024 x 1024), 53 vs 101 (4096 x 1024), 45 vs 57 (1024 x 4096), 105 vs 181
-# (8192 x 2048), 100 vs 121 (4096 x 4096); the 27B projections (31-89M
-# weights) are 5-10% slower fused, and at 64 tokens the two paths trade
-# places, so both limits sit at the last point where fused won everywhere.
+# forward + dX at 1-32 tokens, the materialised path with the workspaces this
+# module passes (K-split last tiles): fused against materialised 35-37 vs 44 us
+# (1024 x 1024), 43-49 vs 50 (3072 -> 1024), 50-53 vs 51 (1024 -> 3072),
+# 71-75 vs 61 (1024 -> 6144), 105-110 vs 73-74 (4096 x 4096), 208-210 vs
+# 99-101 (5120 -> 6144).  At 64 tokens fused loses from 3M weights on, so both
+# limits sit at the last point where fused did not lose.
 FUSED_MAX_TOKENS = 32
-FUSED_MAX_WEIGHTS = 1 << 24
+FUSED_MAX_WEIGHTS = 1 << 22
 
 
 def use_fused(m: int, n: int, d_pad: int) -> bool:
