@@ -87,3 +87,26 @@ def test_synthetic_candidates_are_valid_and_centred():
         w = torch.from_numpy(cdequant.oracle_dequant(qt, qb.numpy(), 16 * 512))
         assert torch.isfinite(w).all()
         assert abs(float(w.mean())) < 0.01 and 0.01 < float(w.std()) < 0.08 and float(w.abs().max()) < 0.2
+
+
+def test_teacher_stream_is_opt_in_and_cpu_runs_in_order():
+    """The teacher's side stream is off by default, and on a CPU model the
+    forwards run in order (no stream), giving the two outputs unchanged."""
+    assert st.StepConfig().teacher_stream is False
+    student, teacher = nn.Linear(4, 3), nn.Linear(4, 3)
+    assert st._make_teacher_stream(st.StepConfig(teacher_stream=True), student) is None
+    x = torch.randn(2, 4)
+    s_out, t_out = st._forwards(student, teacher, x, None)
+    assert torch.equal(s_out, student(x)) and torch.equal(t_out, teacher(x))
+    assert s_out.requires_grad and not t_out.requires_grad
+
+
+def test_fused_path_region():
+    """Few-token products take the fused kernels only up to 32 tokens and
+    2^22 weights (the measured crossover against mix + GEMM)."""
+    from voodoo_quant import layers
+
+    assert layers.use_fused(1, 1024, 1024) and layers.use_fused(32, 2048, 2048)
+    assert not layers.use_fused(33, 1024, 1024)
+    assert not layers.use_fused(16, 4096, 4096)
+    assert not layers.use_fused(0, 1024, 1024)
