@@ -509,3 +509,72 @@ def test_gate_bank_rows_bytes_and_release(isolated_cache):
     bank.release()
     for n, m in mods.items():
         assert m.gates.requires_grad and torch.equal(m.gates.detach(), doubled[n])
+
+
+# ------------------------------------------------------------------ precache (reference tools/precache.py:88-229)
+class _TinyDecoder(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        g = torch.Generator().manual_seed(7)
+        layer = torch.nn.Module()
+        layer.self_attn = torch.nn.Module()
+        layer.self_attn.q_proj = torch.nn.Linear(512, 64, bias=False)
+        layer.mlp = torch.nn.Module()
+        layer.mlp.up_proj = torch.nn.Linear(512, 128, bias=False)
+        layer.linear_attn = torch.nn.Module()
+        layer.linear_attn.in_proj_a = torch.nn.Linear(512, 32, bias=False)  # kept F32 by the recipe
+        layer.norm = torch.nn.LayerNorm(512)                                # 1-D: never gated
+        layer.odd = torch.nn.Linear(100, 16, bias=False)                    # rows of 100: not block-aligned
+        self.model = torch.nn.Module()
+        self.model.layers = torch.nn.ModuleList([layer])
+        for p in self.parameters():
+            if p.dim() == 2:
+                p.data = torch.randn(p.shape, generator=g) * 0.02
+
+
+def test_precache_selection_and_reuse(isolated_cache, monkeypatch):
+    from voodoo_quant import precache
+
+    monkeypatch.setattr(layers, "find_libggml", lambda: None)
+    monkeypatch.setattr(precache, "find_libggml", lambda: None)
+    model = _TinyDecoder()
+    plan = precache.selectable_tensors(model, ["Q8_0", "Q4_K"], attention_candidates=["Q8_0"])
+    assert plan == {"model.layers.0.self_attn.q_proj": ["Q8_0"], "model.layers.0.mlp.up_proj": ["Q8_0", "Q4_K"]}
+    rep = precache.precache_model(model, ["Q8_0", "Q4_K"], attention_candidates=["Q8_0"], workers=2)
+    assert (rep.tensors, rep.built, rep.cached, rep.errors, rep.source) == (2, 3, 0, [], "rtn")
+    # RTN bytes sit under their own key only, and equal the encoder's output
+    w = model.model.layers[0].mlp.up_proj.weight.detach()
+    wh = cache.tensor_hash(w)
+    assert cache.load_candidates("model.layers.0.mlp.up_proj", ["Q8_0"], "lazy", wh, "none", isolated_cache) == {}
+    hit = cache.load_candidates("model.layers.0.mlp.up_proj", ["Q8_0", "Q4_K"], cache.RTN_MODE, wh, "none",
+                                isolated_cache)
+    for qt in ("Q8_0", "Q4_K"):
+        assert torch.equal(hit[qt].reshape(-1), rtn.rtn_quantize_tensor(w.float(), qt).reshape(-1))
+    # a gated layer over the same weight loads the precached bytes
+    lin = layers.MixedQuantLinear(512, 128, ["Q8_0", "Q4_K"], w.clone(), tensor_name="model.layers.0.mlp.up_proj")
+    assert lin.candidate_source == "cache_rtn"
+    assert torch.equal(lin._qweight_1, hit["Q4_K"].reshape(-1))
+    # a second pass finds everything
+    rep2 = precache.precache_model(model, ["Q8_0", "Q4_K"], attention_candidates=["Q8_0"])
+    assert (rep2.built, rep2.cached) == (0, 3)
+
+
+def test_precache_reports_failed_types(isolated_cache, monkeypatch):
+    from voodoo_quant import precache
+
+    monkeypatch.setattr(layers, "find_libggml", lambda: None)
+    monkeypatch.setattr(precache, "find_libggml", lambda: None)
+    real = layers._quantize_candidates
+
+    def flaky(padded, imatrix, types):
+        if types == ["Q4_K"]:
+            raise ValueError("quantizer failed")
+        return real(padded, imatrix, types)
+
+    monkeypatch.setattr(layers, "_quantize_candidates", flaky)
+    rep = precache.precache_model(_TinyDecoder(), ["Q8_0", "Q4_K"])
+    assert rep.built == 2 and len(rep.errors) == 2 and all("Q4_K" in e for e in rep.errors)
+    # decoded entries need libggml or a ROCm device
+    if not torch.cuda.is_available():
+        rep = precache.precache_model(_TinyDecoder(), ["Q8_0"], lazy=False, root=isolated_cache / "dq")
+        assert rep.built == 0 and len(rep.errors) == 2 and "ROCm" in rep.errors[0]
