@@ -41,6 +41,67 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int64_t iters, float* __
     sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// The same stream on data that changes from one MFMA to the next: four
+// fragment pairs of random bf16 values (uniform in [-2, 2), as fresh GEMM
+// operands would be), chain c multiplying pair (c % 4, (c + 1) % 4), so no two
+// consecutive instructions see the same operands.  The matrix pipe's power
+// depends on how many operand bits toggle; constant operands draw the least
+// and let the clock run highest.  Block 0's first lane records the shader
+// clock (s_memtime) and the constant-rate real-time clock (s_memrealtime)
+// before and after its loop, so the host can state the clock the chip held.
+__device__ __forceinline__ uint32_t hash32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352dU;
+    x ^= x >> 15;
+    x *= 0x846ca68bU;
+    x ^= x >> 16;
+    return x;
+}
+
+template <bool kRandom>
+__global__ __launch_bounds__(256) void mfma_clock_kernel(int64_t iters, uint32_t seed, float* __restrict__ sink,
+                                                         uint64_t* __restrict__ clocks) {
+    const int lane = threadIdx.x & 63;
+    constexpr int kSets = kRandom ? 4 : 1;
+    bf16x8_t a[kSets], b[kSets];
+#pragma unroll
+    for (int s = 0; s < kSets; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if constexpr (kRandom) {
+                const uint32_t h = hash32(seed ^ hash32((uint32_t)(blockIdx.x * 256 + threadIdx.x) * 64u + s * 16u + i));
+                a[s][i] = (__bf16)((float)(int32_t)h * (2.0f / 2147483648.0f));
+                b[s][i] = (__bf16)((float)(int32_t)hash32(h + 0x9e3779b9U) * (2.0f / 2147483648.0f));
+            } else {
+                a[s][i] = (__bf16)(1.0f + 0.001f * (float)(lane + i));
+                b[s][i] = (__bf16)(0.5f - 0.001f * (float)(lane - i));
+            }
+        }
+    f32x16 acc[kChains];
+#pragma unroll
+    for (int c = 0; c < kChains; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+    const bool timer = blockIdx.x == 0 && threadIdx.x == 0;
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int64_t it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int c = 0; c < kChains; ++c)
+            acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c % kSets], b[(c + 1) % kSets], acc[c], 0, 0, 0);
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChains; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[c][r];
+    sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
+    if (timer) {
+        clocks[0] = t1 - t0;
+        clocks[1] = r1 - r0;
+    }
+}
+
 // Streams `n16` 16-byte words: each thread reads a strided set and keeps an
 // XOR, written once per thread (so the loads are not removed).
 __global__ __launch_bounds__(256) void hbm_read_kernel(const u32x4* __restrict__ src, int64_t n16,
@@ -82,6 +143,28 @@ int vq_probe_mfma_blocks(void) { return 2 * cus(); }
 int vq_probe_mfma(int64_t iters, float* sink, void* stream) {
     mfma_peak_kernel<<<dim3(vq_probe_mfma_blocks()), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(iters, sink);
     return (int)hipGetLastError();
+}
+
+// The MFMA probe with a clock reading: `random` selects the random-operand
+// stream (else the constant operands of vq_probe_mfma).  Same grid, FLOP and
+// sink as vq_probe_mfma; clocks[0] = shader-clock ticks and clocks[1] =
+// real-time-clock ticks over block 0's loop (2 words on the device).
+int vq_probe_mfma_clock(int random, int64_t iters, uint32_t seed, float* sink, uint64_t* clocks, void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (random)
+        mfma_clock_kernel<true><<<dim3(vq_probe_mfma_blocks()), dim3(256), 0, s>>>(iters, seed, sink, clocks);
+    else
+        mfma_clock_kernel<false><<<dim3(vq_probe_mfma_blocks()), dim3(256), 0, s>>>(iters, seed, sink, clocks);
+    return (int)hipGetLastError();
+}
+
+// Rate of the clock s_memrealtime reads, in kHz (0 when the runtime does not say).
+int vq_probe_wall_clock_khz(void) {
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+        return 0;
+    return khz;
 }
 
 // Workgroups of the HBM probes (a few per CU, grid-stride loops).
