@@ -198,6 +198,20 @@ int vq_gated_linear_group_bwd(const uint16_t *dy, const uint16_t *x, int64_t m, 
                               const uint16_t *w_eff, uint16_t *dx, float *const *dprobs, void *workspace,
                               int64_t ws_bytes, void *stream);
 
+/* vq_gated_linear_group_bwd with the gate gradients finished on `gate_stream`:
+ * the products run on `stream`; the dot pass over dW parts (where the shape
+ * takes it) and the fixed-order reduce into dprobs run on `gate_stream`,
+ * after an event fence on `stream`.  The caller keeps the workspace and
+ * dprobs alive until `gate_stream` has passed them, and makes its readers of
+ * dprobs wait for `gate_stream`.  Values are bit-identical to
+ * vq_gated_linear_group_bwd's.  No counterpart in the reference (its gate
+ * gradients come from autograd in stream order, layers.py:354-363). */
+int vq_gated_linear_group_bwd_gate_stream(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t d, int64_t d_pad,
+                                          int nmembers, const int64_t *n, const int *ncand, const int *qtypes,
+                                          const void *const *qbytes, const uint16_t *w_eff, uint16_t *dx,
+                                          float *const *dprobs, void *workspace, int64_t ws_bytes, void *stream,
+                                          void *gate_stream);
+
 /* Decoder-layer glue of the gate-training step (the model the trainer runs
  * around the gated projections; no counterpart in voodoo_quant itself).
  * vq_rope_qkv_fwd: qkv [B*S][(Hq + 2 Hkv) D] bf16 (stacked q/k/v projection
@@ -270,6 +284,18 @@ int vq_gated_linear_bwd(const uint16_t *dy, const uint16_t *x, int64_t m, int64_
                         int ncand, const int *qtypes, const void *const *qbytes, const float *probs,
                         const uint16_t *w_eff, uint16_t *dx, float *dprobs, void *workspace, int64_t ws_bytes,
                         void *stream);
+
+/* vq_gated_linear_bwd with the gate gradient finished on `gate_stream` (the
+ * dot pass over dW parts where the shape takes it, and the fixed-order
+ * reduce into dprobs), after an event fence on `stream`, where the products
+ * run.  The caller keeps the workspace and dprobs alive until `gate_stream`
+ * has passed them and makes readers of dprobs wait for `gate_stream`.
+ * Values are bit-identical to vq_gated_linear_bwd's.  No counterpart in the
+ * reference (layers.py:354-363 finishes the gate gradient in stream order). */
+int vq_gated_linear_bwd_gate_stream(const uint16_t *dy, const uint16_t *x, int64_t m, int64_t n, int64_t d,
+                                    int64_t d_pad, int ncand, const int *qtypes, const void *const *qbytes,
+                                    const float *probs, const uint16_t *w_eff, uint16_t *dx, float *dprobs,
+                                    void *workspace, int64_t ws_bytes, void *stream, void *gate_stream);
 
 /* Bytes of the library's static scratch (per device, held until the process
  * ends) behind vq_gated_linear_bwd_static. */

@@ -118,3 +118,83 @@ def test_teacher_stream_decoder_step_matches():
     ldiff = float((losses[0] - losses[1]).abs().max())
     print(f"[teacher stream] decoder gates max |diff| {diff:.3e}, losses {ldiff:.3e}", flush=True)
     assert diff < 1e-6 and ldiff < 1e-5
+
+
+def _captured_grads(monkeypatch, make_trainer, run_step, steps: int = 2):
+    """The bank gradients every optimizer step of `steps` sees, and the losses."""
+    from voodoo_quant.training import trainer
+
+    seen = []
+    real = trainer.gate_optimizer_step
+
+    def capture(trainable, opt, sched, max_norm=1.0):
+        seen.append(torch.cat([p.grad.detach().reshape(-1).double().clone() for p in trainable]))
+        real(trainable, opt, sched, max_norm=max_norm)
+
+    monkeypatch.setattr(trainer, "gate_optimizer_step", capture)
+    tr = make_trainer()
+    losses = [run_step(tr) for _ in range(steps)]
+    torch.cuda.synchronize()
+    monkeypatch.setattr(trainer, "gate_optimizer_step", real)
+    return seen, losses, tr
+
+
+def test_deferred_gate_grads_stack_step_matches(monkeypatch):
+    """Gate gradients finished on the bank's second stream: each step's bank
+    gradient matches the in-order backward's to 1e-6 of its largest entry (the
+    deferred dL/dp values are the same reduces; only the softmax Jacobian's
+    arithmetic order differs), and the first step's losses are bit-equal."""
+    _need_gpu()
+    from voodoo_quant.training import step as st
+
+    dev = torch.device("cuda", 0)
+    cfg = st.StackConfig(blocks=2, hidden=512, mlp=1024)
+    types = ["Q2_K", "Q4_K", "Q6_K", "Q8_0"]
+    x = torch.randn(256, cfg.hidden, device=dev, generator=torch.Generator(device=dev).manual_seed(4))
+    x = x.to(torch.bfloat16)
+    res = []
+    for defer in (False, True):
+        student, teacher, replaced = st.build_stack(cfg, types, dev, seed=3)
+        scfg = st.StepConfig(max_steps=10, temp_start=2.0, temp_end=0.5, defer_gate_grads=defer)
+        seen, losses, tr = _captured_grads(
+            monkeypatch,
+            lambda: st.StackTrainer(student, teacher, replaced, scfg, total_8bit_bytes=float(cfg.gated_weights())),
+            lambda tr: torch.stack([v.float() for k, v in tr.step(x).items() if k in ("mse", "size")]))
+        assert bool(tr.bank._streams) == defer
+        res.append((seen, losses))
+    (g0, l0), (g1, l1) = res
+    assert torch.equal(l0[0].view(torch.int32), l1[0].view(torch.int32)), (l0[0], l1[0])
+    for a, b in zip(g0, g1):
+        rel = float((a - b).abs().max() / a.abs().max())
+        print(f"[defer] stack bank grad max rel diff {rel:.3e}", flush=True)
+        assert rel < 1e-6
+
+
+def test_deferred_gate_grads_decoder_step_matches(monkeypatch):
+    """The same on the decoder step (stacked q/k/v and gate/up, single o and
+    down, the parts path's dot pass; the embedding keeps autograd)."""
+    _need_gpu()
+    from voodoo_quant.training import step as st
+
+    dev = torch.device("cuda", 0)
+    cfg = st.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, mlp=512, vocab=1024)
+    types = ["Q3_K", "Q4_K", "Q8_0"]
+    g = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randint(0, cfg.vocab, (2, 128), device=dev, generator=g)
+    y = torch.randint(0, cfg.vocab, (2, 128), device=dev, generator=g)
+    res = []
+    for defer in (False, True):
+        student, teacher, replaced = st.build_models(cfg, types, dev, seed=7, packed=True)
+        scfg = st.StepConfig(max_steps=10, defer_gate_grads=defer)
+        seen, losses, tr = _captured_grads(
+            monkeypatch,
+            lambda: st.GateTrainer(student, teacher, replaced, scfg, total_8bit_bytes=float(cfg.gated_weights())),
+            lambda tr: torch.stack([v.float() for k, v in tr.step(x, y).items() if k in ("lm", "kl")]))
+        assert bool(tr.bank._streams) == defer
+        res.append((seen, losses))
+    (g0, l0), (g1, l1) = res
+    for a, b in zip(g0, g1):
+        rel = float((a - b).abs().max() / a.abs().max())
+        print(f"[defer] decoder bank grad max rel diff {rel:.3e}", flush=True)
+        assert rel < 1e-5
+    assert float((l0[0] - l1[0]).abs().max()) < 1e-5

@@ -110,3 +110,44 @@ def test_fused_path_region():
     assert not layers.use_fused(33, 1024, 1024)
     assert not layers.use_fused(16, 4096, 4096)
     assert not layers.use_fused(0, 1024, 1024)
+
+
+def test_softmax_rows_backward_matches_autograd():
+    """The Jacobian the gate bank applies to deferred gate gradients equals
+    autograd's through softmax(z / T), at the annealing schedule's ends."""
+    from voodoo_quant.training import trainer
+
+    g = torch.Generator().manual_seed(5)
+    for t in (2.0, 1.0, 0.1):
+        z = torch.randn(7, 6, generator=g, dtype=torch.float64, requires_grad=True)
+        up = torch.randn(7, 6, generator=g, dtype=torch.float64)
+        p = torch.softmax(z / t, dim=1)
+        p.backward(up)
+        got = trainer.softmax_rows_backward(p.detach(), up, t)
+        assert torch.allclose(got, z.grad, rtol=1e-12, atol=1e-14), t
+        # rows sum to zero: the softmax is shift-invariant
+        assert float(got.sum(dim=1).abs().max()) < 1e-12
+
+
+def test_gate_bank_defers_only_on_a_rocm_device():
+    """Off the GPU a deferring bank sets no sinks and finish() is a no-op."""
+    from voodoo_quant.training import trainer
+
+    class _M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.num_candidates = 3
+            self.gates = torch.nn.Parameter(torch.zeros(3))
+
+        def _bytes_per_candidate(self):
+            return [1.0, 2.0, 3.0]
+
+    mods = [_M(), _M()]
+    bank = trainer.GateBank(mods, defer_gate_grads=True)
+    b = bank.begin(1.0)
+    assert all(m.__dict__.get("_gate_sink") is None for m in mods)
+    b.backward()
+    bank.finish()
+    bank.end()
+    (param,) = bank.parameters()
+    assert param.grad is not None and param.grad.shape == (2, 3)

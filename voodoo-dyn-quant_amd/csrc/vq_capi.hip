@@ -203,10 +203,12 @@ GateWs gate_ws(int64_t m, int64_t d, int64_t d_pad, int nsets, const int64_t* n,
 // dX and gate products (one launch when both run), the fixed-order reduce.
 // partials: gw.part_bytes of gate partials; tail_ws: dX's split-tail partial
 // tiles, or NULL to run dX's tiles whole; dwp: the gate's dW parts when
-// gw.parts.
+// gw.parts.  gs: the stream the gate gradient is finished on (the parts
+// path's dot pass and the reduce), fenced after the products on s.
 int run_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
             const vq::CandSet& cs, const float* probs, const uint16_t* w_eff, uint16_t* remix_buf, uint16_t* dx,
-            float* dprobs, const GateWs& gw, float* partials, float* tail_ws, float* dwp, hipStream_t s) {
+            float* dprobs, const GateWs& gw, float* partials, float* tail_ws, float* dwp, hipStream_t s,
+            hipStream_t gs) {
     int rc = VQ_OK;
     const int ncand = cs.ncand;
     // the parts path when the shape takes it and its buffer is there
@@ -221,7 +223,7 @@ int run_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t
         if (m > 0 && dprobs) {
             // both products in one launch: each fills the other's last round
             rc = hip_check(vq::launch_gemm_dx_gate(dy, w, d_pad, dx, x, group_of(cs, n), partials, (int)m, (int)n,
-                                                   (int)d, tail_ws, parts, s),
+                                                   (int)d, tail_ws, parts, s, gs),
                            "dX + gate GEMM launch");
             if (rc != VQ_OK) return rc;
         } else if (m > 0) {
@@ -233,18 +235,22 @@ int run_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t
     if (dprobs) {
         if (m == 0) {
             // no tokens: dL/dp = 0 (written by the reduce over zero partials)
-            rc = hip_check(vq::launch_gate_reduce(partials, 0, ncand, dprobs, s), "gate reduce launch");
+            rc = hip_check(vq::stream_fence(s, gs), "stream fence");
+            if (rc == VQ_OK) rc = hip_check(vq::launch_gate_reduce(partials, 0, ncand, dprobs, gs), "gate reduce launch");
             return rc == VQ_OK ? ok() : rc;
         }
         if (!dx) {
-            rc = hip_check(vq::launch_gemm_gate(dy, x, group_of(cs, n), partials, (int)m, (int)n, (int)d, parts, s),
-                           "gate GEMM launch");
+            rc = hip_check(
+                vq::launch_gemm_gate(dy, x, group_of(cs, n), partials, (int)m, (int)n, (int)d, parts, s, gs),
+                "gate GEMM launch");
             if (rc != VQ_OK) return rc;
         }
         // partials: one per dot block on the parts path, one per gate block otherwise
         const int64_t nparts = parts ? vq::gate_dot_blocks(1, &n, d_pad / 256)
                                      : vq::gate_partial_count((int)m, (int)n, (int)d);
-        rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, s), "gate reduce launch");
+        rc = hip_check(vq::stream_fence(s, gs), "stream fence");
+        if (rc != VQ_OK) return rc;
+        rc = hip_check(vq::launch_gate_reduce(partials, nparts, ncand, dprobs, gs), "gate reduce launch");
         if (rc != VQ_OK) return rc;
     }
     return ok();
@@ -644,6 +650,14 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
                         int ncand, const int* qtypes, const void* const* qbytes, const float* probs,
                         const uint16_t* w_eff, uint16_t* dx, float* dprobs, void* workspace, int64_t ws_bytes,
                         void* stream) {
+    return vq_gated_linear_bwd_gate_stream(dy, x, m, n, d, d_pad, ncand, qtypes, qbytes, probs, w_eff, dx, dprobs,
+                                           workspace, ws_bytes, stream, stream);
+}
+
+int vq_gated_linear_bwd_gate_stream(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d,
+                                    int64_t d_pad, int ncand, const int* qtypes, const void* const* qbytes,
+                                    const float* probs, const uint16_t* w_eff, uint16_t* dx, float* dprobs,
+                                    void* workspace, int64_t ws_bytes, void* stream, void* gate_stream) {
     int rc = check_bwd(dy, x, m, n, d, d_pad, ncand, qtypes, qbytes, w_eff, dx);
     if (rc != VQ_OK) return rc;
     const bool remix = dx != nullptr && w_eff == nullptr;
@@ -669,7 +683,7 @@ int vq_gated_linear_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, int64_
         remix_buf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + part_bytes + tail_bytes + gw.dwp_bytes);
     }
     return run_bwd(dy, x, m, n, d, d_pad, make_set(ncand, qtypes, qbytes, d_pad), probs, w_eff, remix_buf, dx, dprobs,
-                   gw, partials, tail_ws, dwp, static_cast<hipStream_t>(stream));
+                   gw, partials, tail_ws, dwp, static_cast<hipStream_t>(stream), static_cast<hipStream_t>(gate_stream));
 }
 
 int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t n, int64_t d, int64_t d_pad,
@@ -695,7 +709,7 @@ int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m,
     if (tail_bytes > 0 && part_bytes + tail_bytes <= kStaticScratchBytes)
         tail_ws = reinterpret_cast<float*>(scratch_ptr + part_bytes);
     return run_bwd(dy, x, m, n, d, d_pad, make_set(ncand, qtypes, qbytes, d_pad), nullptr, w_eff, nullptr, dx, dprobs,
-                   gw, reinterpret_cast<float*>(scratch_ptr), tail_ws, nullptr, s);
+                   gw, reinterpret_cast<float*>(scratch_ptr), tail_ws, nullptr, s, s);
 }
 
 int64_t vq_gated_linear_fused_workspace(int64_t m, int64_t n, int64_t d, int dx) {
@@ -792,6 +806,15 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
                               const int64_t* n, const int* ncand, const int* qtypes, const void* const* qbytes,
                               const uint16_t* w_eff, uint16_t* dx, float* const* dprobs, void* workspace,
                               int64_t ws_bytes, void* stream) {
+    return vq_gated_linear_group_bwd_gate_stream(dy, x, m, d, d_pad, nmembers, n, ncand, qtypes, qbytes, w_eff, dx,
+                                                 dprobs, workspace, ws_bytes, stream, stream);
+}
+
+int vq_gated_linear_group_bwd_gate_stream(const uint16_t* dy, const uint16_t* x, int64_t m, int64_t d, int64_t d_pad,
+                                          int nmembers, const int64_t* n, const int* ncand, const int* qtypes,
+                                          const void* const* qbytes, const uint16_t* w_eff, uint16_t* dx,
+                                          float* const* dprobs, void* workspace, int64_t ws_bytes, void* stream,
+                                          void* gate_stream) {
     vq::CandGroup cg;
     int64_t n_total = 0;
     int rc = check_group(nmembers, n, ncand, qtypes, qbytes, d, d_pad, cg, n_total);
@@ -804,7 +827,7 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
     if (dprobs)
         for (int i = 0; i < nmembers; ++i)
             if (!dprobs[i]) return fail(VQ_ERR_NULL, "dprobs[%d] is NULL", i);
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStream_t s = static_cast<hipStream_t>(stream), gs = static_cast<hipStream_t>(gate_stream);
     const int64_t need = vq_gated_linear_group_bwd_workspace(m, d, nmembers, n, ncand);
     const int nslot = nmembers * cg.kstride;
     const GateWs gw = gate_ws(m, d, d_pad, nmembers, n, n_total, nslot, true);
@@ -833,7 +856,7 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
     if (dx && m > 0) {
         if (dprobs)
             rc = hip_check(vq::launch_gemm_dx_gate(dy, w_eff, d_pad, dx, x, cg, partials, (int)m, (int)n_total, (int)d,
-                                                   tail_ws, dwp, s),
+                                                   tail_ws, dwp, s, gs),
                            "dX + gate GEMM launch");
         else
             rc = hip_check(vq::launch_gemm_dx(dy, w_eff, d_pad, dx, (int)m, (int)n_total, (int)d, tail_ws, s),
@@ -842,7 +865,7 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
     }
     if (dprobs) {
         if (!dx && m > 0) {
-            rc = hip_check(vq::launch_gemm_gate(dy, x, cg, partials, (int)m, (int)n_total, (int)d, dwp, s),
+            rc = hip_check(vq::launch_gemm_gate(dy, x, cg, partials, (int)m, (int)n_total, (int)d, dwp, s, gs),
                            "gate GEMM launch");
             if (rc != VQ_OK) return rc;
         }
@@ -850,7 +873,9 @@ int vq_gated_linear_group_bwd(const uint16_t* dy, const uint16_t* x, int64_t m, 
         const int64_t nparts = m == 0 ? 0
                                : dwp  ? vq::gate_dot_blocks(nmembers, n, d_pad / 256)
                                       : vq::gate_partial_count((int)m, (int)n_total, (int)d);
-        rc = hip_check(vq::launch_gate_reduce_group(partials, nparts, nslot, out, nmembers, s), "gate reduce launch");
+        rc = hip_check(vq::stream_fence(s, gs), "stream fence");
+        if (rc != VQ_OK) return rc;
+        rc = hip_check(vq::launch_gate_reduce_group(partials, nparts, nslot, out, nmembers, gs), "gate reduce launch");
         if (rc != VQ_OK) return rc;
     }
     return ok();

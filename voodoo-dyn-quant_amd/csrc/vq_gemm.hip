@@ -24,6 +24,32 @@ using GateL = DmaNS<256, 64, 64 * kWaves>;
 using GateLA = DmaNS<256, 64, 64 * kWaves, 1>;  // weight rows permuted for the gate epilogue
 constexpr int kGateBI = 256, kGateBJ = 256;
 
+hipError_t stream_fence(hipStream_t from, hipStream_t to) {
+    if (from == to) return hipSuccess;
+    constexpr int kDevices = 64, kRing = 8;
+    static thread_local hipEvent_t ring[kDevices][kRing];  // held until the thread ends
+    static thread_local int next[kDevices];
+    int dev = 0;
+    hipError_t e = from ? hipStreamGetDevice(from, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kDevices) return hipErrorInvalidDevice;
+    hipEvent_t& ev = ring[dev][next[dev]];
+    next[dev] = (next[dev] + 1) % kRing;
+    if (!ev) {  // created on the stream's device
+        int cur = 0;
+        if ((e = hipGetDevice(&cur)) != hipSuccess) return e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess) {
+            ev = nullptr;
+            return e;
+        }
+    }
+    if ((e = hipEventRecord(ev, from)) != hipSuccess) return e;
+    return hipStreamWaitEvent(to, ev, 0);
+}
+
 int device_cus() {
     static int cus = 0;
     if (cus == 0) {
@@ -170,14 +196,14 @@ static GemmParams parts_params(const bf16_t* dY, const bf16_t* X, float* dwp, in
 }
 
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
-                            int D, float* dwp, hipStream_t s) {
+                            int D, float* dwp, hipStream_t s, hipStream_t ds) {
     if (dwp) {
         const int np = gate_parts(M, N, D);
         if (np == 0) return hipErrorInvalidValue;
-        const hipError_t e =
-            launch_gemm_cfg<GatePartsCfg>(parts_params(dY, X, dwp, np, M, N, D), device_cus(), nullptr, s);
+        hipError_t e = launch_gemm_cfg<GatePartsCfg>(parts_params(dY, X, dwp, np, M, N, D), device_cus(), nullptr, s);
+        if (e == hipSuccess) e = stream_fence(s, ds);
         if (e != hipSuccess) return e;
-        return launch_gate_dot(cg, N, D, dwp, np, partials, s);
+        return launch_gate_dot(cg, N, D, dwp, np, partials, ds);
     }
     if (any_iq(cg))
         return launch_gemm_cfg<GateCfg, true>(gate_params(dY, X, cg, partials, M, N, D), device_cus(), nullptr, s);
@@ -188,15 +214,16 @@ hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& 
 // the longer ones, first).
 hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
                                const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
-                               float* dwp, hipStream_t s) {
+                               float* dwp, hipStream_t s, hipStream_t ds) {
     if (dwp) {
         const int np = gate_parts(M, N, D);
         if (np == 0) return hipErrorInvalidValue;
-        const hipError_t e = launch_gemm_dual<DxCfg, GatePartsCfg>(dx_params(dY, W, ldw, dX, M, N, D),
-                                                                   parts_params(dY, X, dwp, np, M, N, D),
-                                                                   device_cus(), tail_ws, s);
+        hipError_t e = launch_gemm_dual<DxCfg, GatePartsCfg>(dx_params(dY, W, ldw, dX, M, N, D),
+                                                             parts_params(dY, X, dwp, np, M, N, D), device_cus(),
+                                                             tail_ws, s);
+        if (e == hipSuccess) e = stream_fence(s, ds);
         if (e != hipSuccess) return e;
-        return launch_gate_dot(cg, N, D, dwp, np, partials, s);
+        return launch_gate_dot(cg, N, D, dwp, np, partials, ds);
     }
     if (any_iq(cg))
         return launch_gemm_dual<DxCfg, GateCfg, true>(dx_params(dY, W, ldw, dX, M, N, D),

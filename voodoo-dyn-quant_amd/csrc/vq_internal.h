@@ -38,6 +38,11 @@ int64_t fwd_tail_bytes(int M, int N, int D);      // forward split-tail workspac
 hipError_t launch_gemm_dx(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, int M, int N, int D,
                           float* tail_ws, hipStream_t s);
 int device_cus();
+// Makes stream `to` wait for everything queued on `from` so far (no-op when
+// they are the same stream).  The events come from a small per-thread,
+// per-device ring: hipStreamWaitEvent takes an event's state when it is
+// called, so an event may be recorded again after it has been waited on.
+hipError_t stream_fence(hipStream_t from, hipStream_t to);
 int64_t gate_partial_count(int M, int N, int D);  // gate partials per candidate (one per grid block)
 int64_t dx_tail_bytes(int M, int N, int D);       // dX split-tail workspace bytes
 // Where the gate reduce writes dL/dp: member i's candidate k from partial
@@ -59,12 +64,13 @@ int64_t gate_parts_bytes(int M, int N, int D);
 int64_t gate_dot_blocks(int nsets, const int64_t* n, int64_t row_groups);
 // dwp: NULL for the fused epilogue (partials: gate_partial_count blocks),
 // else gate_parts_bytes of workspace for the parts path (partials:
-// gate_dot_blocks blocks); either way launch_gate_reduce* sums the partials
+// gate_dot_blocks blocks); either way launch_gate_reduce* sums the partials.
+// ds: the stream the parts path's dot pass runs on, after a fence on s.
 hipError_t launch_gemm_gate(const bf16_t* dY, const bf16_t* X, const CandGroup& cg, float* partials, int M, int N,
-                            int D, float* dwp, hipStream_t s);
+                            int D, float* dwp, hipStream_t s, hipStream_t ds);
 hipError_t launch_gemm_dx_gate(const bf16_t* dY, const bf16_t* W, int64_t ldw, bf16_t* dX, const bf16_t* X,
                                const CandGroup& cg, float* partials, int M, int N, int D, float* tail_ws,
-                               float* dwp, hipStream_t s);
+                               float* dwp, hipStream_t s, hipStream_t ds);
 // partials[block][nsets * kstride] = sum over the block's weights of
 // dW[n][d] * W_k[n][d], dW the sum of the parts dwp in part order
 hipError_t launch_gate_dot(const CandGroup& cg, int N, int D, const float* dwp, int parts, float* partials,

@@ -37,6 +37,8 @@ _SIGNATURES = [
     ("vq_gated_linear_group_fwd", _i, [_p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_group_bwd_workspace", _i64, [_i64, _i64, _i, _p, _p]),
     ("vq_gated_linear_group_bwd", _i, [_p, _p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    ("vq_gated_linear_group_bwd_gate_stream", _i,
+     [_p, _p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p]),
     ("vq_rope_qkv_fwd", _i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p]),
     ("vq_rope_qkv_bwd", _i, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _p, _p, _p]),
     ("vq_swiglu_fwd", _i, [_p, _i64, _i64, _p, _p]),
@@ -50,6 +52,8 @@ _SIGNATURES = [
     ("vq_gated_linear_fwd", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_bwd_workspace", _i64, [_i64, _i64, _i64, _i64, _i, _i]),
     ("vq_gated_linear_bwd", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    ("vq_gated_linear_bwd_gate_stream", _i,
+     [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p]),
     ("vq_gated_linear_bwd_static", _i, [_p, _p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p]),
     ("vq_gated_linear_fused_workspace", _i64, [_i64, _i64, _i64, _i]),
     ("vq_gated_linear_fwd_fused", _i, [_p, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _i64, _p]),
@@ -280,17 +284,24 @@ def group_bwd_workspace_bytes(m: int, d: int, members) -> int:
 
 
 def gated_linear_group_bwd(dy: torch.Tensor, x: torch.Tensor, members, d_pad: int, w_eff: torch.Tensor | None,
-                           dx: torch.Tensor | None, dprobs: list | None, workspace: torch.Tensor | None) -> None:
+                           dx: torch.Tensor | None, dprobs: list | None, workspace: torch.Tensor | None,
+                           gate_stream: torch.cuda.Stream | None = None) -> None:
+    """gate_stream: finish the gate gradients (dot pass, reduce into dprobs)
+    on that stream, after a fence on the current one."""
     m, d = x.shape
     ns, nc, types, qbs = _group_arrays(members)
     dp = None
     if dprobs is not None:
         dp = (ctypes.c_void_p * len(members))(*[_dev_ptr(t, f"dprobs[{i}]") for i, t in enumerate(dprobs)])
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    _check(lib().vq_gated_linear_group_bwd(_dev_ptr(dy, "dy"), _dev_ptr(x, "x"), m, d, d_pad, len(members), ns, nc,
-                                           types, qbs, _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"), dp,
-                                           _dev_ptr(workspace, "workspace"), ws_bytes, _stream(dy.device)),
-           "vq_gated_linear_group_bwd")
+    args = (_dev_ptr(dy, "dy"), _dev_ptr(x, "x"), m, d, d_pad, len(members), ns, nc, types, qbs,
+            _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"), dp, _dev_ptr(workspace, "workspace"), ws_bytes,
+            _stream(dy.device))
+    if gate_stream is None:
+        _check(lib().vq_gated_linear_group_bwd(*args), "vq_gated_linear_group_bwd")
+    else:
+        _check(lib().vq_gated_linear_group_bwd_gate_stream(*args, gate_stream.cuda_stream),
+               "vq_gated_linear_group_bwd_gate_stream")
 
 
 def mix_only_call(members, probs, d_pad: int, w_eff: torch.Tensor, stream: int):
@@ -438,15 +449,20 @@ def bwd_workspace_bytes(m: int, n: int, d: int, d_pad: int, ncand: int, need_w_e
 
 def gated_linear_bwd(dy: torch.Tensor, x: torch.Tensor, ggml_types, qbytes, probs: torch.Tensor | None, n: int,
                      d_pad: int, w_eff: torch.Tensor | None, dx: torch.Tensor | None,
-                     dprobs: torch.Tensor | None, workspace: torch.Tensor | None) -> None:
+                     dprobs: torch.Tensor | None, workspace: torch.Tensor | None,
+                     gate_stream: torch.cuda.Stream | None = None) -> None:
+    """gate_stream: finish the gate gradient (dot pass, reduce into dprobs)
+    on that stream, after a fence on the current one."""
     m, d = x.shape
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    _check(lib().vq_gated_linear_bwd(_dev_ptr(dy, "dy"), _dev_ptr(x, "x"), m, n, d, d_pad, len(ggml_types),
-                                     _int_array(ggml_types), _ptr_array(qbytes, "qbytes"),
-                                     _dev_ptr(probs, "probs"), _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"),
-                                     _dev_ptr(dprobs, "dprobs"), _dev_ptr(workspace, "workspace"), ws_bytes,
-                                     _stream(dy.device)),
-           "vq_gated_linear_bwd")
+    args = (_dev_ptr(dy, "dy"), _dev_ptr(x, "x"), m, n, d, d_pad, len(ggml_types), _int_array(ggml_types),
+            _ptr_array(qbytes, "qbytes"), _dev_ptr(probs, "probs"), _dev_ptr(w_eff, "w_eff"), _dev_ptr(dx, "dx"),
+            _dev_ptr(dprobs, "dprobs"), _dev_ptr(workspace, "workspace"), ws_bytes, _stream(dy.device))
+    if gate_stream is None:
+        _check(lib().vq_gated_linear_bwd(*args), "vq_gated_linear_bwd")
+    else:
+        _check(lib().vq_gated_linear_bwd_gate_stream(*args, gate_stream.cuda_stream),
+               "vq_gated_linear_bwd_gate_stream")
 
 
 def fused_workspace_bytes(m: int, n: int, d: int, dx: bool) -> int:

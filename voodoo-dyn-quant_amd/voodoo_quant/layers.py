@@ -181,18 +181,33 @@ def use_fused(m: int, n: int, d_pad: int) -> bool:
     return 0 < m <= FUSED_MAX_TOKENS and n * d_pad <= FUSED_MAX_WEIGHTS
 
 
+def _finish_on_gate_stream(stream, rows, grads, keep) -> None:
+    """The gate gradients `grads`, reduced on `stream` by the library, are
+    added to the sink rows there; every buffer that stream still reads or
+    writes is marked in use by it, so the allocator does not hand it out again
+    before the stream has passed it."""
+    with torch.cuda.stream(stream):
+        for row, g in zip(rows, grads):
+            row.add_(g)
+    for t in list(grads) + list(keep):
+        if t is not None:
+            t.record_stream(stream)
+
+
 class GatedLinearFunction(Function):
     """y = x W_eff^T with W_eff = sum_k probs_k W_k, on libvoodoo_hip.
 
-    forward(ctx, x [M, D] bf16, probs [K] fp32, meta, premixed, *qbytes) -> y [M, N] bf16
-    where meta = (ggml type ids, N, D_pad) and premixed is None or this
+    forward(ctx, x [M, D] bf16, probs [K] fp32, meta, premixed, sink, *qbytes) -> y [M, N] bf16
+    where meta = (ggml type ids, N, D_pad), premixed is None or this
     step's W_eff [N, D_pad] already mixed from probs (see
-    :class:`MixPrefetch`).  The backward returns dX and dL/dprobs; qbytes
-    receive no gradient (they are constants, as the candidates are for the
-    reference's ``_MixedWeightFunction``)."""
+    :class:`MixPrefetch`), and sink is None or (row, stream): a deferred gate
+    gradient (see ``trainer.GateBank``), finished on `stream` and added to
+    `row` instead of being returned.  The backward returns dX and dL/dprobs;
+    qbytes receive no gradient (they are constants, as the candidates are for
+    the reference's ``_MixedWeightFunction``)."""
 
     @staticmethod
-    def forward(ctx, x, probs, meta, premixed, *qbytes):
+    def forward(ctx, x, probs, meta, premixed, sink, *qbytes):
         types, n, d_pad = meta
         x2 = _aligned(x)
         m, d = x2.shape
@@ -220,12 +235,15 @@ class GatedLinearFunction(Function):
         ctx.meta = meta
         ctx.qbytes = qbytes
         ctx.probs_device = probs.device
+        ctx.sink = sink
         return y
 
     @staticmethod
     def backward(ctx, dy):
         types, n, d_pad = ctx.meta
-        need_dx, need_dp = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        sink = ctx.sink
+        gs = sink[1] if sink is not None else None
+        need_dx, need_dp = ctx.needs_input_grad[0], ctx.needs_input_grad[1] or sink is not None
         dy2 = _aligned(dy.to(torch.bfloat16))
         if ctx.fused:
             x2, p = ctx.saved_tensors
@@ -240,9 +258,13 @@ class GatedLinearFunction(Function):
                 dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device)
                 nbytes = _hip.bwd_workspace_bytes(m, n, d, d_pad, len(types), False)
                 ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
-                _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, None, None, dprobs, ws)
-                dprobs = dprobs.to(ctx.probs_device)
-            return (dx, dprobs, None, None) + (None,) * len(ctx.qbytes)
+                _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, None, None, dprobs, ws, gs)
+                if sink is not None:
+                    _finish_on_gate_stream(gs, [sink[0]], [dprobs], [ws])
+                    dprobs = None
+                else:
+                    dprobs = dprobs.to(ctx.probs_device)
+            return (dx, dprobs, None, None, None) + (None,) * len(ctx.qbytes)
         x2, p, w_eff = ctx.saved_tensors
         dx = torch.empty_like(x2) if need_dx else None
         dprobs = torch.empty(len(types), dtype=torch.float32, device=x2.device) if need_dp else None
@@ -251,10 +273,14 @@ class GatedLinearFunction(Function):
             nbytes = _hip.bwd_workspace_bytes(x2.shape[0], n, x2.shape[1], d_pad, len(types), False)
             ws = torch.empty(nbytes, dtype=torch.uint8, device=x2.device)
         if need_dx or need_dp:
-            _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, w_eff, dx, dprobs, ws)
-        if dprobs is not None:
+            _hip.gated_linear_bwd(dy2, x2, types, ctx.qbytes, p, n, d_pad, w_eff, dx, dprobs, ws,
+                                  gs if dprobs is not None else None)
+        if sink is not None and dprobs is not None:
+            _finish_on_gate_stream(gs, [sink[0]], [dprobs], [ws])
+            dprobs = None
+        elif dprobs is not None:
             dprobs = dprobs.to(ctx.probs_device)
-        return (dx, dprobs, None, None) + (None,) * len(ctx.qbytes)
+        return (dx, dprobs, None, None, None) + (None,) * len(ctx.qbytes)
 
 
 class GatedLinearGroupFunction(Function):
@@ -264,13 +290,15 @@ class GatedLinearGroupFunction(Function):
     backward is one launch for dX (which also sums the members' input
     gradients) and every member's gate gradients.
 
-    forward(ctx, x [M, D] bf16, meta, premixed, *probs_then_qbytes) -> y [M, sum N] bf16
+    forward(ctx, x [M, D] bf16, meta, premixed, sinks, *probs_then_qbytes) -> y [M, sum N] bf16
     with meta = (((ggml types, N) per member), D_pad), premixed None or the
     step's stacked W_eff [sum N, D_pad] mixed ahead (see :class:`MixPrefetch`),
-    then each member's probs [K_i] and finally every member's qbytes in order."""
+    sinks None or one (row, stream) per member (deferred gate gradients, as
+    for :class:`GatedLinearFunction`), then each member's probs [K_i] and
+    finally every member's qbytes in order."""
 
     @staticmethod
-    def forward(ctx, x, meta, premixed, *tensors):
+    def forward(ctx, x, meta, premixed, sinks, *tensors):
         members, d_pad = meta
         nm = len(members)
         probs, qbytes = tensors[:nm], tensors[nm:]
@@ -296,6 +324,7 @@ class GatedLinearGroupFunction(Function):
         ctx.spec = spec
         ctx.meta = meta
         ctx.probs_devices = [p.device for p in probs]
+        ctx.sinks = sinks
         return y
 
     @staticmethod
@@ -303,8 +332,10 @@ class GatedLinearGroupFunction(Function):
         x2, w_eff = ctx.saved_tensors
         members, d_pad = ctx.meta
         nm = len(members)
+        sinks = ctx.sinks
+        gs = sinks[0][1] if sinks is not None else None
         need_dx = ctx.needs_input_grad[0]
-        need_dp = any(ctx.needs_input_grad[3:3 + nm])
+        need_dp = any(ctx.needs_input_grad[4:4 + nm]) or sinks is not None
         dx = torch.empty_like(x2) if need_dx else None
         dprobs = None
         if need_dp:
@@ -313,10 +344,14 @@ class GatedLinearGroupFunction(Function):
             dy2 = _aligned(dy.to(torch.bfloat16))
             nbytes = _hip.group_bwd_workspace_bytes(x2.shape[0], x2.shape[1], ctx.spec)
             ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x2.device)
-            _hip.gated_linear_group_bwd(dy2, x2, ctx.spec, d_pad, w_eff if need_dx else None, dx, dprobs, ws)
+            _hip.gated_linear_group_bwd(dy2, x2, ctx.spec, d_pad, w_eff if need_dx else None, dx, dprobs, ws,
+                                        gs if dprobs is not None else None)
+            if sinks is not None and dprobs is not None:
+                _finish_on_gate_stream(gs, [r for r, _ in sinks], dprobs, [ws])
+                dprobs = None
         grads_p = [None] * nm if dprobs is None else [g.to(d) for g, d in zip(dprobs, ctx.probs_devices)]
         n_q = sum(len(t) for t, _ in members)
-        return (dx, None, None, *grads_p) + (None,) * n_q
+        return (dx, None, None, None, *grads_p) + (None,) * n_q
 
 
 class MixPrefetch:
@@ -451,6 +486,12 @@ def gated_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
     if x2.dtype != torch.bfloat16:
         x2 = x2.to(torch.bfloat16)
     pre = MixPrefetch.take(modules)
+    # deferred gate gradients only when every member has a sink (else autograd
+    # for all); the probabilities stay attached either way, so the product's
+    # backward runs even when its input needs no gradient, and returns None
+    # for them when deferring
+    sinks = [m.__dict__.get("_gate_sink") for m in modules]
+    sinks = None if any(sk is None for sk in sinks) else sinks
     probs, qbytes, members = [], [], []
     for i, m in enumerate(modules):
         m._move_qbytes(x.device)
@@ -459,7 +500,7 @@ def gated_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
         qbytes.extend(m._qbytes())
         members.append((m._ggml_types(), m.out_features))
     meta = (tuple(members), modules[0].padded_in_features)
-    y = GatedLinearGroupFunction.apply(x2, meta, pre[0] if pre is not None else None, *probs, *qbytes)
+    y = GatedLinearGroupFunction.apply(x2, meta, pre[0] if pre is not None else None, sinks, *probs, *qbytes)
     if stacked:
         return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     outs = torch.split(y, [m.out_features for m in modules], dim=1)
@@ -890,7 +931,10 @@ class MixedQuantLinear(_MixedQuantBase):
             y = RoutedLinearFunction.apply(x2, probs, routing, meta, self._bf16_candidates(x.device),
                                            *self._qbytes())
         else:
-            y = GatedLinearFunction.apply(x2, probs, meta, pre[0] if pre is not None else None, *self._qbytes())
+            # with a sink the probabilities stay attached (so the backward runs
+            # even when x needs no gradient); the backward returns None for them
+            y = GatedLinearFunction.apply(x2, probs, meta, pre[0] if pre is not None else None,
+                                          self.__dict__.get("_gate_sink"), *self._qbytes())
         if x.dtype != torch.bfloat16:
             y = y.to(x.dtype)
         out = y.reshape(*lead, self.out_features)

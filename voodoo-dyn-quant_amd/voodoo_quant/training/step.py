@@ -453,6 +453,9 @@ class StepConfig:
     # SwiGLU stress stack 155.5 -> 156.9 ms (its teacher's 4096 x 14336
     # products fill the chip alone), so it is left to the caller
     teacher_stream: bool = False
+    # finish the gated Linears' gate gradients on a second stream and apply
+    # the softmax Jacobian once per bank after the backward (trainer.GateBank)
+    defer_gate_grads: bool = False
 
 
 class GateTrainer:
@@ -463,7 +466,8 @@ class GateTrainer:
         self.student, self.teacher, self.replaced, self.cfg = student, teacher, replaced, cfg
         # the chunked loss runs one backward per chunk, so its probabilities
         # must come from each module's own graph
-        self.bank = trainer.GateBank(replaced.values()) if cfg.gate_bank and cfg.logits_chunk == 0 else None
+        self.bank = (trainer.GateBank(replaced.values(), cfg.defer_gate_grads)
+                     if cfg.gate_bank and cfg.logits_chunk == 0 else None)
         self.trainable = self.bank.parameters() if self.bank else [m.gates for m in replaced.values()]
         self.opt, self.sched = trainer.build_gate_optimizer(self.trainable, cfg.lr, cfg.max_steps)
         self.target_bytes = cfg.target_fraction * total_8bit_bytes
@@ -501,6 +505,8 @@ class GateTrainer:
             else:
                 loss = lm_loss + c.distill_weight * distill + c.size_weight * size
                 loss.backward()
+            if self.bank:
+                self.bank.finish()
         finally:
             if self.bank:
                 self.bank.end()
@@ -665,7 +671,7 @@ class StackTrainer:
 
     def __init__(self, student, teacher, replaced, cfg: StepConfig, total_8bit_bytes: float):
         self.student, self.teacher, self.replaced, self.cfg = student, teacher, replaced, cfg
-        self.bank = trainer.GateBank(replaced.values()) if cfg.gate_bank else None
+        self.bank = trainer.GateBank(replaced.values(), cfg.defer_gate_grads) if cfg.gate_bank else None
         self.trainable = self.bank.parameters() if self.bank else [m.gates for m in replaced.values()]
         self.opt, self.sched = trainer.build_gate_optimizer(self.trainable, cfg.lr, cfg.max_steps)
         self.target_bytes = cfg.target_fraction * total_8bit_bytes
@@ -687,6 +693,8 @@ class StackTrainer:
             gated = bank_bytes if bank_bytes is not None else layers.total_effective_bytes(self.replaced)
             size = trainer.size_loss(gated.to(x.device), self.target_bytes, c.size_tolerance)
             (mse + c.size_weight * size).backward()
+            if self.bank:
+                self.bank.finish()
         finally:
             if self.bank:
                 self.bank.end()

@@ -59,6 +59,12 @@ def build_gate_optimizer(trainable: list[torch.nn.Parameter], lr: float, max_ste
     return opt, sched
 
 
+def softmax_rows_backward(p: torch.Tensor, g: torch.Tensor, temperature: float) -> torch.Tensor:
+    """Gradient w.r.t. the logits z of p = softmax(z / T) along dim 1, given
+    dL/dp = g: (1/T) p (g - <p, g>) per row."""
+    return p * (g - (p * g).sum(dim=1, keepdim=True)) / temperature
+
+
 class GateBank:
     """The gate logits of many gated tensors as one [T, K] parameter per
     (candidate count, device) group.
@@ -72,9 +78,21 @@ class GateBank:
     values and the optimizer update are the same elementwise: AdamW, the
     global-norm clip and the dead-zone size penalty see the same numbers.
     Each module's ``gates`` becomes a row view of its bank, so reading a
-    module's gates (argmax, export) sees the trained values."""
+    module's gates (argmax, export) sees the trained values.
 
-    def __init__(self, modules) -> None:
+    defer_gate_grads (ROCm devices): the gated Linears' backwards leave their
+    gate gradients to a second stream (default priority) -- the dot pass over
+    dW parts and the fixed-order reduce, ~170 small launches per 0.8B-class
+    step -- which adds each into a [T, K] buffer of the bank; :meth:`finish`,
+    after ``backward()``, joins that stream and applies the softmax Jacobian
+    (1/T) p (g - <p, g>) once per bank.  Those launches then overlap the next
+    layer's backward instead of sitting between its products.  Modules that
+    cannot defer (PTQR routing, embeddings) keep autograd through their row."""
+
+    def __init__(self, modules, defer_gate_grads: bool = False) -> None:
+        self.defer = bool(defer_gate_grads)
+        self._streams: dict = {}
+        self._pending: list = []
         groups: dict[tuple, list] = {}
         for m in modules:
             groups.setdefault((m.num_candidates, m.gates.device), []).append(m)
@@ -92,19 +110,45 @@ class GateBank:
     def begin(self, temperature: float) -> torch.Tensor:
         """Softmax every bank at `temperature`, hand each module its row, and
         return the differentiable effective bytes (sum of p_k * bytes_k)."""
+        from voodoo_quant.layers import MixedQuantLinear
+
         total = None
+        self._pending = []
+        t = max(temperature, 1e-6)
         for bank, mods, coef in self.groups:
-            probs = torch.nn.functional.softmax(bank / max(temperature, 1e-6), dim=1)
+            probs = torch.nn.functional.softmax(bank / t, dim=1)
             for m, row in zip(mods, probs.unbind(0)):
                 m._probs_override = row
+            if self.defer and bank.device.type == "cuda":
+                stream = self._streams.get(bank.device)
+                if stream is None:
+                    stream = self._streams[bank.device] = torch.cuda.Stream(device=bank.device)
+                sink = torch.zeros(probs.shape, dtype=torch.float32, device=bank.device)
+                for i, m in enumerate(mods):
+                    if isinstance(m, MixedQuantLinear):
+                        m._gate_sink = (sink[i], stream)
+                self._pending.append((bank, probs.detach(), sink, t, stream))
             b = (probs * coef).sum()
             total = b if total is None else total + b
         return total if total is not None else torch.tensor(0.0)
+
+    def finish(self) -> None:
+        """After ``backward()``: add the deferred gate gradients, through the
+        softmax Jacobian, to each bank's gradient (no-op without deferral)."""
+        for bank, p, g, t, stream in self._pending:
+            torch.cuda.current_stream(bank.device).wait_stream(stream)
+            jac = softmax_rows_backward(p, g, t)
+            if bank.grad is None:
+                bank.grad = jac
+            else:
+                bank.grad.add_(jac)
+        self._pending = []
 
     def end(self) -> None:
         for _, mods, _ in self.groups:
             for m in mods:
                 m._probs_override = None
+                m._gate_sink = None
 
     def release(self) -> None:
         """Give every module back an independent gates parameter (the bank's
