@@ -21,25 +21,24 @@ def anneal_temperature(step: int, max_steps: int, start: float, end: float) -> f
 
 
 def compute_total_8bit_bytes(state_dict_meta: dict[str, tuple[int, int]]) -> float:
-    """Bytes at 8 bits per parameter, shared storages counted once."""
-    seen: set[int] = set()
-    total = 0.0
-    for ptr, numel in state_dict_meta.values():
-        if ptr not in seen:
-            seen.add(ptr)
-            total += numel * 1.0
-    return total
+    """The model's size at one byte per parameter.
+
+    `state_dict_meta` maps each state-dict key to (storage pointer, element
+    count).  Keys that share a storage (tied embeddings) are one tensor, so
+    each pointer's elements count once (reference ``trainer.py:157-176``)."""
+    per_storage = {ptr: float(numel) for ptr, numel in state_dict_meta.values()}
+    return float(sum(per_storage.values()))
 
 
 def compute_non_targeted_8bit_bytes(state_dict_meta: dict[str, tuple[int, int]], targeted_keys: set[str]) -> float:
-    ptr_bytes: dict[int, float] = {}
-    ptr_targeted: dict[int, bool] = {}
-    for k, (ptr, numel) in state_dict_meta.items():
-        ptr_bytes[ptr] = numel * 1.0
-        ptr_targeted.setdefault(ptr, False)
-        if k in targeted_keys:
-            ptr_targeted[ptr] = True
-    return sum(b for ptr, b in ptr_bytes.items() if not ptr_targeted[ptr])
+    """Bytes at one byte per parameter of the storages no gated tensor covers.
+
+    A storage is targeted when any key that points at it is in
+    `targeted_keys`; the rest keep their 8-bit size in the budget (reference
+    ``trainer.py:178-196``)."""
+    per_storage = {ptr: float(numel) for ptr, numel in state_dict_meta.values()}
+    targeted = {ptr for key, (ptr, _) in state_dict_meta.items() if key in targeted_keys}
+    return float(sum(b for ptr, b in per_storage.items() if ptr not in targeted))
 
 
 def size_loss(current_bytes: torch.Tensor, target_bytes: float, tolerance: float) -> torch.Tensor:
@@ -124,6 +123,9 @@ class GateBank:
                 if stream is None:
                     stream = self._streams[bank.device] = torch.cuda.Stream(device=bank.device)
                 sink = torch.zeros(probs.shape, dtype=torch.float32, device=bank.device)
+                # the gate stream adds into the sink: the allocator must not
+                # hand its memory to main-stream work before that stream is done
+                sink.record_stream(stream)
                 for i, m in enumerate(mods):
                     if isinstance(m, MixedQuantLinear):
                         m._gate_sink = (sink[i], stream)
@@ -145,6 +147,11 @@ class GateBank:
         self._pending = []
 
     def end(self) -> None:
+        # a backward that raised leaves deferred work queued on the gate
+        # streams: join them before the sinks are dropped
+        for bank, _, _, _, stream in self._pending:
+            torch.cuda.current_stream(bank.device).wait_stream(stream)
+        self._pending = []
         for _, mods, _ in self.groups:
             for m in mods:
                 m._probs_override = None
@@ -227,43 +234,94 @@ def _hidden(out) -> torch.Tensor:
     return out.last_hidden_state if hasattr(out, "last_hidden_state") else out
 
 
-def chunked_forward_loss(student, teacher, x: torch.Tensor, y: torch.Tensor, temperature: float, chunk: int):
-    """Token-chunked CE + KL with one backward through the student's text
-    stack (reference ``_chunked_forward_loss``, ``trainer.py:751-832``).
+def _fused_loss_ok(logits: torch.Tensor) -> bool:
+    return logits.is_cuda and logits.dtype == torch.bfloat16 and logits.size(-1) % 8 == 0
 
-    Each chunk's head forward, losses and head backward run on a detached copy
-    of the final hidden states, and its input gradient is collected; one
-    backward of the collected gradient then runs through the stack.  As in the
-    reference, the chunk backward differentiates (CE + KL) / tokens, so the
-    distillation weight is not applied on this path.  Returns (CE, KL) as
-    floats, each a mean over tokens."""
+
+def chunk_loss_sums(logits: torch.Tensor, teacher_logits: torch.Tensor, labels: torch.Tensor,
+                    temperature: float) -> torch.Tensor:
+    """fp32 [2] = (CE summed over the labelled rows, T^2 KL(teacher || student)
+    summed over all rows) of one block of rows, differentiable in `logits`.
+
+    On a ROCm device with bf16 logits the sums come from the fused kernels
+    (:class:`DistillLossFunction` returns the two means; each is scaled by
+    its row count, which the backward turns into the kernel's gradient
+    weights).  Elsewhere an fp32 torch restatement of the same sums runs."""
+    labels = labels.reshape(-1)
+    if _fused_loss_ok(logits):
+        v = logits.size(-1)
+        means = DistillLossFunction.apply(logits.reshape(-1, v).contiguous(),
+                                          teacher_logits.reshape(-1, v).contiguous(),
+                                          labels.to(torch.int64).contiguous(), float(temperature))
+        labelled = (labels != -100).sum().to(torch.float32)
+        # a block with no labelled row has CE mean 0/0; its sum is 0
+        ce = torch.where(labelled > 0, means[0] * labelled, torch.zeros_like(means[0]))
+        return torch.stack([ce, means[1] * float(labels.numel())])
     import torch.nn.functional as F
 
-    hidden = _hidden(student.model(input_ids=x))
-    with torch.no_grad():
-        t_hidden = _hidden(teacher.model(input_ids=x))
-    h = hidden.shape[-1]
-    s_flat, t_flat, y_flat = hidden.reshape(-1, h), t_hidden.reshape(-1, h), y.reshape(-1)
-    n_tok = s_flat.shape[0]
-    t = temperature
-    h_grad = torch.zeros_like(s_flat)
-    lm_total = torch.zeros((), dtype=torch.float64, device=s_flat.device)
-    kl_total = torch.zeros((), dtype=torch.float64, device=s_flat.device)
-    for i in range(0, n_tok, chunk):
-        h_c = s_flat[i:i + chunk].detach().requires_grad_(True)
-        logits_c = student.lm_head(h_c)
-        lm_c = F.cross_entropy(logits_c, y_flat[i:i + chunk], reduction="sum")
-        student_log_probs = F.log_softmax(logits_c / t, dim=-1)
-        del logits_c
+    s = logits.float().reshape(labels.numel(), -1)
+    t = teacher_logits.float().reshape_as(s)
+    ce = F.cross_entropy(s, labels, ignore_index=-100, reduction="sum")
+    log_q = F.log_softmax(s / temperature, dim=-1)
+    log_p = F.log_softmax(t / temperature, dim=-1)
+    kl = (log_p.exp() * (log_p - log_q)).sum() * (temperature * temperature)
+    return torch.stack([ce, kl])
+
+
+class ChunkedDistillLoss:
+    """CE + KL over the output head without the [tokens, vocab] logits of the
+    whole batch (the reference's ``_chunked_forward_loss`` route,
+    ``trainer.py:751-832``).
+
+    The student's stack runs once and its final hidden states are taken out
+    of the graph.  Rows are then processed `chunk` at a time: the student's
+    and the teacher's heads give the block's logits, :func:`chunk_loss_sums`
+    gives its loss sums, and ``torch.autograd.grad`` returns the gradient of
+    (CE sum + KL sum) / tokens with respect to the block's hidden rows (and
+    the head's own trainable parameters, which are accumulated into their
+    ``.grad``).  The row gradients fill one buffer, and one backward carries
+    it through the stack.
+
+    Both terms are divided by the batch's token count and weighted 1: on this
+    route the distillation weight of the full-logits loss is not applied, as
+    in the reference (its chunk backward, ``trainer.py:812``), so that the
+    gate gradients are the reference's."""
+
+    def __init__(self, chunk: int, temperature: float) -> None:
+        if chunk <= 0:
+            raise ValueError("chunk must be positive")
+        self.chunk = int(chunk)
+        self.temperature = float(temperature)
+
+    def __call__(self, student, teacher, x: torch.Tensor, y: torch.Tensor) -> tuple[float, float]:
+        hidden = _hidden(student.model(input_ids=x))
         with torch.no_grad():
-            teacher_probs = F.softmax(teacher.lm_head(t_flat[i:i + chunk]) / t, dim=-1)
-        kl_c = F.kl_div(student_log_probs, teacher_probs, reduction="none").sum() * (t * t)
-        del student_log_probs, teacher_probs
-        ((lm_c + kl_c) / n_tok).backward()
-        with torch.no_grad():
-            if h_c.grad is not None:
-                h_grad[i:i + chunk] = h_c.grad
-        lm_total += lm_c.detach().double() / n_tok
-        kl_total += kl_c.detach().double() / n_tok
-    hidden.backward(h_grad.reshape(hidden.shape))
-    return float(lm_total), float(kl_total)
+            teacher_rows = _hidden(teacher.model(input_ids=x)).reshape(-1, hidden.size(-1))
+        rows = teacher_rows.size(0)
+        student_rows = hidden.detach().reshape(rows, -1)
+        labels = y.reshape(-1)
+        head_params = [p for p in student.lm_head.parameters() if p.requires_grad]
+        row_grad = torch.empty_like(student_rows)
+        totals = torch.zeros(2, dtype=torch.float64, device=student_rows.device)
+        for lo in range(0, rows, self.chunk):
+            hi = min(rows, lo + self.chunk)
+            leaf = student_rows[lo:hi].detach().requires_grad_(True)
+            with torch.no_grad():
+                t_logits = teacher.lm_head(teacher_rows[lo:hi])
+            sums = chunk_loss_sums(student.lm_head(leaf), t_logits, labels[lo:hi], self.temperature)
+            grads = torch.autograd.grad(sums.sum() / rows, [leaf] + head_params, allow_unused=True)
+            row_grad[lo:hi].copy_(grads[0] if grads[0] is not None else torch.zeros_like(leaf))
+            for p, g in zip(head_params, grads[1:]):
+                if g is not None:
+                    p.grad = g if p.grad is None else p.grad + g
+            totals += sums.detach().double()
+        hidden.backward(row_grad.view_as(hidden))
+        means = (totals / rows).tolist()
+        return float(means[0]), float(means[1])
+
+
+def chunked_forward_loss(student, teacher, x: torch.Tensor, y: torch.Tensor, temperature: float, chunk: int):
+    """Token-chunked CE + KL with one backward through the student's stack;
+    returns (CE, KL) as floats, each a mean over tokens (see
+    :class:`ChunkedDistillLoss`)."""
+    return ChunkedDistillLoss(chunk, temperature)(student, teacher, x, y)
