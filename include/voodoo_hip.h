@@ -302,13 +302,14 @@ int vq_gated_linear_bwd_gate_stream(const uint16_t *dy, const uint16_t *x, int64
 #define VQ_STATIC_SCRATCH_BYTES (4 << 20)
 
 /* vq_gated_linear_bwd with no workspace and no allocation of any kind: the
- * gate partials (and dX's split-tail tiles, when they fit behind them) live
- * in a static device array of VQ_STATIC_SCRATCH_BYTES, and dx needs the
- * forward's w_eff (no re-mix).  Sizes whose gate partials exceed the scratch
- * return VQ_ERR_WORKSPACE.  Every call on a device shares that device's
- * scratch: calls that overlap on one device (concurrent streams, threads)
- * race and must be serialised by the caller.  dprobs is bit-identical to
- * vq_gated_linear_bwd's; dx too when both split dX the same way.
+ * gate partials live in a static device array of VQ_STATIC_SCRATCH_BYTES,
+ * dX runs whole tiles (no split tail: its partials would need 16 MiB or
+ * more), and dx needs the forward's w_eff (no re-mix).  Sizes whose gate
+ * partials exceed the scratch return VQ_ERR_WORKSPACE.  Every call on a
+ * device shares that device's scratch: calls that overlap on one device
+ * (concurrent streams, threads) race and must be serialised by the caller.
+ * dprobs is bit-identical to vq_gated_linear_bwd's; dx is bit-identical to
+ * vq_gated_linear_bwd's when that one runs without a workspace.
  * No counterpart in the reference: this entry point is for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). */

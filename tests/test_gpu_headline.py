@@ -1,9 +1,11 @@
-"""GPU parity at the 27B-class Linear shapes the benchmark times (needs an MI355X).
+"""GPU parity at the Linear shapes the benchmark times (needs an MI355X).
 
 8192 tokens through each of the four projection shapes of a 27B-class layer
 (hidden 5120: q 5120 -> 6144, o 6144 -> 5120, gate/up 5120 -> 17408,
 down 17408 -> 5120), K = 6 candidates (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0),
-through the C ABI with the forward's split-tail workspace on, so every work
+and 2 x 8192 tokens through one SwiGLU block of the stress stack (hidden
+4096, MLP 14336: 4096 -> 14336 and 14336 -> 4096) with its K = 8 menu (Q2_K,
+IQ2_XXS, Q3_K, IQ3_S, Q4_K, Q5_K, Q6_K, Q8_0), through the C ABI with the forward's split-tail workspace on, so every work
 plan the benchmark runs (whole-tile rounds, K-split tail tiles on every XCD,
 the dual dX + gate launch) is compared with the oracle:
 
@@ -29,14 +31,19 @@ from oracle import blocks, cdequant, mixture
 pytestmark = pytest.mark.gpu
 
 TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
-GGML = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+# the stress stack's wide menu: eight distinct formats, two of them IQ
+STRESS_TYPES = ["Q2_K", "IQ2_XXS", "Q3_K", "IQ3_S", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
+GGML = {"Q8_0": 8, "Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ2_XXS": 16, "IQ3_S": 21}
 TOL = 1e-2
 M = 8192
-SHAPES = [  # (name, in_features D, out_features N)
-    ("q_5120x6144", 5120, 6144),
-    ("o_6144x5120", 6144, 5120),
-    ("up_5120x17408", 5120, 17408),
-    ("down_17408x5120", 17408, 5120),
+SHAPES = [  # (name, in_features D, out_features N, tokens M, candidate menu)
+    ("q_5120x6144", 5120, 6144, M, TYPES),
+    ("o_6144x5120", 6144, 5120, M, TYPES),
+    ("up_5120x17408", 5120, 17408, M, TYPES),
+    ("down_17408x5120", 17408, 5120, M, TYPES),
+    # one SwiGLU block of the stress stack: hidden 4096, MLP 14336, 2 x 8192 tokens, K = 8
+    ("stress_up_4096x14336_k8", 4096, 14336, 2 * M, STRESS_TYPES),
+    ("stress_down_14336x4096_k8", 14336, 4096, 2 * M, STRESS_TYPES),
 ]
 
 
@@ -109,15 +116,15 @@ def _tile_rel(got, ref):
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[s[0] for s in SHAPES])
-def test_27b_linear_shape_8192_tokens(hip, shape):
-    name, d, n = shape
+def test_linear_shape_at_benchmark_tokens(hip, shape):
+    name, d, n, M, types = shape
     d_pad = d
-    k_ = len(TYPES)
+    k_ = len(types)
     _say(f"[headline] {name}: M={M} D={d} N={n} K={k_}: building candidates")
     rng = np.random.default_rng(d * 7 + n)
-    qbs = [_random_candidate(qt, n, d_pad, rng) for qt in TYPES]
+    qbs = [_random_candidate(qt, n, d_pad, rng) for qt in types]
     cands = [torch.from_numpy(cdequant.oracle_dequant_parallel(qt, qb, n * d_pad).reshape(n, d_pad))
-             for qt, qb in zip(TYPES, qbs)]
+             for qt, qb in zip(types, qbs)]
     g = torch.Generator().manual_seed(n + d)
     probs = torch.softmax(torch.randn(k_, generator=g), 0)
     x = torch.randn(M, d, generator=g).to(torch.bfloat16)
@@ -125,7 +132,7 @@ def test_27b_linear_shape_8192_tokens(hip, shape):
 
     dev = torch.device("cuda", 0)
     qd = [torch.from_numpy(q.reshape(-1)).to(dev) for q in qbs]
-    ids = [GGML[t] for t in TYPES]
+    ids = [GGML[t] for t in types]
     xd, dyd, pd = x.to(dev), dy.to(dev), probs.to(dev)
     w_eff = torch.empty(n, d_pad, dtype=torch.bfloat16, device=dev)
     y = torch.empty(M, n, dtype=torch.bfloat16, device=dev)

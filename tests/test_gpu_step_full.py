@@ -1,0 +1,244 @@
+"""The 0.8B-class decoder's gate gradients at the benchmark's full size (needs
+an MI355X): 24 layers, hidden 1024, 16 x 64 query heads, 4 KV heads, SwiGLU
+3072, vocabulary 151936 tied, every Linear and the embedding gated over K = 6
+candidates (Q2_K .. Q8_0), batch 4 x 2048 tokens, CE + KL against the Q8_0
+teacher (``trainer.py:2498-2616``).
+
+The product side is the student as the step harness builds it (stacked q/k/v
+and gate/up products, the fused add + RMSNorm, rotary and SwiGLU kernels,
+gated embedding rows).  The reference side is the same decoder with every
+gated layer replaced by the reference's formulation in torch: W_eff = the fp32
+k-ordered mixture of the oracle's decodes of the same candidate bytes, cast to
+bf16, then ``F.linear`` / ``F.embedding`` (``layers.py:336-363, 1729-1731,
+1842``), with autograd through softmax(gates / T).  Its weight gradient dW is
+formed in fp32 from the bf16 activations and gradients (the reference's fp32
+PyTorch path for <dW, W_k>; its bf16 dW would add its own rounding to the
+comparison).  Both sides run the same torch loss on the same batch, with the
+same non-uniform gate logits.
+
+Over 24 bf16 layers the gate gradients are as sensitive to rounding as that:
+measured on MI355X, the reference against itself with its products evaluated
+in fp32 and rounded once (only the accumulation order changes) differs by
+1.15e-2 relative L2 over all tensors (per tensor: median 1.6e-2, 90th
+percentile 3.2e-2, max 1.1e-1, cosine >= 0.9964), and the same reference step
+run twice by 7.2e-3 (attention's backward accumulates with atomics).  The
+product against the reference: 1.36e-2 (median 1.7e-2, 90th percentile
+3.9e-2, max 8.4e-2, cosine >= 0.9973).
+
+Bars: the loss equal to 1e-3; every tensor's cosine above 0.99; over all
+tensors 3e-2; and the total, the per-tensor median, 90th percentile and
+maximum each at most twice the reference's own spread under the change of
+accumulation order, measured in the same run.
+"""
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import cdequant
+from voodoo_quant import layers
+from voodoo_quant.training import step as st
+from voodoo_quant.training import trainer
+
+pytestmark = pytest.mark.gpu
+
+CFG = st.DecoderConfig()
+TYPES = ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
+BATCH, SEQ = 4, 2048
+TAU = 0.7
+TOTAL_TOL = 3e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+# False: the reference's bf16 products (hipBLASLt, rounded to bf16 after fp32
+# accumulation); True: the same products evaluated in fp32 and rounded once
+# to bf16 (another valid bf16 result, differing only in accumulation order)
+_FP32_PRODUCTS = {"on": False}
+
+
+class _MixedLinearFn(torch.autograd.Function):
+    """y = x bf16(W)^T with dX in bf16 (as torch's bf16 linear backward) and
+    dW = dY^T X in fp32."""
+
+    @staticmethod
+    def forward(ctx, x, w32):
+        wb = w32.to(torch.bfloat16)
+        ctx.save_for_backward(x, wb)
+        if _FP32_PRODUCTS["on"]:
+            return (x.float() @ wb.float().t()).to(torch.bfloat16)
+        return F.linear(x, wb)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, wb = ctx.saved_tensors
+        n, d = wb.shape
+        dy2 = dy.reshape(-1, n)
+        if _FP32_PRODUCTS["on"]:
+            dx = (dy2.float() @ wb.float()).to(torch.bfloat16).reshape(x.shape)
+        else:
+            dx = (dy2 @ wb).reshape(x.shape)
+        dw = torch.mm(dy2.float().t(), x.reshape(-1, d).float())
+        return dx, dw
+
+
+class _MixedEmbeddingFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, ids, w32):
+        wb = w32.to(torch.bfloat16)
+        ctx.save_for_backward(ids)
+        ctx.shape = wb.shape
+        return F.embedding(ids, wb)
+
+    @staticmethod
+    def backward(ctx, dout):
+        (ids,) = ctx.saved_tensors
+        dw = torch.zeros(ctx.shape, dtype=torch.float32, device=dout.device)
+        dw.index_add_(0, ids.reshape(-1), dout.reshape(-1, ctx.shape[1]).float())
+        return None, dw
+
+
+class _RefMixed(nn.Module):
+    def __init__(self, mod, out_f, in_f, d_pad):
+        super().__init__()
+        self.cands = []
+        for k, qt in enumerate(mod.candidate_types):
+            qb = getattr(mod, f"_qweight_{k}").cpu().numpy()
+            w = cdequant.oracle_dequant_parallel(qt, qb, out_f * d_pad).reshape(out_f, d_pad)[:, :in_f]
+            self.cands.append(torch.from_numpy(np.ascontiguousarray(w)).cuda())
+        self.gates = nn.Parameter(mod.gates.detach().clone())
+        self.temperature = mod.temperature
+
+    def weight32(self):
+        p = F.softmax(self.gates / self.temperature, dim=0)
+        w = torch.zeros_like(self.cands[0])
+        for k, c in enumerate(self.cands):
+            w = w + p[k] * c
+        return w
+
+
+class _RefLinear(_RefMixed):
+    def __init__(self, mod):
+        super().__init__(mod, mod.out_features, mod.in_features, mod.padded_in_features)
+
+    def forward(self, x):
+        return _MixedLinearFn.apply(x, self.weight32())
+
+
+class _RefEmbedding(_RefMixed):
+    def __init__(self, mod):
+        super().__init__(mod, mod.num_embeddings, mod.embedding_dim, mod.padded_in_features)
+
+    def forward(self, ids):
+        return _MixedEmbeddingFn.apply(ids, self.weight32())
+
+
+def _reference_student(student):
+    ref = copy.deepcopy(student)
+    mapping = {}
+    for name, mod in list(ref.named_modules()):
+        for cname, child in list(mod.named_children()):
+            full = f"{name}.{cname}" if name else cname
+            if isinstance(child, layers.MixedQuantEmbedding):
+                new = _RefEmbedding(child)
+            elif isinstance(child, layers.MixedQuantLinear):
+                new = _RefLinear(child)
+            else:
+                continue
+            setattr(mod, cname, new)
+            mapping[full] = new
+    return ref, mapping
+
+
+def _loss(model, teacher, x, y):
+    ce, kl = trainer.distill_losses(model(x), teacher(x).detach(), y, 1.0)
+    return ce + kl
+
+
+def _compare(a, b, names):
+    """(total relative L2, per-tensor relative L2 array, min cosine) of two
+    {name: gradient} sets against b."""
+    rel = np.array([float((a[n] - b[n]).norm() / b[n].norm().clamp_min(1e-30)) for n in names])
+    cos = min(float(torch.dot(a[n], b[n]) / (a[n].norm() * b[n].norm()).clamp_min(1e-30)) for n in names)
+    ga, gb = torch.cat([a[n] for n in names]), torch.cat([b[n] for n in names])
+    return float((ga - gb).norm() / gb.norm()), rel, cos
+
+
+def _stats(tag, total, rel, cos):
+    _say(f"[step-full] {tag}: total rel L2 {total:.2e}; per tensor median {np.median(rel):.2e}, "
+         f"90th pct {np.quantile(rel, 0.9):.2e}, max {rel.max():.2e}; min cosine {cos:.6f}")
+
+
+def test_full_decoder_step_gate_gradients_match_reference():
+    """Besides the bars on the product against the reference, two spreads of
+    the reference against itself set the scale of what bf16 arithmetic over
+    24 layers leaves: the same step run again (attention's backward
+    accumulates with atomics, so no two runs are bitwise equal), and the step
+    with its products evaluated in fp32 and rounded to bf16 once (only the
+    accumulation order differs).  The product must sit within the second
+    spread's scale: per-tensor median and 90th percentile at most twice the
+    reference's own."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(0)
+    _say(f"[step-full] building the {CFG.layers}-layer decoder, vocab {CFG.vocab}, K={len(TYPES)}")
+    student, teacher, replaced = st.build_models(CFG, TYPES, dev, seed=11, packed=True)
+    g = torch.Generator(device=dev).manual_seed(12)
+    with torch.no_grad():
+        for m in replaced.values():
+            m.gates.copy_(torch.randn(m.gates.shape, device=dev, generator=g) * 0.5)
+    trainer.set_temperature_all(replaced, TAU)
+    _say("[step-full] reference side: oracle decodes of every candidate")
+    ref, mapping = _reference_student(student)
+    assert set(mapping) == set(replaced) and len(mapping) == 24 * 7 + 1
+    for r in mapping.values():
+        r.temperature = TAU
+    names = list(mapping)
+    x = torch.randint(0, CFG.vocab, (BATCH, SEQ), device=dev, generator=g)
+    y = torch.randint(0, CFG.vocab, (BATCH, SEQ), device=dev, generator=g)
+
+    _say("[step-full] product step (CE + KL, backward)")
+    loss_hip = _loss(student, teacher, x, y)
+    loss_hip.backward()
+    hip = {n: replaced[n].gates.grad.detach().double().clone() for n in names}
+
+    def ref_step(fp32_products):
+        for r in mapping.values():
+            r.gates.grad = None
+        _FP32_PRODUCTS["on"] = fp32_products
+        try:
+            loss = _loss(ref, teacher, x, y)
+            loss.backward()
+        finally:
+            _FP32_PRODUCTS["on"] = False
+        return float(loss), {n: mapping[n].gates.grad.detach().double().clone() for n in names}
+
+    _say("[step-full] reference step, twice, and with fp32-evaluated products")
+    loss_ref, ref_a = ref_step(False)
+    _, ref_b = ref_step(False)
+    _, ref_c = ref_step(True)
+    torch.cuda.synchronize()
+    _say(f"[step-full] loss {float(loss_hip):.6f} vs reference {loss_ref:.6f}")
+
+    t_hip, r_hip, c_hip = _compare(hip, ref_a, names)
+    t_rerun, r_rerun, c_rerun = _compare(ref_b, ref_a, names)
+    t_fp32, r_fp32, c_fp32 = _compare(ref_c, ref_a, names)
+    _stats("product vs reference", t_hip, r_hip, c_hip)
+    _stats("reference rerun vs reference", t_rerun, r_rerun, c_rerun)
+    _stats("reference, fp32-evaluated products, vs reference", t_fp32, r_fp32, c_fp32)
+    worst = names[int(r_hip.argmax())]
+    _say(f"[step-full] worst tensor {worst}: {r_hip.max():.2e} (the reference's own spread there "
+         f"{r_fp32[int(r_hip.argmax())]:.2e})")
+    assert abs(float(loss_hip) - loss_ref) < 1e-3 * abs(loss_ref)
+    assert c_hip > 0.99
+    assert t_hip <= TOTAL_TOL and t_hip <= 2 * t_fp32
+    assert np.median(r_hip) <= 2 * np.median(r_fp32)
+    assert np.quantile(r_hip, 0.9) <= 2 * np.quantile(r_fp32, 0.9)
+    assert r_hip.max() <= 2 * r_fp32.max()

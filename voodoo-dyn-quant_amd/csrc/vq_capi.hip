@@ -703,13 +703,11 @@ int vq_gated_linear_bwd_static(const uint16_t* dy, const uint16_t* x, int64_t m,
     char* scratch_ptr = nullptr;
     rc = static_scratch(s, &scratch_ptr);
     if (rc != VQ_OK) return rc;
-    // dX splits its tail tiles along K only when their partials fit behind the gate partials
-    const int64_t tail_bytes = align256(vq::dx_tail_bytes((int)m, (int)n, (int)d));
-    float* tail_ws = nullptr;
-    if (tail_bytes > 0 && part_bytes + tail_bytes <= kStaticScratchBytes)
-        tail_ws = reinterpret_cast<float*>(scratch_ptr + part_bytes);
+    // dX runs whole tiles: a split tail keeps 8 XCDs x (tiles x parts, at least
+    // 8 for any split the plan makes with 32 CUs per XCD) x 256 KiB of fp32
+    // partials, 16 MiB or more, which the scratch never holds
     return run_bwd(dy, x, m, n, d, d_pad, make_set(ncand, qtypes, qbytes, d_pad), nullptr, w_eff, nullptr, dx, dprobs,
-                   gw, reinterpret_cast<float*>(scratch_ptr), tail_ws, nullptr, s, s);
+                   gw, reinterpret_cast<float*>(scratch_ptr), nullptr, nullptr, s, s);
 }
 
 int64_t vq_gated_linear_fused_workspace(int64_t m, int64_t n, int64_t d, int dx) {

@@ -17,7 +17,10 @@ libggml the candidates come from the labelled RTN encoder and are stored under
 :data:`voodoo_quant.cache.RTN_MODE` (``dequant_rtn`` for decodes), keys that a
 run with libggml, here or in the reference, never reads.
 
-Decodes (``lazy=False``) come from libggml's ``dequantize_row_*`` when it loads,
+The gated layers load packed entries only (``combined_lazy_*``, or the RTN
+key without libggml), so packed is the default here and on the command line;
+decoded entries (``lazy=False``, ``--decoded``) are for other readers.
+Decodes come from libggml's ``dequantize_row_*`` when it loads,
 else from the HIP decoders on a ROCm device (bit-identical fp32, then bf16);
 with neither the call raises.  Quantization runs on the CPU, one tensor at a
 time (bounded memory), its candidate types in a thread pool: libggml's
@@ -149,9 +152,19 @@ def main(argv=None) -> int:
     ap.add_argument("--candidate_types", nargs="+", default=default_candidate_types())
     ap.add_argument("--attention_candidates", nargs="+", default=None)
     ap.add_argument("--non_attention_candidates", nargs="+", default=None)
-    ap.add_argument("--lazy", action="store_true")
+    # The gated layers read only packed ("lazy") entries, so those are the
+    # default; --lazy is accepted for the reference's command lines, and
+    # --decoded writes bf16 decodes for other readers (with a warning)
+    ap.add_argument("--lazy", dest="decoded", action="store_false")
+    ap.add_argument("--decoded", dest="decoded", action="store_true",
+                    help="write bf16 decodes (combined_dequant_*) instead of packed bytes; "
+                         "MixedQuantLinear never reads them")
+    ap.set_defaults(decoded=False)
     ap.add_argument("--device", default="cpu", help="unused: quantization runs on the CPU")
     args = ap.parse_args(argv)
+    if args.decoded:
+        print("precache: --decoded writes combined_dequant_* entries, which the gated layers never read "
+              "(they load combined_lazy_* packed bytes only)", file=sys.stderr)
     base = args.model or os.environ.get("VOODOO_PRECACHE_MODEL")
     if not base:
         ap.error("--model is required (or set VOODOO_PRECACHE_MODEL)")
@@ -162,7 +175,7 @@ def main(argv=None) -> int:
     ckpt = torch.load(args.checkpoint, weights_only=True, map_location="cpu", mmap=True)
     model.load_state_dict(ckpt["model_state_dict"], strict=False, assign=True)
     rep = precache_model(model, args.candidate_types, args.attention_candidates, args.non_attention_candidates,
-                         lazy=args.lazy, log=print)
+                         lazy=not args.decoded, log=print)
     print(f"precache: {rep.tensors} tensors, {rep.built} entries built, {rep.cached} already cached, "
           f"{len(rep.errors)} errors, {rep.seconds:.1f} s (candidates from {rep.source})")
     for e in rep.errors:
