@@ -110,6 +110,13 @@ def test_fused_path_region():
     assert not layers.use_fused(33, 1024, 1024)
     assert not layers.use_fused(16, 4096, 4096)
     assert not layers.use_fused(0, 1024, 1024)
+    # the documented switch forces the bit-exact materialised path
+    saved = layers.FUSED_PRODUCTS
+    try:
+        layers.FUSED_PRODUCTS = False
+        assert not layers.use_fused(1, 1024, 1024)
+    finally:
+        layers.FUSED_PRODUCTS = saved
 
 
 def test_softmax_rows_backward_matches_autograd():
