@@ -461,11 +461,12 @@ __device__ __forceinline__ void decode8_mix(const uint8_t* __restrict__ g, int p
 // not shifts, so one instantiation per consumer serves all eight): the same
 // four operations as the K-quant templates above, on iq_affine's codes.
 // ---------------------------------------------------------------------------
-template <int R>
-__device__ __forceinline__ void decode_run_iq(int qt, const uint8_t* __restrict__ g, int p, float* __restrict__ y) {
+template <int R, class Books = GlobalBooks>
+__device__ __forceinline__ void decode_run_iq(int qt, const uint8_t* __restrict__ g, int p, float* __restrict__ y,
+                                              const Books& bk = Books()) {
     uint32_t uw[R / 4];
     float dl;
-    iq_affine<R>(qt, g, p, uw, dl);
+    iq_affine<R>(qt, g, p, uw, dl, bk);
 #pragma unroll
     for (int r = 0; r < R; ++r) y[r] = dl * ((float)((uw[r >> 2] >> (8 * (r & 3))) & 0xffu) - 128.0f);
 }

@@ -7,10 +7,10 @@
 // Data layout: a candidate is N rows of D_pad/256 groups; every format packs a
 // row's groups contiguously and rows back to back, so the flattened group index
 // g covers weights [256 g, 256 g + 256) of the row-major [N][D_pad] matrix.
-// A workgroup streams kGroupsPerBlock consecutive groups of every candidate
-// into LDS with 16-byte direct-to-LDS loads (the byte range of 16 groups is a multiple of 16
-// for every format), then each thread decodes runs of 8 weights from LDS and
-// writes them with 16-byte (bf16 x8) or 2x16-byte (fp32 x8) stores.
+// A workgroup streams consecutive groups (of every candidate, for the mix)
+// into LDS with 16-byte direct-to-LDS loads (the byte range of 16 groups is a
+// multiple of 16 for every format), then each thread decodes runs of 8
+// weights from LDS and writes them with 16-byte stores.
 #include <mutex>
 #include <unordered_map>
 
@@ -64,75 +64,156 @@ __device__ __forceinline__ void stage_bytes(uint8_t* __restrict__ dst, const uin
 // after it makes everyone's visible).
 __device__ __forceinline__ void stage_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Output placement of one run of 8 weights: lanes 2k and 2k + 1 of a wave
+// decode run k (weights 8k .. 8k + 7) of two neighbouring groups A and B, and
+// swap halves, so that each fp32 store instruction writes one whole group
+// (lane l: weights 4l .. 4l + 3, 1 KB contiguous per instruction) straight from
+// registers.  Against writing each thread's run as two 16-byte halves 32 bytes
+// apart (each instruction covering half of a 2 KB span) this is the 1 KB
+// pattern of an LDS round trip without the LDS buffer and its barrier, which
+// leaves a workgroup's LDS to its staged bytes (and an IQ format's code book).
+template <class OUT>
+__device__ __forceinline__ void store_run(OUT* __restrict__ out, int64_t group_a, const float (&y)[8], int lane) {
+    if constexpr (sizeof(OUT) == 4) {
+        const bool odd = lane & 1;
+        float4 send = odd ? make_float4(y[0], y[1], y[2], y[3]) : make_float4(y[4], y[5], y[6], y[7]);
+        float4 recv;
+        recv.x = __shfl_xor(send.x, 1);
+        recv.y = __shfl_xor(send.y, 1);
+        recv.z = __shfl_xor(send.z, 1);
+        recv.w = __shfl_xor(send.w, 1);
+        const float4 mine_lo = make_float4(y[0], y[1], y[2], y[3]), mine_hi = make_float4(y[4], y[5], y[6], y[7]);
+        const float4 a = odd ? recv : mine_lo;  // group A, weights 4 lane .. + 3
+        const float4 b = odd ? mine_hi : recv;  // group B, weights 4 lane .. + 3
+        reinterpret_cast<float4*>(out + group_a * 256)[lane] = a;
+        reinterpret_cast<float4*>(out + (group_a + 1) * 256)[lane] = b;
+    } else {
+        // bf16: a lane's 8 weights are 16 contiguous bytes already
+        uint4 v;
+        v.x = f2bf2(y[0], y[1]);
+        v.y = f2bf2(y[2], y[3]);
+        v.z = f2bf2(y[4], y[5]);
+        v.w = f2bf2(y[6], y[7]);
+        *reinterpret_cast<uint4*>(out + (group_a + (lane & 1)) * 256 + 8 * (lane >> 1)) = v;
+    }
+}
+
+// Runs of 8 weights per thread, per format: a workgroup of kStreamThreads
+// threads stages and decodes 8 * RUNS groups.  The bytes one workgroup keeps
+// in flight set the rate (the fp32 output stream is the same 235 MB for every
+// format at 4096 x 14336, and a write-only stream of it runs at 6.4-6.5 TB/s
+// on MI355X).  Measured there, fraction of 8 TB/s at 16 / 32 / 64 / 128 / 256
+// groups per workgroup: Q2_K 0.66 / 0.73 / 0.77 / 0.79 / 0.72, Q3_K 0.67 /
+// 0.71 / 0.74 / 0.71-0.76 / 0.64, the code-book IQ formats 0.55-0.61 /
+// 0.58-0.67 / 0.69-0.76 / 0.75-0.78 / 0.70-0.76; Q4_K 0.76 / 0.79 / 0.77,
+// Q5_K and Q6_K best at 32 (0.76, 0.73), IQ4_XS at 32 (0.80), Q8_0 (272
+// bytes per group) at 16 (0.79 against 0.77 at 32).
+__host__ __device__ constexpr int dequant_runs(int qt) {
+    return qt == Q8_0 ? 2 : (qt == Q4_K || qt == Q5_K || qt == Q6_K || qt == IQ4_XS) ? 4 : 16;
+}
+
+// Formats whose code book is copied to LDS by the workgroup (the lookups then
+// read LDS instead of gathering 64 scattered words per wave instruction
+// through L1): measured faster for IQ3_XXS (1 KB book) and IQ3_S (2 KB) at 16
+// and 32 groups per workgroup (0.59 -> 0.67-0.69 at 16), level at 128, and
+// slower for the larger books (IQ2_S 8 KB, IQ1_S / IQ1_M 16 KB: the copy and
+// the LDS it takes cost more than the lookups save) and for IQ2_XXS / IQ2_XS.
+__host__ __device__ constexpr bool dequant_book_in_lds(int qt) { return qt == IQ3_XXS || qt == IQ3_S; }
+
 // OUT = float: ggml's fp32 values bit for bit; OUT = bf16_t: those values
 // rounded to bf16 (torch's rounding), the source-dtype candidate the
-// reference's lazy path holds.
+// reference's lazy path holds.  Wave w decodes groups 2 (w + 4 u) and
+// 2 (w + 4 u) + 1, u < RUNS.  A partial last workgroup with an odd group
+// count decodes the group past its end from stale LDS (every code-book index
+// stays inside its book) and stores nothing of it.
+template <int QT, class OUT, int RUNS, class Books>
+__device__ __forceinline__ void dequant_groups(const uint8_t* __restrict__ lds, OUT* __restrict__ out, int64_t g0,
+                                               int ng, const Books& bk) {
+    constexpr int GB = group_bytes(QT);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int u = 0; u < RUNS; ++u) {
+        const int pair = wave + (kStreamThreads / 64) * u;  // groups 2 pair, 2 pair + 1
+        const int j = 2 * pair + (lane & 1);
+        if (2 * pair < ng) {
+            float y[8];
+            if constexpr (is_iq(QT))
+                decode_run_iq<8>(QT, lds + j * GB, 8 * (lane >> 1), y, bk);
+            else
+                decode_run<QT, 8>(lds + j * GB, 8 * (lane >> 1), y);
+            if (2 * pair + 1 < ng) {
+                store_run<OUT>(out, g0 + 2 * pair, y, lane);
+            } else {  // the last group of an odd count: group A only
+                if constexpr (sizeof(OUT) == 4) {
+                    const bool odd = lane & 1;
+                    float4 send = odd ? make_float4(y[0], y[1], y[2], y[3]) : make_float4(y[4], y[5], y[6], y[7]);
+                    float4 recv;
+                    recv.x = __shfl_xor(send.x, 1);
+                    recv.y = __shfl_xor(send.y, 1);
+                    recv.z = __shfl_xor(send.z, 1);
+                    recv.w = __shfl_xor(send.w, 1);
+                    const float4 a = odd ? recv : make_float4(y[0], y[1], y[2], y[3]);
+                    reinterpret_cast<float4*>(out + (g0 + 2 * pair) * 256)[lane] = a;
+                } else if (!(lane & 1)) {
+                    uint4 v;
+                    v.x = f2bf2(y[0], y[1]);
+                    v.y = f2bf2(y[2], y[3]);
+                    v.z = f2bf2(y[4], y[5]);
+                    v.w = f2bf2(y[6], y[7]);
+                    *reinterpret_cast<uint4*>(out + (g0 + 2 * pair) * 256 + 8 * (lane >> 1)) = v;
+                }
+            }
+        }
+    }
+}
+
 template <int QT, class OUT>
 __global__ __launch_bounds__(kStreamThreads) void dequant_kernel(const uint8_t* __restrict__ q,
                                                                  OUT* __restrict__ out, int64_t ngroups) {
     constexpr int GB = group_bytes(QT);
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kGroupsPerBlock * GB + 16];
-    const int64_t g0 = (int64_t)blockIdx.x * kGroupsPerBlock;
-    const int ng = (int)min<int64_t>(kGroupsPerBlock, ngroups - g0);
+    constexpr int RUNS = dequant_runs(QT);
+    constexpr int GPB = kStreamThreads / 32 * RUNS;  // groups per workgroup
+    constexpr int BOOK = dequant_book_in_lds(QT) ? iq_book_bytes(QT) : 16;
+    static_assert(BOOK % 16 == 0, "a code book of whole 16-byte chunks");
+    __shared__ __attribute__((aligned(16))) uint8_t book[BOOK];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[GPB * GB + 16];
+    const int64_t g0 = (int64_t)blockIdx.x * GPB;
+    const int ng = (int)min<int64_t>(GPB, ngroups - g0);
+    if constexpr (dequant_book_in_lds(QT)) stage_bytes(book, iq_book_src(QT), BOOK);
     stage_bytes(lds, q + g0 * GB, ng * GB);
     stage_wait();
     __syncthreads();
-    const int t = threadIdx.x;
-    // fp32 output goes through LDS so that each store instruction writes 1 KB
-    // in one piece (a thread's own run is two 16-byte halves 32 bytes apart):
-    // 6.2-6.5 against 5.2-5.9 TB/s for the K-quants and Q8_0 at 4096 x 14336,
-    // 4.5-4.8 against 3.9-4.2 for the code-book IQ formats
-    __shared__ __attribute__((aligned(16))) float ob[sizeof(OUT) == 4 ? kGroupsPerBlock * 256 : 1];
-#pragma unroll
-    for (int u = 0; u < kRunsPerThread; ++u) {
-        const int j = (t >> 5) + 8 * u;
-        if (j < ng) {
-            float y[8];
-            if constexpr (is_iq(QT))
-                decode_run_iq<8>(QT, lds + j * GB, 8 * (t & 31), y);  // the type is a constant: the switch folds
-            else
-                decode_run<QT, 8>(lds + j * GB, 8 * (t & 31), y);
-            if constexpr (sizeof(OUT) == 4) {
-                float4* o = reinterpret_cast<float4*>(ob + j * 256 + 8 * (t & 31));
-                o[0] = make_float4(y[0], y[1], y[2], y[3]);
-                o[1] = make_float4(y[4], y[5], y[6], y[7]);
-            } else {
-                uint4 v;
-                v.x = f2bf2(y[0], y[1]);
-                v.y = f2bf2(y[2], y[3]);
-                v.z = f2bf2(y[4], y[5]);
-                v.w = f2bf2(y[6], y[7]);
-                *reinterpret_cast<uint4*>(out + (g0 + j) * 256 + 8 * (t & 31)) = v;
-            }
-        }
-    }
-    if constexpr (sizeof(OUT) == 4) {
-        __syncthreads();
-        const float4* src = reinterpret_cast<const float4*>(ob);
-        float4* dst = reinterpret_cast<float4*>(out + g0 * 256);
-        for (int i = t; i < ng * 64; i += kStreamThreads) dst[i] = src[i];
-    }
+    if constexpr (dequant_book_in_lds(QT))
+        dequant_groups<QT, OUT, RUNS>(lds, out, g0, ng, LdsBook{(const __attribute__((address_space(3))) uint8_t*)book});
+    else
+        dequant_groups<QT, OUT, RUNS>(lds, out, g0, ng, GlobalBooks());
+}
+
+template <int QT, class OUT>
+static void launch_dequant_qt(const uint8_t* q, OUT* out, int64_t ngroups, hipStream_t s) {
+    constexpr int GPB = kStreamThreads / 32 * dequant_runs(QT);
+    const dim3 grid((unsigned)((ngroups + GPB - 1) / GPB));
+    dequant_kernel<QT, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups);
 }
 
 template <class OUT>
 static hipError_t launch_dequant_t(int qtype, const uint8_t* q, OUT* out, int64_t ngroups, hipStream_t s) {
     if (ngroups <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((ngroups + kGroupsPerBlock - 1) / kGroupsPerBlock));
     switch (qtype) {
-    case Q8_0: dequant_kernel<Q8_0, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q2_K: dequant_kernel<Q2_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q3_K: dequant_kernel<Q3_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q4_K: dequant_kernel<Q4_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q5_K: dequant_kernel<Q5_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case Q6_K: dequant_kernel<Q6_K, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ2_XXS: dequant_kernel<IQ2_XXS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ2_XS: dequant_kernel<IQ2_XS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ2_S: dequant_kernel<IQ2_S, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ3_XXS: dequant_kernel<IQ3_XXS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ3_S: dequant_kernel<IQ3_S, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ1_S: dequant_kernel<IQ1_S, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ1_M: dequant_kernel<IQ1_M, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
-    case IQ4_XS: dequant_kernel<IQ4_XS, OUT><<<grid, kStreamThreads, 0, s>>>(q, out, ngroups); break;
+    case Q8_0: launch_dequant_qt<Q8_0, OUT>(q, out, ngroups, s); break;
+    case Q2_K: launch_dequant_qt<Q2_K, OUT>(q, out, ngroups, s); break;
+    case Q3_K: launch_dequant_qt<Q3_K, OUT>(q, out, ngroups, s); break;
+    case Q4_K: launch_dequant_qt<Q4_K, OUT>(q, out, ngroups, s); break;
+    case Q5_K: launch_dequant_qt<Q5_K, OUT>(q, out, ngroups, s); break;
+    case Q6_K: launch_dequant_qt<Q6_K, OUT>(q, out, ngroups, s); break;
+    case IQ2_XXS: launch_dequant_qt<IQ2_XXS, OUT>(q, out, ngroups, s); break;
+    case IQ2_XS: launch_dequant_qt<IQ2_XS, OUT>(q, out, ngroups, s); break;
+    case IQ2_S: launch_dequant_qt<IQ2_S, OUT>(q, out, ngroups, s); break;
+    case IQ3_XXS: launch_dequant_qt<IQ3_XXS, OUT>(q, out, ngroups, s); break;
+    case IQ3_S: launch_dequant_qt<IQ3_S, OUT>(q, out, ngroups, s); break;
+    case IQ1_S: launch_dequant_qt<IQ1_S, OUT>(q, out, ngroups, s); break;
+    case IQ1_M: launch_dequant_qt<IQ1_M, OUT>(q, out, ngroups, s); break;
+    case IQ4_XS: launch_dequant_qt<IQ4_XS, OUT>(q, out, ngroups, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -28,9 +28,57 @@
 
 namespace vq {
 
-#define VQ_IQ_TABLE(type, name, n) static __device__ const type name[n]
+// 16-byte aligned, so a kernel can copy a table to LDS with direct-to-LDS loads
+#define VQ_IQ_TABLE(type, name, n) static __device__ const type name[n] __attribute__((aligned(16)))
 #include "vq_iq_grids.inc"
 #undef VQ_IQ_TABLE
+
+// Where the code-book lookups of a decode read from.  GlobalBooks: the tables
+// in global memory (every decode site; the lookups go through L1).  LdsBook:
+// a kernel that decodes one IQ format has copied that format's table to LDS
+// (iq_book_bytes / iq_book_src) and reads it there.
+struct GlobalBooks {
+    __device__ __forceinline__ uint64_t q2xxs(uint32_t i) const { return iq2xxs_grid[i]; }
+    __device__ __forceinline__ uint64_t q2xs(uint32_t i) const { return iq2xs_grid[i]; }
+    __device__ __forceinline__ uint64_t q2s(uint32_t i) const { return iq2s_grid[i]; }
+    __device__ __forceinline__ uint32_t q3xxs(uint32_t i) const { return iq3xxs_grid[i]; }
+    __device__ __forceinline__ uint32_t q3s(uint32_t i) const { return iq3s_grid[i]; }
+    __device__ __forceinline__ uint64_t q1s(uint32_t i) const { return iq1s_grid[i]; }
+};
+
+struct LdsBook {
+    const __attribute__((address_space(3))) uint8_t* p;
+    __device__ __forceinline__ uint64_t u64(uint32_t i) const {
+        return reinterpret_cast<const __attribute__((address_space(3))) uint64_t*>(p)[i];
+    }
+    __device__ __forceinline__ uint32_t u32(uint32_t i) const {
+        return reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(p)[i];
+    }
+    __device__ __forceinline__ uint64_t q2xxs(uint32_t i) const { return u64(i); }
+    __device__ __forceinline__ uint64_t q2xs(uint32_t i) const { return u64(i); }
+    __device__ __forceinline__ uint64_t q2s(uint32_t i) const { return u64(i); }
+    __device__ __forceinline__ uint32_t q3xxs(uint32_t i) const { return u32(i); }
+    __device__ __forceinline__ uint32_t q3s(uint32_t i) const { return u32(i); }
+    __device__ __forceinline__ uint64_t q1s(uint32_t i) const { return u64(i); }
+};
+
+// Bytes of the code book a format's decode reads (0: none, IQ4_XS's 16
+// values sit in registers), and its address in global memory.
+__host__ __device__ constexpr int iq_book_bytes(int qt) {
+    return qt == IQ2_XXS ? 256 * 8 : qt == IQ2_XS ? 512 * 8 : qt == IQ2_S ? 1024 * 8 : qt == IQ3_XXS ? 256 * 4
+         : qt == IQ3_S ? 512 * 4 : (qt == IQ1_S || qt == IQ1_M) ? 2048 * 8 : 0;
+}
+
+__device__ __forceinline__ const uint8_t* iq_book_src(int qt) {
+    switch (qt) {
+    case IQ2_XXS: return reinterpret_cast<const uint8_t*>(iq2xxs_grid);
+    case IQ2_XS: return reinterpret_cast<const uint8_t*>(iq2xs_grid);
+    case IQ2_S: return reinterpret_cast<const uint8_t*>(iq2s_grid);
+    case IQ3_XXS: return reinterpret_cast<const uint8_t*>(iq3xxs_grid);
+    case IQ3_S: return reinterpret_cast<const uint8_t*>(iq3s_grid);
+    default: return reinterpret_cast<const uint8_t*>(iq1s_grid);
+    }
+}
 
 __host__ __device__ constexpr bool is_iq(int qt) {
     return qt == IQ2_XXS || qt == IQ2_XS || qt == IQ3_XXS || qt == IQ1_S || qt == IQ3_S || qt == IQ2_S ||
@@ -63,12 +111,13 @@ __device__ __forceinline__ uint32_t iq1_codes(uint32_t g4, bool neg) {
 // Eight consecutive weights 8 l .. 8 l + 7 of sub-block ib (32 weights), as
 // biased codes in two words.  g may point into LDS or global memory; IQ
 // groups are only 2-byte aligned, so every multi-byte field is read in halves.
+template <class Books = GlobalBooks>
 __device__ __forceinline__ void iq_group8(int qt, const uint8_t* __restrict__ g, int ib, int l, uint32_t& w0,
-                                          uint32_t& w1) {
+                                          uint32_t& w1, const Books& bk = Books()) {
     switch (qt) {
     case IQ2_XXS: {
         const uint8_t* q = g + 2 + 8 * ib;
-        const uint64_t gr = iq2xxs_grid[q[l]];
+        const uint64_t gr = bk.q2xxs(q[l]);
         const uint32_t s = parity_signs((rd_u32(q + 4) >> (7 * l)) & 127u);
         w0 = signed_grid((uint32_t)gr, s);
         w1 = signed_grid((uint32_t)(gr >> 32), s >> 4);
@@ -76,7 +125,7 @@ __device__ __forceinline__ void iq_group8(int qt, const uint8_t* __restrict__ g,
     }
     case IQ2_XS: {
         const uint32_t q = rd_u16(g + 2 + 2 * (4 * ib + l));
-        const uint64_t gr = iq2xs_grid[q & 511u];
+        const uint64_t gr = bk.q2xs(q & 511u);
         const uint32_t s = parity_signs(q >> 9);
         w0 = signed_grid((uint32_t)gr, s);
         w1 = signed_grid((uint32_t)(gr >> 32), s >> 4);
@@ -84,7 +133,7 @@ __device__ __forceinline__ void iq_group8(int qt, const uint8_t* __restrict__ g,
     }
     case IQ2_S: {
         const uint32_t idx = g[2 + 4 * ib + l] | (((uint32_t)g[66 + ib] << (8 - 2 * l)) & 0x300u);
-        const uint64_t gr = iq2s_grid[idx];
+        const uint64_t gr = bk.q2s(idx);
         const uint32_t s = g[34 + 4 * ib + l];
         w0 = signed_grid((uint32_t)gr, s);
         w1 = signed_grid((uint32_t)(gr >> 32), s >> 4);
@@ -92,20 +141,20 @@ __device__ __forceinline__ void iq_group8(int qt, const uint8_t* __restrict__ g,
     }
     case IQ3_XXS: {
         const uint32_t s = parity_signs((rd_u32(g + 66 + 4 * ib) >> (7 * l)) & 127u);
-        w0 = signed_grid(iq3xxs_grid[g[2 + 8 * ib + 2 * l]], s);
-        w1 = signed_grid(iq3xxs_grid[g[2 + 8 * ib + 2 * l + 1]], s >> 4);
+        w0 = signed_grid(bk.q3xxs(g[2 + 8 * ib + 2 * l]), s);
+        w1 = signed_grid(bk.q3xxs(g[2 + 8 * ib + 2 * l + 1]), s >> 4);
         break;
     }
     case IQ3_S: {
         const uint32_t h = g[66 + ib];
         const uint32_t s = g[74 + 4 * ib + l];
-        w0 = signed_grid(iq3s_grid[g[2 + 8 * ib + 2 * l] | ((h << (8 - 2 * l)) & 256u)], s);
-        w1 = signed_grid(iq3s_grid[g[2 + 8 * ib + 2 * l + 1] | ((h << (7 - 2 * l)) & 256u)], s >> 4);
+        w0 = signed_grid(bk.q3s(g[2 + 8 * ib + 2 * l] | ((h << (8 - 2 * l)) & 256u)), s);
+        w1 = signed_grid(bk.q3s(g[2 + 8 * ib + 2 * l + 1] | ((h << (7 - 2 * l)) & 256u)), s >> 4);
         break;
     }
     case IQ1_S: {
         const uint32_t qh = rd_u16(g + 34 + 2 * ib);
-        const uint64_t gr = iq1s_grid[g[2 + 4 * ib + l] | (((qh >> (3 * l)) & 7u) << 8)];
+        const uint64_t gr = bk.q1s(g[2 + 4 * ib + l] | (((qh >> (3 * l)) & 7u) << 8));
         const bool neg = (qh & 0x8000u) != 0;
         w0 = iq1_codes((uint32_t)gr, neg);
         w1 = iq1_codes((uint32_t)(gr >> 32), neg);
@@ -114,7 +163,7 @@ __device__ __forceinline__ void iq_group8(int qt, const uint8_t* __restrict__ g,
     case IQ1_M: {
         const uint32_t h = g[32 + 2 * ib + (l >> 1)];
         const uint32_t idx = g[4 * ib + l] | ((h << ((l & 1) ? 4 : 8)) & 0x700u);
-        const uint64_t gr = iq1s_grid[idx];
+        const uint64_t gr = bk.q1s(idx);
         const bool neg = (h & ((l & 1) ? 0x80u : 0x08u)) != 0;
         w0 = iq1_codes((uint32_t)gr, neg);
         w1 = iq1_codes((uint32_t)(gr >> 32), neg);
@@ -182,14 +231,14 @@ __device__ __forceinline__ float iq_scale(int qt, const uint8_t* __restrict__ g,
 }
 
 // Weights p .. p + R - 1 (p a multiple of R) of the 256-weight group at g.
-template <int R>
+template <int R, class Books = GlobalBooks>
 __device__ __forceinline__ void iq_affine(int qt, const uint8_t* __restrict__ g, int p, uint32_t (&uw)[R / 4],
-                                          float& dl) {
+                                          float& dl, const Books& bk = Books()) {
     static_assert(R == 8 || R == 16, "runs of 8 or 16 weights");
     const int ib = p >> 5, l = (p >> 3) & 3;
     dl = iq_scale(qt, g, ib, l);
 #pragma unroll
-    for (int h = 0; h < R / 8; ++h) iq_group8(qt, g, ib, l + h, uw[2 * h], uw[2 * h + 1]);
+    for (int h = 0; h < R / 8; ++h) iq_group8(qt, g, ib, l + h, uw[2 * h], uw[2 * h + 1], bk);
 }
 
 }  // namespace vq
