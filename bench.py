@@ -135,7 +135,8 @@ def measured_peaks(torch, dev) -> dict:
     """Sustained bf16 MFMA rate (a long register-only stream of
     v_mfma_f32_32x32x16_bf16 on every SIMD, about 0.3 s, so the clock settles
     where the power limit puts it) and HBM bandwidth (a 4 GiB read, a
-    2 GiB -> 2 GiB copy), timed with HIP events on the launch stream."""
+    2 GiB -> 2 GiB copy, a 4 GiB write), timed with HIP events on the launch
+    stream.""" 
     import ctypes
 
     lib = ctypes.CDLL(str(ROOT / "voodoo-dyn-quant_amd" / "voodoo_quant" / "libvq_probe.so"))
@@ -183,6 +184,9 @@ def measured_peaks(torch, dev) -> dict:
     half = nbytes // 2
     t = time_events(torch, lambda: lib.vq_probe_hbm_copy(buf.data_ptr(), buf.data_ptr() + half, half, stream), 5)
     rec["hbm_copy_GBps"] = round(2 * half / (t * 1e-3) / 1e9, 1)
+    lib.vq_probe_hbm_write.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    t = time_events(torch, lambda: lib.vq_probe_hbm_write(buf.data_ptr(), nbytes, stream), 5)
+    rec["hbm_write_GBps"] = round(nbytes / (t * 1e-3) / 1e9, 1)
     del buf
     torch.cuda.empty_cache()
     log(f"measured peaks: {rec}")
@@ -333,9 +337,12 @@ SWEEP_SHAPES = [("27b_q", 5120, 6144), ("27b_o", 6144, 5120), ("27b_gate_up", 51
 
 
 def shape_sweep(torch, dev, gen, m: int = 8192, reps: int = 5) -> dict:
-    """Per shape: the mix, the forward GEMM (forward minus mix) and the
-    backward launch (dX + gate products, plus the gate reduce), HIP events on
-    the stream the C ABI uses, with their TFLOP/s (2 m n d per product)."""
+    """Per shape: the mix, the forward GEMM (``vq_linear_fwd`` over the
+    premixed W_eff, timed on its own: at 1024-wide shapes the mix is a
+    launch-latency-bound ~10-25 us that a difference of two timings would
+    mostly measure) and the backward launch (dX + gate products, plus the gate
+    reduce), HIP events on the stream the C ABI uses, with their TFLOP/s
+    (2 m n d per product)."""
     from voodoo_quant import _hip
 
     ids = [GGML[t] for t in TYPES]
@@ -352,16 +359,18 @@ def shape_sweep(torch, dev, gen, m: int = 8192, reps: int = 5) -> dict:
         ws = torch.empty(_hip.bwd_workspace_bytes(m, n, d, d, len(TYPES), False), dtype=torch.uint8, device=dev)
         fws = torch.empty(max(_hip.fwd_workspace_bytes(m, n, d), 256), dtype=torch.uint8, device=dev)
         t_mix = time_events(torch, lambda: _hip.mix_weight(ids, qbytes, probs, n, d, w_eff), reps)
+        t_gemm = time_events(torch, lambda: _hip.linear_fwd(x, w_eff, n, y, fws), reps)
         t_fwd = time_events(torch, lambda: _hip.gated_linear_fwd(x, ids, qbytes, probs, n, d, w_eff, y, fws), reps)
         t_bwd = time_events(torch, lambda: _hip.gated_linear_bwd(dy, x, ids, qbytes, probs, n, d, w_eff, dx, dp, ws),
                             reps)
         f = 2.0 * m * n * d
-        res[name] = {"in": d, "out": n, "mix_ms": round(t_mix, 4), "fwd_gemm_ms": round(t_fwd - t_mix, 4),
-                     "bwd_dx_gate_ms": round(t_bwd, 4),
-                     "fwd_TFLOPs": round(f / ((t_fwd - t_mix) * 1e-3) / 1e12, 1),
+        res[name] = {"in": d, "out": n, "mix_ms": round(t_mix, 4), "fwd_gemm_ms": round(t_gemm, 4),
+                     "fwd_ms": round(t_fwd, 4), "bwd_dx_gate_ms": round(t_bwd, 4),
+                     "fwd_TFLOPs": round(f / (t_gemm * 1e-3) / 1e12, 1),
                      "bwd_TFLOPs": round(2 * f / (t_bwd * 1e-3) / 1e12, 1),
                      "step_TFLOPs": round(3 * f / ((t_fwd + t_bwd) * 1e-3) / 1e12, 1)}
-        log(f"shape {name} {d}->{n}: mix {t_mix:.3f} ms, fwd gemm {t_fwd - t_mix:.3f} ms, bwd {t_bwd:.3f} ms")
+        log(f"shape {name} {d}->{n}: mix {t_mix:.3f} ms, fwd gemm {t_gemm:.3f} ms (mix + gemm {t_fwd:.3f}), "
+            f"bwd {t_bwd:.3f} ms")
         del qbytes, x, dy, w_eff, y, dx, ws, fws
     return res
 

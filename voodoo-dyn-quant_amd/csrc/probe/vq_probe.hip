@@ -115,11 +115,32 @@ __global__ __launch_bounds__(256) void hbm_read_kernel(const u32x4* __restrict__
     sink[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = x[0] ^ x[1] ^ x[2] ^ x[3];
 }
 
+// Copy with 8 16-byte loads in flight per thread (a workgroup moves 32 KB
+// per iteration, consecutive threads on consecutive words): the memory-level
+// parallelism of the dequant kernels, which a one-word-per-iteration copy
+// (about 4.9 TB/s) does not reach.  n16 is a multiple of 8 * 256 here.
+constexpr int kCopyUnroll = 8;
+
 __global__ __launch_bounds__(256) void hbm_copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
                                                        int64_t n16) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
-        __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+    const int64_t per_block = 256 * kCopyUnroll;
+    for (int64_t base = (int64_t)blockIdx.x * per_block; base < n16; base += (int64_t)gridDim.x * per_block) {
+        u32x4 v[kCopyUnroll];
+#pragma unroll
+        for (int k = 0; k < kCopyUnroll; ++k) v[k] = src[base + k * 256 + threadIdx.x];
+#pragma unroll
+        for (int k = 0; k < kCopyUnroll; ++k) dst[base + k * 256 + threadIdx.x] = v[k];
+    }
+}
+
+// Write-only stream of n16 16-byte words (the output side of dequant alone).
+__global__ __launch_bounds__(256) void hbm_write_kernel(u32x4* __restrict__ dst, int64_t n16) {
+    const int64_t per_block = 256 * kCopyUnroll;
+    const u32x4 v = {1u, 2u, 3u, (uint32_t)threadIdx.x};
+    for (int64_t base = (int64_t)blockIdx.x * per_block; base < n16; base += (int64_t)gridDim.x * per_block) {
+#pragma unroll
+        for (int k = 0; k < kCopyUnroll; ++k) dst[base + k * 256 + threadIdx.x] = v;
+    }
 }
 
 int cus() {
@@ -177,10 +198,19 @@ int vq_probe_hbm_read(const void* src, int64_t bytes, uint32_t* sink, void* stre
     return (int)hipGetLastError();
 }
 
-// Copy `bytes` (a multiple of 16) from src to dst.
+// Copy `bytes` (a multiple of 32 KiB) from src to dst.
 int vq_probe_hbm_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+    if (bytes % (16 * 256 * kCopyUnroll)) return (int)hipErrorInvalidValue;
     hbm_copy_kernel<<<dim3(vq_probe_hbm_blocks()), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
         static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), bytes / 16);
+    return (int)hipGetLastError();
+}
+
+// Write `bytes` (a multiple of 32 KiB) at dst.
+int vq_probe_hbm_write(void* dst, int64_t bytes, void* stream) {
+    if (bytes % (16 * 256 * kCopyUnroll)) return (int)hipErrorInvalidValue;
+    hbm_write_kernel<<<dim3(vq_probe_hbm_blocks()), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<u32x4*>(dst), bytes / 16);
     return (int)hipGetLastError();
 }
 
