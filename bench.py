@@ -518,6 +518,69 @@ def stack_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
     return rec
 
 
+def stream_schedule_bench(torch, dev, steps: int = 3, warmup: int = 2, slots: int = 6, depth: int = 5) -> dict:
+    """The stress step with its candidates in pinned host memory instead of
+    HBM (a model whose candidates do not fit on the GPU): every product's
+    packed bytes are copied host -> device before its forward and again
+    before its backward, as the reference does every step
+    (``layers.py:348, 362``).  Timed three ways on one model: candidates
+    resident (no copies), streamed in stream order (each copy in front of its
+    product, the reference's pattern), and streamed ahead of use on a copy
+    stream (``streaming.CandidateStreamer``, `depth` products ahead through
+    `slots` device slots).  Also the host -> device rate of one 1 GiB pinned
+    copy."""
+    from voodoo_quant.training import step as st
+
+    cfg = st.StackConfig()
+    types = ["Q2_K", "IQ2_XXS", "Q3_K", "IQ3_S", "Q4_K", "Q5_K", "Q6_K", "Q8_0"]
+    student, teacher, replaced = st.build_stack(cfg, types, dev, seed=1)
+    tokens = 2 * 8192
+    g = torch.Generator(device=dev).manual_seed(6)
+    x = torch.randn(tokens, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
+    cand_bytes = sum(q.numel() for m in replaced.values() for q in m._qbytes())
+
+    def timed(**stream):
+        tr = st.StackTrainer(student, teacher, replaced,
+                             st.StepConfig(max_steps=200, temp_start=2.0, temp_end=0.1, **stream),
+                             total_8bit_bytes=float(cfg.gated_weights()))
+        for _ in range(warmup):
+            tr.step(x)
+        torch.cuda.synchronize()
+        copied0 = tr.streamer.bytes_copied if tr.streamer else 0
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tr.step(x)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / max(steps, 1) * 1e3
+        copied = ((tr.streamer.bytes_copied - copied0) / max(steps, 1)) if tr.streamer else 0
+        if tr.streamer:
+            tr.streamer.release()
+        tr.bank.release()
+        return ms, copied
+
+    resident_ms, _ = timed()
+    serial_ms, serial_bytes = timed(stream_candidates=True, stream_overlap=False, stream_slots=slots,
+                                    stream_depth=depth)
+    overlap_ms, overlap_bytes = timed(stream_candidates=True, stream_slots=slots, stream_depth=depth)
+    host = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+    devbuf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    t = time_events(torch, lambda: devbuf.copy_(host, non_blocking=True), 3)
+    h2d = (1 << 30) / (t * 1e-3) / 1e9
+    rec = {"resident_ms": round(resident_ms, 2), "streamed_serial_ms": round(serial_ms, 2),
+           "streamed_overlap_ms": round(overlap_ms, 2),
+           "overlap_speedup_vs_serial": round(serial_ms / overlap_ms, 3),
+           "candidate_bytes": cand_bytes, "copied_bytes_per_step_serial": int(serial_bytes),
+           "copied_bytes_per_step_overlap": int(overlap_bytes), "h2d_GBps": round(h2d, 1),
+           "copy_floor_ms": round(overlap_bytes / (h2d * 1e9) * 1e3, 2), "slots": slots, "depth": depth,
+           "workload": "the stress step (8 SwiGLU blocks, hidden 4096, MLP 14336, K=8, 2 x 8192 tokens) with "
+                       "its 24 tensors' candidates in pinned host memory, copied before each forward and backward"}
+    log(f"stream schedule: resident {resident_ms:.1f} ms, streamed in order {serial_ms:.1f} ms, overlapped "
+        f"{overlap_ms:.1f} ms (copies {overlap_bytes / 1e9:.2f} GB/step at {h2d:.1f} GB/s)")
+    del student, teacher, replaced, x, host, devbuf
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -529,6 +592,10 @@ def main() -> int:
     ap.add_argument("--only-train", action="store_true",
                     help="measure only the decoder gate-training step and print its record")
     ap.add_argument("--no-stack", action="store_true", help="skip the 8-block SwiGLU stress measurement")
+    ap.add_argument("--no-stream", action="store_true",
+                    help="skip the stress step with candidates streamed from host memory")
+    ap.add_argument("--only-stream", action="store_true",
+                    help="measure only the stress step with streamed candidates and print its record")
     ap.add_argument("--only-stack", action="store_true",
                     help="measure only the 8-block SwiGLU stress step and print its record")
     ap.add_argument("--prefetch-mix", action="store_true",
@@ -567,6 +634,9 @@ def main() -> int:
         return 0
     if args.only_train:
         print(json.dumps({"train": train_step_bench(torch, dev, args.train_steps, 2, args.prefetch_mix, args.defer_gate_grads)}), flush=True)
+        return 0
+    if args.only_stream:
+        print(json.dumps({"stream_schedule": stream_schedule_bench(torch, dev)}), flush=True)
         return 0
     if args.only_stack:
         print(json.dumps({"stress": stack_step_bench(torch, dev, 3, 2, args.prefetch_mix, args.defer_gate_grads)}), flush=True)
@@ -707,6 +777,9 @@ def main() -> int:
     stack = None
     if not args.no_stack:
         stack = stack_step_bench(torch, dev, 3, 2, args.prefetch_mix, args.defer_gate_grads)
+    stream = None
+    if not args.no_stream and not args.no_stack:
+        stream = stream_schedule_bench(torch, dev)
 
     if args.copy_calibration:
         copy_calibration(torch, dev)
@@ -757,6 +830,7 @@ def main() -> int:
         "shapes": shapes,
         "train": train,
         "stress": stack,
+        "stream_schedule": stream,
         "cpu_baseline": cpu,
         "cpu_extra": extra,
         "host": host_info(),

@@ -158,3 +158,20 @@ def test_gate_bank_defers_only_on_a_rocm_device():
     bank.end()
     (param,) = bank.parameters()
     assert param.grad is not None and param.grad.shape == (2, 3)
+
+
+def test_candidate_streamer_argument_checks():
+    """The streamer needs 1 <= depth < slots (a prefetch must never reach a
+    slot whose last user the fence has not covered) and a non-empty product
+    list; the checks come before any device work."""
+    from voodoo_quant.streaming import CandidateStreamer
+
+    with pytest.raises(ValueError, match="depth"):
+        CandidateStreamer([[object()]], "cpu", slots=2, depth=2)
+    with pytest.raises(ValueError, match="depth"):
+        CandidateStreamer([[object()]], "cpu", slots=4, depth=0)
+    with pytest.raises(ValueError, match="no products"):
+        CandidateStreamer([], "cpu")
+    # streaming excludes the mix prefetch and deferred gate gradients
+    with pytest.raises(ValueError, match="streamed candidates"):
+        st._make_streamer(st.StepConfig(stream_candidates=True, prefetch_mix=True), nn.Linear(2, 2))

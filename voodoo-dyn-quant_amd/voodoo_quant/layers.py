@@ -492,7 +492,14 @@ def gated_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
     x2 = x.reshape(-1, x.shape[-1])
     if x2.dtype != torch.bfloat16:
         x2 = x2.to(torch.bfloat16)
-    pre = MixPrefetch.take(modules)
+    streamer = modules[0].__dict__.get("_streamer")
+    if streamer is not None:
+        if any(m.__dict__.get("_streamer") is not streamer for m in modules) or \
+                any(m.__dict__.get("_gate_sink") is not None for m in modules):
+            raise RuntimeError("a stacked product's members must share one candidate streamer and run without "
+                               "deferred gate gradients")
+        streamer.forward_fence(modules[0])
+    pre = MixPrefetch.take(modules) if streamer is None else None
     # deferred gate gradients only when every member has a sink (else autograd
     # for all); the probabilities stay attached either way, so the product's
     # backward runs even when its input needs no gradient, and returns None
@@ -508,6 +515,8 @@ def gated_linear_group(x: torch.Tensor, modules: list, stacked: bool = False):
         members.append((m._ggml_types(), m.out_features))
     meta = (tuple(members), modules[0].padded_in_features)
     y = GatedLinearGroupFunction.apply(x2, meta, pre[0] if pre is not None else None, sinks, *probs, *qbytes)
+    if streamer is not None:
+        y = streamer.fenced(y, modules[0])
     if stacked:
         return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     outs = torch.split(y, [m.out_features for m in modules], dim=1)
@@ -737,9 +746,14 @@ class _MixedQuantBase(nn.Module):
 
     # -- candidate storage ----------------------------------------------------
     def _qbytes(self) -> list[torch.Tensor]:
+        streamer = self.__dict__.get("_streamer")
+        if streamer is not None:  # views of this product's device slot (streaming.CandidateStreamer)
+            return streamer.views(self)
         return [getattr(self, f"_qweight_{k}") for k in range(self.num_candidates)]
 
     def _move_qbytes(self, device) -> None:
+        if self.__dict__.get("_streamer") is not None:  # the streamer stages the bytes
+            return
         device = torch.device(device)
         for k in range(self.num_candidates):
             qb = getattr(self, f"_qweight_{k}")
@@ -924,7 +938,13 @@ class MixedQuantLinear(_MixedQuantBase):
         if x.device.type != "cuda":
             raise RuntimeError(f"{self._tensor_name}: MixedQuantLinear runs on a ROCm device only (got {x.device})")
         self._move_qbytes(x.device)
-        pre = None if _PTQR_STATE.enabled else MixPrefetch.take([self])
+        streamer = self.__dict__.get("_streamer")
+        if streamer is not None:
+            if _PTQR_STATE.enabled or self.__dict__.get("_gate_sink") is not None:
+                raise RuntimeError(f"{self._tensor_name}: streamed candidates run without PTQR routing and "
+                                   "without deferred gate gradients")
+            streamer.forward_fence(self)
+        pre = None if _PTQR_STATE.enabled or streamer is not None else MixPrefetch.take([self])
         probs = pre[1][0] if pre is not None else self.get_probs()
         if probs.device != x.device:
             probs = probs.to(x.device)
@@ -942,6 +962,8 @@ class MixedQuantLinear(_MixedQuantBase):
             # even when x needs no gradient); the backward returns None for them
             y = GatedLinearFunction.apply(x2, probs, meta, pre[0] if pre is not None else None,
                                           self.__dict__.get("_gate_sink"), *self._qbytes())
+            if streamer is not None:
+                y = streamer.fenced(y, self)
         if x.dtype != torch.bfloat16:
             y = y.to(x.dtype)
         out = y.reshape(*lead, self.out_features)
