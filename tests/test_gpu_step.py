@@ -9,7 +9,7 @@ the embedding gated, a Q8_0 teacher).
   relative L2 over all gate gradients (measured on MI355X: 9.7e-3; the
   Linear-level bar is 1e-2, and bf16 activations through two layers and
   torch's attention add their rounding) and every tensor's gradient within
-  25 degrees of the reference's.
+  8 degrees of the reference's (cosine above 0.99; measured minimum 0.9987).
 * The chunked loss path reproduces the full-logits path's gradients.
 * Several optimizer steps stay finite and move the gates.
 """
@@ -113,9 +113,14 @@ def test_step_gate_gradients_match_reference_formulation(models):
     print(f"gate-gradient relative L2 {rel:.2e} over {len(mapping)} tensors", flush=True)
     assert rel < 1.5e-2
     # per tensor: every gradient points the same way
+    coss = {}
     for n in mapping:
         a, b = replaced[n].gates.grad.double(), mapping[n].gates.grad.double()
-        assert float(torch.dot(a, b)) > 0.9 * float(a.norm() * b.norm()), n
+        coss[n] = float(torch.dot(a, b)) / float(a.norm() * b.norm())
+    worst = min(coss, key=coss.get)
+    print(f"per-tensor cosine: min {coss[worst]:.6f} ({worst})", flush=True)
+    for n, c in coss.items():
+        assert c > 0.99, n
 
 
 def test_chunked_path_matches_full_logits(models):
