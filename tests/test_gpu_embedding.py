@@ -280,6 +280,59 @@ def test_bf16_module_rows_and_duplicates(hip):
         emb(torch.tensor([0, vocab], device="cuda"))
 
 
+def test_mixture_gate_gradient_with_repeated_ids(hip):
+    """Without PTQR every position decodes its own row: a repeated id's
+    gate-gradient terms add up, dL/dp_k = sum_t <G_t, W_k[id_t]>, as the
+    reference's unique-row lookup scattered back (layers.py:670-750)."""
+    torch.manual_seed(29)
+    vocab, dim = 40, 512
+    qts = ["Q3_K", "Q5_K", "IQ4_XS"]
+    emb = layers.MixedQuantEmbedding(vocab, dim, qts, torch.randn(vocab, dim, dtype=torch.float32) * 0.05,
+                                     tensor_name="tests.emb.repeats").cuda()
+    ids = torch.randint(0, 6, (3, 50)).cuda()  # every id repeated many times
+    cands = [c.cuda().double() for c in _oracle_candidates(emb, dim)]
+    y = emb(ids)
+    G = torch.randn_like(y)
+    y.backward(G)
+    flat = ids.reshape(-1)
+    gp = torch.stack([(G.reshape(-1, dim).double() * c[flat]).sum() for c in cands])
+    p = emb.soft_probs().detach().double()
+    gates_ref = (torch.diag(p) - torch.outer(p, p)) @ gp
+    err = float((emb.gates.grad.double() - gates_ref).norm() / gates_ref.norm())
+    assert err < 1e-5, err
+
+
+def test_deferred_id_check(hip):
+    """id_check = "deferred": the lookup returns at once (zero rows for the
+    out-of-range ids, as the row kernels give), and raise_pending_id_errors
+    raises the IndexError afterwards; valid lookups leave nothing pending."""
+    from voodoo_quant.training.q8_teacher import Q8Embedding
+
+    torch.manual_seed(31)
+    vocab, dim = 50, 256
+    emb = layers.MixedQuantEmbedding(vocab, dim, ["Q4_K", "Q8_0"], torch.randn(vocab, dim) * 0.05,
+                                     tensor_name="tests.emb.deferred").cuda()
+    qb, _ = _q8_bytes(vocab, dim, seed=7)
+    q8 = Q8Embedding(qb.cuda(), vocab, dim)
+    layers.raise_pending_id_errors()
+    for mod in (emb, q8):
+        with pytest.raises(IndexError):
+            mod(torch.tensor([1, vocab], device="cuda"))
+        mod.id_check = "deferred"
+        try:
+            y = mod(torch.tensor([[1, vocab], [-1, 2]], device="cuda"))
+            assert y.shape == (2, 2, dim)
+            assert torch.count_nonzero(y[0, 1]) == 0 and torch.count_nonzero(y[1, 0]) == 0
+            assert torch.count_nonzero(y[0, 0]) > 0
+            with pytest.raises(IndexError, match="index out of range"):
+                layers.raise_pending_id_errors()
+            mod(torch.tensor([0, vocab - 1], device="cuda"))
+            layers.raise_pending_id_errors()  # nothing pending raises
+        finally:
+            mod.id_check = "sync"
+    assert not layers._PENDING_ID_CHECKS
+
+
 # ----------------------------------------------------------------------------- Q8_0 teacher
 def _q8_bytes(rows, cols, seed):
     from voodoo_quant import rtn

@@ -12,6 +12,8 @@ the embedding gated, a Q8_0 teacher).
   8 degrees of the reference's (cosine above 0.99; measured minimum 0.9987).
 * The chunked loss path reproduces the full-logits path's gradients.
 * Several optimizer steps stay finite and move the gates.
+* A step makes no device synchronisation (the embeddings' id checks deferred),
+  and an out-of-range id raises at the next step.
 """
 
 import copy
@@ -149,6 +151,38 @@ def test_steps_are_finite_and_move_the_gates(models):
     assert all(torch.isfinite(torch.as_tensor(v)).all() for v in out.values())
     after = torch.cat([m.gates.detach() for m in replaced.values()])
     assert torch.isfinite(after).all() and float((after - before).abs().max()) > 1e-3
+
+
+def test_step_makes_no_device_synchronisation(models):
+    """With the embeddings' id checks deferred (the harness default) a whole
+    step (both forwards on two streams, the fused loss, the backward, clip and
+    AdamW) queues its work without waiting for the device: torch's sync debug
+    mode, set to raise, sees no synchronising call.  An out-of-range id then
+    surfaces at the next step."""
+    student, teacher, replaced = models
+    x, y = _batch(torch.device("cuda", 0))
+    tr = st.GateTrainer(student, teacher, replaced, st.StepConfig(max_steps=6, teacher_stream=True),
+                        float(CFG.gated_weights()))
+    try:
+        for _ in range(2):
+            tr.step(x, y)
+        torch.cuda.synchronize()
+        layers.raise_pending_id_errors()  # nothing left for the next step to wait on
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            tr.step(x, y)
+        finally:
+            torch.cuda.set_sync_debug_mode(0)
+        torch.cuda.synchronize()
+        bad = x.clone()
+        bad[0, 3] = CFG.vocab
+        tr.step(bad, y)
+        with pytest.raises(IndexError, match="index out of range"):
+            tr.step(x, y)
+    finally:
+        layers._PENDING_ID_CHECKS.clear()
+        for m in st._embeddings(student, teacher):
+            m.id_check = "sync"
 
 
 def test_swiglu_stack_steps_with_repeated_formats():

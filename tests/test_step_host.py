@@ -175,3 +175,21 @@ def test_candidate_streamer_argument_checks():
     # streaming excludes the mix prefetch and deferred gate gradients
     with pytest.raises(ValueError, match="streamed candidates"):
         st._make_streamer(st.StepConfig(stream_candidates=True, prefetch_mix=True), nn.Linear(2, 2))
+
+
+def test_embedding_id_check_modes_on_the_host():
+    """check_embedding_ids: "sync" raises IndexError for ids outside the
+    table (either end) and passes ids inside it; an unknown mode is a
+    ValueError; the training harness defers the check by default."""
+    from voodoo_quant import layers
+
+    layers.check_embedding_ids(torch.tensor([0, 9, 3]), 10, "t", "sync")
+    layers.check_embedding_ids(torch.empty(0, dtype=torch.int64), 10, "t", "bogus")  # nothing to check
+    for bad in ([0, 10], [-1, 3]):
+        with pytest.raises(IndexError, match="index out of range"):
+            layers.check_embedding_ids(torch.tensor(bad), 10, "t", "sync")
+    with pytest.raises(ValueError, match="id_check"):
+        layers.check_embedding_ids(torch.tensor([1]), 10, "t", "bogus")
+    assert st.StepConfig().deferred_id_check
+    assert layers.MixedQuantEmbedding.id_check == "sync"
+    layers.raise_pending_id_errors()  # nothing pending

@@ -114,6 +114,62 @@ def _sample_token_routing(probs: torch.Tensor, num_tokens: int) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# embedding id checks
+# ---------------------------------------------------------------------------
+# Lookups whose id check is deferred: (module name, num_embeddings, pinned
+# host flag, event after its copy).
+_PENDING_ID_CHECKS: list = []
+
+
+def check_embedding_ids(ids: torch.Tensor, num_embeddings: int, name: str, mode: str) -> None:
+    """Raise IndexError for ids outside [0, num_embeddings) (torch's embedding
+    message).  mode "sync" reads the ids' range on the host now, a device
+    synchronisation.  mode "deferred" leaves an out-of-range flag on the
+    device, copied into pinned host memory behind an event, and returns at
+    once; :func:`raise_pending_id_errors` raises later.  The row kernels give
+    zero rows for out-of-range ids in the meantime (they never read past the
+    table).  A training loop that defers the check lets the host queue the
+    next step while the device still runs the last one."""
+    if ids.numel() == 0:
+        return
+    if mode == "sync":
+        lo, hi = torch.aminmax(ids)
+        lo, hi = torch.stack([lo, hi]).tolist()
+        if lo < 0 or hi >= num_embeddings:
+            raise IndexError(f"{name}: index out of range in self "
+                             f"(ids span [{lo}, {hi}], num_embeddings={num_embeddings})")
+        return
+    if mode != "deferred":
+        raise ValueError(f"{name}: id_check must be 'sync' or 'deferred', got {mode!r}")
+    bad = ((ids < 0) | (ids >= num_embeddings)).any().reshape(1)
+    host = torch.empty(1, dtype=torch.bool, pin_memory=True)
+    host.copy_(bad, non_blocking=True)
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(ids.device))
+    _PENDING_ID_CHECKS.append((name, num_embeddings, host, done))
+
+
+def raise_pending_id_errors(block: bool = True) -> None:
+    """Raise IndexError for the first deferred lookup that saw an out-of-range
+    id (see :func:`check_embedding_ids`).  block=True waits for every pending
+    check's copy; block=False looks only at the finished ones and keeps the
+    rest pending."""
+    keep = []
+    err = None
+    for entry in _PENDING_ID_CHECKS:
+        name, num, host, done = entry
+        if not block and not done.query():
+            keep.append(entry)
+            continue
+        done.synchronize()
+        if err is None and bool(host[0]):
+            err = IndexError(f"{name}: index out of range in self (an id outside [0, {num}) in a deferred lookup)")
+    _PENDING_ID_CHECKS[:] = keep
+    if err is not None:
+        raise err
+
+
+# ---------------------------------------------------------------------------
 # padding (reference layers.py:973-997)
 # ---------------------------------------------------------------------------
 def _pad_weight_and_imatrix(weight: torch.Tensor, imatrix: torch.Tensor | None):
@@ -982,13 +1038,21 @@ class MixedQuantEmbedding(_MixedQuantBase):
     (reference ``layers.py:1743-1842``): the weight is the [num_embeddings,
     embedding_dim] matrix, padded along embedding_dim to a multiple of 256.
 
-    Every lookup takes the reference's row-select route (``layers.py:1805-1828``):
-    the batch's unique ids are looked up once, decoding only those rows of the
-    candidates, and the rows are scattered back to the positions.  Under PTQR
-    each unique row takes one candidate, sampled per row as there.  Rows come
-    in fp32 when the source weight is fp32 (the mixture before the reference's
-    final cast, and exact candidate values when routed) and as bf16 otherwise
-    (then cast to the source dtype)."""
+    Every lookup takes the reference's row-select route (``layers.py:1805-1828``),
+    decoding only the looked-up rows of the candidates.  Under PTQR the batch's
+    unique ids are looked up once, each taking one candidate sampled per row as
+    there, and the rows are scattered back to the positions; without it every
+    position decodes its own row (a repeated id gives the same row, and its
+    gate-gradient terms add up as the reference's scattered rows do), so no
+    sort and no host round trip is needed.  Rows come in fp32 when the source
+    weight is fp32 (the mixture before the reference's final cast, and exact
+    candidate values when routed) and as bf16 otherwise (then cast to the
+    source dtype).
+
+    ``id_check`` ("sync", the default, or "deferred"): when out-of-range ids
+    raise IndexError (:func:`check_embedding_ids`)."""
+
+    id_check = "sync"
 
     def __init__(self, num_embeddings: int, embedding_dim: int, candidate_types: list[str],
                  source_weight: torch.Tensor, imatrix: torch.Tensor | None = None, device=None, lazy: bool = False,
@@ -1030,13 +1094,13 @@ class MixedQuantEmbedding(_MixedQuantBase):
                                f"(got {input.device})")
         dev = input.device
         self._move_qbytes(dev)
-        rows, inverse = torch.unique(input.reshape(-1), return_inverse=True)
-        rows = rows.to(torch.int64)
-        if rows.numel():
-            lo, hi = torch.stack([rows[0], rows[-1]]).tolist()
-            if lo < 0 or hi >= self.num_embeddings:
-                raise IndexError(f"{self._tensor_name}: index out of range in self "
-                                 f"(ids span [{lo}, {hi}], num_embeddings={self.num_embeddings})")
+        ids = input.reshape(-1).to(torch.int64)
+        if _PTQR_STATE.enabled:
+            # one routing draw per distinct id, as the reference's lookup
+            rows, inverse = torch.unique(ids, return_inverse=True)
+        else:
+            rows, inverse = ids.contiguous(), None
+        check_embedding_ids(rows, self.num_embeddings, self._tensor_name, self.id_check)
         probs = self.get_probs()
         if probs.device != dev:
             probs = probs.to(dev)
@@ -1046,7 +1110,9 @@ class MixedQuantEmbedding(_MixedQuantBase):
         row_vals = EmbeddingRowsFunction.apply(probs, routing, rows, meta, *self._qbytes())
         if dim8 != self.embedding_dim:
             row_vals = row_vals[:, : self.embedding_dim]
-        out = row_vals[inverse].reshape(*input.shape, self.embedding_dim)
+        if inverse is not None:
+            row_vals = row_vals[inverse]
+        out = row_vals.reshape(*input.shape, self.embedding_dim)
         return out if out.dtype == self.source_dtype else out.to(self.source_dtype)
 
     def extra_repr(self) -> str:

@@ -34,6 +34,7 @@ import torch
 import torch.nn as nn
 
 from voodoo_quant import _hip
+from voodoo_quant.layers import check_embedding_ids
 
 _Q8_0 = 8            # ggml type id
 _Q8_BLOCK = 32       # weights per block
@@ -165,7 +166,12 @@ class Q8Linear(nn.Module):
 
 class Q8Embedding(nn.Module):
     """nn.Embedding stand-in keeping Q8_0 bytes on the device; a forward
-    decodes only the batch's rows (reference ``q8_teacher.py:131-173``)."""
+    decodes only the batch's rows, one per position (reference
+    ``q8_teacher.py:131-173``, which decodes the unique ids' rows and scatters
+    them: the same values, without the sort).  ``id_check`` as in
+    :class:`voodoo_quant.layers.MixedQuantEmbedding`."""
+
+    id_check = "sync"
 
     def __init__(self, qbytes: torch.Tensor, num_embeddings: int, embedding_dim: int,
                  device: torch.device | None = None):
@@ -196,19 +202,14 @@ class Q8Embedding(nn.Module):
         if x.device.type != "cuda":
             raise RuntimeError(f"Q8Embedding runs on a ROCm device only (got {x.device})")
         qb, d_pad = self._packed()
-        rows, inverse = torch.unique(x.reshape(-1), return_inverse=True)
-        rows = rows.to(device=qb.device, dtype=torch.int64)
-        if rows.numel():
-            lo, hi = torch.stack([rows[0], rows[-1]]).tolist()
-            if lo < 0 or hi >= self.num_embeddings:
-                raise IndexError(f"Q8Embedding: index out of range in self (ids span [{lo}, {hi}], "
-                                 f"num_embeddings={self.num_embeddings})")
+        rows = x.reshape(-1).to(device=qb.device, dtype=torch.int64).contiguous()
+        check_embedding_ids(rows, self.num_embeddings, "Q8Embedding", self.id_check)
         dim8 = (self.embedding_dim + 7) // 8 * 8
         routing = torch.zeros_like(rows)  # every row from the one candidate: exact decode
         w_rows = _hip.embedding_rows_fwd((_Q8_0,), [qb], None, routing, rows, self.num_embeddings, dim8, d_pad)
         if dim8 != self.embedding_dim:
             w_rows = w_rows[:, : self.embedding_dim]
-        return w_rows[inverse.to(w_rows.device)].reshape(*x.shape, self.embedding_dim)
+        return w_rows.reshape(*x.shape, self.embedding_dim)
 
 
 _GROUP_DECODES: dict[tuple, torch.Tensor] = {}

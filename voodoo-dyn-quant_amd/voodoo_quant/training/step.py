@@ -469,6 +469,17 @@ class StepConfig:
     stream_slots: int = 6
     stream_depth: int = 5
     stream_overlap: bool = True
+    # check the embeddings' ids on the device and raise an out-of-range id at
+    # the next step (layers.check_embedding_ids) instead of reading the ids'
+    # range on the host in every lookup: with no device synchronisation left
+    # in the step, the host queues the next step's forward while the device
+    # runs this step's backward.  Measured on MI355X, the 0.8B-class decoder
+    # step 51.6 -> 49.3 ms.
+    deferred_id_check: bool = True
+
+
+def _embeddings(*models: nn.Module) -> list[nn.Module]:
+    return [m for model in models for m in model.modules() if isinstance(m, (layers.MixedQuantEmbedding, Q8Embedding))]
 
 
 class GateTrainer:
@@ -490,10 +501,17 @@ class GateTrainer:
         self.prefetch = _make_prefetch(cfg, student)
         self.t_stream = _make_teacher_stream(cfg, student)
         self.streamer = _make_streamer(cfg, student)
+        if cfg.deferred_id_check:
+            for m in _embeddings(student, teacher):
+                m.id_check = "deferred"
 
     def step(self, x: torch.Tensor, y: torch.Tensor) -> dict[str, torch.Tensor]:
-        """One optimizer step on batch (x, y); returns the detached losses (no host sync)."""
+        """One optimizer step on batch (x, y); returns the detached losses (no
+        host sync).  An out-of-range token id of the previous step raises
+        IndexError here (StepConfig.deferred_id_check); waiting for that
+        step's id checks also keeps the host at most about one step ahead."""
         c = self.cfg
+        layers.raise_pending_id_errors()
         tau = trainer.anneal_temperature(self.step_index, c.max_steps, c.temp_start, c.temp_end)
         trainer.set_temperature_all(self.replaced, tau)
         dev = x.device
