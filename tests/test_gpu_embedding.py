@@ -331,6 +331,18 @@ def test_deferred_id_check(hip):
         finally:
             mod.id_check = "sync"
     assert not layers._PENDING_ID_CHECKS
+    # a caller that never collects: finished checks are taken along the way
+    emb.id_check = "deferred"
+    try:
+        ids = torch.tensor([0, 1, 2], device="cuda")
+        for _ in range(3 * layers._MAX_PENDING_ID_CHECKS):
+            emb(ids)
+            torch.cuda.synchronize()
+        assert len(layers._PENDING_ID_CHECKS) <= layers._MAX_PENDING_ID_CHECKS
+        layers.raise_pending_id_errors()
+    finally:
+        emb.id_check = "sync"
+    assert not layers._PENDING_ID_CHECKS
 
 
 # ----------------------------------------------------------------------------- Q8_0 teacher

@@ -119,6 +119,7 @@ def _sample_token_routing(probs: torch.Tensor, num_tokens: int) -> torch.Tensor:
 # Lookups whose id check is deferred: (module name, num_embeddings, pinned
 # host flag, event after its copy).
 _PENDING_ID_CHECKS: list = []
+_MAX_PENDING_ID_CHECKS = 64
 
 
 def check_embedding_ids(ids: torch.Tensor, num_embeddings: int, name: str, mode: str) -> None:
@@ -141,6 +142,10 @@ def check_embedding_ids(ids: torch.Tensor, num_embeddings: int, name: str, mode:
         return
     if mode != "deferred":
         raise ValueError(f"{name}: id_check must be 'sync' or 'deferred', got {mode!r}")
+    if len(_PENDING_ID_CHECKS) >= _MAX_PENDING_ID_CHECKS:
+        # a caller that never collects: take the finished checks (no wait),
+        # so the list stays bounded; an earlier bad id raises here
+        raise_pending_id_errors(block=False)
     bad = ((ids < 0) | (ids >= num_embeddings)).any().reshape(1)
     host = torch.empty(1, dtype=torch.bool, pin_memory=True)
     host.copy_(bad, non_blocking=True)
