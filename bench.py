@@ -461,6 +461,9 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
         out = tr.step(x, y)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / max(steps, 1) * 1e3
+    from voodoo_quant import layers
+
+    layers.raise_pending_id_errors()  # the last step's deferred embedding id checks
     tokens = b * s
     fl = st.step_flops(cfg, tokens, s)
     rec = {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "steps": steps,
