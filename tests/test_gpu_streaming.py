@@ -86,3 +86,39 @@ def test_decoder_steps_match_with_streamed_candidates():
     ref = run()
     got = run(stream_candidates=True, stream_slots=3, stream_depth=2)
     assert float((got - ref).abs().max()) < 1e-6
+
+
+def test_streamed_modules_refuse_ptqr_and_release_back():
+    """A streamed module refuses PTQR routing (its candidates live in the slots
+    only while their product runs); release() gives every module resident
+    device copies of its bytes back, bit-identical to the host copies, and
+    the modules then run unstreamed with the same outputs."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    from voodoo_quant import layers
+    from voodoo_quant.streaming import CandidateStreamer
+
+    dev = torch.device("cuda", 0)
+    cfg = st.StackConfig(blocks=1, hidden=512, mlp=1024)
+    student, _, replaced = st.build_stack(cfg, TYPES, dev, seed=8)
+    mods = list(replaced.values())
+    x = torch.randn(64, cfg.hidden, device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    x = x.to(torch.bfloat16)
+    before = [m(x) for m in mods if m.in_features == cfg.hidden]
+    streamer = CandidateStreamer([[m] for m in mods], dev, slots=2, depth=1)
+    layers.set_ptqr(True)
+    try:
+        with pytest.raises(RuntimeError, match="PTQR"):
+            mods[0](x)
+    finally:
+        layers.set_ptqr(False)
+    host = [[getattr(m, f"_qweight_{k}").clone() for k in range(m.num_candidates)] for m in mods]
+    streamer.release()
+    torch.cuda.synchronize()
+    for m, hq in zip(mods, host):
+        assert m.__dict__.get("_streamer") is None
+        for k, h in enumerate(hq):
+            q = getattr(m, f"_qweight_{k}")
+            assert q.is_cuda and torch.equal(q.cpu(), h)
+    after = [m(x) for m in mods if m.in_features == cfg.hidden]
+    assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(before, after))
