@@ -21,9 +21,12 @@ Also reported in the same JSON line:
                 8 TB/s
   cpu_baseline  the oracle's fp32 torch restatement of the reference step on
                 the host cores, on a row sample of the same layer
-  peaks         the chip's sustained bf16 MFMA rate and HBM read / copy
-                bandwidth, measured by probe kernels (libvq_probe.so) in the
-                same run; the roofline is also stated against them
+  peaks         the chip's sustained bf16 MFMA rate (random and constant
+                operands) and HBM read / copy / write bandwidth, measured by
+                probe kernels (libvq_probe.so) in the same run; the roofline
+                is also stated against the random-operand MFMA rate
+  ptqr          the routed (per-token candidate) forward at the headline shape,
+                and the bf16 decode of the six candidates it reads
   cpu_extra     the single-Linear configuration (512 tokens x 1024 -> 1024,
                 K = 4) on the host (median of 5) and on the GPU, and the C
                 dequant restatement per format, single- and multi-threaded
@@ -35,6 +38,12 @@ Also reported in the same JSON line:
                 memory) against mix + GEMM, forward + dX, at 1-64 tokens on
                 three tensor sizes: the measured crossover behind the module's
                 choice of path
+  train         the 0.8B-class decoder gate-training step (4 x 2048 tokens,
+                every Linear and the embedding gated, Q8_0 teacher): tokens/s
+  stress        the 8-block SwiGLU stack at hidden 4096, MLP 14336, K = 8,
+                2 x 8192 tokens: tokens/s
+  stream_schedule  that stack with its candidates in pinned host memory:
+                resident, copied in stream order, and copied ahead of use
 
   python bench.py --fused-workload runs only that comparison's kernels at 16
   tokens (three passes each), the workload the rocprof HBM-traffic summary of
