@@ -570,10 +570,53 @@ def stream_schedule_bench(torch, dev, steps: int = 3, warmup: int = 2, slots: in
         tr.bank.release()
         return ms, copied
 
+    def timeline():
+        """One overlapped step with the streamer's timing events: when the copy
+        engine is busy, by phase (forward, the turn between the last forward
+        fence and the first backward fence, backward)."""
+        tr = st.StackTrainer(student, teacher, replaced,
+                             st.StepConfig(max_steps=200, temp_start=2.0, temp_end=0.1, stream_candidates=True,
+                                           stream_slots=slots, stream_depth=depth, stream_timeline=True),
+                             total_8bit_bytes=float(cfg.gated_weights()))
+        for _ in range(warmup):
+            tr.step(x)
+        torch.cuda.synchronize()
+        tr.streamer.timeline.clear()
+        origin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        origin.record()
+        tr.step(x)
+        end.record()
+        torch.cuda.synchronize()
+        events = tr.streamer.timeline_ms(origin)
+        step_ms = origin.elapsed_time(end)
+        tr.streamer.release()
+        tr.bank.release()
+        copies = sorted((a, b) for kind, _, a, b in events if kind == "copy")
+        fwd_end = max((a for kind, _, a, _ in events if kind == "forward"), default=0.0)
+        bwd_start = min((a for kind, _, a, _ in events if kind == "backward"), default=step_ms)
+
+        def busy(lo, hi):  # copy-engine time inside [lo, hi]
+            total, cur = 0.0, lo
+            for a, b in copies:
+                a, b = max(a, cur), min(b, hi)
+                if b > a:
+                    total += b - a
+                    cur = b
+            return total
+
+        phases = {"forward": (0.0, fwd_end), "turn": (fwd_end, bwd_start), "backward": (bwd_start, step_ms)}
+        out = {"step_ms": round(step_ms, 2), "copies": len(copies),
+               "copy_busy_ms": round(busy(0.0, step_ms), 2)}
+        for name, (lo, hi) in phases.items():
+            out[f"{name}_ms"] = round(hi - lo, 2)
+            out[f"{name}_copy_busy_frac"] = round(busy(lo, hi) / (hi - lo), 3) if hi > lo else None
+        return out
+
     resident_ms, _ = timed()
     serial_ms, serial_bytes = timed(stream_candidates=True, stream_overlap=False, stream_slots=slots,
                                     stream_depth=depth)
     overlap_ms, overlap_bytes = timed(stream_candidates=True, stream_slots=slots, stream_depth=depth)
+    tl = timeline()
     host = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
     devbuf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     t = time_events(torch, lambda: devbuf.copy_(host, non_blocking=True), 3)
@@ -584,10 +627,12 @@ def stream_schedule_bench(torch, dev, steps: int = 3, warmup: int = 2, slots: in
            "candidate_bytes": cand_bytes, "copied_bytes_per_step_serial": int(serial_bytes),
            "copied_bytes_per_step_overlap": int(overlap_bytes), "h2d_GBps": round(h2d, 1),
            "copy_floor_ms": round(overlap_bytes / (h2d * 1e9) * 1e3, 2), "slots": slots, "depth": depth,
+           "overlap_timeline": tl,
            "workload": "the stress step (8 SwiGLU blocks, hidden 4096, MLP 14336, K=8, 2 x 8192 tokens) with "
                        "its 24 tensors' candidates in pinned host memory, copied before each forward and backward"}
     log(f"stream schedule: resident {resident_ms:.1f} ms, streamed in order {serial_ms:.1f} ms, overlapped "
         f"{overlap_ms:.1f} ms (copies {overlap_bytes / 1e9:.2f} GB/step at {h2d:.1f} GB/s)")
+    log(f"stream schedule timeline (one overlapped step): {tl}")
     del student, teacher, replaced, x, host, devbuf
     torch.cuda.empty_cache()
     return rec

@@ -122,3 +122,36 @@ def test_streamed_modules_refuse_ptqr_and_release_back():
             assert q.is_cuda and torch.equal(q.cpu(), h)
     after = [m(x) for m in mods if m.in_features == cfg.hidden]
     assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(before, after))
+
+
+def test_streamer_timeline():
+    """timeline=True records every copy (end after start) and every fence
+    (forward fences in product order, then backward fences in reverse), with
+    the same results as without it; timeline_ms clears the record."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    ref_g, ref_l, _ = _stack_run(stream_candidates=True, stream_slots=4, stream_depth=3)
+    dev = torch.device("cuda", 0)
+    cfg = st.StackConfig(blocks=3, hidden=512, mlp=1024)
+    student, teacher, replaced = st.build_stack(cfg, TYPES, dev, seed=4)
+    tr = st.StackTrainer(student, teacher, replaced,
+                         st.StepConfig(max_steps=STEPS, temp_start=2.0, temp_end=0.1, stream_candidates=True,
+                                       stream_slots=4, stream_depth=3, stream_timeline=True),
+                         float(cfg.gated_weights()))
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(300, cfg.hidden, device=dev, generator=g).to(torch.bfloat16)
+    origin = torch.cuda.Event(enable_timing=True)
+    origin.record()
+    for _ in range(STEPS):
+        tr.step(x)
+    torch.cuda.synchronize()
+    gates = torch.cat([m.gates.detach().reshape(-1) for m in replaced.values()])
+    assert torch.equal(gates.view(torch.int32), ref_g.view(torch.int32))
+    events = tr.streamer.timeline_ms(origin)
+    n = len(tr.streamer.products)
+    copies = [e for e in events if e[0] == "copy"]
+    assert copies and all(0.0 <= a <= b for _, _, a, b in copies)
+    fwd = [i for kind, i, _, _ in events if kind == "forward"]
+    bwd = [i for kind, i, _, _ in events if kind == "backward"]
+    assert fwd == list(range(n)) * STEPS and bwd == list(range(n - 1, -1, -1)) * STEPS
+    assert tr.streamer.timeline == []

@@ -66,7 +66,8 @@ class CandidateStreamer:
     in forward order) from pinned host memory through `slots` device slots,
     `depth` products ahead, on a copy stream of default priority."""
 
-    def __init__(self, products: list[list], device, slots: int = 4, depth: int = 2, overlap: bool = True):
+    def __init__(self, products: list[list], device, slots: int = 4, depth: int = 2, overlap: bool = True,
+                 timeline: bool = False):
         if not products:
             raise ValueError("no products to stream")
         if not 1 <= depth < slots:
@@ -114,6 +115,9 @@ class CandidateStreamer:
         self.ready: list[torch.cuda.Event | None] = [None] * len(self.products)
         self.copy_stream = torch.cuda.Stream(device=self.device) if self.overlap else None
         self.bytes_copied = 0
+        # timeline=True: timing events around every copy and after every fence
+        # (see timeline_ms); off by default, as each costs two event records
+        self.timeline: list | None = [] if timeline else None
 
     # -- views handed to the autograd Functions ------------------------------
     def views(self, module) -> list[torch.Tensor]:
@@ -131,16 +135,28 @@ class CandidateStreamer:
         s = i % self.slots_n
         mem = self.slot_mem[s]
         with torch.cuda.stream(stream):
+            if self.timeline is not None:
+                start = torch.cuda.Event(enable_timing=True)
+                start.record(stream)
             for hq, spans in zip(self.host[i], self.layout[i]):
                 for h, (off, n) in zip(hq, spans):
                     mem[off:off + n].copy_(h, non_blocking=True)
-            ev = torch.cuda.Event()
+            ev = torch.cuda.Event(enable_timing=self.timeline is not None)
             ev.record(stream)
+        if self.timeline is not None:
+            self.timeline.append(("copy", i, start, ev))
         self.ready[i] = ev
         self.resident[s] = i
         self.bytes_copied += self.product_bytes[i]
 
     def fence(self, i: int, backward: bool) -> None:
+        self._fence(i, backward)
+        if self.timeline is not None:
+            passed = torch.cuda.Event(enable_timing=True)
+            passed.record(torch.cuda.current_stream(self.device))
+            self.timeline.append(("backward" if backward else "forward", i, passed, None))
+
+    def _fence(self, i: int, backward: bool) -> None:
         compute = torch.cuda.current_stream(self.device)
         s = i % self.slots_n
         if not self.overlap:
@@ -161,6 +177,19 @@ class CandidateStreamer:
             self.copy_stream.wait_event(before)
             for j in ahead:
                 self._copy(j, self.copy_stream)
+
+    def timeline_ms(self, origin: torch.cuda.Event) -> list[tuple]:
+        """The recorded copies and fences (timeline=True) as milliseconds after
+        `origin`, a timing event recorded on the compute stream before them:
+        ("copy", product, start, end) and ("forward" | "backward", product,
+        time the compute stream passed the fence, None).  Call once the device
+        has finished the recorded work; clears the record."""
+        if self.timeline is None:
+            raise ValueError("the streamer was built without timeline=True")
+        out = [(kind, i, origin.elapsed_time(a), origin.elapsed_time(b) if b is not None else None)
+               for kind, i, a, b in self.timeline]
+        self.timeline.clear()
+        return out
 
     def forward_fence(self, module) -> None:
         self.fence(self.index[id(module)], backward=False)

@@ -469,6 +469,7 @@ class StepConfig:
     stream_slots: int = 6
     stream_depth: int = 5
     stream_overlap: bool = True
+    stream_timeline: bool = False   # record timing events per copy and fence (CandidateStreamer.timeline_ms)
     # check the embeddings' ids on the device and raise an out-of-range id at
     # the next step (layers.check_embedding_ids) instead of reading the ids'
     # range on the host in every lookup: with no device synchronisation left
@@ -576,7 +577,7 @@ def _make_streamer(cfg: StepConfig, student: nn.Module):
 
     dev = next(p for p in student.parameters()).device
     return CandidateStreamer(prefetch_groups(student), dev, slots=cfg.stream_slots, depth=cfg.stream_depth,
-                             overlap=cfg.stream_overlap)
+                             overlap=cfg.stream_overlap, timeline=cfg.stream_timeline)
 
 
 def _make_teacher_stream(cfg: StepConfig, student: nn.Module):
