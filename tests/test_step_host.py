@@ -102,12 +102,14 @@ def test_teacher_stream_is_opt_in_and_cpu_runs_in_order():
 
 
 def test_fused_path_region():
-    """Few-token products take the fused kernels only up to 32 tokens and
-    2^22 weights (the measured crossover against mix + GEMM)."""
+    """Few-token products take the fused kernels only up to 32 tokens, 2^22
+    weights and 2048 output rows (the measured crossover against mix + GEMM)."""
     from voodoo_quant import layers
 
     assert layers.use_fused(1, 1024, 1024) and layers.use_fused(32, 2048, 2048)
+    assert layers.use_fused(16, 1024, 4096)
     assert not layers.use_fused(33, 1024, 1024)
+    assert not layers.use_fused(16, 3072, 1024) and not layers.use_fused(16, 4096, 1024)
     assert not layers.use_fused(16, 4096, 4096)
     assert not layers.use_fused(0, 1024, 1024)
     # the documented switch forces the bit-exact materialised path

@@ -226,15 +226,20 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
 # The fused few-token products (vq_gated_linear_fwd_fused / _dx_fused: W_eff
 # built tile by tile in LDS, never written) replace mix + GEMM when a call
 # has at most FUSED_MAX_TOKENS tokens and the tensor at most
-# FUSED_MAX_WEIGHTS weights.  Measured on MI355X, K = 6 (Q2_K..Q8_0),
-# forward + dX at 1-32 tokens, the materialised path with the workspaces this
-# module passes (K-split last tiles): fused against materialised 35-37 vs 44 us
-# (1024 x 1024), 43-49 vs 50 (3072 -> 1024), 50-53 vs 51 (1024 -> 3072),
-# 71-75 vs 61 (1024 -> 6144), 105-110 vs 73-74 (4096 x 4096), 208-210 vs
-# 99-101 (5120 -> 6144).  At 64 tokens fused loses from 3M weights on, so both
-# limits sit at the last point where fused did not lose.
+# FUSED_MAX_WEIGHTS weights and FUSED_MAX_ROWS output rows.  Measured on
+# MI355X, K = 6 (Q2_K..Q8_0), forward + dX at 1-32 tokens, the materialised
+# path with the workspaces this module passes (K-split last tiles), both
+# interleaved in one process, materialised time over fused:
+#   out x in     1024x1024 1.22-1.29, 1024x2048 1.17-1.28, 1024x3072
+#   1.06-1.17, 1024x4096 1.10-1.18, 2048x1024 1.04-1.14, 2048x2048
+#   0.95-1.05, 3072x1024 0.97-1.07, 4096x1024 0.97-1.03;
+# 4096 x 4096 and 5120 -> 6144 lose by 1.4-2x, and at 64 tokens fused loses
+# from 3M weights on.  The fused forward and dX spread their work over the
+# output rows, so it is the row count, not the size, that sets the edge:
+# the limits sit at the last points where fused did not lose.
 FUSED_MAX_TOKENS = 32
 FUSED_MAX_WEIGHTS = 1 << 22
+FUSED_MAX_ROWS = 2048
 # The fused kernels build each W_eff tile as fma(p_k dl, u, acc) + p_k c, which
 # is within one bf16 ulp of the reference's separately rounded fp32 mixture,
 # not bitwise equal to it.  FUSED_PRODUCTS = False (or VOODOO_FUSED=0 in the
@@ -246,7 +251,7 @@ FUSED_PRODUCTS = os.environ.get("VOODOO_FUSED", "1") not in ("0", "off", "false"
 def use_fused(m: int, n: int, d_pad: int) -> bool:
     """Whether a gated product of m tokens over an [n, d_pad] tensor takes the
     fused path."""
-    return FUSED_PRODUCTS and 0 < m <= FUSED_MAX_TOKENS and n * d_pad <= FUSED_MAX_WEIGHTS
+    return FUSED_PRODUCTS and 0 < m <= FUSED_MAX_TOKENS and n <= FUSED_MAX_ROWS and n * d_pad <= FUSED_MAX_WEIGHTS
 
 
 def _finish_on_gate_stream(stream, rows, grads, keep) -> None:
