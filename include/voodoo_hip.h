@@ -246,6 +246,22 @@ int vq_add_rmsnorm_fwd(const uint16_t *h, const uint16_t *a, const uint16_t *w, 
 int vq_rmsnorm_bwd(const uint16_t *dn, const uint16_t *ds, const uint16_t *s, const uint16_t *w, const float *rstd,
                    int64_t rows, int64_t dim, uint16_t *dh, void *stream);
 
+/* Causal self-attention forward of the decoder step: per (batch b, query
+ * head h), o[i] = sum_{j <= i} softmax_j(scale q[i].k[j]) v[j] over positions
+ * 0 .. S-1 (torch's scaled_dot_product_attention with is_causal=True), key/
+ * value head h / (Hq / Hk).  q, o: bf16 [B][S][Hq][64]-indexed through
+ * element strides {batch, position, head} (q_strides, o_strides), k, v
+ * likewise with Hk heads; unit stride along the head dim, strides multiples
+ * of 8, pointers 16-byte aligned.  Scores and softmax in fp32, probabilities
+ * rounded to bf16 for the value product.  lse (fp32 [B][Hq][S], natural-log
+ * log-sum-exp of the scaled scores per query; may be NULL) is the saved
+ * state torch's memory-efficient attention backward reads.  Only head dim 64.
+ * No counterpart in voodoo_quant (the step's attention is outside the gated
+ * path); it replaces F.scaled_dot_product_attention's forward in the step. */
+int vq_attention_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *o, float *lse, int64_t B,
+                     int64_t S, int Hq, int Hk, int D, const int64_t *q_strides, const int64_t *k_strides,
+                     const int64_t *v_strides, const int64_t *o_strides, float scale, void *stream);
+
 /* Workspace bytes of the distillation loss (per-row log-sum-exps and losses;
  * written by vq_distill_loss_fwd, read by vq_distill_loss_bwd). */
 int64_t vq_distill_loss_workspace(int64_t rows);

@@ -150,3 +150,24 @@ def test_backward_workspace_keeps_the_fused_gate_elsewhere(m, n, d):
     ws = _hip.bwd_workspace_bytes(m, n, d, d, 6, False)
     tiles = ((n + 255) // 256) * ((d + 255) // 256)
     assert ws < 2 * tiles * TILE
+
+
+def test_attention_fwd_argument_checks():
+    """vq_attention_fwd refuses other head dims, a query-head count that the
+    key/value heads do not divide, missing pointers and unaligned strides
+    before any device work."""
+    import ctypes
+
+    lib = _hip.lib()
+    st = (ctypes.c_int64 * 3)(64 * 16 * 8, 64 * 16, 64)
+    bad = (ctypes.c_int64 * 3)(64 * 16 * 8, 64 * 16 + 4, 64)
+    p = 4096  # never dereferenced: every call below fails its checks first
+    assert lib.vq_attention_fwd(p, p, p, p, None, 1, 8, 16, 4, 128, st, st, st, st, 0.125, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_attention_fwd(p, p, p, p, None, 1, 8, 16, 5, 64, st, st, st, st, 0.125, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_attention_fwd(p, p, p, p, None, 1, 8, 16, 4, 64, st, st, st, st, -1.0, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_attention_fwd(None, p, p, p, None, 1, 8, 16, 4, 64, st, st, st, st, 0.125, None) == _hip.VQ_ERR_NULL
+    assert lib.vq_attention_fwd(p, p, p, p, None, 1, 8, 16, 4, 64, st, bad, st, st, 0.125, None) == _hip.VQ_ERR_ALIGN
+    assert lib.vq_attention_fwd(p + 8, p, p, p, None, 1, 8, 16, 4, 64, st, st, st, st, 0.125, None) == _hip.VQ_ERR_ALIGN
+    # nothing to do: no pointer is needed
+    assert lib.vq_attention_fwd(None, None, None, None, None, 0, 8, 16, 4, 64, None, None, None, None, 0.125,
+                                None) == _hip.VQ_OK

@@ -560,6 +560,32 @@ int vq_rmsnorm_bwd(const uint16_t* dn, const uint16_t* ds, const uint16_t* s, co
     return rc == VQ_OK ? ok() : rc;
 }
 
+int vq_attention_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, float* lse, int64_t B,
+                     int64_t S, int Hq, int Hk, int D, const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides, float scale, void* stream) {
+    if (B < 0 || S < 0 || S > INT32_MAX / 2 || Hq <= 0 || Hk <= 0 || Hq % Hk)
+        return fail(VQ_ERR_SHAPE, "B=%lld S=%lld Hq=%d Hk=%d", (long long)B, (long long)S, Hq, Hk);
+    if (D != 64) return fail(VQ_ERR_SHAPE, "head dim %d: only 64 is supported", D);
+    if (B * Hq * ((S + 127) / 128) > INT32_MAX)
+        return fail(VQ_ERR_SHAPE, "B=%lld Hq=%d S=%lld: too many query tiles", (long long)B, Hq, (long long)S);
+    if (!(scale > 0.0f) || scale > 1e30f) return fail(VQ_ERR_SHAPE, "scale must be positive and finite");
+    if (B == 0 || S == 0) return ok();
+    if (!q || !k || !v || !o) return fail(VQ_ERR_NULL, "q/k/v/o is NULL");
+    if (!q_strides || !k_strides || !v_strides || !o_strides) return fail(VQ_ERR_NULL, "a stride array is NULL");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || (lse && (reinterpret_cast<uintptr_t>(lse) & 3)))
+        return fail(VQ_ERR_ALIGN, "q/k/v/o not 16-byte aligned (or lse not 4-byte aligned)");
+    for (const int64_t* st : {q_strides, k_strides, v_strides, o_strides})
+        for (int i = 0; i < 3; ++i)
+            if (st[i] < 0 || st[i] % 8) return fail(VQ_ERR_ALIGN, "strides must be non-negative multiples of 8");
+    int rc = hip_check(vq::launch_attention_fwd(reinterpret_cast<const vq::bf16_t*>(q),
+                                                reinterpret_cast<const vq::bf16_t*>(k),
+                                                reinterpret_cast<const vq::bf16_t*>(v), reinterpret_cast<vq::bf16_t*>(o),
+                                                lse, (int)B, (int)S, Hq, Hk, q_strides, k_strides, v_strides, o_strides,
+                                                scale, static_cast<hipStream_t>(stream)),
+                       "attention launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int64_t vq_distill_loss_workspace(int64_t rows) {
     if (rows < 0) return -1;
     return align256((5 * rows + 2) * (int64_t)sizeof(float));

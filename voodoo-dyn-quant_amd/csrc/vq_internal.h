@@ -127,6 +127,13 @@ hipError_t launch_rmsnorm_bwd(const bf16_t* dn, const bf16_t* ds, const bf16_t* 
                               int64_t rows, int dim, bf16_t* dh, hipStream_t s);
 hipError_t launch_swiglu_bwd(const bf16_t* gu, const bf16_t* dy, int64_t tokens, int F, bf16_t* dgu, hipStream_t s);
 
+// Causal self-attention forward, head dim 64 (vq_attention.hip).  Strides are
+// element strides (batch, position, head) of q, k, v, o; lse [B][H][S] fp32
+// (natural log) or NULL; kv head of query head h is h / (H / Hk).
+hipError_t launch_attention_fwd(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* o, float* lse, int B,
+                                int S, int H, int Hk, const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                                const int64_t* os, float scale, hipStream_t s);
+
 // Distillation loss over full logits (vq_loss.hip).  ws: 5 * rows + 2 floats
 // (per-row log-sum-exps and losses, then 1/N_ce and 1/N), written by the
 // forward and read by the backward.

@@ -8,6 +8,7 @@ built, or a tensor is not on a ROCm device, calls raise.
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 from pathlib import Path
 
@@ -45,6 +46,7 @@ _SIGNATURES = [
     ("vq_swiglu_bwd", _i, [_p, _p, _i64, _i64, _p, _p]),
     ("vq_add_rmsnorm_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _p]),
     ("vq_rmsnorm_bwd", _i, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p]),
+    ("vq_attention_fwd", _i, [_p, _p, _p, _p, _p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, ctypes.c_float, _p]),
     ("vq_distill_loss_workspace", _i64, [_i64]),
     ("vq_distill_loss_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _i64, _p]),
     ("vq_distill_loss_bwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _i64, _p]),
@@ -353,6 +355,42 @@ def rope_qkv_bwd(dq, dk, dv, B: int, S: int, Hq: int, Hkv: int, D: int, cos, sin
                                  _dev_ptr(sin, "sin"), _dev_ptr(out, "dqkv"), _stream(dev)),
            "vq_rope_qkv_bwd")
     return out
+
+
+def _bsh_strides(t: torch.Tensor, name: str):
+    """(batch, position, head) element strides of a [B, H, S, D] bf16 tensor,
+    copying it to the [B, S, H, D] layout when they do not suit the kernel."""
+    if t.device.type != "cuda" or t.dtype != torch.bfloat16 or t.dim() != 4:
+        raise ValueError(f"{name} must be a bf16 [B, H, S, D] tensor on a ROCm device")
+    sb, sh, ss, sd = t.stride()
+    if sd != 1 or sb % 8 or sh % 8 or ss % 8 or t.data_ptr() % 16:
+        t = t.transpose(1, 2).contiguous().transpose(1, 2)
+        sb, sh, ss, sd = t.stride()
+    return t, (ctypes.c_int64 * 3)(sb, ss, sh)
+
+
+def attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None,
+                  need_lse: bool = True):
+    """Causal attention forward, head dim 64: q [B, Hq, S, 64], k/v
+    [B, Hk, S, 64] bf16 (Hq % Hk == 0) -> (out [B, Hq, S, 64] over
+    [B, S, Hq, 64] memory, lse fp32 [B, Hq, S] natural log, or None)."""
+    B, Hq, S, D = q.shape
+    Hk = k.shape[1]
+    if k.shape != (B, Hk, S, D) or v.shape != k.shape:
+        raise ValueError(f"k/v shape {tuple(k.shape)}/{tuple(v.shape)} does not match q {tuple(q.shape)}")
+    q, qs = _bsh_strides(q, "q")
+    k, ks = _bsh_strides(k, "k")
+    v, vs = _bsh_strides(v, "v")
+    dev = q.device
+    out = torch.empty(B, S, Hq, D, dtype=torch.bfloat16, device=dev).transpose(1, 2)
+    os_ = (ctypes.c_int64 * 3)(out.stride(0), out.stride(2), out.stride(1))
+    lse = torch.empty(B, Hq, S, dtype=torch.float32, device=dev) if need_lse else None
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    _check(lib().vq_attention_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                  lse.data_ptr() if lse is not None else None, B, S, Hq, Hk, D, qs, ks, vs, os_, sc,
+                                  _stream(dev)),
+           "vq_attention_fwd")
+    return out, lse
 
 
 def swiglu_fwd(gu: torch.Tensor) -> torch.Tensor:
