@@ -130,3 +130,40 @@ def test_attention_forward_pairs_with_torch_backward(S):
         err = _rel(got, want)
         print(f"[attention] {name} rel {err:.2e}", flush=True)
         assert err < 1e-2, name
+
+
+def test_step_attention_matches_sdpa_forward_and_backward():
+    """The decoder step's attention (this forward + torch's backward) against
+    the same step with torch's SDPA forward and backward, and both against
+    fp32 autograd; grouped-query heads are repeated before either."""
+    _need_gpu()
+    from voodoo_quant.training import step as st
+
+    B, Hq, Hk, S = 2, 8, 2, 512
+    q, k, v = _inputs(B, Hq, Hk, S, "bshd", seed=21)
+    g = torch.Generator().manual_seed(2)
+    dout = torch.randn(B, Hq, S, 64, generator=g).to(torch.bfloat16).cuda()
+    res = {}
+    saved = st.HIP_ATTENTION
+    try:
+        for flag in (True, False):
+            st.HIP_ATTENTION = flag
+            qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+            out = st._attention(qq, kk, vv)
+            out.backward(dout)
+            res[flag] = (out.detach(), qq.grad, kk.grad, vv.grad)
+            with torch.no_grad():  # the teacher's path: no log-sum-exp, same output
+                assert torch.equal(st._attention(q, k, v), out.detach()) or not flag
+    finally:
+        st.HIP_ATTENTION = saved
+    qf, kf, vf = (t.detach().float().requires_grad_(True) for t in (q, k, v))
+    rep = Hq // Hk
+    mask = torch.ones(S, S, dtype=torch.bool, device="cuda").triu(1)
+    s = (qf @ kf.repeat_interleave(rep, 1).transpose(-1, -2)) / 8.0
+    o = torch.softmax(s.masked_fill(mask, float("-inf")), -1) @ vf.repeat_interleave(rep, 1)
+    o.backward(dout.float())
+    want = (o.detach(), qf.grad, kf.grad, vf.grad)
+    for i, name in enumerate(("out", "dq", "dk", "dv")):
+        hip_err, torch_err = _rel(res[True][i], want[i]), _rel(res[False][i], want[i])
+        print(f"[attention] step {name}: hip {hip_err:.2e} torch {torch_err:.2e}", flush=True)
+        assert hip_err < 1e-2 and hip_err <= 1.5 * torch_err + 1e-3, name

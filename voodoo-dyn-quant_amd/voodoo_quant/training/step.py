@@ -16,13 +16,16 @@ SwiGLU MLP, tied embeddings):
   the gates only (every other weight is frozen), temperature annealed per step.
 
 Only the gates train, so the backward runs dX through every layer and the
-gate gradients of every gated tensor; no weight gradient is formed.  Attention
-uses torch's fused scaled-dot-product kernels (flash or memory-efficient);
-without one of them it runs the math path in fp32.
+gate gradients of every gated tensor; no weight gradient is formed.  Causal
+attention at head dim 64 runs ``vq_attention_fwd`` forward and torch's fused
+memory-efficient backward; other head dims use torch's fused
+scaled-dot-product kernels (flash or memory-efficient), and without one of
+them the math path in fp32.
 """
 
 from __future__ import annotations
 
+import math
 import warnings
 from dataclasses import dataclass
 
@@ -74,6 +77,32 @@ def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.
 
 
 _SDPA_FUSED: bool | None = None
+# head dim 64 on the GPU: the forward is vq_attention_fwd, the backward torch's
+# memory-efficient attention backward over its output and log-sum-exp
+HIP_ATTENTION = True
+
+
+class _CausalAttention(torch.autograd.Function):
+    """Causal attention with Hq == Hk: forward ``vq_attention_fwd``; backward
+    torch's memory-efficient attention backward (``aten::_scaled_dot_product_
+    efficient_attention_backward``, the kernel SDPA's own backward runs) over
+    the saved output and natural-log log-sum-exp, which it reads as SDPA's
+    forward leaves them."""
+
+    @staticmethod
+    def forward(ctx, q, k, v):
+        out, lse = _hip.attention_fwd(q, k, v, need_lse=True)
+        ctx.save_for_backward(q, k, v, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        zero = torch.zeros((), dtype=torch.int64)  # philox seed/offset: unused without dropout
+        dq, dk, dv, _ = torch.ops.aten._scaled_dot_product_efficient_attention_backward(
+            dout, q, k, v, None, out, lse, zero, zero, 0.0, [True, True, True, False], True,
+            scale=1.0 / math.sqrt(q.shape[-1]))
+        return dq, dk, dv
 
 
 def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -83,6 +112,10 @@ def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tenso
     if rep > 1:
         k = k.repeat_interleave(rep, dim=1)
         v = v.repeat_interleave(rep, dim=1)
+    if HIP_ATTENTION and q.is_cuda and q.dtype == torch.bfloat16 and q.shape[-1] == 64:
+        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+            return _CausalAttention.apply(q, k, v)
+        return _hip.attention_fwd(q, k, v, need_lse=False)[0]
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     if _SDPA_FUSED is not False:
