@@ -5,16 +5,18 @@
 //
 // One workgroup takes 128 queries of one (batch, head): four waves of 32
 // queries.  Keys stream through LDS in tiles of 64 (K and V, 8 KiB each,
-// double-buffered; each thread stages four 16-byte chunks in registers while
-// the tile before is computed).  Per tile a wave forms S^T = K Q^T (keys x
+// double-buffered, copied by direct-to-LDS buffer loads issued while the tile
+// before is computed).  Per tile a wave forms S^T = K Q^T (keys x
 // queries) so each lane holds 32 scores of one query: the row maximum is a
 // reduction within the lane plus one exchange between the two lane halves,
 // and the probabilities P^T are already in the register layout of the B
 // operand of O^T = V^T P^T (the key order inside each 16-key MFMA step is
 // permuted the same way on both operands).  V^T fragments come from LDS by
 // ds_read_b64_tr_b16.  Online softmax in base 2 (scores scaled by
-// scale * log2 e), P rounded to bf16 for the second product, O accumulated in
-// fp32 and divided by the row sum once at the end.  The log-sum-exp per query
+// scale * log2 e; the running maximum moves only when a tile's exceeds it by
+// more than 2^8, so most tiles skip rescaling O), P rounded to bf16 for the
+// second product, O accumulated in fp32 and divided by the row sum once at
+// the end.  The log-sum-exp per query
 // (natural log, [B][H][S] fp32) is what torch's memory-efficient attention
 // backward reads, so the step pairs this forward with that backward.
 //
@@ -45,6 +47,15 @@ constexpr float kLn2 = 0.693147180559945309f;
 // by the row so the 32 rows one fragment read touches spread over the banks.
 __device__ __forceinline__ int tile_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ (row & 7)) << 4); }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr uint32_t kRange = 0x7ffffff0u;  // buffer descriptor size in bytes
+constexpr uint32_t kOOB = 0x80000000u;    // an offset past kRange: the load returns zeros
+constexpr float kSlack = 8.0f;            // log2 units the running maximum may lag the true one
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16_t* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, (int)kRange, 0x00020000);
+}
+
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                        const bf16_t* __restrict__ v, bf16_t* __restrict__ o,
                                                        float* __restrict__ lse, int S, int H, int Hk, int BH, int nqt,
@@ -59,7 +70,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
     const int bh = bid - (bid / BH) * BH;
     const int b = bh / H, h = bh - (bh / H) * H;
     const int hk = h / (H / Hk);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, col = lane & 31;
     const int q0 = qt * kQTile;
     const int qw0 = q0 + 32 * wave;
@@ -74,26 +86,30 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
         for (int c = 0; c < 4; ++c) qf[c] = *reinterpret_cast<const bf16x8_t*>(qp + 16 * c);
     }
 
+    // K and V tiles go global -> LDS by direct-to-LDS buffer loads: lane l of
+    // wave w's instruction i writes LDS slot s = 64 (4 i + w) + l of the stage
+    // (16 bytes each; slots 0-511 K, 512-1023 V), which is tile_off(row, c) for
+    // row = (s % 512) / 8 and chunk c = (s % 8) ^ (row % 8), so the lane loads
+    // that chunk.  Keys past S read zeros.
     const bf16_t* kb0 = k + (int64_t)b * ksb + (int64_t)hk * ksh;
     const bf16_t* vb0 = v + (int64_t)b * vsb + (int64_t)hk * vsh;
-    // staging: chunk i of this thread is row (tid + 256 (i & 1)) / 8, chunk
-    // tid % 8 of K (i < 2) or V (i >= 2)
-    u32x4 st[4];
-    auto load = [&](int j) {
+    uint32_t voff[4];
+    int vrow[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int w = tid + 256 * (i & 1);
-            const int key = j * kKTile + (w >> 3);
-            const bf16_t* src = (i < 2 ? kb0 + (int64_t)key * kss : vb0 + (int64_t)key * vss) + 8 * (w & 7);
-            st[i] = key < S ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
-        }
-    };
-    auto store = [&](int buf) {
+    for (int i = 0; i < 4; ++i) {
+        const int w = ((4 * i + wave) * 64 + lane) & 511;
+        const int row = w >> 3, c = (w & 7) ^ (row & 7);
+        vrow[i] = row;
+        voff[i] = (uint32_t)(row * (i < 2 ? kss : vss) * 2 + 16 * c);
+    }
+    auto issue = [&](int j, int buf) {
+        const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kb0 + (int64_t)j * kKTile * kss);
+        const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vb0 + (int64_t)j * kKTile * vss);
+        const int lim = S - j * kKTile;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int w = tid + 256 * (i & 1);
-            *reinterpret_cast<u32x4*>(&smem[buf][(i >> 1) * kMatBytes + tile_off(w >> 3, w & 7)]) = st[i];
-        }
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < 2 ? rk : rv, (lds_void_t*)(&smem[buf][(4 * i + wave) * 1024]),
+                                                     16, vrow[i] < lim ? voff[i] : kOOB, 0, 0, 0);
     };
 
     const int S_tiles = (S + kKTile - 1) / kKTile;
@@ -105,11 +121,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
         for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    load(0);
-    store(0);
-    __syncthreads();
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     for (int j = 0; j < nt; ++j) {
-        if (j + 1 < nt) load(j + 1);
+        if (j + 1 < nt) issue(j + 1, (j + 1) & 1);  // that stage's last readers passed the last barrier
         const int k0 = j * kKTile;
         if (k0 <= qw0 + 31) {  // some key of the tile is visible to some query of the wave
             const uint8_t* ks = smem[j & 1];
@@ -135,29 +150,32 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
                         if (key > qrow) s[kb][r] = -INFINITY;
                     }
             }
-            float mx = s[0][0];
+            float mx = fmaxf(s[0][0], s[1][0]);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+            mx = fmaxf(mx, __shfl_xor(mx, 32)) * c2;
+            // the running maximum moves only when the tile's exceeds it by more
+            // than kSlack, so most tiles skip the rescale (exponents stay <= 2^8)
+            if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack)) {
+                const float m_new = fmaxf(m_run, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                l_run *= alpha;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx * c2);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+            }
             float sum = 0.0f;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], c2, -m_new));
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], c2, -m_run));
                     s[kb][r] = p;
                     sum += p;
                 }
-            l_run = l_run * alpha + sum;
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+            l_run += sum;
             // O^T += V^T P^T over the tile's 64 keys, 16 per MFMA: step t takes
             // keys 16 t + 4 g + {0..3} and 16 t + 8 + 4 g + {0..3} in lane half g
 #pragma unroll
@@ -187,8 +205,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
                 }
             }
         }
-        if (j + 1 < nt) store((j + 1) & 1);
-        __syncthreads();
+        // this wave's copies of tile j + 1 have landed and every wave is past
+        // its reads of tile j
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
 
     const float lt = l_run + __shfl_xor(l_run, 32);

@@ -577,6 +577,9 @@ int vq_attention_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
     for (const int64_t* st : {q_strides, k_strides, v_strides, o_strides})
         for (int i = 0; i < 3; ++i)
             if (st[i] < 0 || st[i] % 8) return fail(VQ_ERR_ALIGN, "strides must be non-negative multiples of 8");
+    // a 64-key tile is addressed by 32-bit byte offsets from its first row
+    if (k_strides[1] > (1 << 22) || v_strides[1] > (1 << 22))
+        return fail(VQ_ERR_SHAPE, "k/v position strides above 2^22 elements");
     int rc = hip_check(vq::launch_attention_fwd(reinterpret_cast<const vq::bf16_t*>(q),
                                                 reinterpret_cast<const vq::bf16_t*>(k),
                                                 reinterpret_cast<const vq::bf16_t*>(v), reinterpret_cast<vq::bf16_t*>(o),
