@@ -36,6 +36,14 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
+# Extra hipcc flags per source file.
+FILE_FLAGS = {
+    # MFMA accumulators in VGPRs: the attention softmax reads and rescales the
+    # accumulators with VALU ops, which AGPR accumulators would copy out and
+    # back for every key tile (255 v_accvgpr moves per tile)
+    "vq_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
@@ -69,7 +77,8 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     objs = [OUT_DIR / (s.stem + ".o") for s in sources]
     probe_objs = [OUT_DIR / ("probe_" + s.stem + ".o") for s in probes]
     with ThreadPoolExecutor(max_workers=jobs or min(8, len(sources) + len(probes))) as ex:
-        list(ex.map(lambda so: _run([hipcc, *HIPCC_FLAGS, "-c", str(so[0]), "-o", str(so[1])]),
+        list(ex.map(lambda so: _run([hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(so[0].name, []), "-c", str(so[0]),
+                                     "-o", str(so[1])]),
                     zip(sources + probes, objs + probe_objs)))
     _link(hipcc, objs, LIB)
     if probe_objs:
