@@ -102,13 +102,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
         vrow[i] = row;
         voff[i] = (uint32_t)(row * (i < 2 ? kss : vss) * 2 + 16 * c);
     }
-    auto issue = [&](int j, int buf) {
+    auto issue = [&](int j, uint8_t* dst) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kb0 + (int64_t)j * kKTile * kss);
         const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vb0 + (int64_t)j * kKTile * vss);
         const int lim = S - j * kKTile;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < 2 ? rk : rv, (lds_void_t*)(&smem[buf][(4 * i + wave) * 1024]),
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < 2 ? rk : rv, (lds_void_t*)(dst + (4 * i + wave) * 1024),
                                                      16, vrow[i] < lim ? voff[i] : kOOB, 0, 0, 0);
     };
 
@@ -121,15 +121,21 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
         for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    issue(0, 0);
+    issue(0, smem[0]);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // tile j: read this tile's K and V fragments, then copy tile j + 1 into
+    // the other stage (whose last readers passed the last barrier), then the
+    // softmax and the value product, then the barrier.  The copies come after
+    // the tile's last LDS read because the compiler cannot tell the stages
+    // apart and would make every later read wait for them.
     for (int j = 0; j < nt; ++j) {
-        if (j + 1 < nt) issue(j + 1, (j + 1) & 1);  // that stage's last readers passed the last barrier
+        const uint8_t* ks = smem[j & 1];
+        const uint8_t* vs = ks + kMatBytes;
         const int k0 = j * kKTile;
-        if (k0 <= qw0 + 31) {  // some key of the tile is visible to some query of the wave
-            const uint8_t* ks = smem[j & 1];
-            const uint8_t* vs = ks + kMatBytes;
-            f32x16 s[2];
+        const bool active = k0 <= qw0 + 31;  // some key of the tile is visible to some query of the wave
+        f32x16 s[2];
+        bf16x8_t vf[4][2];
+        if (active) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -141,6 +147,29 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
                     s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], s[kb], 0, 0, 0);
                 }
             }
+            // V^T fragments of the value product: step t takes keys
+            // 16 t + 4 g + {0..3} and 16 t + 8 + 4 g + {0..3} in lane half g.
+            // ds_read_b64_tr_b16: output lane l element e = element l%4 of the
+            // 8 bytes addressed by lane 16 (l/16) + 4 e + (l%16)/4, so lane l
+            // receives V[key0 + e][d0 + l%16] when the lane at index u of its
+            // 16-lane group G addresses V[key0 + u/4][d0 + 4 (u%4)]
+            const int G = lane >> 4, u = lane & 15;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int key = 16 * t + 4 * (G >> 1) + (u >> 2);
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    const int d = 32 * db + 16 * (G & 1) + 4 * (u & 3);
+                    const uint8_t* lo = vs + tile_off(key, d >> 3) + ((d & 7) << 1);
+                    const uint8_t* hi = vs + tile_off(key + 8, d >> 3) + ((d & 7) << 1);
+                    const v4i16 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lo));
+                    const v4i16 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(hi));
+                    vf[t][db] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(vlo, vhi, 0, 1, 2, 3, 4, 5, 6, 7));
+                }
+            }
+        }
+        if (j + 1 < nt) issue(j + 1, smem[(j + 1) & 1]);
+        if (active) {
             if (k0 + kKTile - 1 > qw0) {  // the causal edge crosses the wave's queries
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
@@ -176,8 +205,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
                     sum += p;
                 }
             l_run += sum;
-            // O^T += V^T P^T over the tile's 64 keys, 16 per MFMA: step t takes
-            // keys 16 t + 4 g + {0..3} and 16 t + 8 + 4 g + {0..3} in lane half g
+            // O^T += V^T P^T over the tile's 64 keys, 16 per MFMA
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const f32x16& sp = s[t >> 1];
@@ -186,23 +214,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
                 const u32x4v pw = {pk_bf16(sp[r0], sp[r0 + 1]), pk_bf16(sp[r0 + 2], sp[r0 + 3]),
                                    pk_bf16(sp[r0 + 4], sp[r0 + 5]), pk_bf16(sp[r0 + 6], sp[r0 + 7])};
                 const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pw);
-                // ds_read_b64_tr_b16: output lane l element e = element l%4 of
-                // the 8 bytes addressed by lane 16 (l/16) + 4 e + (l%16)/4, so
-                // lane l receives V[key0 + e][d0 + l%16] when the lane at index
-                // u of its 16-lane group G addresses V[key0 + u/4][d0 + 4 (u%4)]
-                const int G = lane >> 4, u = lane & 15;
-                const int key = 16 * t + 4 * (G >> 1) + (u >> 2);
 #pragma unroll
-                for (int db = 0; db < 2; ++db) {
-                    const int d = 32 * db + 16 * (G & 1) + 4 * (u & 3);
-                    const uint8_t* lo = vs + tile_off(key, d >> 3) + ((d & 7) << 1);
-                    const uint8_t* hi = vs + tile_off(key + 8, d >> 3) + ((d & 7) << 1);
-                    const v4i16 vlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lo));
-                    const v4i16 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(hi));
-                    const v8i16 vv = __builtin_shufflevector(vlo, vhi, 0, 1, 2, 3, 4, 5, 6, 7);
-                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vv), pf, oacc[db],
-                                                                       0, 0, 0);
-                }
+                for (int db = 0; db < 2; ++db)
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t][db], pf, oacc[db], 0, 0, 0);
             }
         }
         // this wave's copies of tile j + 1 have landed and every wave is past
