@@ -44,8 +44,13 @@ constexpr int kMatBytes = kKTile * kRowBytes;  // 8 KiB: one K or V tile
 constexpr float kLn2 = 0.693147180559945309f;
 
 // Byte offset of (key row, 16-byte chunk) in a tile: chunks are XOR-swizzled
-// by the row so the 32 rows one fragment read touches spread over the banks.
-__device__ __forceinline__ int tile_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ (row & 7)) << 4); }
+// by swz(row) = 4 ((row / 2) % 2) + (row / 4) % 4, so the 16 rows of one
+// 16-byte fragment read pass (same chunk) and the 4 rows x 4 chunks of one
+// transposed 8-byte read pass each cover 256 distinct bytes of the 64 banks
+// (a row is 128 bytes: rows of one parity share banks, and swz takes 8
+// distinct values over the 8 rows of each parity in 16 consecutive rows).
+__device__ __forceinline__ int swz(int row) { return (((row >> 1) & 1) << 2) | ((row >> 2) & 3); }
+__device__ __forceinline__ int tile_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ swz(row)) << 4); }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr uint32_t kRange = 0x7ffffff0u;  // buffer descriptor size in bytes
@@ -89,7 +94,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
     // K and V tiles go global -> LDS by direct-to-LDS buffer loads: lane l of
     // wave w's instruction i writes LDS slot s = 64 (4 i + w) + l of the stage
     // (16 bytes each; slots 0-511 K, 512-1023 V), which is tile_off(row, c) for
-    // row = (s % 512) / 8 and chunk c = (s % 8) ^ (row % 8), so the lane loads
+    // row = (s % 512) / 8 and chunk c = (s % 8) ^ swz(row), so the lane loads
     // that chunk.  Keys past S read zeros.
     const bf16_t* kb0 = k + (int64_t)b * ksb + (int64_t)hk * ksh;
     const bf16_t* vb0 = v + (int64_t)b * vsb + (int64_t)hk * vsh;
@@ -98,7 +103,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int w = ((4 * i + wave) * 64 + lane) & 511;
-        const int row = w >> 3, c = (w & 7) ^ (row & 7);
+        const int row = w >> 3, c = (w & 7) ^ swz(row);
         vrow[i] = row;
         voff[i] = (uint32_t)(row * (i < 2 ? kss : vss) * 2 + 16 * c);
     }
