@@ -184,10 +184,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
                         if (key > qrow) s[kb][r] = -INFINITY;
                     }
             }
-            float mx = fmaxf(s[0][0], s[1][0]);
+            // IEEE maximum (NaN-propagating: v_maximum3_f32), which needs no
+            // canonicalisation of the MFMA results as fmaxf would
+            float mx = __builtin_elementwise_maximum(s[0][0], s[1][0]);
 #pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
-            mx = fmaxf(mx, __shfl_xor(mx, 32)) * c2;
+            for (int r = 1; r < 16; ++r)
+                mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[0][r], s[1][r]));
+            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32)) * c2;
             // the running maximum moves only when the tile's exceeds it by more
             // than kSlack, so most tiles skip the rescale (exponents stay <= 2^8)
             if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack)) {
