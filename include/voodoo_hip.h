@@ -262,6 +262,20 @@ int vq_attention_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, ui
                      int64_t S, int Hq, int Hk, int D, const int64_t *q_strides, const int64_t *k_strides,
                      const int64_t *v_strides, const int64_t *o_strides, float scale, void *stream);
 
+/* Backward of vq_attention_fwd (Hq == Hk): dq, dk, dv (bf16, softmax scale
+ * `scale`) from dout and the forward's o and lse.  strides: 24 int64, the
+ * {batch, position, head} element strides of q, k, v, o, dout, dq, dk, dv
+ * (multiples of 8; unit stride along the head dim).  Two launches, no atomics:
+ * dq (which also writes lse log2 e and D = rowsum(dout o o) per query into
+ * the workspace), then dk and dv; deterministic.  workspace:
+ * vq_attention_bwd_workspace(B, S, Hq) bytes, 16-byte aligned, device memory.
+ * Only head dim 64.  No counterpart in voodoo_quant; it replaces the
+ * memory-efficient attention backward of the step. */
+int64_t vq_attention_bwd_workspace(int64_t B, int64_t S, int Hq);
+int vq_attention_bwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *o, const uint16_t *dout,
+                     const float *lse, uint16_t *dq, uint16_t *dk, uint16_t *dv, int64_t B, int64_t S, int Hq, int D,
+                     const int64_t *strides, float scale, void *workspace, int64_t ws_bytes, void *stream);
+
 /* Workspace bytes of the distillation loss (per-row log-sum-exps and losses;
  * written by vq_distill_loss_fwd, read by vq_distill_loss_bwd). */
 int64_t vq_distill_loss_workspace(int64_t rows);

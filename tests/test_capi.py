@@ -171,3 +171,24 @@ def test_attention_fwd_argument_checks():
     # nothing to do: no pointer is needed
     assert lib.vq_attention_fwd(None, None, None, None, None, 0, 8, 16, 4, 64, None, None, None, None, 0.125,
                                 None) == _hip.VQ_OK
+
+
+def test_attention_bwd_argument_checks():
+    """vq_attention_bwd refuses other head dims, a short workspace and
+    unaligned strides before any device work; its workspace holds two floats
+    per query padded to 64 queries."""
+    import ctypes
+
+    lib = _hip.lib()
+    assert lib.vq_attention_bwd_workspace(2, 100, 16) == 2 * 16 * 128 * 8
+    assert lib.vq_attention_bwd_workspace(-1, 100, 16) == -1
+    st = (ctypes.c_int64 * 24)(*([64 * 16 * 8, 64 * 16, 64] * 8))
+    bad = (ctypes.c_int64 * 24)(*([64 * 16 * 8, 64 * 16 + 4, 64] * 8))
+    p = 4096
+    args = [p] * 6 + [p] * 3
+    need = lib.vq_attention_bwd_workspace(1, 8, 16)
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 128, st, 0.125, p, need, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 64, bad, 0.125, p, need, None) == _hip.VQ_ERR_ALIGN
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 64, st, 0.125, p, need - 1, None) == _hip.VQ_ERR_WORKSPACE
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 64, st, 0.125, None, need, None) == _hip.VQ_ERR_WORKSPACE
+    assert lib.vq_attention_bwd(None, *args[1:], 1, 8, 16, 64, st, 0.125, p, need, None) == _hip.VQ_ERR_NULL

@@ -133,9 +133,9 @@ def test_attention_forward_pairs_with_torch_backward(S):
 
 
 def test_step_attention_matches_sdpa_forward_and_backward():
-    """The decoder step's attention (this forward + torch's backward) against
-    the same step with torch's SDPA forward and backward, and both against
-    fp32 autograd; grouped-query heads are repeated before either."""
+    """The decoder step's attention (HIP forward and backward; HIP forward with
+    torch's backward) against torch's SDPA forward and backward, all against
+    fp32 autograd; grouped-query heads are repeated before each."""
     _need_gpu()
     from voodoo_quant.training import step as st
 
@@ -144,10 +144,11 @@ def test_step_attention_matches_sdpa_forward_and_backward():
     g = torch.Generator().manual_seed(2)
     dout = torch.randn(B, Hq, S, 64, generator=g).to(torch.bfloat16).cuda()
     res = {}
-    saved = st.HIP_ATTENTION
+    saved = st.HIP_ATTENTION, st.HIP_ATTENTION_BWD
     try:
-        for flag in (True, False):
-            st.HIP_ATTENTION = flag
+        for flag in ("hip", "hip_fwd", False):
+            st.HIP_ATTENTION = bool(flag)
+            st.HIP_ATTENTION_BWD = flag == "hip"
             qq, kk, vv = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
             out = st._attention(qq, kk, vv)
             out.backward(dout)
@@ -155,7 +156,7 @@ def test_step_attention_matches_sdpa_forward_and_backward():
             with torch.no_grad():  # the teacher's path: no log-sum-exp, same output
                 assert torch.equal(st._attention(q, k, v), out.detach()) or not flag
     finally:
-        st.HIP_ATTENTION = saved
+        st.HIP_ATTENTION, st.HIP_ATTENTION_BWD = saved
     qf, kf, vf = (t.detach().float().requires_grad_(True) for t in (q, k, v))
     rep = Hq // Hk
     mask = torch.ones(S, S, dtype=torch.bool, device="cuda").triu(1)
@@ -164,6 +165,56 @@ def test_step_attention_matches_sdpa_forward_and_backward():
     o.backward(dout.float())
     want = (o.detach(), qf.grad, kf.grad, vf.grad)
     for i, name in enumerate(("out", "dq", "dk", "dv")):
-        hip_err, torch_err = _rel(res[True][i], want[i]), _rel(res[False][i], want[i])
-        print(f"[attention] step {name}: hip {hip_err:.2e} torch {torch_err:.2e}", flush=True)
-        assert hip_err < 1e-2 and hip_err <= 1.5 * torch_err + 1e-3, name
+        torch_err = _rel(res[False][i], want[i])
+        for mode in ("hip", "hip_fwd"):
+            hip_err = _rel(res[mode][i], want[i])
+            print(f"[attention] step {name} ({mode}): {hip_err:.2e}, torch {torch_err:.2e}", flush=True)
+            assert hip_err < 1e-2 and hip_err <= 1.5 * torch_err + 1e-3, (name, mode)
+
+
+BWD_CASES = [  # B, H, S, magnitude
+    (1, 1, 1, 1.0),
+    (1, 2, 64, 1.0),
+    (2, 3, 65, 1.0),
+    (1, 4, 129, 2.0),
+    (2, 8, 300, 1.0),
+    (1, 3, 777, 4.0),  # peaked softmax
+    (4, 16, 2048, 1.0),  # the 0.8B-class step
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES, ids=[f"B{c[0]}_H{c[1]}_S{c[2]}_x{c[3]}" for c in BWD_CASES])
+def test_attention_backward_matches_fp32(case):
+    """vq_attention_bwd's dq, dk, dv against fp32 autograd of the causal
+    softmax attention on the same bf16 inputs, and no worse than 1.5x torch's
+    memory-efficient backward on the same forward (+ 1e-3); bit-identical when
+    run twice (no atomics)."""
+    _need_gpu()
+    from voodoo_quant import _hip
+
+    B, H, S, mag = case
+    print(f"[attention] backward B={B} H={H} S={S} x{mag}", flush=True)
+    q, k, v = _inputs(B, H, H, S, "bshd", seed=7 * S + H, mag=mag)
+    g = torch.Generator().manual_seed(S)
+    dout = torch.randn(B, S, H, 64, generator=g).to(torch.bfloat16).cuda().transpose(1, 2)
+    scale = 1.0 / math.sqrt(64)
+    out, lse = _hip.attention_fwd(q, k, v)
+    dq, dk, dv = _hip.attention_bwd(dout, q, k, v, out, lse)
+    again = _hip.attention_bwd(dout, q, k, v, out, lse)
+    assert all(torch.equal(a, b) for a, b in zip((dq, dk, dv), again))
+    zero = torch.zeros((), dtype=torch.int64)
+    tq, tk, tv, _ = torch.ops.aten._scaled_dot_product_efficient_attention_backward(
+        dout, q, k, v, None, out, lse, zero, zero, 0.0, [True, True, True, False], True, scale=scale)
+    want = []
+    for b in range(B):  # fp32 autograd per batch to bound memory
+        qf, kf, vf = (t[b].detach().float().requires_grad_(True) for t in (q, k, v))
+        mask = torch.ones(S, S, dtype=torch.bool, device="cuda").triu(1)
+        s = (qf @ kf.transpose(-1, -2)) * scale
+        o = torch.softmax(s.masked_fill(mask, float("-inf")), -1) @ vf
+        o.backward(dout[b].float())
+        want.append((qf.grad, kf.grad, vf.grad))
+    for i, (name, got, ref_t) in enumerate((("dq", dq, tq), ("dk", dk, tk), ("dv", dv, tv))):
+        w = torch.stack([x[i] for x in want])
+        err, terr = _rel(got, w), _rel(ref_t, w)
+        print(f"[attention] {name} rel {err:.2e} (torch {terr:.2e})", flush=True)
+        assert err < 1e-2 and err <= 1.5 * terr + 1e-3, name

@@ -250,6 +250,325 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
     }
 }
 
+// ---------------------------------------------------------------- backward
+// Two kernels, no atomics, deterministic (the sums run in a fixed order):
+//   attn_bwd_dq_kernel: per 128-query tile (4 waves x 32 queries), over the
+//     key tiles up to the diagonal: S^T = K Q^T, dP^T = V dO^T, P = exp(S
+//     scale - lse), dS = P (dP - D), dQ^T += K^T dS^T; D = rowsum(dO o O) is
+//     formed from the wave's own rows first and written, with lse log2 e, to
+//     the workspace the second kernel reads.
+//   attn_bwd_dkdv_kernel: per 128-key block (4 waves x 32 keys), over the
+//     query tiles from the diagonal on: S = Q K^T, dP = dO V^T, P, dS,
+//     dV^T += dO^T P, dK^T += Q^T dS.
+// P and dS are rounded to bf16 for the products (as the forward's P); the
+// softmax scale is applied to dQ and dK once at the end.
+
+struct AttnStrides {
+    int64_t q[3], k[3], v[3], o[3], d[3], dq[3], dk[3], dv[3];  // {batch, position, head}, elements
+};
+
+// A-operand fragment (16 bytes, rows k-contiguous) of a 64 x 64 tile
+__device__ __forceinline__ bf16x8_t tile_frag(const uint8_t* t, int row, int chunk) {
+    return *reinterpret_cast<const bf16x8_t*>(t + tile_off(row, chunk));
+}
+
+// Transposed fragment of a 64 x 64 tile T[row][d] for MFMA step `ts`, d-block
+// db: lane l receives T[16 ts + 4 (l/32) + {0..3}, 16 ts + 8 + 4 (l/32) +
+// {0..3}][32 db + l%32] (ds_read_b64_tr_b16: output lane l element e = element
+// l%4 of the 8 bytes addressed by lane 16 (l/16) + 4 e + (l%16)/4)
+__device__ __forceinline__ bf16x8_t tile_frag_tr(const uint8_t* t, int ts, int db, int lane) {
+    const int G = lane >> 4, u = lane & 15;
+    const int row = 16 * ts + 4 * (G >> 1) + (u >> 2);
+    const int d = 32 * db + 16 * (G & 1) + 4 * (u & 3);
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + tile_off(row, d >> 3) + ((d & 7) << 1)));
+    const v4i16 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(t + tile_off(row + 8, d >> 3) + ((d & 7) << 1)));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Registers r0 .. r0 + 7 of an accumulator as a bf16 B (or A) fragment
+__device__ __forceinline__ bf16x8_t pack8(const f32x16& a, int r0) {
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v w = {pk_bf16(a[r0], a[r0 + 1]), pk_bf16(a[r0 + 2], a[r0 + 3]), pk_bf16(a[r0 + 4], a[r0 + 5]),
+                      pk_bf16(a[r0 + 6], a[r0 + 7])};
+    return __builtin_bit_cast(bf16x8_t, w);
+}
+
+__device__ __forceinline__ void zero16(f32x16& a) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a[r] = 0.0f;
+}
+
+// Row `row` of a [.., 64] bf16 tensor as 4 B fragments (lane holds elements
+// 16 c + 8 (l/32) .. +7)
+__device__ __forceinline__ void row_frags(const bf16_t* p, int g, bf16x8_t (&f)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) f[c] = *reinterpret_cast<const bf16x8_t*>(p + 16 * c + 8 * g);
+}
+
+// Stores a transposed accumulator pair (registers of lane l: T[8 (r/4) + 4 (l/32)
+// + r%4 (+32 for the second)][l%32]) times `mul` as the bf16 row of lane l.
+__device__ __forceinline__ void store_row(bf16_t* p, const f32x16 (&acc)[2], float mul, int g) {
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            uint2 w;
+            w.x = pk_bf16(acc[db][4 * a] * mul, acc[db][4 * a + 1] * mul);
+            w.y = pk_bf16(acc[db][4 * a + 2] * mul, acc[db][4 * a + 3] * mul);
+            *reinterpret_cast<uint2*>(p + 32 * db + 8 * a + 4 * g) = w;
+        }
+}
+
+constexpr float kLog2e = 1.44269504088896340736f;
+
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
+                                                          const bf16_t* __restrict__ v, const bf16_t* __restrict__ o,
+                                                          const bf16_t* __restrict__ dout,
+                                                          const float* __restrict__ lse, float* __restrict__ stats,
+                                                          bf16_t* __restrict__ dq, int S, int S_pad, int H, int BH,
+                                                          int nqt, AttnStrides st, float c2, float scale) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * kMatBytes];  // K tile, V tile
+    const int bid = blockIdx.x;
+    const int qt = nqt - 1 - bid / BH;  // heaviest query tiles first
+    const int bh = bid - (bid / BH) * BH;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5, col = lane & 31;
+    const int q0 = qt * kQTile;
+    const int qw0 = q0 + 32 * wave;
+    const int qrow = qw0 + col;
+    const int qc = min(qrow, S - 1);
+
+    // Q^T and dO^T as B operands (lane: row qc, elements 16 c + 8 g ..), and
+    // D = rowsum(dO o O) in fp32
+    bf16x8_t qf[4], df[4], of[4];
+    row_frags(q + (int64_t)b * st.q[0] + (int64_t)qc * st.q[1] + (int64_t)h * st.q[2], g, qf);
+    row_frags(dout + (int64_t)b * st.d[0] + (int64_t)qc * st.d[1] + (int64_t)h * st.d[2], g, df);
+    row_frags(o + (int64_t)b * st.o[0] + (int64_t)qc * st.o[1] + (int64_t)h * st.o[2], g, of);
+    float dsum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dsum = fmaf((float)df[c][e], (float)of[c][e], dsum);
+    dsum += __shfl_xor(dsum, 32);
+    const float lse2 = lse[(int64_t)bh * S + qc] * kLog2e;
+    // (lse log2 e, D) per query for the key-side kernel; padding queries up
+    // to S_pad get zeros
+    if (g == 0 && qrow < S_pad) {
+        float2 w;
+        w.x = qrow < S ? lse2 : 0.0f;
+        w.y = qrow < S ? dsum : 0.0f;
+        *reinterpret_cast<float2*>(stats + ((int64_t)bh * S_pad + qrow) * 2) = w;
+    }
+
+    // K and V tiles by direct-to-LDS loads (the forward's slot mapping)
+    const bf16_t* kb0 = k + (int64_t)b * st.k[0] + (int64_t)h * st.k[2];
+    const bf16_t* vb0 = v + (int64_t)b * st.v[0] + (int64_t)h * st.v[2];
+    uint32_t voff[4];
+    int vrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int w = ((4 * i + wave) * 64 + lane) & 511;
+        const int row = w >> 3, c = (w & 7) ^ swz(row);
+        vrow[i] = row;
+        voff[i] = (uint32_t)(row * (i < 2 ? st.k[1] : st.v[1]) * 2 + 16 * c);
+    }
+    auto issue = [&](int j, uint8_t* dst) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kb0 + (int64_t)j * kKTile * st.k[1]);
+        const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vb0 + (int64_t)j * kKTile * st.v[1]);
+        const int lim = S - j * kKTile;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(i < 2 ? rk : rv, (lds_void_t*)(dst + (4 * i + wave) * 1024),
+                                                     16, vrow[i] < lim ? voff[i] : kOOB, 0, 0, 0);
+    };
+
+    const int S_tiles = (S + kKTile - 1) / kKTile;
+    const int nt = min(S_tiles, (q0 + kQTile + kKTile - 1) / kKTile);
+    f32x16 acc[2];
+    zero16(acc[0]);
+    zero16(acc[1]);
+    issue(0, smem[0]);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    // as the forward: the tile's LDS reads come before the next tile's copies
+    for (int j = 0; j < nt; ++j) {
+        const uint8_t* ks = smem[j & 1];
+        const uint8_t* vs = ks + kMatBytes;
+        const int k0 = j * kKTile;
+        const bool active = k0 <= qw0 + 31;
+        f32x16 s[2], dp[2];
+        bf16x8_t kt[4][2];
+        if (active) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                zero16(s[kb]);
+                zero16(dp[kb]);
+                const int row = 32 * kb + col;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_frag(ks, row, 2 * c + g), qf[c], s[kb], 0, 0, 0);
+                    dp[kb] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_frag(vs, row, 2 * c + g), df[c], dp[kb], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int db = 0; db < 2; ++db) kt[t][db] = tile_frag_tr(ks, t, db, lane);
+        }
+        if (j + 1 < nt) issue(j + 1, smem[(j + 1) & 1]);
+        if (active) {
+            const bool edge = k0 + kKTile - 1 > qw0;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float x = s[kb][r];
+                    if (edge && k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) x = -INFINITY;
+                    const float p = __builtin_amdgcn_exp2f(fmaf(x, c2, -lse2));
+                    s[kb][r] = p * (dp[kb][r] - dsum);
+                }
+            // dQ^T += K^T dS^T, 16 keys per MFMA (the forward's key order)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const bf16x8_t dsf = pack8(s[t >> 1], 8 * (t & 1));
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+                    acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kt[t][db], dsf, acc[db], 0, 0, 0);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    if (qrow < S) store_row(dq + (int64_t)b * st.dq[0] + (int64_t)qrow * st.dq[1] + (int64_t)h * st.dq[2], acc, scale, g);
+}
+
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __restrict__ q,
+                                                            const bf16_t* __restrict__ k,
+                                                            const bf16_t* __restrict__ v,
+                                                            const bf16_t* __restrict__ dout,
+                                                            const float* __restrict__ stats, bf16_t* __restrict__ dk,
+                                                            bf16_t* __restrict__ dv, int S, int S_pad, int H, int BH,
+                                                            AttnStrides st, float c2, float scale) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * kMatBytes];  // Q tile, dO tile (64 queries)
+    __shared__ __attribute__((aligned(16))) float stat[2][2 * 64];           // (lse log2 e, D) per query
+    const int bid = blockIdx.x;
+    const int kt_idx = bid / BH;  // key block 0 sees the most queries: first
+    const int bh = bid - kt_idx * BH;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5, col = lane & 31;
+    const int kv0 = kt_idx * 128;
+    const int kw0 = kv0 + 32 * wave;
+    const int key = kw0 + col;
+    const int kc = min(key, S - 1);
+
+    // K^T and V^T as B operands (lane: row kc, elements 16 c + 8 g ..)
+    bf16x8_t kf[4], vf[4];
+    row_frags(k + (int64_t)b * st.k[0] + (int64_t)kc * st.k[1] + (int64_t)h * st.k[2], g, kf);
+    row_frags(v + (int64_t)b * st.v[0] + (int64_t)kc * st.v[1] + (int64_t)h * st.v[2], g, vf);
+
+    // Q, dO and stats tiles staged through registers: thread chunk i is row
+    // (tid + 256 (i & 1)) / 8, chunk tid % 8 of Q (i < 2) or dO (i >= 2); the
+    // first 32 threads also carry 4 floats of the stats
+    const bf16_t* qb0 = q + (int64_t)b * st.q[0] + (int64_t)h * st.q[2];
+    const bf16_t* db0 = dout + (int64_t)b * st.d[0] + (int64_t)h * st.d[2];
+    const float* sb0 = stats + (int64_t)bh * S_pad * 2;
+    u32x4 stg[4];
+    float4 sst = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto load = [&](int i) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const int w = tid + 256 * (ii & 1);
+            const int qq = i * 64 + (w >> 3);
+            const bf16_t* src = (ii < 2 ? qb0 + (int64_t)qq * st.q[1] : db0 + (int64_t)qq * st.d[1]) + 8 * (w & 7);
+            stg[ii] = qq < S ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
+        }
+        if (tid < 32) sst = *reinterpret_cast<const float4*>(sb0 + (int64_t)i * 128 + 4 * tid);
+    };
+    auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const int w = tid + 256 * (ii & 1);
+            *reinterpret_cast<u32x4*>(&smem[buf][(ii >> 1) * kMatBytes + tile_off(w >> 3, w & 7)]) = stg[ii];
+        }
+        if (tid < 32) *reinterpret_cast<float4*>(&stat[buf][4 * tid]) = sst;
+    };
+
+    f32x16 dka[2], dva[2];
+    zero16(dka[0]);
+    zero16(dka[1]);
+    zero16(dva[0]);
+    zero16(dva[1]);
+    const int i0 = kv0 / 64;
+    const int ni = S_pad / 64;
+    if (i0 < ni) {
+        load(i0);
+        store(0);
+    }
+    __syncthreads();
+    for (int i = i0; i < ni; ++i) {
+        const int buf = (i - i0) & 1;
+        if (i + 1 < ni) load(i + 1);
+        const uint8_t* qs = smem[buf];
+        const uint8_t* ds_ = qs + kMatBytes;
+        const float* sts = stat[buf];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qs0 = i * 64 + 32 * qb;  // first query of the sub-block
+            if (qs0 + 31 < kw0) continue;      // every query precedes every key of the wave
+            f32x16 sc, dp;
+            zero16(sc);
+            zero16(dp);
+            const int row = 32 * qb + col;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_frag(qs, row, 2 * c + g), kf[c], sc, 0, 0, 0);
+                dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_frag(ds_, row, 2 * c + g), vf[c], dp, 0, 0, 0);
+            }
+            // register r of lane l: query qs0 + 8 (r/4) + 4 g + r%4, key `key`
+            const bool edge = kw0 + 31 > qs0;
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const float4 s01 = *reinterpret_cast<const float4*>(sts + 2 * (32 * qb + 8 * a + 4 * g));
+                const float4 s23 = *reinterpret_cast<const float4*>(sts + 2 * (32 * qb + 8 * a + 4 * g) + 4);
+                const float l2[4] = {s01.x, s01.z, s23.x, s23.z};
+                const float dd[4] = {s01.y, s01.w, s23.y, s23.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * a + e;
+                    float x = sc[r];
+                    if (edge && key > qs0 + 8 * a + 4 * g + e) x = -INFINITY;
+                    const float p = __builtin_amdgcn_exp2f(fmaf(x, c2, -l2[e]));
+                    sc[r] = p;
+                    dp[r] = p * (dp[r] - dd[e]);
+                }
+            }
+            // dV^T += dO^T P and dK^T += Q^T dS, 16 queries per MFMA
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const bf16x8_t pf = pack8(sc, 8 * t);
+                const bf16x8_t dsf = pack8(dp, 8 * t);
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_frag_tr(ds_, 2 * qb + t, db, lane), pf,
+                                                                      dva[db], 0, 0, 0);
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_frag_tr(qs, 2 * qb + t, db, lane), dsf,
+                                                                      dka[db], 0, 0, 0);
+                }
+            }
+        }
+        if (i + 1 < ni) store(buf ^ 1);  // that stage's last readers passed the last barrier
+        __syncthreads();
+    }
+    if (key < S) {
+        store_row(dk + (int64_t)b * st.dk[0] + (int64_t)key * st.dk[1] + (int64_t)h * st.dk[2], dka, scale, g);
+        store_row(dv + (int64_t)b * st.dv[0] + (int64_t)key * st.dv[1] + (int64_t)h * st.dv[2], dva, 1.0f, g);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_attention_fwd(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* o, float* lse, int B,
@@ -263,6 +582,40 @@ hipError_t launch_attention_fwd(const bf16_t* q, const bf16_t* k, const bf16_t* 
     attn_fwd_kernel<<<dim3((unsigned)blocks), 256, 0, s>>>(q, k, v, o, lse, S, H, Hk, BH, nqt, qs[0], qs[1], qs[2],
                                                           ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
                                                           os[2], c2);
+    return hipGetLastError();
+}
+
+int64_t attention_bwd_workspace(int B, int S, int H) {
+    const int64_t S_pad = (int64_t)(S + 63) / 64 * 64;
+    return (int64_t)B * H * S_pad * 2 * (int64_t)sizeof(float);
+}
+
+hipError_t launch_attention_bwd(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
+                                const bf16_t* dout, const float* lse, bf16_t* dq, bf16_t* dk, bf16_t* dv, int B,
+                                int S, int H, const int64_t* strides, float scale, float* stats, hipStream_t s) {
+    const int BH = B * H;
+    if (BH == 0 || S == 0) return hipSuccess;
+    AttnStrides st;
+    for (int i = 0; i < 3; ++i) {
+        st.q[i] = strides[i];
+        st.k[i] = strides[3 + i];
+        st.v[i] = strides[6 + i];
+        st.o[i] = strides[9 + i];
+        st.d[i] = strides[12 + i];
+        st.dq[i] = strides[15 + i];
+        st.dk[i] = strides[18 + i];
+        st.dv[i] = strides[21 + i];
+    }
+    const int S_pad = (S + 63) / 64 * 64;
+    const int nqt = (S + kQTile - 1) / kQTile;
+    const float c2 = scale * kLog2e;
+    attn_bwd_dq_kernel<<<dim3((unsigned)(BH * nqt)), 256, 0, s>>>(q, k, v, o, dout, lse, stats, dq, S, S_pad, H, BH,
+                                                                 nqt, st, c2, scale);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nkt = (S + 127) / 128;
+    attn_bwd_dkdv_kernel<<<dim3((unsigned)(BH * nkt)), 256, 0, s>>>(q, k, v, dout, stats, dk, dv, S, S_pad, H, BH, st,
+                                                                   c2, scale);
     return hipGetLastError();
 }
 

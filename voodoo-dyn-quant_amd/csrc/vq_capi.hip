@@ -589,6 +589,46 @@ int vq_attention_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, ui
     return rc == VQ_OK ? ok() : rc;
 }
 
+int64_t vq_attention_bwd_workspace(int64_t B, int64_t S, int Hq) {
+    if (B < 0 || S < 0 || S > INT32_MAX / 2 || Hq <= 0 || B * Hq > INT32_MAX) return -1;
+    return align256(vq::attention_bwd_workspace((int)B, (int)S, Hq));
+}
+
+int vq_attention_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o, const uint16_t* dout,
+                     const float* lse, uint16_t* dq, uint16_t* dk, uint16_t* dv, int64_t B, int64_t S, int Hq, int D,
+                     const int64_t* strides, float scale, void* workspace, int64_t ws_bytes, void* stream) {
+    if (B < 0 || S < 0 || S > INT32_MAX / 2 || Hq <= 0) return fail(VQ_ERR_SHAPE, "B=%lld S=%lld Hq=%d", (long long)B, (long long)S, Hq);
+    if (D != 64) return fail(VQ_ERR_SHAPE, "head dim %d: only 64 is supported", D);
+    if (B * Hq * ((S + 127) / 128) > INT32_MAX)
+        return fail(VQ_ERR_SHAPE, "B=%lld Hq=%d S=%lld: too many tiles", (long long)B, Hq, (long long)S);
+    if (!(scale > 0.0f) || scale > 1e30f) return fail(VQ_ERR_SHAPE, "scale must be positive and finite");
+    if (B == 0 || S == 0) return ok();
+    if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv) return fail(VQ_ERR_NULL, "a tensor pointer is NULL");
+    if (!strides) return fail(VQ_ERR_NULL, "strides is NULL");
+    for (const void* p : {(const void*)q, (const void*)k, (const void*)v, (const void*)o, (const void*)dout,
+                          (const void*)dq, (const void*)dk, (const void*)dv})
+        if (!aligned16(p)) return fail(VQ_ERR_ALIGN, "tensors must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(lse) & 3) return fail(VQ_ERR_ALIGN, "lse not 4-byte aligned");
+    for (int i = 0; i < 24; ++i)
+        if (strides[i] < 0 || strides[i] % 8) return fail(VQ_ERR_ALIGN, "strides must be non-negative multiples of 8");
+    if (strides[4] > (1 << 22) || strides[7] > (1 << 22))
+        return fail(VQ_ERR_SHAPE, "k/v position strides above 2^22 elements");
+    const int64_t need = vq_attention_bwd_workspace(B, S, Hq);
+    if (!workspace || ws_bytes < need || !aligned16(workspace))
+        return fail(VQ_ERR_WORKSPACE, "workspace %lld bytes at %p, need %lld (16-byte aligned)", (long long)ws_bytes,
+                    workspace, (long long)need);
+    int rc = hip_check(vq::launch_attention_bwd(reinterpret_cast<const vq::bf16_t*>(q),
+                                                reinterpret_cast<const vq::bf16_t*>(k),
+                                                reinterpret_cast<const vq::bf16_t*>(v),
+                                                reinterpret_cast<const vq::bf16_t*>(o),
+                                                reinterpret_cast<const vq::bf16_t*>(dout), lse,
+                                                reinterpret_cast<vq::bf16_t*>(dq), reinterpret_cast<vq::bf16_t*>(dk),
+                                                reinterpret_cast<vq::bf16_t*>(dv), (int)B, (int)S, Hq, strides, scale,
+                                                static_cast<float*>(workspace), static_cast<hipStream_t>(stream)),
+                       "attention backward launch");
+    return rc == VQ_OK ? ok() : rc;
+}
+
 int64_t vq_distill_loss_workspace(int64_t rows) {
     if (rows < 0) return -1;
     return align256((5 * rows + 2) * (int64_t)sizeof(float));

@@ -134,6 +134,14 @@ hipError_t launch_attention_fwd(const bf16_t* q, const bf16_t* k, const bf16_t* 
                                 int S, int H, int Hk, const int64_t* qs, const int64_t* ks, const int64_t* vs,
                                 const int64_t* os, float scale, hipStream_t s);
 
+// Its backward: dq, dk, dv (softmax scale `scale`) from dout, the forward's
+// o and lse; strides: 8 x {batch, position, head} for q, k, v, o, dout, dq,
+// dk, dv; Hk == H.  stats: attention_bwd_workspace(B, S, H) bytes.
+int64_t attention_bwd_workspace(int B, int S, int H);
+hipError_t launch_attention_bwd(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
+                                const bf16_t* dout, const float* lse, bf16_t* dq, bf16_t* dk, bf16_t* dv, int B,
+                                int S, int H, const int64_t* strides, float scale, float* stats, hipStream_t s);
+
 // Distillation loss over full logits (vq_loss.hip).  ws: 5 * rows + 2 floats
 // (per-row log-sum-exps and losses, then 1/N_ce and 1/N), written by the
 // forward and read by the backward.

@@ -47,6 +47,9 @@ _SIGNATURES = [
     ("vq_add_rmsnorm_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _p]),
     ("vq_rmsnorm_bwd", _i, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p]),
     ("vq_attention_fwd", _i, [_p, _p, _p, _p, _p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, ctypes.c_float, _p]),
+    ("vq_attention_bwd_workspace", _i64, [_i64, _i64, _i]),
+    ("vq_attention_bwd", _i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i, _i, _p, ctypes.c_float, _p, _i64,
+                              _p]),
     ("vq_distill_loss_workspace", _i64, [_i64]),
     ("vq_distill_loss_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _i64, _p]),
     ("vq_distill_loss_bwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _i64, _p]),
@@ -391,6 +394,34 @@ def attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: floa
                                   _stream(dev)),
            "vq_attention_fwd")
     return out, lse
+
+
+def attention_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                  lse: torch.Tensor, scale: float | None = None):
+    """Backward of :func:`attention_fwd` with Hq == Hk: (dq, dk, dv), each
+    bf16 [B, H, S, 64] over [B, S, H, 64] memory."""
+    B, H, S, D = q.shape
+    if k.shape != q.shape or v.shape != q.shape or out.shape != q.shape or dout.shape != q.shape:
+        raise ValueError("attention_bwd needs q, k, v, out and dout of one shape (Hq == Hk)")
+    if lse.shape != (B, H, S) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("lse must be contiguous fp32 [B, H, S]")
+    ts, strides = [], []
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (dout, "dout")):
+        t, st = _bsh_strides(t, name)
+        ts.append(t)
+        strides += list(st)
+    dev = q.device
+    grads = [torch.empty(B, S, H, D, dtype=torch.bfloat16, device=dev).transpose(1, 2) for _ in range(3)]
+    for g in grads:
+        strides += [g.stride(0), g.stride(2), g.stride(1)]
+    ws_bytes = lib().vq_attention_bwd_workspace(B, S, H)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
+    _check(lib().vq_attention_bwd(*(t.data_ptr() for t in ts), lse.data_ptr(), *(g.data_ptr() for g in grads), B, S,
+                                  H, D, (ctypes.c_int64 * 24)(*strides), sc, ws.data_ptr(), ws.numel(),
+                                  _stream(dev)),
+           "vq_attention_bwd")
+    return tuple(grads)
 
 
 def swiglu_fwd(gu: torch.Tensor) -> torch.Tensor:

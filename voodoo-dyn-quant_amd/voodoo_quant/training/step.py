@@ -17,8 +17,8 @@ SwiGLU MLP, tied embeddings):
 
 Only the gates train, so the backward runs dX through every layer and the
 gate gradients of every gated tensor; no weight gradient is formed.  Causal
-attention at head dim 64 runs ``vq_attention_fwd`` forward and torch's fused
-memory-efficient backward; other head dims use torch's fused
+attention at head dim 64 runs ``vq_attention_fwd`` / ``vq_attention_bwd``;
+other head dims use torch's fused
 scaled-dot-product kernels (flash or memory-efficient), and without one of
 them the math path in fp32.
 """
@@ -77,17 +77,18 @@ def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.
 
 
 _SDPA_FUSED: bool | None = None
-# head dim 64 on the GPU: the forward is vq_attention_fwd, the backward torch's
-# memory-efficient attention backward over its output and log-sum-exp
+# head dim 64 on the GPU: causal attention on vq_attention_fwd / _bwd
 HIP_ATTENTION = True
+# False: the backward is torch's memory-efficient attention backward over the
+# HIP forward's output and log-sum-exp (the kernel SDPA's own backward runs)
+HIP_ATTENTION_BWD = True
 
 
 class _CausalAttention(torch.autograd.Function):
-    """Causal attention with Hq == Hk: forward ``vq_attention_fwd``; backward
-    torch's memory-efficient attention backward (``aten::_scaled_dot_product_
-    efficient_attention_backward``, the kernel SDPA's own backward runs) over
-    the saved output and natural-log log-sum-exp, which it reads as SDPA's
-    forward leaves them."""
+    """Causal attention with Hq == Hk: forward ``vq_attention_fwd`` (it saves
+    the natural-log log-sum-exp per query); backward ``vq_attention_bwd``, or
+    torch's ``aten::_scaled_dot_product_efficient_attention_backward``, which
+    reads that log-sum-exp as SDPA's forward leaves it."""
 
     @staticmethod
     def forward(ctx, q, k, v):
@@ -98,6 +99,8 @@ class _CausalAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         q, k, v, out, lse = ctx.saved_tensors
+        if HIP_ATTENTION_BWD:
+            return _hip.attention_bwd(dout, q, k, v, out, lse)
         zero = torch.zeros((), dtype=torch.int64)  # philox seed/offset: unused without dropout
         dq, dk, dv, _ = torch.ops.aten._scaled_dot_product_efficient_attention_backward(
             dout, q, k, v, None, out, lse, zero, zero, 0.0, [True, True, True, False], True,
