@@ -215,6 +215,10 @@ def test_attention_backward_matches_fp32(case):
         want.append((qf.grad, kf.grad, vf.grad))
     for i, (name, got, ref_t) in enumerate((("dq", dq, tq), ("dk", dk, tk), ("dv", dv, tv))):
         w = torch.stack([x[i] for x in want])
-        err, terr = _rel(got, w), _rel(ref_t, w)
+        # relative L2 with a floor of 1e-3 on the reference's norm: at S = 1
+        # dq and dk are zero and both sides leave ~1e-7 of fp32 cancellation
+        den = max(float(w.float().norm()), 1e-3)
+        err = float((got.float() - w).norm()) / den
+        terr = float((ref_t.float() - w).norm()) / den
         print(f"[attention] {name} rel {err:.2e} (torch {terr:.2e})", flush=True)
         assert err < 1e-2 and err <= 1.5 * terr + 1e-3, name

@@ -255,8 +255,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
 //   attn_bwd_dq_kernel: per 128-query tile (4 waves x 32 queries), over the
 //     key tiles up to the diagonal: S^T = K Q^T, dP^T = V dO^T, P = exp(S
 //     scale - lse), dS = P (dP - D), dQ^T += K^T dS^T; D = rowsum(dO o O) is
-//     formed from the wave's own rows first and written, with lse log2 e, to
-//     the workspace the second kernel reads.
+//     formed from the wave's own rows first; lse log2 e and -D per query go
+//     to the workspace the second kernel reads.  dP accumulates onto -D, so
+//     the MFMAs give dP - D with no subtraction.
 //   attn_bwd_dkdv_kernel: per 128-key block (4 waves x 32 keys), over the
 //     query tiles from the diagonal on: S = Q K^T, dP = dO V^T, P, dS,
 //     dV^T += dO^T P, dK^T += Q^T dS.
@@ -354,14 +355,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16_t* __restri
         for (int e = 0; e < 8; ++e) dsum = fmaf((float)df[c][e], (float)of[c][e], dsum);
     dsum += __shfl_xor(dsum, 32);
     const float lse2 = lse[(int64_t)bh * S + qc] * kLog2e;
-    // (lse log2 e, D) per query for the key-side kernel; padding queries up
-    // to S_pad get zeros
+    // per (batch, head): lse log2 e for S_pad queries, then -D, for the
+    // key-side kernel; padding queries up to S_pad get zeros
     if (g == 0 && qrow < S_pad) {
-        float2 w;
-        w.x = qrow < S ? lse2 : 0.0f;
-        w.y = qrow < S ? dsum : 0.0f;
-        *reinterpret_cast<float2*>(stats + ((int64_t)bh * S_pad + qrow) * 2) = w;
+        stats[(int64_t)bh * 2 * S_pad + qrow] = qrow < S ? lse2 : 0.0f;
+        stats[(int64_t)bh * 2 * S_pad + S_pad + qrow] = qrow < S ? -dsum : 0.0f;
     }
+    // dP^T accumulates onto -D, so the MFMAs give dP^T - D directly
+    f32x16 negd;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negd[r] = -dsum;
 
     // K and V tiles by direct-to-LDS loads (the forward's slot mapping)
     const bf16_t* kb0 = k + (int64_t)b * st.k[0] + (int64_t)h * st.k[2];
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16_t* __restri
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 zero16(s[kb]);
-                zero16(dp[kb]);
+                dp[kb] = negd;
                 const int row = 32 * kb + col;
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -420,15 +423,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16_t* __restri
         }
         if (j + 1 < nt) issue(j + 1, smem[(j + 1) & 1]);
         if (active) {
-            const bool edge = k0 + kKTile - 1 > qw0;
+            if (k0 + kKTile - 1 > qw0) {  // the causal edge crosses the wave's queries (a branch of its own)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) s[kb][r] = -INFINITY;
+            }
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float x = s[kb][r];
-                    if (edge && k0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) x = -INFINITY;
-                    const float p = __builtin_amdgcn_exp2f(fmaf(x, c2, -lse2));
-                    s[kb][r] = p * (dp[kb][r] - dsum);
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][r], c2, -lse2));
+                    s[kb][r] = p * dp[kb][r];
                 }
             // dQ^T += K^T dS^T, 16 keys per MFMA (the forward's key order)
 #pragma unroll
@@ -452,7 +459,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
                                                             bf16_t* __restrict__ dv, int S, int S_pad, int H, int BH,
                                                             AttnStrides st, float c2, float scale) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * kMatBytes];  // Q tile, dO tile (64 queries)
-    __shared__ __attribute__((aligned(16))) float stat[2][2 * 64];           // (lse log2 e, D) per query
+    __shared__ __attribute__((aligned(16))) float stat[2][2 * 64];           // lse log2 e [64], then -D [64]
     const int bid = blockIdx.x;
     const int kt_idx = bid / BH;  // key block 0 sees the most queries: first
     const int bh = bid - kt_idx * BH;
@@ -475,7 +482,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
     // first 32 threads also carry 4 floats of the stats
     const bf16_t* qb0 = q + (int64_t)b * st.q[0] + (int64_t)h * st.q[2];
     const bf16_t* db0 = dout + (int64_t)b * st.d[0] + (int64_t)h * st.d[2];
-    const float* sb0 = stats + (int64_t)bh * S_pad * 2;
+    const float* sb0 = stats + (int64_t)bh * S_pad * 2;  // lse log2 e [S_pad], then -D [S_pad]
     u32x4 stg[4];
     float4 sst = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     auto load = [&](int i) __attribute__((always_inline)) {
@@ -486,7 +493,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
             const bf16_t* src = (ii < 2 ? qb0 + (int64_t)qq * st.q[1] : db0 + (int64_t)qq * st.d[1]) + 8 * (w & 7);
             stg[ii] = qq < S ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
         }
-        if (tid < 32) sst = *reinterpret_cast<const float4*>(sb0 + (int64_t)i * 128 + 4 * tid);
+        if (tid < 32) sst = *reinterpret_cast<const float4*>(sb0 + (tid < 16 ? 0 : S_pad - 64) + i * 64 + 4 * tid);
     };
     auto store = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -520,8 +527,17 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
             const int qs0 = i * 64 + 32 * qb;  // first query of the sub-block
             if (qs0 + 31 < kw0) continue;      // every query precedes every key of the wave
             f32x16 sc, dp;
+            // dP accumulates onto -D of each register's query (4 consecutive
+            // queries per 16-byte read), so the MFMAs give dP - D directly
             zero16(sc);
-            zero16(dp);
+            float l2[16];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const float4 x = *reinterpret_cast<const float4*>(sts + 32 * qb + 8 * a + 4 * g);
+                const float4 y = *reinterpret_cast<const float4*>(sts + 64 + 32 * qb + 8 * a + 4 * g);
+                l2[4 * a] = x.x, l2[4 * a + 1] = x.y, l2[4 * a + 2] = x.z, l2[4 * a + 3] = x.w;
+                dp[4 * a] = y.x, dp[4 * a + 1] = y.y, dp[4 * a + 2] = y.z, dp[4 * a + 3] = y.w;
+            }
             const int row = 32 * qb + col;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -529,22 +545,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
                 dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tile_frag(ds_, row, 2 * c + g), vf[c], dp, 0, 0, 0);
             }
             // register r of lane l: query qs0 + 8 (r/4) + 4 g + r%4, key `key`
-            const bool edge = kw0 + 31 > qs0;
+            if (kw0 + 31 > qs0) {  // the causal edge crosses the sub-block (a branch of its own)
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
-                const float4 s01 = *reinterpret_cast<const float4*>(sts + 2 * (32 * qb + 8 * a + 4 * g));
-                const float4 s23 = *reinterpret_cast<const float4*>(sts + 2 * (32 * qb + 8 * a + 4 * g) + 4);
-                const float l2[4] = {s01.x, s01.z, s23.x, s23.z};
-                const float dd[4] = {s01.y, s01.w, s23.y, s23.w};
+                for (int r = 0; r < 16; ++r)
+                    if (key > qs0 + 8 * (r >> 2) + 4 * g + (r & 3)) sc[r] = -INFINITY;
+            }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * a + e;
-                    float x = sc[r];
-                    if (edge && key > qs0 + 8 * a + 4 * g + e) x = -INFINITY;
-                    const float p = __builtin_amdgcn_exp2f(fmaf(x, c2, -l2[e]));
-                    sc[r] = p;
-                    dp[r] = p * (dp[r] - dd[e]);
-                }
+            for (int r = 0; r < 16; ++r) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(sc[r], c2, -l2[r]));
+                sc[r] = p;
+                dp[r] *= p;
             }
             // dV^T += dO^T P and dK^T += Q^T dS, 16 queries per MFMA
 #pragma unroll
