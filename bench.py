@@ -38,6 +38,9 @@ Also reported in the same JSON line:
                 memory) against mix + GEMM, forward + dX, at 1-64 tokens on
                 three tensor sizes: the measured crossover behind the module's
                 choice of path
+  attention     the decoder step's causal attention (batch 4, 16 heads, 2048
+                positions, head dim 64): the HIP forward and backward against
+                torch's memory-efficient SDPA kernels, us and TFLOP/s
   train         the 0.8B-class decoder gate-training step (4 x 2048 tokens,
                 every Linear and the embedding gated, Q8_0 teacher): tokens/s
   stress        the 8-block SwiGLU stack at hidden 4096, MLP 14336, K = 8,
@@ -47,7 +50,8 @@ Also reported in the same JSON line:
 
   python bench.py --fused-workload runs only that comparison's kernels at 16
   tokens (three passes each), the workload the rocprof HBM-traffic summary of
-  the fused kernels is taken on; --shapes-workload runs only the shape sweep.
+  the fused kernels is taken on; --shapes-workload runs only the shape sweep;
+  --attention-workload only the attention comparison.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 """
@@ -440,6 +444,52 @@ def cpu_baseline(torch, m: int, n_total: int, d: int, budget_s: float = 12.0) ->
     }
 
 
+def attention_bench(torch, dev, reps: int = 20) -> dict:
+    """The decoder step's causal attention at its shape (batch 4, 16 heads,
+    2048 positions, head dim 64, q/k/v/dO as [B, H, S, D] views of [B, S, H, D]
+    memory, as the rotary kernel leaves them): vq_attention_fwd / _bwd against
+    torch's memory-efficient SDPA forward and its backward kernel (run over the
+    same forward's output and log-sum-exp).  FLOPs: forward 4 B H S^2 D / 2
+    (causal), backward 2.5 x that (five products, S recomputed)."""
+    import math
+
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from voodoo_quant import _hip
+
+    B, H, S, D = 4, 16, 2048, 64
+    gen = torch.Generator(device=dev).manual_seed(3)
+    q, k, v, do = (torch.randn(B, S, H, D, device=dev, generator=gen).to(torch.bfloat16).transpose(1, 2)
+                   for _ in range(4))
+    out, lse = _hip.attention_fwd(q, k, v)
+    zero = torch.zeros((), dtype=torch.int64)
+    scale = 1.0 / math.sqrt(D)
+
+    def torch_fwd():
+        with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+
+    def torch_bwd():
+        return torch.ops.aten._scaled_dot_product_efficient_attention_backward(
+            do, q, k, v, None, out, lse, zero, zero, 0.0, [True, True, True, False], True, scale=scale)
+
+    t = {"fwd": time_events(torch, lambda: _hip.attention_fwd(q, k, v), reps, 2),
+         "bwd": time_events(torch, lambda: _hip.attention_bwd(do, q, k, v, out, lse), reps, 2),
+         "torch_fwd": time_events(torch, torch_fwd, reps, 2),
+         "torch_bwd": time_events(torch, torch_bwd, reps, 2)}
+    fwd_fl = 4.0 * B * H * S * S * D / 2
+    fl = {"fwd": fwd_fl, "bwd": 2.5 * fwd_fl, "torch_fwd": fwd_fl, "torch_bwd": 2.5 * fwd_fl}
+    rec = {"workload": "causal attention, batch 4, 16 heads, 2048 positions, head dim 64, bf16"}
+    for key, ms in t.items():
+        rec[f"{key}_us"] = round(ms * 1e3, 1)
+        rec[f"{key}_TFLOPs"] = round(fl[key] / (ms * 1e-3) / 1e12, 1)
+    rec["fwd_frac_of_spec"] = round(rec["fwd_TFLOPs"] / PEAK_BF16_TFLOPS, 3)
+    rec["bwd_frac_of_spec"] = round(rec["bwd_TFLOPs"] / PEAK_BF16_TFLOPS, 3)
+    log("attention us: " + ", ".join(f"{k} {v * 1e3:.1f}" for k, v in t.items()))
+    return rec
+
+
 def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False, defer: bool = False) -> dict:
     """Gate-training steps of the 0.8B-class decoder (24 layers, hidden 1024,
     16x64 query heads, 4 KV heads, SwiGLU 3072, vocabulary 151936 tied; every
@@ -666,6 +716,8 @@ def main() -> int:
                     help="only run the fused and materialising few-token products (16 tokens, 3 passes each)")
     ap.add_argument("--shapes-workload", action="store_true",
                     help="only time the 27B-class and 0.8B-class gated Linear shapes and print their record")
+    ap.add_argument("--attention-workload", action="store_true",
+                    help="only time the decoder step's attention forward and backward (HIP and torch) and print them")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (known bytes) to scale rocprof FETCH/WRITE_SIZE")
     args = ap.parse_args()
@@ -688,6 +740,9 @@ def main() -> int:
     if args.shapes_workload:
         print(json.dumps({"shapes": shape_sweep(torch, dev, torch.Generator(device=dev).manual_seed(0))}),
               flush=True)
+        return 0
+    if args.attention_workload:
+        print(json.dumps({"attention": attention_bench(torch, dev)}), flush=True)
         return 0
     if args.only_train:
         print(json.dumps({"train": train_step_bench(torch, dev, args.train_steps, 2, args.prefetch_mix, args.defer_gate_grads)}), flush=True)
@@ -827,6 +882,7 @@ def main() -> int:
     del qbytes, w_eff, y, dx, ws, fws, out
     torch.cuda.empty_cache()
     shapes = None if args.no_sweeps else shape_sweep(torch, dev, gen)
+    attention = None if args.no_sweeps else attention_bench(torch, dev)
     train = None
     if not args.no_train:
         torch.cuda.empty_cache()
@@ -885,6 +941,7 @@ def main() -> int:
         "dequant_gbps": dq,
         "ptqr": ptqr,
         "shapes": shapes,
+        "attention": attention,
         "train": train,
         "stress": stack,
         "stream_schedule": stream,
