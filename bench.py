@@ -42,7 +42,8 @@ Also reported in the same JSON line:
                 positions, head dim 64): the HIP forward and backward against
                 torch's memory-efficient SDPA kernels, us and TFLOP/s
   train         the 0.8B-class decoder gate-training step (4 x 2048 tokens,
-                every Linear and the embedding gated, Q8_0 teacher): tokens/s
+                every Linear and the embedding gated, Q8_0 teacher): tokens/s,
+                and the step time with torch's SDPA attention in its place
   stress        the 8-block SwiGLU stack at hidden 4096, MLP 14336, K = 8,
                 2 x 8192 tokens: tokens/s
   stream_schedule  that stack with its candidates in pinned host memory:
@@ -522,17 +523,33 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
     ms = (time.perf_counter() - t0) / max(steps, 1) * 1e3
     from voodoo_quant import layers
 
+    # the same step with torch's SDPA attention (AOTriton forward, its fused
+    # backward) in place of the HIP attention kernels, for comparison
+    saved = st.HIP_ATTENTION
+    try:
+        st.HIP_ATTENTION = False
+        tr.step(x, y)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tr.step(x, y)
+        torch.cuda.synchronize()
+        ms_sdpa = (time.perf_counter() - t0) / max(steps, 1) * 1e3
+    finally:
+        st.HIP_ATTENTION = saved
     layers.raise_pending_id_errors()  # the last step's deferred embedding id checks
     tokens = b * s
     fl = st.step_flops(cfg, tokens, s)
-    rec = {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3), "steps": steps,
+    rec = {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3),
+           "ms_per_step_torch_attention": round(ms_sdpa, 3), "steps": steps,
            "warmup": warmup, "model_TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
            "loss": {k: round(float(v), 4) for k, v in out.items()},
            "workload": "0.8B-class decoder gate-training step: 24 layers, hidden 1024, 16x64 q heads, 4 KV heads, "
                        "SwiGLU 3072, vocab 151936 tied; 168 gated Linears + gated embedding, K=6; Q8_0 teacher; "
                        "batch 4x2048 uniform-random ids; CE + KL + dead-zone size loss at 45% of 8-bit",
            "candidate_bytes": "random valid GGUF blocks, scales sized for N(0, 0.02)-like weights"}
-    log(f"train: {ms:.1f} ms/step -> {rec['tokens_per_s']:.0f} tokens/s ({rec['model_TFLOPs']} model TFLOP/s)")
+    log(f"train: {ms:.1f} ms/step -> {rec['tokens_per_s']:.0f} tokens/s ({rec['model_TFLOPs']} model TFLOP/s); "
+        f"{ms_sdpa:.1f} ms/step with torch's attention")
     del student, teacher, replaced, tr
     torch.cuda.empty_cache()
     return rec
