@@ -19,11 +19,12 @@ same non-uniform gate logits.
 Over 24 bf16 layers the gate gradients are as sensitive to rounding as that:
 measured on MI355X, the reference against itself with its products evaluated
 in fp32 and rounded once (only the accumulation order changes) differs by
-1.15e-2 relative L2 over all tensors (per tensor: median 1.6e-2, 90th
-percentile 3.2e-2, max 1.1e-1, cosine >= 0.9964), and the same reference step
-run twice by 7.2e-3 (attention's backward accumulates with atomics).  The
-product against the reference: 1.36e-2 (median 1.7e-2, 90th percentile
-3.9e-2, max 8.4e-2, cosine >= 0.9973).
+1.11e-2 relative L2 over all tensors (per tensor: median 1.5e-2, 90th
+percentile 3.6e-2, max 6.8e-2, cosine >= 0.9982); the same reference step run
+twice is bitwise equal (the attention kernels sum in a fixed order; with
+torch's attention backward, fp32 atomics on dq, it differed by 7.2e-3).  The
+product against the reference: 1.47e-2 (median 1.7e-2, 90th percentile
+4.2e-2, max 9.0e-2, cosine >= 0.9968).
 
 Bars: the loss equal to 1e-3; every tensor's cosine above 0.99; over all
 tensors 3e-2; and the total, the per-tensor median, 90th percentile and
