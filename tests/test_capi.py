@@ -176,7 +176,7 @@ def test_attention_fwd_argument_checks():
 def test_attention_bwd_argument_checks():
     """vq_attention_bwd refuses other head dims, a short workspace and
     unaligned strides before any device work; its workspace holds two floats
-    per query padded to 64 queries."""
+    per query padded to 128 queries."""
     import ctypes
 
     lib = _hip.lib()

@@ -458,8 +458,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
                                                             const float* __restrict__ stats, bf16_t* __restrict__ dk,
                                                             bf16_t* __restrict__ dv, int S, int S_pad, int H, int BH,
                                                             AttnStrides st, float c2, float scale) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * kMatBytes];  // Q tile, dO tile (64 queries)
-    __shared__ __attribute__((aligned(16))) float stat[2][2 * 64];           // lse log2 e [64], then -D [64]
+    // a stage: Q tile and dO tile of 128 queries (16 KiB each), then lse log2 e
+    // [128] and -D [128] of those queries
+    constexpr int kQBytes = 128 * kRowBytes;
+    constexpr int kStage = 2 * kQBytes + 1024;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2][kStage];
     const int bid = blockIdx.x;
     const int kt_idx = bid / BH;  // key block 0 sees the most queries: first
     const int bh = bid - kt_idx * BH;
@@ -477,31 +480,36 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
     row_frags(k + (int64_t)b * st.k[0] + (int64_t)kc * st.k[1] + (int64_t)h * st.k[2], g, kf);
     row_frags(v + (int64_t)b * st.v[0] + (int64_t)kc * st.v[1] + (int64_t)h * st.v[2], g, vf);
 
-    // Q, dO and stats tiles staged through registers: thread chunk i is row
-    // (tid + 256 (i & 1)) / 8, chunk tid % 8 of Q (i < 2) or dO (i >= 2); the
-    // first 32 threads also carry 4 floats of the stats
+    // Q and dO tiles by direct-to-LDS loads: lane l of wave w's instruction i
+    // (0-7) writes stage slot s = 64 (4 i + w) + l (slots 0-1023 Q, 1024-2047
+    // dO), which is tile_off(row, c) for row = (s % 1024) / 8 and chunk
+    // c = (s % 8) ^ swz(row); queries past S read zeros.  Wave 0 also copies
+    // the stats: lanes 0-31 four lse log2 e each, lanes 32-63 four -D each.
     const bf16_t* qb0 = q + (int64_t)b * st.q[0] + (int64_t)h * st.q[2];
     const bf16_t* db0 = dout + (int64_t)b * st.d[0] + (int64_t)h * st.d[2];
     const float* sb0 = stats + (int64_t)bh * S_pad * 2;  // lse log2 e [S_pad], then -D [S_pad]
-    u32x4 stg[4];
-    float4 sst = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    auto load = [&](int i) __attribute__((always_inline)) {
+    uint32_t voff[8];
+    int vrow[8];
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            const int w = tid + 256 * (ii & 1);
-            const int qq = i * 64 + (w >> 3);
-            const bf16_t* src = (ii < 2 ? qb0 + (int64_t)qq * st.q[1] : db0 + (int64_t)qq * st.d[1]) + 8 * (w & 7);
-            stg[ii] = qq < S ? *reinterpret_cast<const u32x4*>(src) : u32x4{0u, 0u, 0u, 0u};
-        }
-        if (tid < 32) sst = *reinterpret_cast<const float4*>(sb0 + (tid < 16 ? 0 : S_pad - 64) + i * 64 + 4 * tid);
-    };
-    auto store = [&](int buf) __attribute__((always_inline)) {
+    for (int i = 0; i < 8; ++i) {
+        const int w = ((4 * i + wave) * 64 + lane) & 1023;
+        const int row = w >> 3, c = (w & 7) ^ swz(row);
+        vrow[i] = row;
+        voff[i] = (uint32_t)(row * (i < 4 ? st.q[1] : st.d[1]) * 2 + 16 * c);
+    }
+    const uint32_t soff = (uint32_t)(((lane < 32 ? 0 : S_pad - 128) + 4 * lane) * 4);
+    auto issue = [&](int i, uint8_t* dst) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t rq = tile_rsrc(qb0 + (int64_t)i * 128 * st.q[1]);
+        const __amdgpu_buffer_rsrc_t rd = tile_rsrc(db0 + (int64_t)i * 128 * st.d[1]);
+        const int lim = S - i * 128;
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            const int w = tid + 256 * (ii & 1);
-            *reinterpret_cast<u32x4*>(&smem[buf][(ii >> 1) * kMatBytes + tile_off(w >> 3, w & 7)]) = stg[ii];
-        }
-        if (tid < 32) *reinterpret_cast<float4*>(&stat[buf][4 * tid]) = sst;
+        for (int ii = 0; ii < 8; ++ii)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ii < 4 ? rq : rd, (lds_void_t*)(dst + (4 * ii + wave) * 1024),
+                                                     16, vrow[ii] < lim ? voff[ii] : kOOB, 0, 0, 0);
+        if (wave == 0)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(sb0 + i * 128), (short)0, (int)kRange, 0x00020000),
+                (lds_void_t*)(dst + 2 * kQBytes), 16, soff, 0, 0, 0);
     };
 
     f32x16 dka[2], dva[2];
@@ -509,23 +517,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
     zero16(dka[1]);
     zero16(dva[0]);
     zero16(dva[1]);
-    const int i0 = kv0 / 64;
-    const int ni = S_pad / 64;
-    if (i0 < ni) {
-        load(i0);
-        store(0);
-    }
-    __syncthreads();
-    for (int i = i0; i < ni; ++i) {
-        const int buf = (i - i0) & 1;
-        if (i + 1 < ni) load(i + 1);
-        const uint8_t* qs = smem[buf];
-        const uint8_t* ds_ = qs + kMatBytes;
-        const float* sts = stat[buf];
+    // query tile i: copy tile i + 1 into the other stage (whose last readers
+    // passed the last barrier), compute on this one, then the barrier.
+    // Unrolled by two so each step names its two stages as fixed buffers: the
+    // compiler then tells the copies into one from the reads of the other.
+    auto step = [&](int i, const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt, int ni)
+                    __attribute__((always_inline)) {
+        if (i + 1 < ni) issue(i + 1, nxt);
+        const uint8_t* qs = cur;
+        const uint8_t* ds_ = cur + kQBytes;
+        const float* sts = reinterpret_cast<const float*>(cur + 2 * kQBytes);
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const int qs0 = i * 64 + 32 * qb;  // first query of the sub-block
-            if (qs0 + 31 < kw0) continue;      // every query precedes every key of the wave
+        for (int qb = 0; qb < 4; ++qb) {
+            const int qs0 = i * 128 + 32 * qb;  // first query of the sub-block
+            if (qs0 + 31 < kw0) continue;       // every query precedes every key of the wave
             f32x16 sc, dp;
             // dP accumulates onto -D of each register's query (4 consecutive
             // queries per 16-byte read), so the MFMAs give dP - D directly
@@ -534,7 +539,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
 #pragma unroll
             for (int a = 0; a < 4; ++a) {
                 const float4 x = *reinterpret_cast<const float4*>(sts + 32 * qb + 8 * a + 4 * g);
-                const float4 y = *reinterpret_cast<const float4*>(sts + 64 + 32 * qb + 8 * a + 4 * g);
+                const float4 y = *reinterpret_cast<const float4*>(sts + 128 + 32 * qb + 8 * a + 4 * g);
                 l2[4 * a] = x.x, l2[4 * a + 1] = x.y, l2[4 * a + 2] = x.z, l2[4 * a + 3] = x.w;
                 dp[4 * a] = y.x, dp[4 * a + 1] = y.y, dp[4 * a + 2] = y.z, dp[4 * a + 3] = y.w;
             }
@@ -570,8 +575,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
                 }
             }
         }
-        if (i + 1 < ni) store(buf ^ 1);  // that stage's last readers passed the last barrier
-        __syncthreads();
+        // this wave's copies of tile i + 1 have landed and every wave is past
+        // its reads of tile i
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    const int i0 = kv0 / 128;  // queries before the key block see none of its keys
+    const int ni = S_pad / 128;
+    issue(i0, smem[0]);
+    // a wait the compiler sees (the K/V fragments and the first copies are in),
+    // so it does not wait again for the fragments inside the loop
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("s_barrier" ::: "memory");
+    for (int i = i0; i < ni; i += 2) {
+        step(i, smem[0], smem[1], ni);
+        if (i + 1 < ni) step(i + 1, smem[1], smem[0], ni);
     }
     if (key < S) {
         store_row(dk + (int64_t)b * st.dk[0] + (int64_t)key * st.dk[1] + (int64_t)h * st.dk[2], dka, scale, g);
@@ -596,7 +613,7 @@ hipError_t launch_attention_fwd(const bf16_t* q, const bf16_t* k, const bf16_t* 
 }
 
 int64_t attention_bwd_workspace(int B, int S, int H) {
-    const int64_t S_pad = (int64_t)(S + 63) / 64 * 64;
+    const int64_t S_pad = (int64_t)(S + 127) / 128 * 128;
     return (int64_t)B * H * S_pad * 2 * (int64_t)sizeof(float);
 }
 
@@ -616,7 +633,7 @@ hipError_t launch_attention_bwd(const bf16_t* q, const bf16_t* k, const bf16_t* 
         st.dk[i] = strides[18 + i];
         st.dv[i] = strides[21 + i];
     }
-    const int S_pad = (S + 63) / 64 * 64;
+    const int S_pad = (S + 127) / 128 * 128;  // the key-side kernel's query tiles
     const int nqt = (S + kQTile - 1) / kQTile;
     const float c2 = scale * kLog2e;
     attn_bwd_dq_kernel<<<dim3((unsigned)(BH * nqt)), 256, 0, s>>>(q, k, v, o, dout, lse, stats, dq, S, S_pad, H, BH,

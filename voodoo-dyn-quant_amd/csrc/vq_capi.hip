@@ -611,8 +611,9 @@ int vq_attention_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
     if (reinterpret_cast<uintptr_t>(lse) & 3) return fail(VQ_ERR_ALIGN, "lse not 4-byte aligned");
     for (int i = 0; i < 24; ++i)
         if (strides[i] < 0 || strides[i] % 8) return fail(VQ_ERR_ALIGN, "strides must be non-negative multiples of 8");
-    if (strides[4] > (1 << 22) || strides[7] > (1 << 22))
-        return fail(VQ_ERR_SHAPE, "k/v position strides above 2^22 elements");
+    // 64-key and 128-query tiles are addressed by 32-bit byte offsets from their first row
+    if (strides[1] > (1 << 22) || strides[4] > (1 << 22) || strides[7] > (1 << 22) || strides[13] > (1 << 22))
+        return fail(VQ_ERR_SHAPE, "q/k/v/dout position strides above 2^22 elements");
     const int64_t need = vq_attention_bwd_workspace(B, S, Hq);
     if (!workspace || ws_bytes < need || !aligned16(workspace))
         return fail(VQ_ERR_WORKSPACE, "workspace %lld bytes at %p, need %lld (16-byte aligned)", (long long)ws_bytes,
