@@ -265,10 +265,12 @@ int vq_attention_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, ui
 /* Backward of vq_attention_fwd (Hq == Hk): dq, dk, dv (bf16, softmax scale
  * `scale`) from dout and the forward's o and lse.  strides: 24 int64, the
  * {batch, position, head} element strides of q, k, v, o, dout, dq, dk, dv
- * (multiples of 8; unit stride along the head dim).  Two launches, no atomics:
- * dq (which also writes lse log2 e and D = rowsum(dout o o) per query into
- * the workspace), then dk and dv; deterministic.  workspace:
- * vq_attention_bwd_workspace(B, S, Hq) bytes, 16-byte aligned, device memory.
+ * (multiples of 8; unit stride along the head dim; q/k/v/dout position
+ * strides at most 2^22).  Two launches, no atomics: dq (which also writes
+ * lse log2 e and -D, D = rowsum(dout o o), per query into the workspace,
+ * padded to a multiple of 128 queries), then dk and dv; deterministic.
+ * workspace: vq_attention_bwd_workspace(B, S, Hq) bytes, 16-byte aligned,
+ * device memory.
  * Only head dim 64.  No counterpart in voodoo_quant; it replaces the
  * memory-efficient attention backward of the step. */
 int64_t vq_attention_bwd_workspace(int64_t B, int64_t S, int Hq);
