@@ -252,7 +252,8 @@ int vq_rmsnorm_bwd(const uint16_t *dn, const uint16_t *ds, const uint16_t *s, co
  * value head h / (Hq / Hk).  q, o: bf16 [B][S][Hq][64]-indexed through
  * element strides {batch, position, head} (q_strides, o_strides), k, v
  * likewise with Hk heads; unit stride along the head dim, strides multiples
- * of 8, pointers 16-byte aligned.  Scores and softmax in fp32, probabilities
+ * of 8 (k/v position strides at most 2^22), pointers 16-byte aligned.
+ * Scores and softmax in fp32, probabilities
  * rounded to bf16 for the value product.  lse (fp32 [B][Hq][S], natural-log
  * log-sum-exp of the scaled scores per query; may be NULL) is the saved
  * state torch's memory-efficient attention backward reads.  Only head dim 64.
