@@ -61,6 +61,35 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const bf16_t* base) 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, (int)kRange, 0x00020000);
 }
 
+// The register's values in lanes l % 32 and 32 + l % 32, one in each output,
+// in every lane l (v_permlane32_swap_b32 of the register with itself: a VALU
+// exchange of the two 32-lane halves, no LDS round trip).  lo + hi and
+// max(lo, hi) are then the same in both halves.
+__device__ __forceinline__ void halves(float x, float& lo, float& hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+
+// IEEE maximum (NaN-propagating: v_maximum3_f32, which needs no
+// canonicalisation of the MFMA results as fmaxf would) of 32 values as a
+// tree of three-input maxima: 16 instructions instead of 24 pairwise ones
+__device__ __forceinline__ float max_of_32(const f32x16& a, const f32x16& b) {
+    float m[11];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        m[2 * i] = max3f(a[3 * i], a[3 * i + 1], a[3 * i + 2]);
+        m[2 * i + 1] = max3f(b[3 * i], b[3 * i + 1], b[3 * i + 2]);
+    }
+    m[10] = __builtin_elementwise_maximum(a[15], b[15]);
+    const float n0 = max3f(m[0], m[1], m[2]), n1 = max3f(m[3], m[4], m[5]), n2 = max3f(m[6], m[7], m[8]);
+    return max3f(n0, n1, max3f(n2, m[9], m[10]));
+}
+
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                                                        const bf16_t* __restrict__ v, bf16_t* __restrict__ o,
                                                        float* __restrict__ lse, int S, int H, int Hk, int BH, int nqt,
@@ -184,13 +213,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
                         if (key > qrow) s[kb][r] = -INFINITY;
                     }
             }
-            // IEEE maximum (NaN-propagating: v_maximum3_f32), which needs no
-            // canonicalisation of the MFMA results as fmaxf would
-            float mx = __builtin_elementwise_maximum(s[0][0], s[1][0]);
-#pragma unroll
-            for (int r = 1; r < 16; ++r)
-                mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s[0][r], s[1][r]));
-            mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32)) * c2;
+            float mx = max_of_32(s[0], s[1]);
+            float mlo, mhi;
+            halves(mx, mlo, mhi);
+            mx = __builtin_elementwise_maximum(mlo, mhi) * c2;
             // the running maximum moves only when the tile's exceeds it by more
             // than kSlack, so most tiles skip the rescale (exponents stay <= 2^8)
             if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack)) {
@@ -232,7 +258,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
 
-    const float lt = l_run + __shfl_xor(l_run, 32);
+    float llo, lhi;
+    halves(l_run, llo, lhi);
+    const float lt = llo + lhi;
     if (qrow < S) {
         const float inv = 1.0f / lt;
         bf16_t* op = o + (int64_t)b * osb + (int64_t)qrow * oss + (int64_t)h * osh;
