@@ -215,11 +215,13 @@ int vq_gated_linear_group_bwd_gate_stream(const uint16_t *dy, const uint16_t *x,
 /* Decoder-layer glue of the gate-training step (the model the trainer runs
  * around the gated projections; no counterpart in voodoo_quant itself).
  * vq_rope_qkv_fwd: qkv [B*S][(Hq + 2 Hkv) D] bf16 (stacked q/k/v projection
- * output) -> q, k, v, each [B*S][Hq][D] bf16: rotary embedding on q and k
- * (y = x cos + [-x2, x1] sin with cos/sin fp32 [S][D]), K/V heads repeated
- * Hq / Hkv times.  D % 16 == 0, Hq % Hkv == 0. */
-int vq_rope_qkv_fwd(const uint16_t *qkv, int64_t B, int64_t S, int Hq, int Hkv, int D, const float *cosb,
-                    const float *sinb, uint16_t *q, uint16_t *k, uint16_t *v, void *stream);
+ * output) -> q [B*S][Hq][D] and k, v [B*S][kv_heads_out][D] bf16: rotary
+ * embedding on q and k (y = x cos + [-x2, x1] sin with cos/sin fp32 [S][D]);
+ * kv_heads_out = Hq repeats each K/V head Hq / Hkv times, kv_heads_out = Hkv
+ * keeps them as they are (for vq_attention_fwd/_bwd, which read K/V head
+ * h / (Hq/Hkv) themselves).  D % 16 == 0, Hq % Hkv == 0. */
+int vq_rope_qkv_fwd(const uint16_t *qkv, int64_t B, int64_t S, int Hq, int Hkv, int kv_heads_out, int D,
+                    const float *cosb, const float *sinb, uint16_t *q, uint16_t *k, uint16_t *v, void *stream);
 
 /* Backward of vq_rope_qkv_fwd: dq, dk, dv [B][Hq][S][D] with element strides
  * (stride_b, stride_h, stride_s; multiples of 8; unit stride along D) ->
@@ -263,11 +265,15 @@ int vq_attention_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, ui
                      int64_t S, int Hq, int Hk, int D, const int64_t *q_strides, const int64_t *k_strides,
                      const int64_t *v_strides, const int64_t *o_strides, float scale, void *stream);
 
-/* Backward of vq_attention_fwd (Hq == Hk): dq, dk, dv (bf16, softmax scale
- * `scale`) from dout and the forward's o and lse.  strides: 24 int64, the
- * {batch, position, head} element strides of q, k, v, o, dout, dq, dk, dv
- * (multiples of 8; unit stride along the head dim; q/k/v/dout position
- * strides at most 2^22).  Two launches, no atomics: dq (which also writes
+/* Backward of vq_attention_fwd: dq, dk, dv (bf16, softmax scale `scale`)
+ * from dout and the forward's o and lse.  q, o, dout, dq, dk, dv have Hq
+ * heads, k and v Hk (Hq % Hk == 0; query head h reads K/V head h / (Hq/Hk)).
+ * dk and dv are per query head, [B][S][Hq][D]: the gradients of K and V with
+ * each head repeated Hq/Hk times, so at Hk < Hq the gradient of K/V head j is
+ * the sum of query heads j (Hq/Hk) .. (j+1) (Hq/Hk) - 1 (the decoder step's
+ * vq_rope_qkv_bwd forms it).  strides: 24 int64, the {batch, position, head}
+ * element strides of q, k, v, o, dout, dq, dk, dv (multiples of 8; unit
+ * stride along the head dim; q/k/v/dout position strides at most 2^22).  Two launches, no atomics: dq (which also writes
  * lse log2 e and -D, D = rowsum(dout o o), per query into the workspace,
  * padded to a multiple of 128 queries), then dk and dv; deterministic.
  * workspace: vq_attention_bwd_workspace(B, S, Hq) bytes, 16-byte aligned,
@@ -276,8 +282,8 @@ int vq_attention_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, ui
  * memory-efficient attention backward of the step. */
 int64_t vq_attention_bwd_workspace(int64_t B, int64_t S, int Hq);
 int vq_attention_bwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, const uint16_t *o, const uint16_t *dout,
-                     const float *lse, uint16_t *dq, uint16_t *dk, uint16_t *dv, int64_t B, int64_t S, int Hq, int D,
-                     const int64_t *strides, float scale, void *workspace, int64_t ws_bytes, void *stream);
+                     const float *lse, uint16_t *dq, uint16_t *dk, uint16_t *dv, int64_t B, int64_t S, int Hq, int Hk,
+                     int D, const int64_t *strides, float scale, void *workspace, int64_t ws_bytes, void *stream);
 
 /* Workspace bytes of the distillation loss (per-row log-sum-exps and losses;
  * written by vq_distill_loss_fwd, read by vq_distill_loss_bwd). */

@@ -174,9 +174,10 @@ def test_attention_fwd_argument_checks():
 
 
 def test_attention_bwd_argument_checks():
-    """vq_attention_bwd refuses other head dims, a short workspace and
-    unaligned strides before any device work; its workspace holds two floats
-    per query padded to 128 queries."""
+    """vq_attention_bwd refuses other head dims, K/V head counts that do not
+    divide the query heads, a short workspace and unaligned strides before
+    any device work; its workspace holds two floats per query padded to 128
+    queries."""
     import ctypes
 
     lib = _hip.lib()
@@ -187,8 +188,24 @@ def test_attention_bwd_argument_checks():
     p = 4096
     args = [p] * 6 + [p] * 3
     need = lib.vq_attention_bwd_workspace(1, 8, 16)
-    assert lib.vq_attention_bwd(*args, 1, 8, 16, 128, st, 0.125, p, need, None) == _hip.VQ_ERR_SHAPE
-    assert lib.vq_attention_bwd(*args, 1, 8, 16, 64, bad, 0.125, p, need, None) == _hip.VQ_ERR_ALIGN
-    assert lib.vq_attention_bwd(*args, 1, 8, 16, 64, st, 0.125, p, need - 1, None) == _hip.VQ_ERR_WORKSPACE
-    assert lib.vq_attention_bwd(*args, 1, 8, 16, 64, st, 0.125, None, need, None) == _hip.VQ_ERR_WORKSPACE
-    assert lib.vq_attention_bwd(None, *args[1:], 1, 8, 16, 64, st, 0.125, p, need, None) == _hip.VQ_ERR_NULL
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 4, 128, st, 0.125, p, need, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 3, 64, st, 0.125, p, need, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 0, 64, st, 0.125, p, need, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 4, 64, bad, 0.125, p, need, None) == _hip.VQ_ERR_ALIGN
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 4, 64, st, 0.125, p, need - 1, None) == _hip.VQ_ERR_WORKSPACE
+    assert lib.vq_attention_bwd(*args, 1, 8, 16, 4, 64, st, 0.125, None, need, None) == _hip.VQ_ERR_WORKSPACE
+    assert lib.vq_attention_bwd(None, *args[1:], 1, 8, 16, 16, 64, st, 0.125, p, need, None) == _hip.VQ_ERR_NULL
+
+
+def test_rope_qkv_fwd_argument_checks():
+    """vq_rope_qkv_fwd takes K/V output heads of Hq (each head repeated) or
+    Hkv and refuses any other count, and a head count that does not divide,
+    before any device work."""
+    lib = _hip.lib()
+    p = 4096
+    assert lib.vq_rope_qkv_fwd(p, 1, 8, 16, 4, 8, 64, p, p, p, p, p, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_rope_qkv_fwd(p, 1, 8, 16, 3, 16, 64, p, p, p, p, p, None) == _hip.VQ_ERR_SHAPE
+    assert lib.vq_rope_qkv_fwd(p, 1, 8, 16, 4, 4, 40, p, p, p, p, p, None) == _hip.VQ_ERR_ALIGN
+    assert lib.vq_rope_qkv_fwd(p, 1, 8, 16, 4, 16, 64, None, p, p, p, p, None) == _hip.VQ_ERR_NULL
+    # nothing to do at B = 0: no pointer is needed
+    assert lib.vq_rope_qkv_fwd(None, 0, 8, 16, 4, 4, 64, p, p, None, None, None, None) == _hip.VQ_OK

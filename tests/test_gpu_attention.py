@@ -222,3 +222,111 @@ def test_attention_backward_matches_fp32(case):
         terr = float((ref_t.float() - w).norm()) / den
         print(f"[attention] {name} rel {err:.2e} (torch {terr:.2e})", flush=True)
         assert err < 1e-2 and err <= 1.5 * terr + 1e-3, name
+
+
+GQA_CASES = [  # B, Hq, Hk, S, magnitude
+    (1, 4, 1, 65, 1.0),
+    (2, 8, 2, 300, 1.0),
+    (1, 6, 3, 777, 4.0),
+    (4, 16, 4, 2048, 1.0),  # the 0.8B-class step's heads
+]
+
+
+@pytest.mark.parametrize("case", GQA_CASES, ids=[f"B{c[0]}_H{c[1]}_{c[2]}_S{c[3]}_x{c[4]}" for c in GQA_CASES])
+def test_attention_backward_grouped_kv(case):
+    """vq_attention_bwd with Hk < Hq K/V heads: dq and the per-query-head dk,
+    dv bit for bit those of the same call on K/V repeated to Hq heads; the
+    group sums of dk, dv against fp32 autograd through the repeat (1e-2
+    relative L2)."""
+    _need_gpu()
+    from voodoo_quant import _hip
+
+    B, Hq, Hk, S, mag = case
+    rep = Hq // Hk
+    print(f"[attention] grouped backward B={B} Hq={Hq} Hk={Hk} S={S} x{mag}", flush=True)
+    q, k, v = _inputs(B, Hq, Hk, S, "bshd", seed=3 * S + Hq, mag=mag)
+    g = torch.Generator().manual_seed(S + 1)
+    dout = torch.randn(B, S, Hq, 64, generator=g).to(torch.bfloat16).cuda().transpose(1, 2)
+    out, lse = _hip.attention_fwd(q, k, v)
+    grads = _hip.attention_bwd(dout, q, k, v, out, lse)
+    kr, vr = k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1)
+    out_r, lse_r = _hip.attention_fwd(q, kr, vr)
+    assert torch.equal(out, out_r) and torch.equal(lse, lse_r)
+    grads_r = _hip.attention_bwd(dout, q, kr, vr, out_r, lse_r)
+    for name, a, b_ in zip(("dq", "dk", "dv"), grads, grads_r):
+        assert a.shape == (B, Hq, S, 64), name
+        assert torch.equal(a, b_), name
+    scale = 1.0 / math.sqrt(64)
+    mask = torch.ones(S, S, dtype=torch.bool, device="cuda").triu(1)
+    for bi in range(B):  # fp32 autograd per batch to bound memory
+        qf, kf, vf = (t[bi].detach().float().requires_grad_(True) for t in (q, k, v))
+        s_ = (qf @ kf.repeat_interleave(rep, 0).transpose(-1, -2)) * scale
+        o = torch.softmax(s_.masked_fill(mask, float("-inf")), -1) @ vf.repeat_interleave(rep, 0)
+        o.backward(dout[bi].float())
+        for name, got, want in (("dq", grads[0][bi], qf.grad),
+                                ("dk", grads[1][bi].float().unflatten(0, (Hk, rep)).sum(1), kf.grad),
+                                ("dv", grads[2][bi].float().unflatten(0, (Hk, rep)).sum(1), vf.grad)):
+            err = float((got.float() - want).norm()) / max(float(want.norm()), 1e-3)
+            print(f"[attention] batch {bi} {name} rel {err:.2e}", flush=True)
+            assert err < 1e-2, (bi, name)
+
+
+def test_step_rope_attention_node_matches_unfused():
+    """The decoder step's rotary + attention node (K/V at their own heads)
+    against the rotary node with repeated heads followed by the attention
+    node: output and the stacked projection's gradient bit for bit with the
+    HIP backward, and the no-grad path's output the same; with torch's
+    backward, within 1e-2 of fp32 autograd."""
+    _need_gpu()
+    from voodoo_quant.training import step as st
+
+    b, s, hq, hkv, d = 2, 300, 8, 2, 64
+    g = torch.Generator().manual_seed(9)
+    qkv = torch.randn(b * s, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).cuda()
+    dout = torch.randn(b, hq, s, d, generator=g).to(torch.bfloat16).cuda()
+    cos, sin = st._rope_tables_f32(s, d, 1.0e6, "cuda")
+    shape = (b, s, hq, hkv, d)
+
+    def fused():
+        x = qkv.detach().clone().requires_grad_(True)
+        out = st._rope_attention(x, cos, sin, shape)
+        out.backward(dout)
+        return out.detach(), x.grad
+
+    def unfused():
+        x = qkv.detach().clone().requires_grad_(True)
+        q, k, v = st._RopeQKV.apply(x, cos, sin, shape)
+        out = st._CausalAttention.apply(q, k, v)
+        out.backward(dout)
+        return out.detach(), x.grad
+
+    saved = st.HIP_ATTENTION_BWD
+    try:
+        st.HIP_ATTENTION_BWD = True
+        (o1, g1), (o2, g2) = fused(), unfused()
+        assert torch.equal(o1, o2) and torch.equal(g1, g2)
+        with torch.no_grad():
+            assert torch.equal(st._rope_attention(qkv, cos, sin, shape), o1)
+        st.HIP_ATTENTION_BWD = False
+        o3, g3 = fused()
+        assert torch.equal(o3, o1)
+    finally:
+        st.HIP_ATTENTION_BWD = saved
+    # fp32 autograd of rotary + attention with the K/V heads repeated
+    xr = qkv.float().cpu().requires_grad_(True)
+    c, sn = cos.cpu(), sin.cpu()
+    half = d // 2
+
+    def rope(t):
+        return t * c + torch.cat([-t[..., half:], t[..., :half]], dim=-1) * sn
+
+    qr = rope(xr[:, : hq * d].view(b, s, hq, d).transpose(1, 2))
+    kr = rope(xr[:, hq * d:(hq + hkv) * d].view(b, s, hkv, d).transpose(1, 2)).repeat_interleave(hq // hkv, 1)
+    vr = xr[:, (hq + hkv) * d:].view(b, s, hkv, d).transpose(1, 2).repeat_interleave(hq // hkv, 1)
+    mask = torch.ones(s, s, dtype=torch.bool).triu(1)
+    o = torch.softmax(((qr @ kr.transpose(-1, -2)) / 8.0).masked_fill(mask, float("-inf")), -1) @ vr
+    o.backward(dout.float().cpu())
+    for name, got in (("HIP backward", g1), ("torch backward", g3)):
+        err = _rel(got.cpu(), xr.grad)
+        print(f"[attention] rotary + attention node, {name}: dqkv rel {err:.2e}", flush=True)
+        assert err < 1e-2, name

@@ -51,6 +51,26 @@ def test_rope_qkv_matches_torch(b, s, hq, hkv, d):
     assert _rel(x.grad.cpu(), xr.grad) < 1e-2
 
 
+@pytest.mark.parametrize("b,s,hq,hkv,d", [(2, 48, 8, 2, 64), (1, 33, 4, 4, 32)])
+def test_rope_qkv_unrepeated_kv_matches_repeated(b, s, hq, hkv, d):
+    """kv_heads_out = Hkv writes each K/V head once: bit for bit every copy
+    of it in the repeated output, with q unchanged."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    from voodoo_quant import _hip
+
+    g = torch.Generator().manual_seed(s + hq)
+    qkv = torch.randn(b * s, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).cuda()
+    cos, sin = st._rope_tables_f32(s, d, 1.0e6, "cuda")
+    q1, k1, v1 = _hip.rope_qkv_fwd(qkv, b, s, hq, hkv, d, cos, sin)
+    q2, k2, v2 = _hip.rope_qkv_fwd(qkv, b, s, hq, hkv, d, cos, sin, repeat_kv=False)
+    rep = hq // hkv
+    assert k2.shape == (b * s, hkv, d) and v2.shape == (b * s, hkv, d)
+    assert torch.equal(q1, q2)
+    for full, one in ((k1, k2), (v1, v2)):
+        assert torch.equal(full.view(b * s, hkv, rep, d), one.unsqueeze(2).expand(b * s, hkv, rep, d))
+
+
 @pytest.mark.parametrize("t,f", [(100, 64), (4096, 3072)])
 def test_swiglu_matches_torch(t, f):
     if not torch.cuda.is_available():

@@ -355,13 +355,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16_t* __restri
                                                           const bf16_t* __restrict__ v, const bf16_t* __restrict__ o,
                                                           const bf16_t* __restrict__ dout,
                                                           const float* __restrict__ lse, float* __restrict__ stats,
-                                                          bf16_t* __restrict__ dq, int S, int S_pad, int H, int BH,
-                                                          int nqt, AttnStrides st, float c2, float scale) {
+                                                          bf16_t* __restrict__ dq, int S, int S_pad, int H, int Hk,
+                                                          int BH, int nqt, AttnStrides st, float c2, float scale) {
     __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * kMatBytes];  // K tile, V tile
     const int bid = blockIdx.x;
     const int qt = nqt - 1 - bid / BH;  // heaviest query tiles first
     const int bh = bid - (bid / BH) * BH;
     const int b = bh / H, h = bh - (bh / H) * H;
+    const int hk = h / (H / Hk);  // the K/V head the query head reads
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, col = lane & 31;
@@ -395,8 +396,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const bf16_t* __restri
     for (int r = 0; r < 16; ++r) negd[r] = -dsum;
 
     // K and V tiles by direct-to-LDS loads (the forward's slot mapping)
-    const bf16_t* kb0 = k + (int64_t)b * st.k[0] + (int64_t)h * st.k[2];
-    const bf16_t* vb0 = v + (int64_t)b * st.v[0] + (int64_t)h * st.v[2];
+    const bf16_t* kb0 = k + (int64_t)b * st.k[0] + (int64_t)hk * st.k[2];
+    const bf16_t* vb0 = v + (int64_t)b * st.v[0] + (int64_t)hk * st.v[2];
     uint32_t voff[4];
     int vrow[4];
 #pragma unroll
@@ -484,8 +485,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
                                                             const bf16_t* __restrict__ v,
                                                             const bf16_t* __restrict__ dout,
                                                             const float* __restrict__ stats, bf16_t* __restrict__ dk,
-                                                            bf16_t* __restrict__ dv, int S, int S_pad, int H, int BH,
-                                                            AttnStrides st, float c2, float scale) {
+                                                            bf16_t* __restrict__ dv, int S, int S_pad, int H, int Hk,
+                                                            int BH, AttnStrides st, float c2, float scale) {
     // a stage: Q tile and dO tile of 128 queries (16 KiB each), then lse log2 e
     // [128] and -D [128] of those queries
     constexpr int kQBytes = 128 * kRowBytes;
@@ -495,6 +496,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
     const int kt_idx = bid / BH;  // key block 0 sees the most queries: first
     const int bh = bid - kt_idx * BH;
     const int b = bh / H, h = bh - (bh / H) * H;
+    const int hk = h / (H / Hk);  // the K/V head the query head reads
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, col = lane & 31;
@@ -505,8 +507,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const bf16_t* __rest
 
     // K^T and V^T as B operands (lane: row kc, elements 16 c + 8 g ..)
     bf16x8_t kf[4], vf[4];
-    row_frags(k + (int64_t)b * st.k[0] + (int64_t)kc * st.k[1] + (int64_t)h * st.k[2], g, kf);
-    row_frags(v + (int64_t)b * st.v[0] + (int64_t)kc * st.v[1] + (int64_t)h * st.v[2], g, vf);
+    row_frags(k + (int64_t)b * st.k[0] + (int64_t)kc * st.k[1] + (int64_t)hk * st.k[2], g, kf);
+    row_frags(v + (int64_t)b * st.v[0] + (int64_t)kc * st.v[1] + (int64_t)hk * st.v[2], g, vf);
 
     // Q and dO tiles by direct-to-LDS loads: lane l of wave w's instruction i
     // (0-7) writes stage slot s = 64 (4 i + w) + l (slots 0-1023 Q, 1024-2047
@@ -647,7 +649,7 @@ int64_t attention_bwd_workspace(int B, int S, int H) {
 
 hipError_t launch_attention_bwd(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
                                 const bf16_t* dout, const float* lse, bf16_t* dq, bf16_t* dk, bf16_t* dv, int B,
-                                int S, int H, const int64_t* strides, float scale, float* stats, hipStream_t s) {
+                                int S, int H, int Hk, const int64_t* strides, float scale, float* stats, hipStream_t s) {
     const int BH = B * H;
     if (BH == 0 || S == 0) return hipSuccess;
     AttnStrides st;
@@ -664,13 +666,13 @@ hipError_t launch_attention_bwd(const bf16_t* q, const bf16_t* k, const bf16_t* 
     const int S_pad = (S + 127) / 128 * 128;  // the key-side kernel's query tiles
     const int nqt = (S + kQTile - 1) / kQTile;
     const float c2 = scale * kLog2e;
-    attn_bwd_dq_kernel<<<dim3((unsigned)(BH * nqt)), 256, 0, s>>>(q, k, v, o, dout, lse, stats, dq, S, S_pad, H, BH,
-                                                                 nqt, st, c2, scale);
+    attn_bwd_dq_kernel<<<dim3((unsigned)(BH * nqt)), 256, 0, s>>>(q, k, v, o, dout, lse, stats, dq, S, S_pad, H, Hk,
+                                                                 BH, nqt, st, c2, scale);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int nkt = (S + 127) / 128;
-    attn_bwd_dkdv_kernel<<<dim3((unsigned)(BH * nkt)), 256, 0, s>>>(q, k, v, dout, stats, dk, dv, S, S_pad, H, BH, st,
-                                                                   c2, scale);
+    attn_bwd_dkdv_kernel<<<dim3((unsigned)(BH * nkt)), 256, 0, s>>>(q, k, v, dout, stats, dk, dv, S, S_pad, H, Hk,
+                                                                   BH, st, c2, scale);
     return hipGetLastError();
 }
 

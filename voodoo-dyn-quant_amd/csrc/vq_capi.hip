@@ -459,16 +459,18 @@ int check_rope(int64_t B, int64_t S, int Hq, int Hkv, int D, const void* cosb, c
 }
 }  // namespace
 
-int vq_rope_qkv_fwd(const uint16_t* qkv, int64_t B, int64_t S, int Hq, int Hkv, int D, const float* cosb,
-                    const float* sinb, uint16_t* q, uint16_t* k, uint16_t* v, void* stream) {
+int vq_rope_qkv_fwd(const uint16_t* qkv, int64_t B, int64_t S, int Hq, int Hkv, int kv_heads_out, int D,
+                    const float* cosb, const float* sinb, uint16_t* q, uint16_t* k, uint16_t* v, void* stream) {
     int rc = check_rope(B, S, Hq, Hkv, D, cosb, sinb);
     if (rc != VQ_OK) return rc;
+    if (kv_heads_out != Hq && kv_heads_out != Hkv)
+        return fail(VQ_ERR_SHAPE, "kv_heads_out=%d: Hq (%d, heads repeated) or Hkv (%d)", kv_heads_out, Hq, Hkv);
     if (B == 0) return ok();
     if (!qkv || !q || !k || !v) return fail(VQ_ERR_NULL, "qkv/q/k/v is NULL");
     if (!aligned16(qkv) || !aligned16(q) || !aligned16(k) || !aligned16(v))
         return fail(VQ_ERR_ALIGN, "qkv/q/k/v not 16-byte aligned");
-    rc = hip_check(vq::launch_rope_qkv_fwd(reinterpret_cast<const vq::bf16_t*>(qkv), B * S, (int)S, Hq, Hkv, D, cosb,
-                                           sinb, reinterpret_cast<vq::bf16_t*>(q), reinterpret_cast<vq::bf16_t*>(k),
+    rc = hip_check(vq::launch_rope_qkv_fwd(reinterpret_cast<const vq::bf16_t*>(qkv), B * S, (int)S, Hq, Hkv,
+                                           kv_heads_out, D, cosb, sinb, reinterpret_cast<vq::bf16_t*>(q), reinterpret_cast<vq::bf16_t*>(k),
                                            reinterpret_cast<vq::bf16_t*>(v), static_cast<hipStream_t>(stream)),
                    "rope launch");
     return rc == VQ_OK ? ok() : rc;
@@ -595,9 +597,10 @@ int64_t vq_attention_bwd_workspace(int64_t B, int64_t S, int Hq) {
 }
 
 int vq_attention_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* o, const uint16_t* dout,
-                     const float* lse, uint16_t* dq, uint16_t* dk, uint16_t* dv, int64_t B, int64_t S, int Hq, int D,
-                     const int64_t* strides, float scale, void* workspace, int64_t ws_bytes, void* stream) {
-    if (B < 0 || S < 0 || S > INT32_MAX / 2 || Hq <= 0) return fail(VQ_ERR_SHAPE, "B=%lld S=%lld Hq=%d", (long long)B, (long long)S, Hq);
+                     const float* lse, uint16_t* dq, uint16_t* dk, uint16_t* dv, int64_t B, int64_t S, int Hq, int Hk,
+                     int D, const int64_t* strides, float scale, void* workspace, int64_t ws_bytes, void* stream) {
+    if (B < 0 || S < 0 || S > INT32_MAX / 2 || Hq <= 0 || Hk <= 0 || Hq % Hk)
+        return fail(VQ_ERR_SHAPE, "B=%lld S=%lld Hq=%d Hk=%d", (long long)B, (long long)S, Hq, Hk);
     if (D != 64) return fail(VQ_ERR_SHAPE, "head dim %d: only 64 is supported", D);
     if (B * Hq * ((S + 127) / 128) > INT32_MAX)
         return fail(VQ_ERR_SHAPE, "B=%lld Hq=%d S=%lld: too many tiles", (long long)B, Hq, (long long)S);
@@ -624,7 +627,7 @@ int vq_attention_bwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
                                                 reinterpret_cast<const vq::bf16_t*>(o),
                                                 reinterpret_cast<const vq::bf16_t*>(dout), lse,
                                                 reinterpret_cast<vq::bf16_t*>(dq), reinterpret_cast<vq::bf16_t*>(dk),
-                                                reinterpret_cast<vq::bf16_t*>(dv), (int)B, (int)S, Hq, strides, scale,
+                                                reinterpret_cast<vq::bf16_t*>(dv), (int)B, (int)S, Hq, Hk, strides, scale,
                                                 static_cast<float*>(workspace), static_cast<hipStream_t>(stream)),
                        "attention backward launch");
     return rc == VQ_OK ? ok() : rc;

@@ -53,7 +53,8 @@ __device__ __forceinline__ void ld8f(const float* p, float (&v)[8]) {
 // One thread: 8 weights of the first half of one head and the matching 8 of
 // the second half, for one token.  Items per token: (Hq + 2 Hkv) * D / 16.
 __global__ __launch_bounds__(256) void rope_qkv_fwd_kernel(const bf16_t* __restrict__ qkv, int64_t tokens, int S,
-                                                           int Hq, int Hkv, int D, const float* __restrict__ cosb,
+                                                           int Hq, int Hkv, int kv_out, int D,
+                                                           const float* __restrict__ cosb,
                                                            const float* __restrict__ sinb, bf16_t* __restrict__ q,
                                                            bf16_t* __restrict__ k, bf16_t* __restrict__ v) {
     const int per_head = D / 16;
@@ -69,11 +70,11 @@ __global__ __launch_bounds__(256) void rope_qkv_fwd_kernel(const bf16_t* __restr
     float x1[8], x2[8];
     ld8(src + d0, x1);
     ld8(src + half + d0, x2);
-    const int rep = Hq / Hkv;
-    if (hh >= Hq + Hkv) {  // v: copied into its rep query-head slots
+    const int rep = kv_out / Hkv;  // copies of each K/V head: Hq / Hkv, or 1
+    if (hh >= Hq + Hkv) {  // v: copied into its rep output head slots
         const int kv = hh - Hq - Hkv;
         for (int r = 0; r < rep; ++r) {
-            bf16_t* dst = v + (m * Hq + (int64_t)kv * rep + r) * D;
+            bf16_t* dst = v + (m * kv_out + (int64_t)kv * rep + r) * D;
             st8(dst + d0, x1);
             st8(dst + half + d0, x2);
         }
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(256) void rope_qkv_fwd_kernel(const bf16_t* __restr
     } else {
         const int kv = hh - Hq;
         for (int r = 0; r < rep; ++r) {
-            bf16_t* dst = k + (m * Hq + (int64_t)kv * rep + r) * D;
+            bf16_t* dst = k + (m * kv_out + (int64_t)kv * rep + r) * D;
             st8(dst + d0, y1);
             st8(dst + half + d0, y2);
         }
@@ -305,11 +306,11 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const bf16_t* __restric
 
 static unsigned blocks_for(int64_t items) { return (unsigned)((items + 255) / 256); }
 
-hipError_t launch_rope_qkv_fwd(const bf16_t* qkv, int64_t tokens, int S, int Hq, int Hkv, int D, const float* cosb,
-                               const float* sinb, bf16_t* q, bf16_t* k, bf16_t* v, hipStream_t s) {
+hipError_t launch_rope_qkv_fwd(const bf16_t* qkv, int64_t tokens, int S, int Hq, int Hkv, int kv_out, int D,
+                               const float* cosb, const float* sinb, bf16_t* q, bf16_t* k, bf16_t* v, hipStream_t s) {
     const int64_t items = tokens * (Hq + 2 * Hkv) * (D / 16);
     if (items == 0) return hipSuccess;
-    rope_qkv_fwd_kernel<<<blocks_for(items), 256, 0, s>>>(qkv, tokens, S, Hq, Hkv, D, cosb, sinb, q, k, v);
+    rope_qkv_fwd_kernel<<<blocks_for(items), 256, 0, s>>>(qkv, tokens, S, Hq, Hkv, kv_out, D, cosb, sinb, q, k, v);
     return hipGetLastError();
 }
 

@@ -115,8 +115,8 @@ hipError_t launch_embed_rows_bwd(const CandSet& cs, const int64_t* ids, int64_t 
                                  const void* grad, bool grad_f32, float* partials, float* dprobs, hipStream_t s);
 
 // Decoder glue (vq_decoder.hip).
-hipError_t launch_rope_qkv_fwd(const bf16_t* qkv, int64_t tokens, int S, int Hq, int Hkv, int D, const float* cosb,
-                               const float* sinb, bf16_t* q, bf16_t* k, bf16_t* v, hipStream_t s);
+hipError_t launch_rope_qkv_fwd(const bf16_t* qkv, int64_t tokens, int S, int Hq, int Hkv, int kv_out, int D,
+                               const float* cosb, const float* sinb, bf16_t* q, bf16_t* k, bf16_t* v, hipStream_t s);
 hipError_t launch_rope_qkv_bwd(const bf16_t* dq, const bf16_t* dk, const bf16_t* dv, int64_t sb, int64_t sh,
                                int64_t ss, int64_t tokens, int S, int Hq, int Hkv, int D, const float* cosb,
                                const float* sinb, bf16_t* dqkv, hipStream_t s);
@@ -136,11 +136,14 @@ hipError_t launch_attention_fwd(const bf16_t* q, const bf16_t* k, const bf16_t* 
 
 // Its backward: dq, dk, dv (softmax scale `scale`) from dout, the forward's
 // o and lse; strides: 8 x {batch, position, head} for q, k, v, o, dout, dq,
-// dk, dv; Hk == H.  stats: attention_bwd_workspace(B, S, H) bytes.
+// dk, dv; q, o, dout, dq, dk, dv have H heads, k and v Hk (kv head of query
+// head h is h / (H / Hk)); dk and dv are per query head, unsummed.  stats:
+// attention_bwd_workspace(B, S, H) bytes.
 int64_t attention_bwd_workspace(int B, int S, int H);
 hipError_t launch_attention_bwd(const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
                                 const bf16_t* dout, const float* lse, bf16_t* dq, bf16_t* dk, bf16_t* dv, int B,
-                                int S, int H, const int64_t* strides, float scale, float* stats, hipStream_t s);
+                                int S, int H, int Hk, const int64_t* strides, float scale, float* stats,
+                                hipStream_t s);
 
 // Distillation loss over full logits (vq_loss.hip).  ws: 5 * rows + 2 floats
 // (per-row log-sum-exps and losses, then 1/N_ce and 1/N), written by the

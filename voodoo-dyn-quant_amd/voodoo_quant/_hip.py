@@ -40,7 +40,7 @@ _SIGNATURES = [
     ("vq_gated_linear_group_bwd", _i, [_p, _p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     ("vq_gated_linear_group_bwd_gate_stream", _i,
      [_p, _p, _i64, _i64, _i64, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p]),
-    ("vq_rope_qkv_fwd", _i, [_p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p]),
+    ("vq_rope_qkv_fwd", _i, [_p, _i64, _i64, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p]),
     ("vq_rope_qkv_bwd", _i, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _i, _i, _p, _p, _p, _p]),
     ("vq_swiglu_fwd", _i, [_p, _i64, _i64, _p, _p]),
     ("vq_swiglu_bwd", _i, [_p, _p, _i64, _i64, _p, _p]),
@@ -48,8 +48,8 @@ _SIGNATURES = [
     ("vq_rmsnorm_bwd", _i, [_p, _p, _p, _p, _p, _i64, _i64, _p, _p]),
     ("vq_attention_fwd", _i, [_p, _p, _p, _p, _p, _i64, _i64, _i, _i, _i, _p, _p, _p, _p, ctypes.c_float, _p]),
     ("vq_attention_bwd_workspace", _i64, [_i64, _i64, _i]),
-    ("vq_attention_bwd", _i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i, _i, _p, ctypes.c_float, _p, _i64,
-                              _p]),
+    ("vq_attention_bwd", _i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i, _i, _i, _p, ctypes.c_float, _p,
+                              _i64, _p]),
     ("vq_distill_loss_workspace", _i64, [_i64]),
     ("vq_distill_loss_fwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _i64, _p]),
     ("vq_distill_loss_bwd", _i, [_p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _i64, _p]),
@@ -334,12 +334,18 @@ def mix_only_call(members, probs, d_pad: int, w_eff: torch.Tensor, stream: int):
     return call
 
 
-def rope_qkv_fwd(qkv: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, D: int, cos: torch.Tensor, sin: torch.Tensor):
-    """(q, k, v), each bf16 [B*S, Hq, D], from the stacked projection output."""
+def rope_qkv_fwd(qkv: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, D: int, cos: torch.Tensor, sin: torch.Tensor,
+                 repeat_kv: bool = True):
+    """(q, k, v) from the stacked projection output: q bf16 [B*S, Hq, D],
+    k and v [B*S, Hq, D] with each K/V head repeated (repeat_kv) or
+    [B*S, Hkv, D]."""
     dev = qkv.device
-    q, k, v = (torch.empty(B * S, Hq, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
-    _check(lib().vq_rope_qkv_fwd(_dev_ptr(qkv, "qkv"), B, S, Hq, Hkv, D, _dev_ptr(cos, "cos"), _dev_ptr(sin, "sin"),
-                                 _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"), _stream(dev)),
+    kv_out = Hq if repeat_kv else Hkv
+    q = torch.empty(B * S, Hq, D, dtype=torch.bfloat16, device=dev)
+    k, v = (torch.empty(B * S, kv_out, D, dtype=torch.bfloat16, device=dev) for _ in range(2))
+    _check(lib().vq_rope_qkv_fwd(_dev_ptr(qkv, "qkv"), B, S, Hq, Hkv, kv_out, D, _dev_ptr(cos, "cos"),
+                                 _dev_ptr(sin, "sin"), _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"),
+                                 _stream(dev)),
            "vq_rope_qkv_fwd")
     return q, k, v
 
@@ -398,11 +404,16 @@ def attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: floa
 
 def attention_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
                   lse: torch.Tensor, scale: float | None = None):
-    """Backward of :func:`attention_fwd` with Hq == Hk: (dq, dk, dv), each
-    bf16 [B, H, S, 64] over [B, S, H, 64] memory."""
+    """Backward of :func:`attention_fwd`: (dq, dk, dv), each bf16 [B, Hq, S, 64]
+    over [B, S, Hq, 64] memory.  k and v may have Hk heads (Hq % Hk == 0):
+    dk and dv are per query head either way, the gradients of K and V with
+    each head repeated Hq/Hk times (K/V head j's gradient is the sum over
+    query heads j*Hq/Hk .. (j+1)*Hq/Hk - 1)."""
     B, H, S, D = q.shape
-    if k.shape != q.shape or v.shape != q.shape or out.shape != q.shape or dout.shape != q.shape:
-        raise ValueError("attention_bwd needs q, k, v, out and dout of one shape (Hq == Hk)")
+    Hk = k.shape[1]
+    if (k.shape != (B, Hk, S, D) or v.shape != k.shape or out.shape != q.shape or dout.shape != q.shape
+            or H % Hk):
+        raise ValueError("attention_bwd needs q, out, dout [B, Hq, S, D] and k, v [B, Hk, S, D] with Hq % Hk == 0")
     if lse.shape != (B, H, S) or lse.dtype != torch.float32 or not lse.is_contiguous():
         raise ValueError("lse must be contiguous fp32 [B, H, S]")
     ts, strides = [], []
@@ -418,7 +429,7 @@ def attention_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(D)
     _check(lib().vq_attention_bwd(*(t.data_ptr() for t in ts), lse.data_ptr(), *(g.data_ptr() for g in grads), B, S,
-                                  H, D, (ctypes.c_int64 * 24)(*strides), sc, ws.data_ptr(), ws.numel(),
+                                  H, Hk, D, (ctypes.c_int64 * 24)(*strides), sc, ws.data_ptr(), ws.numel(),
                                   _stream(dev)),
            "vq_attention_bwd")
     return tuple(grads)

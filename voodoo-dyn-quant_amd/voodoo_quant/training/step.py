@@ -17,8 +17,10 @@ SwiGLU MLP, tied embeddings):
 
 Only the gates train, so the backward runs dX through every layer and the
 gate gradients of every gated tensor; no weight gradient is formed.  Causal
-attention at head dim 64 runs ``vq_attention_fwd`` / ``vq_attention_bwd``;
-other head dims use torch's fused
+attention at head dim 64 runs ``vq_attention_fwd`` / ``vq_attention_bwd``,
+fused with the rotary embedding into one autograd node that keeps K/V at
+their own heads (the kernels read K/V head h / (Hq/Hkv)); other head dims use
+torch's fused
 scaled-dot-product kernels (flash or memory-efficient), and without one of
 them the math path in fp32.
 """
@@ -82,6 +84,9 @@ HIP_ATTENTION = True
 # False: the backward is torch's memory-efficient attention backward over the
 # HIP forward's output and log-sum-exp (the kernel SDPA's own backward runs)
 HIP_ATTENTION_BWD = True
+# rotary embedding and HIP attention as one autograd node with K/V at their
+# own heads (False: the rotary kernel writes each K/V head once per query head)
+ROPE_ATTENTION = True
 
 
 class _CausalAttention(torch.autograd.Function):
@@ -101,11 +106,17 @@ class _CausalAttention(torch.autograd.Function):
         q, k, v, out, lse = ctx.saved_tensors
         if HIP_ATTENTION_BWD:
             return _hip.attention_bwd(dout, q, k, v, out, lse)
-        zero = torch.zeros((), dtype=torch.int64)  # philox seed/offset: unused without dropout
-        dq, dk, dv, _ = torch.ops.aten._scaled_dot_product_efficient_attention_backward(
-            dout, q, k, v, None, out, lse, zero, zero, 0.0, [True, True, True, False], True,
-            scale=1.0 / math.sqrt(q.shape[-1]))
-        return dq, dk, dv
+        return _torch_attention_bwd(dout, q, k, v, out, lse)
+
+
+def _torch_attention_bwd(dout, q, k, v, out, lse):
+    """torch's memory-efficient attention backward (Hq == Hk) over the HIP
+    forward's output and log-sum-exp."""
+    zero = torch.zeros((), dtype=torch.int64)  # philox seed/offset: unused without dropout
+    dq, dk, dv, _ = torch.ops.aten._scaled_dot_product_efficient_attention_backward(
+        dout, q, k, v, None, out, lse, zero, zero, 0.0, [True, True, True, False], True,
+        scale=1.0 / math.sqrt(q.shape[-1]))
+    return dq, dk, dv
 
 
 def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
@@ -191,6 +202,55 @@ class _RopeQKV(torch.autograd.Function):
         return _hip.rope_qkv_bwd(*grads, b, s_, hq, hkv, d, cos, sin), None, None, None
 
 
+class _RopeCausalAttention(torch.autograd.Function):
+    """Rotary embedding of the stacked q/k/v projection output and causal
+    attention over it as one autograd node, with K and V kept at their Hkv
+    heads: ``vq_rope_qkv_fwd`` writes them unrepeated, ``vq_attention_fwd`` /
+    ``_bwd`` read K/V head h / (Hq / Hkv) for query head h, and the backward's
+    per-query-head dK/dV go straight into ``vq_rope_qkv_bwd``, which sums each
+    group.  Bitwise the same as :class:`_RopeQKV` (heads repeated) followed by
+    :class:`_CausalAttention`, without writing the repeated heads."""
+
+    @staticmethod
+    def forward(ctx, qkv, cos, sin, shape):
+        b, s_, hq, hkv, d = shape
+        q, k, v = _hip.rope_qkv_fwd(qkv.contiguous(), b, s_, hq, hkv, d, cos, sin, repeat_kv=False)
+        q = q.view(b, s_, hq, d).transpose(1, 2)
+        k = k.view(b, s_, hkv, d).transpose(1, 2)
+        v = v.view(b, s_, hkv, d).transpose(1, 2)
+        out, lse = _hip.attention_fwd(q, k, v, need_lse=True)
+        ctx.save_for_backward(q, k, v, out, lse, cos, sin)
+        ctx.shape = shape
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, cos, sin = ctx.saved_tensors
+        b, s_, hq, hkv, d = ctx.shape
+        dout = dout.to(torch.bfloat16)
+        if HIP_ATTENTION_BWD:
+            dq, dk, dv = _hip.attention_bwd(dout, q, k, v, out, lse)
+        else:  # torch's backward reads one K/V head per query head
+            rep = hq // hkv
+            grads = _torch_attention_bwd(dout, q, k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1),
+                                         out, lse)
+            # the rotary backward reads the three with one set of strides
+            dq, dk, dv = (g.transpose(1, 2).contiguous().transpose(1, 2) for g in grads)
+        return _hip.rope_qkv_bwd(dq, dk, dv, b, s_, hq, hkv, d, cos, sin), None, None, None
+
+
+def _rope_attention(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, shape: tuple) -> torch.Tensor:
+    """Causal attention [B, Hq, S, D] over the rotary-embedded stacked
+    projection output qkv [B*S, (Hq + 2 Hkv) D] (HIP kernels, head dim 64),
+    K/V at their Hkv heads; without a backward the log-sum-exp is not kept."""
+    if torch.is_grad_enabled() and qkv.requires_grad:
+        return _RopeCausalAttention.apply(qkv, cos, sin, shape)
+    b, s_, hq, hkv, d = shape
+    q, k, v = _hip.rope_qkv_fwd(qkv.contiguous(), b, s_, hq, hkv, d, cos, sin, repeat_kv=False)
+    return _hip.attention_fwd(q.view(b, s_, hq, d).transpose(1, 2), k.view(b, s_, hkv, d).transpose(1, 2),
+                              v.view(b, s_, hkv, d).transpose(1, 2), need_lse=False)[0]
+
+
 class _SwiGLU(torch.autograd.Function):
     """silu(gate) * up from the stacked gate/up output [tokens, 2F] (``vq_swiglu_fwd/bwd``)."""
 
@@ -273,7 +333,11 @@ class _Attention(nn.Module):
         qkv = _project_stacked(x, [self.q_proj, self.k_proj, self.v_proj])
         if qkv is not None and c.head_dim % 16 == 0:
             cos32, sin32 = _rope_tables_f32(s, c.head_dim, c.rope_theta, x.device)
-            q, k, v = _RopeQKV.apply(qkv.reshape(b * s, -1), cos32, sin32, (b, s, c.heads, c.kv_heads, c.head_dim))
+            shape = (b, s, c.heads, c.kv_heads, c.head_dim)
+            if HIP_ATTENTION and ROPE_ATTENTION and qkv.dtype == torch.bfloat16 and c.head_dim == 64:
+                a = _rope_attention(qkv.reshape(b * s, -1), cos32, sin32, shape)
+                return self.o_proj(a.transpose(1, 2).reshape(b, s, c.heads * c.head_dim))
+            q, k, v = _RopeQKV.apply(qkv.reshape(b * s, -1), cos32, sin32, shape)
         else:
             q, k, v = _project(x, [self.q_proj, self.k_proj, self.v_proj])
             q = q.view(b, s, c.heads, c.head_dim).transpose(1, 2)
