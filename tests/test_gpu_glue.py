@@ -88,7 +88,8 @@ def test_swiglu_matches_torch(t, f):
     assert _rel(x.grad.cpu(), xr.grad) < 1e-2
 
 
-@pytest.mark.parametrize("rows,dim,with_add", [(300, 1024, True), (7, 4096, True), (65, 1032, False), (1, 8, True)])
+@pytest.mark.parametrize("rows,dim,with_add", [(300, 1024, True), (7, 4096, True), (65, 1032, False), (1, 8, True),
+                                                (33, 2048, True)])
 def test_add_rmsnorm_matches_torch(rows, dim, with_add):
     if not torch.cuda.is_available():
         pytest.skip("no ROCm device")

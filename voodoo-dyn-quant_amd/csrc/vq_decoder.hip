@@ -183,6 +183,10 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// NIT > 0 (dim <= 512 NIT): each lane keeps its 8 NIT values in registers
+// between the reduction and the second sweep, so a row is read once; NIT = 0:
+// two sweeps over any dim.  Same arithmetic in the same order either way.
+template <int NIT>
 __global__ __launch_bounds__(64 * kNormWaves) void add_rmsnorm_fwd_kernel(
     const bf16_t* __restrict__ h, const bf16_t* __restrict__ a, const bf16_t* __restrict__ w, int64_t rows, int dim,
     float eps, bf16_t* __restrict__ s_out, bf16_t* __restrict__ n_out, float* __restrict__ rstd_out) {
@@ -190,6 +194,40 @@ __global__ __launch_bounds__(64 * kNormWaves) void add_rmsnorm_fwd_kernel(
     const int64_t r = (int64_t)blockIdx.x * kNormWaves + (threadIdx.x >> 6);
     if (r >= rows) return;
     const int64_t base = r * dim;
+    if constexpr (NIT > 0) {
+        float x[NIT][8];
+        float ss = 0.0f;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int c = 8 * lane + 512 * it;
+            if (c < dim) {
+                ld8(h + base + c, x[it]);
+                if (a) {
+                    float y[8];
+                    ld8(a + base + c, y);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) x[it][j] = bf16_round(x[it][j] + y[j]);
+                    if (s_out) st8(s_out + base + c, x[it]);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ss += x[it][j] * x[it][j];
+            }
+        }
+        const float rstd = rsqrtf(wave_sum(ss) / (float)dim + eps);
+        if (rstd_out && lane == 0) rstd_out[r] = rstd;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int c = 8 * lane + 512 * it;
+            if (c < dim) {
+                float wv[8];
+                ld8(w + c, wv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[it][j] = x[it][j] * rstd * wv[j];
+                st8(n_out + base + c, x[it]);
+            }
+        }
+        return;
+    }
     float ss = 0.0f;
     for (int c = 8 * lane; c < dim; c += 512) {
         float x[8];
@@ -226,6 +264,9 @@ __global__ __launch_bounds__(64 * kNormWaves) void add_rmsnorm_fwd_kernel(
     }
 }
 
+// NIT as in add_rmsnorm_fwd_kernel: dn and s stay in registers between the
+// dot product and the second sweep.
+template <int NIT>
 __global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_kernel(
     const bf16_t* __restrict__ dn, const bf16_t* __restrict__ ds, const bf16_t* __restrict__ s,
     const bf16_t* __restrict__ w, const float* __restrict__ rstd_in, int64_t rows, int dim, bf16_t* __restrict__ dh) {
@@ -234,6 +275,41 @@ __global__ __launch_bounds__(64 * kNormWaves) void rmsnorm_bwd_kernel(
     if (r >= rows) return;
     const int64_t base = r * dim;
     const float rstd = rstd_in[r];
+    if constexpr (NIT > 0) {
+        float g[NIT][8], x[NIT][8];
+        float dot = 0.0f;  // sum dn w s
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int c = 8 * lane + 512 * it;
+            if (c < dim) {
+                float wv[8];
+                ld8(dn + base + c, g[it]);
+                ld8(s + base + c, x[it]);
+                ld8(w + c, wv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dot += g[it][j] * wv[j] * x[it][j];
+            }
+        }
+        const float k = wave_sum(dot) * rstd * rstd / (float)dim;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int c = 8 * lane + 512 * it;
+            if (c < dim) {
+                float wv[8], o[8];
+                ld8(w + c, wv);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = rstd * (g[it][j] * wv[j] - x[it][j] * k);
+                if (ds) {
+                    float d[8];
+                    ld8(ds + base + c, d);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] += d[j];
+                }
+                st8(dh + base + c, o);
+            }
+        }
+        return;
+    }
     float dot = 0.0f;  // sum dn w s
     for (int c = 8 * lane; c < dim; c += 512) {
         float g[8], x[8], wv[8];
@@ -328,7 +404,13 @@ hipError_t launch_add_rmsnorm_fwd(const bf16_t* h, const bf16_t* a, const bf16_t
                                  bf16_t* s_out, bf16_t* n_out, float* rstd_out, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     const dim3 grid((unsigned)((rows + kNormWaves - 1) / kNormWaves));
-    add_rmsnorm_fwd_kernel<<<grid, 64 * kNormWaves, 0, s>>>(h, a, w, rows, dim, eps, s_out, n_out, rstd_out);
+    switch ((dim + 511) / 512) {  // row sweeps of 512 per wave: kept in registers up to 4
+        case 1: add_rmsnorm_fwd_kernel<1><<<grid, 64 * kNormWaves, 0, s>>>(h, a, w, rows, dim, eps, s_out, n_out, rstd_out); break;
+        case 2: add_rmsnorm_fwd_kernel<2><<<grid, 64 * kNormWaves, 0, s>>>(h, a, w, rows, dim, eps, s_out, n_out, rstd_out); break;
+        case 3: add_rmsnorm_fwd_kernel<3><<<grid, 64 * kNormWaves, 0, s>>>(h, a, w, rows, dim, eps, s_out, n_out, rstd_out); break;
+        case 4: add_rmsnorm_fwd_kernel<4><<<grid, 64 * kNormWaves, 0, s>>>(h, a, w, rows, dim, eps, s_out, n_out, rstd_out); break;
+        default: add_rmsnorm_fwd_kernel<0><<<grid, 64 * kNormWaves, 0, s>>>(h, a, w, rows, dim, eps, s_out, n_out, rstd_out);
+    }
     return hipGetLastError();
 }
 
@@ -336,7 +418,13 @@ hipError_t launch_rmsnorm_bwd(const bf16_t* dn, const bf16_t* ds, const bf16_t* 
                               int64_t rows, int dim, bf16_t* dh, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     const dim3 grid((unsigned)((rows + kNormWaves - 1) / kNormWaves));
-    rmsnorm_bwd_kernel<<<grid, 64 * kNormWaves, 0, s>>>(dn, ds, x, w, rstd, rows, dim, dh);
+    switch ((dim + 511) / 512) {
+        case 1: rmsnorm_bwd_kernel<1><<<grid, 64 * kNormWaves, 0, s>>>(dn, ds, x, w, rstd, rows, dim, dh); break;
+        case 2: rmsnorm_bwd_kernel<2><<<grid, 64 * kNormWaves, 0, s>>>(dn, ds, x, w, rstd, rows, dim, dh); break;
+        case 3: rmsnorm_bwd_kernel<3><<<grid, 64 * kNormWaves, 0, s>>>(dn, ds, x, w, rstd, rows, dim, dh); break;
+        case 4: rmsnorm_bwd_kernel<4><<<grid, 64 * kNormWaves, 0, s>>>(dn, ds, x, w, rstd, rows, dim, dh); break;
+        default: rmsnorm_bwd_kernel<0><<<grid, 64 * kNormWaves, 0, s>>>(dn, ds, x, w, rstd, rows, dim, dh);
+    }
     return hipGetLastError();
 }
 
