@@ -209,3 +209,16 @@ def test_rope_qkv_fwd_argument_checks():
     assert lib.vq_rope_qkv_fwd(p, 1, 8, 16, 4, 16, 64, None, p, p, p, p, None) == _hip.VQ_ERR_NULL
     # nothing to do at B = 0: no pointer is needed
     assert lib.vq_rope_qkv_fwd(None, 0, 8, 16, 4, 4, 64, p, p, None, None, None, None) == _hip.VQ_OK
+
+
+def test_attention_bwd_wrapper_head_checks():
+    """The Python wrapper refuses K/V head counts that do not divide the query
+    heads (zero included) with ValueError, before any device work."""
+    import torch
+
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.bfloat16)
+    lse = torch.zeros(1, 4, 8)
+    for hk in (0, 3):
+        kv = torch.zeros(1, hk, 8, 64, dtype=torch.bfloat16)
+        with pytest.raises(ValueError):
+            _hip.attention_bwd(q, q, kv, kv, q, lse)

@@ -412,7 +412,7 @@ def attention_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch
     B, H, S, D = q.shape
     Hk = k.shape[1]
     if (k.shape != (B, Hk, S, D) or v.shape != k.shape or out.shape != q.shape or dout.shape != q.shape
-            or H % Hk):
+            or Hk <= 0 or H % Hk):
         raise ValueError("attention_bwd needs q, out, dout [B, Hq, S, D] and k, v [B, Hk, S, D] with Hq % Hk == 0")
     if lse.shape != (B, H, S) or lse.dtype != torch.float32 or not lse.is_contiguous():
         raise ValueError("lse must be contiguous fp32 [B, H, S]")
