@@ -290,7 +290,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const bf16_t* __restrict_
 //     query tiles from the diagonal on: S = Q K^T, dP = dO V^T, P, dS,
 //     dV^T += dO^T P, dK^T += Q^T dS.
 // P and dS are rounded to bf16 for the products (as the forward's P); the
-// softmax scale is applied to dQ and dK once at the end.
+// softmax scale is applied to dQ and dK once at the end.  Grouped-query K/V:
+// query head h reads K/V head h / (H / Hk) in both kernels, and dK, dV are
+// written per query head (the gradients of the repeated heads; a caller sums
+// each group), so no workgroup walks several query heads.
 
 struct AttnStrides {
     int64_t q[3], k[3], v[3], o[3], d[3], dq[3], dk[3], dv[3];  // {batch, position, head}, elements
