@@ -27,6 +27,39 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_hip.EXPORTED), "ctypes binding and header disagree"
 
 
+def _declarations():
+    """{name: (return type, [parameter types])} of the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(r"\b((?:const\s+)?[a-z0-9_]+\s*\**)\s*\b(vq_[a-z0-9_]+)\s*\(([^)]*)\)\s*;",
+                                        text):
+        params = [q.strip() for q in params.split(",") if q.strip() and q.strip() != "void"]
+        types = [re.sub(r"\s*\b[A-Za-z_][A-Za-z0-9_]*(\s*\[\])?$", "", q) for q in params]
+        out[name] = (ret.replace(" ", ""), types)
+    return out
+
+
+def _ctype_of(c_type: str):
+    c = c_type.replace("const", "").replace(" ", "")
+    if "*" in c:
+        return ctypes.c_char_p if c == "char*" else ctypes.c_void_p
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float, "void": None}[c]
+
+
+def test_ctypes_signatures_match_the_header():
+    """Every ctypes signature the bindings set has the header's parameter
+    count, parameter types and return type (a pointer is c_void_p, except
+    the error string's char*)."""
+    decl = _declarations()
+    assert set(decl) == set(declared_functions())
+    for name, res, args in _hip._SIGNATURES:
+        ret, params = decl[name]
+        assert res is _ctype_of(ret), (name, ret)
+        assert len(args) == len(params), (name, len(args), params)
+        for i, (a, c_type) in enumerate(zip(args, params)):
+            assert a is _ctype_of(c_type), (name, i, c_type)
+
+
 def test_version_and_group_bytes():
     lib = _hip.lib()
     assert lib.vq_version() >= 100
