@@ -497,7 +497,9 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
     Linear and the embedding gated over 6 candidates; Q8_0 teacher), batch
     4 x 2048 uniform-random token ids: tokens per second of the whole step
     (forwards, CE + KL + size loss, backward, clip, AdamW).  The teacher's
-    forward runs on a second stream beside the student's."""
+    forward runs on a second stream beside the student's; the plain GEMMs
+    (teacher projections, heads) use the TunableOp results of
+    step.use_tuned_gemms."""
     from voodoo_quant.training import step as st
 
     cfg = st.DecoderConfig()
@@ -511,7 +513,7 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
     y = torch.randint(0, cfg.vocab, (b, s), device=dev, generator=g)
     tr = st.GateTrainer(student, teacher, replaced,
                         st.StepConfig(max_steps=max(steps + warmup, 2), prefetch_mix=prefetch,
-                                      teacher_stream=True, defer_gate_grads=defer),
+                                      teacher_stream=True, defer_gate_grads=defer, tuned_gemms=True),
                         total_8bit_bytes=float(cfg.gated_weights()))
     for _ in range(warmup):
         tr.step(x, y)
@@ -541,7 +543,7 @@ def train_step_bench(torch, dev, steps: int, warmup: int, prefetch: bool = False
     tokens = b * s
     fl = st.step_flops(cfg, tokens, s)
     rec = {"tokens_per_s": round(tokens / (ms * 1e-3), 1), "ms_per_step": round(ms, 3),
-           "ms_per_step_torch_attention": round(ms_sdpa, 3), "steps": steps,
+           "ms_per_step_torch_attention": round(ms_sdpa, 3), "steps": steps, "tuned_gemms": tr.tuned_gemms,
            "warmup": warmup, "model_TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
            "loss": {k: round(float(v), 4) for k, v in out.items()},
            "workload": "0.8B-class decoder gate-training step: 24 layers, hidden 1024, 16x64 q heads, 4 KV heads, "

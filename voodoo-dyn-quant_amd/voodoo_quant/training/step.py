@@ -30,6 +30,7 @@ from __future__ import annotations
 import math
 import warnings
 from dataclasses import dataclass
+from pathlib import Path
 
 import torch
 import torch.nn as nn
@@ -569,6 +570,11 @@ class StepConfig:
     stream_slots: int = 6
     stream_depth: int = 5
     stream_overlap: bool = True
+    # run the plain GEMMs (the Q8_0 teacher's projections, the vocabulary
+    # heads) with the library solutions PyTorch's TunableOp measured fastest
+    # for these shapes on MI355X (use_tuned_gemms); process-wide, so off
+    # unless asked for.  0.8B-class step: 42.2 -> 41.7 ms, one box
+    tuned_gemms: bool = False
     stream_timeline: bool = False   # record timing events per copy and fence (CandidateStreamer.timeline_ms)
     # check the embeddings' ids on the device and raise an out-of-range id at
     # the next step (layers.check_embedding_ids) instead of reading the ids'
@@ -583,12 +589,48 @@ def _embeddings(*models: nn.Module) -> list[nn.Module]:
     return [m for model in models for m in model.modules() if isinstance(m, (layers.MixedQuantEmbedding, Q8Embedding))]
 
 
+# TunableOp results for the step's plain GEMMs on MI355X (ROCm 7, torch
+# 2.10): the Q8_0 teacher's four projections and the tied vocabulary head at
+# 8192 tokens, forward, and the student head's dX (solutions measured by
+# torch.cuda.tunable, a data file, not code)
+GEMM_TUNING_FILE = Path(__file__).resolve().with_name("gemm_tuning_mi355x.csv")
+
+
+def use_tuned_gemms(path: Path | str = GEMM_TUNING_FILE) -> bool:
+    """Turn PyTorch's TunableOp on without tuning, with the results in `path`:
+    GEMMs of the listed shapes then run the hipBLASLt / rocBLAS solution
+    measured fastest for them, every other GEMM the library's default.
+    Process-wide.  Returns False (and changes nothing) without a ROCm device,
+    or when the file's validators (torch, HIP, hipBLASLt and rocBLAS
+    versions, GPU architecture) differ from the running ones."""
+    tun = getattr(torch.cuda, "tunable", None)
+    if tun is None or not torch.cuda.is_available():
+        return False
+    want = {}
+    for line in Path(path).read_text().splitlines():
+        parts = line.split(",")
+        if parts[0] == "Validator" and len(parts) >= 3:
+            want[parts[1]] = ",".join(parts[2:])
+    have = dict(tun.get_validators())
+    if not want or any(have.get(k) != v for k, v in want.items()):
+        warnings.warn(f"{path}: TunableOp validators differ from this runtime; GEMMs keep the library defaults")
+        return False
+    tun.tuning_enable(False)
+    tun.enable(True)
+    if not tun.read_file(str(path)):
+        tun.enable(False)
+        return False
+    return True
+
+
 class GateTrainer:
     """Runs the reference's per-batch gate-training step (``trainer.py:2498-2616``)."""
 
     def __init__(self, student: Decoder, teacher: Decoder, replaced: dict[str, nn.Module], cfg: StepConfig,
                  total_8bit_bytes: float, non_targeted_bytes: float = 0.0):
         self.student, self.teacher, self.replaced, self.cfg = student, teacher, replaced, cfg
+        # whether the plain GEMMs run the tuned solutions (cfg.tuned_gemms)
+        self.tuned_gemms = use_tuned_gemms() if cfg.tuned_gemms else False
         # the chunked loss runs one backward per chunk, so its probabilities
         # must come from each module's own graph
         self.bank = (trainer.GateBank(replaced.values(), cfg.defer_gate_grads)
