@@ -32,10 +32,6 @@ def test_tuned_gemms_match_the_default():
         x = torch.randn(8192, din, device="cuda", generator=g).to(torch.bfloat16)
         w = (torch.randn(dout, din, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
         cases.append((x, w, F.linear(x, w)))
-    # the head's dX product (dlogits W), the one backward shape in the file
-    dl = torch.randn(8192, 151936, device="cuda", generator=g).to(torch.bfloat16)
-    whead = cases[-1][1]
-    dx_default = dl @ whead
     torch.cuda.synchronize()
     try:
         assert st.use_tuned_gemms(), "validators of the tuning file differ from this runtime"
@@ -47,10 +43,6 @@ def test_tuned_gemms_match_the_default():
             assert err_default < 5e-3
             if ref is not None:
                 assert _rel(y1, ref) < 1e-2
-        dx = dl @ whead
-        err = _rel(dx, dx_default)
-        print(f"[tuned] head dX: tuned vs default {err:.2e}", flush=True)
-        assert err < 5e-3
     finally:
         torch.cuda.tunable.enable(False)
 

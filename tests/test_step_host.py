@@ -199,9 +199,9 @@ def test_embedding_id_check_modes_on_the_host():
 
 def test_gemm_tuning_file_lists_the_step_shapes():
     """The TunableOp results file carries validators and one tuned solution
-    for each plain GEMM of the 0.8B-class step (the Q8_0 teacher's four
-    projections and the vocabulary head at 8192 tokens, the head's dX); without
-    a ROCm device use_tuned_gemms changes nothing."""
+    for each plain forward GEMM of the 0.8B-class step (the Q8_0 teacher's four
+    projections and the vocabulary head at 8192 tokens); without a ROCm device
+    use_tuned_gemms changes nothing."""
     from voodoo_quant.training import step as st
 
     rows = [line.split(",") for line in st.GEMM_TUNING_FILE.read_text().splitlines()]
@@ -210,6 +210,5 @@ def test_gemm_tuning_file_lists_the_step_shapes():
     ops = {r[1] for r in rows if r[0].startswith("GemmTunableOp_BFloat16")}
     for n, k in ((1536, 1024), (1024, 1024), (6144, 1024), (1024, 3072), (151936, 1024)):
         assert f"tn_{n}_8192_{k}_ld_{k}_{k}_{n}" in ops
-    assert "nn_1024_8192_151936_ld_1024_151936_1024" in ops
     if not torch.cuda.is_available():
         assert st.use_tuned_gemms() is False

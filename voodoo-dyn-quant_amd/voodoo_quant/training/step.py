@@ -573,7 +573,7 @@ class StepConfig:
     # run the plain GEMMs (the Q8_0 teacher's projections, the vocabulary
     # heads) with the library solutions PyTorch's TunableOp measured fastest
     # for these shapes on MI355X (use_tuned_gemms); process-wide, so off
-    # unless asked for.  0.8B-class step: 42.2 -> 41.7 ms, one box
+    # unless asked for.  0.8B-class step: 42.0 -> 41.6 and 41.2 -> 40.9 ms (two boxes)
     tuned_gemms: bool = False
     stream_timeline: bool = False   # record timing events per copy and fence (CandidateStreamer.timeline_ms)
     # check the embeddings' ids on the device and raise an out-of-range id at
@@ -590,9 +590,9 @@ def _embeddings(*models: nn.Module) -> list[nn.Module]:
 
 
 # TunableOp results for the step's plain GEMMs on MI355X (ROCm 7, torch
-# 2.10): the Q8_0 teacher's four projections and the tied vocabulary head at
-# 8192 tokens, forward, and the student head's dX (solutions measured by
-# torch.cuda.tunable, a data file, not code)
+# 2.10): the Q8_0 teacher's four projections and the vocabulary head at 8192
+# tokens, forward (solutions measured by torch.cuda.tunable; a data file, not
+# code)
 GEMM_TUNING_FILE = Path(__file__).resolve().with_name("gemm_tuning_mi355x.csv")
 
 
