@@ -212,3 +212,43 @@ def test_gemm_tuning_file_lists_the_step_shapes():
         assert f"tn_{n}_8192_{k}_ld_{k}_{k}_{n}" in ops
     if not torch.cuda.is_available():
         assert st.use_tuned_gemms() is False
+
+
+def test_use_tuned_gemms_refuses_other_runtimes(monkeypatch):
+    """With validators that differ from the file's (another torch, ROCm or
+    library build), use_tuned_gemms warns, returns False and leaves TunableOp
+    off; with matching ones it enables it, tuning off, and reads the file."""
+    from voodoo_quant.training import step as st
+
+    calls = []
+
+    class FakeTunable:
+        def __init__(self, validators):
+            self.validators = validators
+
+        def get_validators(self):
+            return self.validators
+
+        def enable(self, on=True):
+            calls.append(("enable", on))
+
+        def tuning_enable(self, on=True):
+            calls.append(("tuning", on))
+
+        def read_file(self, path):
+            calls.append(("read", path))
+            return True
+
+    rows = [line.split(",") for line in st.GEMM_TUNING_FILE.read_text().splitlines()]
+    good = tuple((r[1], ",".join(r[2:])) for r in rows if r[0] == "Validator")
+    bad = tuple((k, v + "-other") if k == "HIPBLASLT_VERSION" else (k, v) for k, v in good)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    monkeypatch.setattr(torch.cuda, "tunable", FakeTunable(bad))
+    with pytest.warns(UserWarning, match="validators"):
+        assert st.use_tuned_gemms() is False
+    assert calls == []
+    monkeypatch.setattr(torch.cuda, "tunable", FakeTunable(good))
+    assert st.use_tuned_gemms() is True
+    assert ("tuning", False) in calls and ("enable", True) in calls
+    assert ("read", str(st.GEMM_TUNING_FILE)) in calls
+    assert calls.index(("tuning", False)) < calls.index(("enable", True))
